@@ -1,0 +1,112 @@
+// Internal types shared by the kernels (moe_kernels.hip) and the layer /
+// C-ABI code (moe_layer.hip).  gfx950 (CDNA4) only, wave64.
+//
+// HBM layout of one layer (all experts resident; the reference streams them
+// over PCIe into an LRU of GPU slots instead, src/session.hip:689-745):
+//   code planes   gate/up [E'][I][H/32][16 B], down [E'][H][I/32][16 B]
+//   scale planes  gate/up [E'][I][H/32] fp16,  down [E'][H][I/32] fp16
+// where E' = E + shared.  Canonical 18-byte Q4_0 blocks (src/quant.hpp:8) are
+// split into a 16-byte-aligned code plane (one dwordx4 per block, coalesced
+// across a wave) and a scale plane.  Activations use the same split:
+//   Q8 code plane [rows][blocks][32 B] and a header plane [rows][blocks] of
+//   u32 = half d | half s << 16 (the two header fields of the 36-byte Q8_1).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+namespace moe {
+
+// Routing and tiling constants.
+inline constexpr int kStreamTokens = 4;     // tokens per streaming (decode) work item
+inline constexpr int kMfmaTile = 128;       // tokens per MFMA work item (4 waves x 32)
+inline constexpr int kSmallGroupTokens = 256;  // single-workgroup grouping limit
+
+struct Bank {
+    const uint8_t *gate_codes, *up_codes, *down_codes;
+    const uint16_t *gate_scales, *up_scales, *down_scales;
+};
+
+// A work item: one expert group slice of <= kStreamTokens (stream path) or
+// <= kMfmaTile (MFMA path) consecutive grouped pairs.
+struct Item {
+    int expert, first, ncols, pad;
+};
+
+struct Shape {
+    int H, I, E, Ep, k;   // Ep = E + has_shared
+};
+
+struct RouteOut {
+    int32_t *counts;       // [Ep]
+    int32_t *offsets;      // [Ep+1]
+    int32_t *pair_token;   // [P']
+    int32_t *pair_rank;    // [P']  (rank k = shared expert)
+    int32_t *pos_of;       // [N*k] grouped position of (t, r) or -1
+    Item *stream_items;    // [<= P'/kStreamTokens + Ep]
+    Item *mfma_items;      // [<= P'/kMfmaTile + Ep]
+    int32_t *item_counts;  // [0] stream, [1] mfma, [2] active experts
+    uint32_t *bitmap;      // large path: [W][Ep] token bitmaps
+    uint32_t *wprefix;     // large path: [W][Ep] per-word exclusive popcount prefix
+};
+
+struct Act {               // split-plane Q8 rows
+    uint8_t *codes;        // [rows][blocks][32]
+    uint32_t *heads;       // [rows][blocks]
+};
+
+// ----------------------------------------------------------------------------
+// Kernel launchers (moe_kernels.hip).  All return hipGetLastError() after the
+// enqueue; argument validation is done by the callers in moe_layer.hip.
+hipError_t launch_quantize_canonical(const float *x, void *q8, int width, int columns, int *error,
+                                     hipStream_t s);
+hipError_t launch_quantize_planes(const float *x, Act out, int width, int columns, int *error,
+                                  hipStream_t s);
+hipError_t launch_canonical_to_planes(const void *q8, Act out, int blocks, hipStream_t s);
+hipError_t launch_planes_to_canonical(Act in, void *q8, int blocks, hipStream_t s);
+
+hipError_t launch_repack_weights(const uint8_t *canonical, uint8_t *codes, uint16_t *scales,
+                                 size_t blocks, hipStream_t s);
+hipError_t launch_unpack_weights(const uint8_t *codes, const uint16_t *scales, uint8_t *canonical,
+                                 size_t blocks, hipStream_t s);
+hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, size_t blocks, size_t block0,
+                                    uint64_t seed, hipStream_t s);
+
+// Quantize x into `xq` and group routes (tokens <= kSmallGroupTokens path or
+// the multi-kernel path).  mfma_min = smallest group that goes to MFMA (0 = never).
+hipError_t launch_prepare(const float *x, const int32_t *ids, const float *weights, int tokens,
+                          Shape shape, Act xq, RouteOut routes, int mfma_min, int *error,
+                          hipStream_t s);
+
+// Single-expert stage setup: pairs 0..columns-1 = tokens 0..columns-1 of
+// expert `expert`; all columns go to one path (use_mfma).
+hipError_t launch_single_expert_items(Shape shape, RouteOut routes, int expert, int columns,
+                                      int use_mfma, hipStream_t s);
+
+struct FfnArgs {
+    Shape shape;
+    Bank bank;
+    Act xq;            // activations [tokens]
+    Act mq;            // middle [pairs]
+    RouteOut routes;
+    float *out;        // contributions: row = token*out_stride_k + rank
+    int out_stride_k;  // rows per token in `out` (k+1 for forward, 1 for stages)
+    int tokens;
+    int pairs_bound;   // upper bound on grouped pairs (for grid sizing)
+    float *middle_f32; // optional [pairs][I]
+    int32_t *gate_dots, *up_dots, *down_dots;  // optional per-block dots [pair][rows][blocks]
+    int *error;
+};
+
+hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s);
+hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s);
+
+hipError_t launch_fold(const float *contributions, size_t token_stride, const float *weights, int k,
+                       const int32_t *pos_of, const float *shared, size_t shared_stride,
+                       const float *shared_gate, int tokens, int H, float *y, int *error,
+                       hipStream_t s);
+
+hipError_t launch_fill_u32(uint32_t *p, uint32_t value, size_t count, hipStream_t s);
+
+}  // namespace moe

@@ -1,0 +1,837 @@
+// Routed-MoE Q4_0 x Q8_1 expert FFN kernels for MI355X (gfx950, CDNA4, wave64).
+//
+// Arithmetic contract (reference 0FL01/gfx906-qwen3.8fn):
+//   Q8_1 quantization  src/quant.cpp:275-325, GPU form src/hip/linear.hip:99-150
+//   Q4_0 block dot     src/quant.cpp:48-55   (unsigned nibbles x signed codes)
+//   block scaling      src/quant.cpp:88-93   d4 * (I*d8 - 8*s8)
+//   SiLU(gate)*up      src/hip/linear.hip:106-120 (sanitised, device expf)
+//   rank-order fold    src/hip/session_ops.hip:307-324, shared add :375-391
+// The per-block int32 dots and the Q8 codes are bit-exact with the reference;
+// the fp32 accumulation order across blocks is this implementation's own.
+#include "moe_internal.hpp"
+
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+
+#if defined(__FAST_MATH__)
+#error "moe kernels require strict IEEE fp32 (correctly rounded division for Q8 scales)"
+#endif
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "moe kernels are written for gfx950 (CDNA4)"
+#endif
+#pragma clang fp contract(off)
+
+namespace moe {
+namespace {
+
+// ------------------------------------------------------------ primitives ---
+__device__ __forceinline__ float h2f(uint32_t bits) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(bits & 0xffffu)));
+}
+__device__ __forceinline__ uint32_t f2h(float v) {
+    return __half_as_ushort(__float2half_rn(v));
+}
+
+// Integer block dot over one Q4_0 code chunk (16 bytes: byte j holds element j
+// in its low nibble and element j+16 in its high nibble) and 32 Q8 codes
+// (x0 = codes 0..15, x1 = codes 16..31).  Nibbles are 0..15, so v_dot4_i32_i8
+// on the masked bytes is the exact unsigned-nibble x signed-code sum.
+__device__ __forceinline__ int dot_block(uint4 w, uint4 x0, uint4 x1) {
+    constexpr uint32_t m = 0x0f0f0f0fu;
+    int s = 0;
+    s = __builtin_amdgcn_sdot4(static_cast<int>(w.x & m), static_cast<int>(x0.x), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>(w.y & m), static_cast<int>(x0.y), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>(w.z & m), static_cast<int>(x0.z), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>(w.w & m), static_cast<int>(x0.w), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((w.x >> 4) & m), static_cast<int>(x1.x), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((w.y >> 4) & m), static_cast<int>(x1.y), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((w.z >> 4) & m), static_cast<int>(x1.z), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((w.w >> 4) & m), static_cast<int>(x1.w), s, false);
+    return s;
+}
+
+__device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
+
+// One Q8_1 block from 32 lanes (lane32 = element index).  Semantics of the
+// reference GPU quantizer (src/hip/linear.hip:121-149): a nonfinite element
+// poisons its block (bit 1), an unrepresentable scale/sum/code sets bit 2,
+// and a failing block is written as all zero.  The raw sum is the ascending
+// XOR butterfly 1,2,4,8,16 of the (sanitised) inputs -- each stage adds the
+// partner's value, so both partners hold the same sum as in the reference.
+struct Q8Lane {
+    int8_t code;
+    uint32_t head;   // half d | half s << 16 (valid in every lane)
+    int flags;       // per-block flags (valid in every lane)
+};
+
+__device__ __forceinline__ Q8Lane quantize32(float x) {
+    int bad = !isfinite(x);
+    if (bad) x = 0.0f;
+    float amax = fabsf(x);
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+        bad |= __shfl_xor(bad, m, 32);
+    }
+    float sum = x;
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) sum = sum + __shfl_xor(sum, m, 32);
+    const float d = amax / 127.0f;
+    const uint32_t hd = f2h(d), hs = f2h(sum);
+    const bool representable = isfinite(sum) && (hs & 0x7c00u) != 0x7c00u &&
+                               (hd & 0x7c00u) != 0x7c00u && (amax == 0.0f || d > 0.0f);
+    const float code = (!bad && representable && amax != 0.0f) ? roundf(x / d) : 0.0f;
+    int bad_code = !isfinite(code) || code < -127.0f || code > 127.0f;
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) bad_code |= __shfl_xor(bad_code, m, 32);
+    const bool valid = !bad && representable && !bad_code;
+    Q8Lane q;
+    q.code = valid ? static_cast<int8_t>(code) : int8_t{0};
+    q.head = (valid && amax != 0.0f) ? (hd | (hs << 16)) : 0u;
+    q.flags = (bad ? 1 : 0) | ((representable && !bad_code) ? 0 : 2);
+    return q;
+}
+
+// SiLU(g)*u with the reference's sanitisation (src/hip/linear.hip:106-120).
+__device__ __forceinline__ float silu_mul(float g, float u, int &flags) {
+    if (!isfinite(g)) { flags |= 1; g = 0.0f; }
+    if (!isfinite(u)) { flags |= 1; u = 0.0f; }
+    float a = g / (1.0f + expf(-g));
+    if (!isfinite(a)) { flags |= 2; a = 0.0f; }
+    float v = a * u;
+    if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+    return flags ? 0.0f : v;
+}
+
+// ------------------------------------------------------------ quantizers ---
+// One thread per element; 32-lane groups are whole Q8 blocks.
+template<bool Canonical>
+__global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ x, uint8_t *codes,
+                                                  uint32_t *heads, size_t elements, int *error) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= elements) return;   // elements is a multiple of 32: whole groups exit together
+    const Q8Lane q = quantize32(x[i]);
+    const size_t block = i >> 5;
+    const int lane = static_cast<int>(i & 31);
+    if constexpr (Canonical) {
+        codes[block * 36 + 4 + lane] = static_cast<uint8_t>(q.code);
+        if (lane == 0) *reinterpret_cast<uint32_t *>(codes + block * 36) = q.head;
+    } else {
+        codes[block * 32 + lane] = static_cast<uint8_t>(q.code);
+        if (lane == 0) heads[block] = q.head;
+    }
+    if (lane == 0 && q.flags) atomicOr(error, q.flags);
+}
+
+__global__ __launch_bounds__(256) void k_canonical_to_planes(const uint8_t *q8, uint8_t *codes,
+                                                             uint32_t *heads, size_t blocks) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= blocks * 9) return;
+    const size_t b = i / 9, w = i % 9;
+    const uint32_t v = reinterpret_cast<const uint32_t *>(q8)[i];
+    if (w == 0) heads[b] = v;
+    else reinterpret_cast<uint32_t *>(codes)[b * 8 + (w - 1)] = v;
+}
+
+__global__ __launch_bounds__(256) void k_planes_to_canonical(const uint8_t *codes, const uint32_t *heads,
+                                                             uint8_t *q8, size_t blocks) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= blocks * 9) return;
+    const size_t b = i / 9, w = i % 9;
+    const uint32_t v = w == 0 ? heads[b] : reinterpret_cast<const uint32_t *>(codes)[b * 8 + (w - 1)];
+    reinterpret_cast<uint32_t *>(q8)[i] = v;
+}
+
+// ---------------------------------------------------------- weight planes ---
+// Canonical blocks are 18 bytes with 2-byte alignment: read them as 9 u16.
+__global__ __launch_bounds__(256) void k_repack(const uint16_t *canonical, uint32_t *codes,
+                                                uint16_t *scales, size_t blocks) {
+    const size_t b = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    const uint16_t *src = canonical + b * 9;
+    scales[b] = src[0];
+    uint4 c;
+    c.x = src[1] | (static_cast<uint32_t>(src[2]) << 16);
+    c.y = src[3] | (static_cast<uint32_t>(src[4]) << 16);
+    c.z = src[5] | (static_cast<uint32_t>(src[6]) << 16);
+    c.w = src[7] | (static_cast<uint32_t>(src[8]) << 16);
+    reinterpret_cast<uint4 *>(codes)[b] = c;
+}
+
+__global__ __launch_bounds__(256) void k_unpack(const uint32_t *codes, const uint16_t *scales,
+                                                uint16_t *canonical, size_t blocks) {
+    const size_t b = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    const uint4 c = reinterpret_cast<const uint4 *>(codes)[b];
+    uint16_t *dst = canonical + b * 9;
+    dst[0] = scales[b];
+    dst[1] = c.x & 0xffffu; dst[2] = c.x >> 16;
+    dst[3] = c.y & 0xffffu; dst[4] = c.y >> 16;
+    dst[5] = c.z & 0xffffu; dst[6] = c.z >> 16;
+    dst[7] = c.w & 0xffffu; dst[8] = c.w >> 16;
+}
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+// Synthetic Q4_0 blocks: codes uniform 0..15 (16 random bytes), d =
+// half(|N(0, 0.02)|) by Box-Muller, all from a counter hash of (seed, block).
+__global__ __launch_bounds__(256) void k_synthetic(uint32_t *codes, uint16_t *scales, size_t blocks,
+                                                   size_t block0, uint64_t seed) {
+    const size_t b = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    const uint64_t g = block0 + b;
+    const uint64_t h0 = mix64(seed ^ mix64(4 * g + 0)), h1 = mix64(seed ^ mix64(4 * g + 1));
+    const uint64_t h2 = mix64(seed ^ mix64(4 * g + 2));
+    uint4 c;
+    c.x = static_cast<uint32_t>(h0); c.y = static_cast<uint32_t>(h0 >> 32);
+    c.z = static_cast<uint32_t>(h1); c.w = static_cast<uint32_t>(h1 >> 32);
+    reinterpret_cast<uint4 *>(codes)[b] = c;
+    const float u1 = (static_cast<float>(h2 >> 40) + 1.0f) * 0x1p-24f;          // (0, 1]
+    const float u2 = static_cast<float>((h2 >> 16) & 0xffffffu) * 0x1p-24f;      // [0, 1)
+    const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    scales[b] = static_cast<uint16_t>(f2h(fabsf(z) * 0.02f));
+}
+
+__global__ __launch_bounds__(256) void k_fill_u32(uint32_t *p, uint32_t v, size_t n) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// ------------------------------------------------------------- grouping ----
+// Grouping replaces RouteGroups::prepare (src/routes.cpp:126-182): groups
+// ascend by expert, within a group by token then rank.  Each expert keeps a
+// token bitmap; a pair's position is offset[e] + (popcount of the expert's
+// bits for earlier tokens), which is the stable counting-sort position,
+// computed without any ordering between threads.  The shared expert is group
+// E, holding every token once (rank = k).
+
+// Validates entry (t, r) (src/routes.cpp:145-157); returns the expert or -1 if
+// the entry cannot be grouped (bad id or duplicate of an earlier rank).
+__device__ __forceinline__ int route_entry(const int32_t *ids, const float *weights, int t, int r, int k,
+                                           int E, int &flags) {
+    const size_t base = static_cast<size_t>(t) * k;
+    const int e = ids[base + r];
+    const float w = weights[base + r];
+    if (!isfinite(w) || w < 0.0f) flags |= 1;
+    if (e < 0 || e >= E) { flags |= 1; return -1; }
+    for (int q = 0; q < r; ++q)
+        if (ids[base + q] == e) { flags |= 1; return -1; }
+    return e;
+}
+
+// Block-wide exclusive scan of n ints (any n) by a 1024-thread block.
+__device__ int block_exclusive_scan(const int32_t *in, int32_t *out, int n, int32_t *tmp) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int per = (n + blockDim.x - 1) / blockDim.x;
+    const int lo = min(n, tid * per), hi = min(n, lo + per);
+    int local = 0;
+    for (int i = lo; i < hi; ++i) local += in[i];
+    int incl = local;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += v;
+    }
+    if (lane == 63) tmp[wave] = incl;
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int w = 0; w < nw; ++w) { const int v = tmp[w]; tmp[w] = run; run += v; }
+        tmp[nw] = run;
+    }
+    __syncthreads();
+    int run = tmp[wave] + incl - local;
+    for (int i = lo; i < hi; ++i) { const int v = in[i]; out[i] = run; run += v; }
+    const int total = tmp[nw];
+    __syncthreads();
+    return total;
+}
+
+struct GroupParams {
+    const int32_t *ids;
+    const float *weights;
+    int tokens;
+    Shape shape;
+    RouteOut r;
+    int mfma_min;
+    int *error;
+};
+
+// Items from group counts/offsets: groups below mfma_min (or all groups when
+// mfma_min == 0) become streaming items of <= kStreamTokens pairs, larger
+// groups become MFMA items of <= kMfmaTile pairs.  cnt/off may live in LDS.
+__device__ void build_items(const GroupParams &p, const int32_t *cnt, const int32_t *off, int32_t *ns,
+                            int32_t *nm, int32_t *tmp) {
+    const int Ep = p.shape.Ep;
+    for (int e = threadIdx.x; e < Ep; e += blockDim.x) {
+        const int n = cnt[e];
+        const bool big = p.mfma_min > 0 && n >= p.mfma_min;
+        ns[e] = (n > 0 && !big) ? (n + kStreamTokens - 1) / kStreamTokens : 0;
+        nm[e] = big ? (n + kMfmaTile - 1) / kMfmaTile : 0;
+    }
+    __syncthreads();
+    const int total_s = block_exclusive_scan(ns, ns, Ep, tmp);
+    const int total_m = block_exclusive_scan(nm, nm, Ep, tmp);
+    for (int e = threadIdx.x; e < Ep; e += blockDim.x) {
+        const int n = cnt[e];
+        if (n == 0) continue;
+        const bool big = p.mfma_min > 0 && n >= p.mfma_min;
+        const int size = big ? kMfmaTile : kStreamTokens;
+        Item *dst = big ? p.r.mfma_items + nm[e] : p.r.stream_items + ns[e];
+        for (int c = 0, f = 0; f < n; ++c, f += size) {
+            Item it;
+            it.expert = e; it.first = off[e] + f; it.ncols = min(size, n - f); it.pad = 0;
+            dst[c] = it;
+        }
+    }
+    if (threadIdx.x == 0) {
+        int active = 0;
+        for (int e = 0; e < Ep; ++e) active += cnt[e] > 0;
+        p.r.item_counts[0] = total_s;
+        p.r.item_counts[1] = total_m;
+        p.r.item_counts[2] = active;
+    }
+}
+
+// Small path: block 0 groups (bitmaps in LDS), blocks 1.. quantize x.
+__global__ __launch_bounds__(1024) void k_prepare_small(GroupParams p, const float *__restrict__ x,
+                                                        Act xq, size_t q_elements) {
+    extern __shared__ uint32_t lds[];
+    if (blockIdx.x > 0) {
+        const size_t i = static_cast<size_t>(blockIdx.x - 1) * blockDim.x + threadIdx.x;
+        if (i >= q_elements) return;
+        const Q8Lane q = quantize32(x[i]);
+        const size_t block = i >> 5;
+        const int lane = static_cast<int>(i & 31);
+        xq.codes[block * 32 + lane] = static_cast<uint8_t>(q.code);
+        if (lane == 0) {
+            xq.heads[block] = q.head;
+            if (q.flags) atomicOr(p.error, q.flags);
+        }
+        return;
+    }
+    const int N = p.tokens, k = p.shape.k, E = p.shape.E, Ep = p.shape.Ep;
+    const int W = (N + 31) / 32;
+    uint32_t *bits = lds;                                               // [E][W]
+    uint32_t *wpre = bits + E * W;                                      // [E][W]
+    int32_t *cnt = reinterpret_cast<int32_t *>(wpre + E * W);           // [Ep]
+    int32_t *off = cnt + Ep;                                            // [Ep+1]
+    int32_t *ns = off + Ep + 1;                                         // [Ep]
+    int32_t *nm = ns + Ep;                                              // [Ep]
+    int32_t *tmp = nm + Ep;                                             // [17]
+    for (int i = threadIdx.x; i < E * W; i += blockDim.x) bits[i] = 0;
+    __syncthreads();
+    int flags = 0;
+    for (int t = threadIdx.x; t < N; t += blockDim.x)
+        for (int r = 0; r < k; ++r) {
+            const int e = route_entry(p.ids, p.weights, t, r, k, E, flags);
+            if (e >= 0) atomicOr(&bits[e * W + (t >> 5)], 1u << (t & 31));
+        }
+    __syncthreads();
+    for (int e = threadIdx.x; e < Ep; e += blockDim.x) {
+        if (e >= E) { cnt[e] = N; continue; }   // shared expert: every token
+        int run = 0;
+        for (int w = 0; w < W; ++w) { wpre[e * W + w] = run; run += __popc(bits[e * W + w]); }
+        cnt[e] = run;
+    }
+    __syncthreads();
+    const int total = block_exclusive_scan(cnt, off, Ep, tmp);
+    if (threadIdx.x == 0) off[Ep] = total;
+    __syncthreads();
+    for (int t = threadIdx.x; t < N; t += blockDim.x) {
+        for (int r = 0; r < k; ++r) {
+            int dummy = 0;
+            const int e = route_entry(p.ids, p.weights, t, r, k, E, dummy);
+            int pos = -1;
+            if (e >= 0) {
+                const uint32_t word = bits[e * W + (t >> 5)];
+                pos = off[e] + static_cast<int>(wpre[e * W + (t >> 5)]) +
+                      __popc(word & ((1u << (t & 31)) - 1u));
+                p.r.pair_token[pos] = t;
+                p.r.pair_rank[pos] = r;
+            }
+            p.r.pos_of[static_cast<size_t>(t) * k + r] = pos;
+        }
+        if (Ep > E) { p.r.pair_token[off[E] + t] = t; p.r.pair_rank[off[E] + t] = k; }
+    }
+    for (int e = threadIdx.x; e < Ep; e += blockDim.x) { p.r.counts[e] = cnt[e]; p.r.offsets[e] = off[e]; }
+    if (threadIdx.x == 0) p.r.offsets[Ep] = off[Ep];
+    build_items(p, cnt, off, ns, nm, tmp);
+    if (flags) atomicOr(p.error, flags);
+}
+
+// Large path, step 1: blocks [0, mark_blocks) set bitmap bits (one thread per
+// token), the rest quantize x.  The bitmap is [W][Ep] (word-major) so the
+// per-expert prefix kernel reads it coalesced.
+__global__ __launch_bounds__(256) void k_mark_quantize(GroupParams p, int mark_blocks,
+                                                       const float *__restrict__ x, Act xq,
+                                                       size_t q_elements) {
+    if (static_cast<int>(blockIdx.x) < mark_blocks) {
+        const int t = blockIdx.x * blockDim.x + threadIdx.x;
+        if (t >= p.tokens) return;
+        int flags = 0;
+        for (int r = 0; r < p.shape.k; ++r) {
+            const int e = route_entry(p.ids, p.weights, t, r, p.shape.k, p.shape.E, flags);
+            if (e >= 0) atomicOr(&p.r.bitmap[static_cast<size_t>(t >> 5) * p.shape.Ep + e], 1u << (t & 31));
+        }
+        if (flags) atomicOr(p.error, flags);
+        return;
+    }
+    const size_t i = static_cast<size_t>(blockIdx.x - mark_blocks) * blockDim.x + threadIdx.x;
+    if (i >= q_elements) return;
+    const Q8Lane q = quantize32(x[i]);
+    const size_t block = i >> 5;
+    const int lane = static_cast<int>(i & 31);
+    xq.codes[block * 32 + lane] = static_cast<uint8_t>(q.code);
+    if (lane == 0) {
+        xq.heads[block] = q.head;
+        if (q.flags) atomicOr(p.error, q.flags);
+    }
+}
+
+// Step 2: one wave per routed expert: exclusive popcount prefix over words.
+__global__ __launch_bounds__(256) void k_word_prefix(GroupParams p) {
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (e >= p.shape.E) return;
+    const int W = (p.tokens + 31) / 32, Ep = p.shape.Ep;
+    int carry = 0;
+    for (int w0 = 0; w0 < W; w0 += 64) {
+        const int w = w0 + lane;
+        const int c = w < W ? __popc(p.r.bitmap[static_cast<size_t>(w) * Ep + e]) : 0;
+        int incl = c;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int v = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += v;
+        }
+        if (w < W) p.r.wprefix[static_cast<size_t>(w) * Ep + e] = static_cast<uint32_t>(carry + incl - c);
+        carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) p.r.counts[e] = carry;
+}
+
+// Step 3 (single block): offsets, shared group, items.
+__global__ __launch_bounds__(1024) void k_offsets_items(GroupParams p) {
+    extern __shared__ uint32_t lds[];
+    const int Ep = p.shape.Ep;
+    int32_t *cnt = reinterpret_cast<int32_t *>(lds);
+    int32_t *off = cnt + Ep;
+    int32_t *ns = off + Ep + 1;
+    int32_t *nm = ns + Ep;
+    int32_t *tmp = nm + Ep;
+    for (int e = threadIdx.x; e < Ep; e += blockDim.x) cnt[e] = e < p.shape.E ? p.r.counts[e] : p.tokens;
+    __syncthreads();
+    const int total = block_exclusive_scan(cnt, off, Ep, tmp);
+    if (threadIdx.x == 0) off[Ep] = total;
+    __syncthreads();
+    for (int e = threadIdx.x; e < Ep; e += blockDim.x) { p.r.counts[e] = cnt[e]; p.r.offsets[e] = off[e]; }
+    if (threadIdx.x == 0) p.r.offsets[Ep] = off[Ep];
+    build_items(p, cnt, off, ns, nm, tmp);
+}
+
+// Step 4: one thread per token places its pairs.
+__global__ __launch_bounds__(256) void k_scatter_pairs(GroupParams p) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= p.tokens) return;
+    const int k = p.shape.k, E = p.shape.E, Ep = p.shape.Ep;
+    for (int r = 0; r < k; ++r) {
+        int dummy = 0;
+        const int e = route_entry(p.ids, p.weights, t, r, k, E, dummy);
+        int pos = -1;
+        if (e >= 0) {
+            const size_t wi = static_cast<size_t>(t >> 5) * Ep + e;
+            pos = p.r.offsets[e] + static_cast<int>(p.r.wprefix[wi]) +
+                  __popc(p.r.bitmap[wi] & ((1u << (t & 31)) - 1u));
+            p.r.pair_token[pos] = t;
+            p.r.pair_rank[pos] = r;
+        }
+        p.r.pos_of[static_cast<size_t>(t) * k + r] = pos;
+    }
+    if (Ep > E) {
+        const int s = p.r.offsets[E] + t;
+        p.r.pair_token[s] = t;
+        p.r.pair_rank[s] = k;
+    }
+}
+
+// Single-expert stage setup (one block).
+__global__ void k_single_items(Shape shape, RouteOut r, int expert, int columns, int use_mfma) {
+    for (int j = threadIdx.x; j < columns; j += blockDim.x) { r.pair_token[j] = j; r.pair_rank[j] = 0; }
+    if (threadIdx.x == 0) {
+        const int size = use_mfma ? kMfmaTile : kStreamTokens;
+        Item *dst = use_mfma ? r.mfma_items : r.stream_items;
+        int c = 0;
+        for (int f = 0; f < columns; f += size, ++c) {
+            Item it;
+            it.expert = expert; it.first = f; it.ncols = min(size, columns - f); it.pad = 0;
+            dst[c] = it;
+        }
+        r.item_counts[0] = use_mfma ? 0 : c;
+        r.item_counts[1] = use_mfma ? c : 0;
+        r.item_counts[2] = 1;
+        (void)shape;
+    }
+}
+
+// ------------------------------------------------ streaming (decode) path ---
+// gate/up + SiLU + Q8.  One work unit = (item, slice of 32 intermediate rows).
+// 8 waves: waves 0-3 take gate rows slice*32 + 8w .. +7, waves 4-7 the same
+// up rows.  Lane l takes blocks l, l+64, ...: each row is one coalesced
+// 16-byte-per-lane wave load of the code plane.  After the K loop the 8 row
+// sums of each token are reduced across the wave by a transposing butterfly
+// (xor 32/16/8 halve the row set, xor 4/2/1 finish the sum), the 64 sums go
+// through LDS, and wave j quantizes token j's 32 SiLU(g)*u values into one
+// Q8_1 block of the middle.
+template<bool Dbg>
+__global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
+    constexpr int T = kStreamTokens;
+    __shared__ float gu[2][32][T];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32, S = I / 32;
+    const int units = a.routes.item_counts[0] * S;
+    const int mat = wave >> 2;
+    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+        const Item it = a.routes.stream_items[u / S];
+        const int s = u % S;
+        const int row0 = s * 32 + (wave & 3) * 8;
+        const size_t mrow = static_cast<size_t>(it.expert) * I + row0;
+        const uint8_t *codes = (mat ? a.bank.up_codes : a.bank.gate_codes) + mrow * nbh * 16;
+        const uint16_t *scales = (mat ? a.bank.up_scales : a.bank.gate_scales) + mrow * nbh;
+        int tok[T];
+#pragma unroll
+        for (int j = 0; j < T; ++j) tok[j] = a.routes.pair_token[it.first + min(j, it.ncols - 1)];
+        float acc[8][T];
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int j = 0; j < T; ++j) acc[r][j] = 0.0f;
+        for (int kb = lane; kb < nbh; kb += 64) {
+            uint4 w[8];
+            float d4[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                w[r] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbh + kb) * 16);
+                d4[r] = h2f(scales[static_cast<size_t>(r) * nbh + kb]);
+            }
+#pragma unroll
+            for (int j = 0; j < T; ++j) {
+                if (j >= it.ncols) break;
+                const size_t xb = static_cast<size_t>(tok[j]) * nbh + kb;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(a.xq.codes + xb * 32);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(a.xq.codes + xb * 32 + 16);
+                const uint32_t hd = a.xq.heads[xb];
+                const float d8 = h2f(hd), c8 = -8.0f * h2f(hd >> 16);
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    const int dot = dot_block(w[r], x0, x1);
+                    if constexpr (Dbg) {
+                        int32_t *dots = mat ? a.up_dots : a.gate_dots;
+                        if (dots) dots[(static_cast<size_t>(it.first + j) * I + row0 + r) * nbh + kb] = dot;
+                    }
+                    acc[r][j] = fmaf(d4[r], fmaf(static_cast<float>(dot), d8, c8), acc[r][j]);
+                }
+            }
+        }
+        // Transposing reduction: lane ends with the sum of row rho(lane).
+        const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+        const int rho = (b5 ? 4 : 0) + (b4 ? 2 : 0) + (b3 ? 1 : 0);
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+            if (j >= it.ncols) break;
+            float v4[4], v2[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float send = b5 ? acc[i][j] : acc[i + 4][j];
+                const float keep = b5 ? acc[i + 4][j] : acc[i][j];
+                v4[i] = keep + __shfl_xor(send, 32, 64);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float send = b4 ? v4[i] : v4[i + 2];
+                const float keep = b4 ? v4[i + 2] : v4[i];
+                v2[i] = keep + __shfl_xor(send, 16, 64);
+            }
+            float v = (b3 ? v2[1] : v2[0]) + __shfl_xor(b3 ? v2[0] : v2[1], 8, 64);
+            v = xor_sum(v, 4);
+            v = xor_sum(v, 2);
+            v = xor_sum(v, 1);
+            if ((lane & 7) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
+        }
+        __syncthreads();
+        if (wave < it.ncols) {
+            const int j = wave, i = lane & 31;
+            int flags = 0;
+            const float m = silu_mul(gu[0][i][j], gu[1][i][j], flags);
+            const Q8Lane q = quantize32(m);
+            if (lane < 32) {
+                const size_t pair = static_cast<size_t>(it.first + j);
+                const size_t mb = pair * nbi + s;
+                a.mq.codes[mb * 32 + i] = static_cast<uint8_t>(q.code);
+                if (i == 0) a.mq.heads[mb] = q.head;
+                if (Dbg && a.middle_f32) a.middle_f32[pair * I + s * 32 + i] = m;
+                const int f = flags | (i == 0 ? q.flags : 0);
+                if (f) atomicOr(a.error, f);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Down projection, streaming path.  Work unit = (item, slice of 64 output
+// rows); 8 waves x 8 rows.  With I/32 = 16 blocks a row is 256 code bytes, so
+// a wave load covers 4 rows (16 lanes per row).  Unweighted results go to the
+// contribution row (token * out_stride_k + rank) like the reference's scatter
+// (src/hip/session_ops.hip:357-373).
+template<int LPR, bool Dbg>
+__global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
+    constexpr int T = kStreamTokens, RPL = 64 / LPR, LOADS = 8 / RPL;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int H = a.shape.H, I = a.shape.I, nbi = I / 32, S = H / 64;
+    const int units = a.routes.item_counts[0] * S;
+    const int sub = lane / LPR, kb0 = lane % LPR;
+    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+        const Item it = a.routes.stream_items[u / S];
+        const int row0 = (u % S) * 64 + wave * 8;
+        const size_t mrow = static_cast<size_t>(it.expert) * H + row0;
+        const uint8_t *codes = a.bank.down_codes + mrow * nbi * 16;
+        const uint16_t *scales = a.bank.down_scales + mrow * nbi;
+        float acc[LOADS][T];
+#pragma unroll
+        for (int l = 0; l < LOADS; ++l)
+#pragma unroll
+            for (int j = 0; j < T; ++j) acc[l][j] = 0.0f;
+        for (int kb = kb0; kb < nbi; kb += LPR) {
+            uint4 w[LOADS];
+            float d4[LOADS];
+#pragma unroll
+            for (int l = 0; l < LOADS; ++l) {
+                const int r = l * RPL + sub;
+                w[l] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbi + kb) * 16);
+                d4[l] = h2f(scales[static_cast<size_t>(r) * nbi + kb]);
+            }
+#pragma unroll
+            for (int j = 0; j < T; ++j) {
+                if (j >= it.ncols) break;
+                const size_t xb = static_cast<size_t>(it.first + j) * nbi + kb;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(a.mq.codes + xb * 32);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(a.mq.codes + xb * 32 + 16);
+                const uint32_t hd = a.mq.heads[xb];
+                const float d8 = h2f(hd), c8 = -8.0f * h2f(hd >> 16);
+#pragma unroll
+                for (int l = 0; l < LOADS; ++l) {
+                    const int dot = dot_block(w[l], x0, x1);
+                    if constexpr (Dbg) {
+                        if (a.down_dots)
+                            a.down_dots[(static_cast<size_t>(it.first + j) * H + row0 + l * RPL + sub) * nbi + kb] = dot;
+                    }
+                    acc[l][j] = fmaf(d4[l], fmaf(static_cast<float>(dot), d8, c8), acc[l][j]);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+            if (j >= it.ncols) break;
+            const int pair = it.first + j;
+            const size_t orow = static_cast<size_t>(a.routes.pair_token[pair]) * a.out_stride_k +
+                                a.routes.pair_rank[pair];
+#pragma unroll
+            for (int l = 0; l < LOADS; ++l) {
+                float v = acc[l][j];
+#pragma unroll
+                for (int m = LPR / 2; m >= 1; m >>= 1) v = xor_sum(v, m);
+                if (kb0 == 0) a.out[orow * H + row0 + l * RPL + sub] = v;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ fold ---
+// y = +0; y = y + (w_r * c_r) for r = 0..k-1 (separately rounded, rank
+// order); then y = y + scale * shared with scale = 1/(1+expf(-g)) or 1.
+// Nonfinite operands set bit 1, nonfinite results bit 2, and zero the output
+// element (src/hip/session_ops.hip:307-324, 375-391).  Pairs that could not
+// be grouped (pos_of < 0: bad id / duplicate, already flagged) contribute 0.
+__global__ __launch_bounds__(256) void k_fold(const float *__restrict__ c, size_t token_stride,
+                                              const float *__restrict__ w, int k, const int32_t *pos_of,
+                                              const float *__restrict__ shared, size_t shared_stride,
+                                              const float *__restrict__ shared_gate, int tokens, int H,
+                                              float *__restrict__ y, int *error) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<size_t>(tokens) * H) return;
+    const size_t t = i / H, h = i % H;
+    int flags = 0;
+    float v = 0.0f;
+    for (int r = 0; r < k; ++r) {
+        if (pos_of && pos_of[t * k + r] < 0) continue;
+        float x = c[t * token_stride + static_cast<size_t>(r) * H + h];
+        float s = w[t * k + r];
+        if (!isfinite(x)) { flags |= 1; x = 0.0f; }
+        if (!isfinite(s)) { flags |= 1; s = 0.0f; }
+        float p = s * x;
+        if (!isfinite(p)) { flags |= 2; p = 0.0f; }
+        v = v + p;
+        if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+    }
+    if (shared) {
+        float x = shared[t * shared_stride + h];
+        if (!isfinite(x)) { flags |= 1; x = 0.0f; }
+        float scale = 1.0f;
+        if (shared_gate) {
+            float g = shared_gate[t];
+            if (!isfinite(g)) { flags |= 1; g = 0.0f; }
+            scale = 1.0f / (1.0f + expf(-g));
+            if (!isfinite(scale)) { flags |= 2; scale = 0.0f; }
+        }
+        float p = scale * x;
+        if (!isfinite(p)) { flags |= 2; p = 0.0f; }
+        v = v + p;
+        if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+    }
+    y[i] = flags ? 0.0f : v;
+    if (flags) atomicOr(error, flags);
+}
+
+inline unsigned blocks_for(size_t n, unsigned per) { return static_cast<unsigned>((n + per - 1) / per); }
+
+}  // namespace
+
+// -------------------------------------------------------------- launchers ---
+hipError_t launch_quantize_canonical(const float *x, void *q8, int width, int columns, int *error,
+                                     hipStream_t s) {
+    const size_t n = static_cast<size_t>(width) * columns;
+    k_quantize<true><<<blocks_for(n, 256), 256, 0, s>>>(x, static_cast<uint8_t *>(q8), nullptr, n, error);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_planes(const float *x, Act out, int width, int columns, int *error,
+                                  hipStream_t s) {
+    const size_t n = static_cast<size_t>(width) * columns;
+    k_quantize<false><<<blocks_for(n, 256), 256, 0, s>>>(x, out.codes, out.heads, n, error);
+    return hipGetLastError();
+}
+
+hipError_t launch_canonical_to_planes(const void *q8, Act out, int blocks, hipStream_t s) {
+    const size_t n = static_cast<size_t>(blocks) * 9;
+    k_canonical_to_planes<<<blocks_for(n, 256), 256, 0, s>>>(static_cast<const uint8_t *>(q8), out.codes,
+                                                              out.heads, static_cast<size_t>(blocks));
+    return hipGetLastError();
+}
+
+hipError_t launch_planes_to_canonical(Act in, void *q8, int blocks, hipStream_t s) {
+    const size_t n = static_cast<size_t>(blocks) * 9;
+    k_planes_to_canonical<<<blocks_for(n, 256), 256, 0, s>>>(in.codes, in.heads, static_cast<uint8_t *>(q8),
+                                                              static_cast<size_t>(blocks));
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_weights(const uint8_t *canonical, uint8_t *codes, uint16_t *scales, size_t blocks,
+                                 hipStream_t s) {
+    k_repack<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<const uint16_t *>(canonical),
+                                                      reinterpret_cast<uint32_t *>(codes), scales, blocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpack_weights(const uint8_t *codes, const uint16_t *scales, uint8_t *canonical,
+                                 size_t blocks, hipStream_t s) {
+    k_unpack<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<const uint32_t *>(codes), scales,
+                                                      reinterpret_cast<uint16_t *>(canonical), blocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, size_t blocks, size_t block0,
+                                    uint64_t seed, hipStream_t s) {
+    k_synthetic<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<uint32_t *>(codes), scales, blocks,
+                                                         block0, seed);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_u32(uint32_t *p, uint32_t value, size_t count, hipStream_t s) {
+    if (count == 0) return hipSuccess;
+    k_fill_u32<<<blocks_for(count, 256), 256, 0, s>>>(p, value, count);
+    return hipGetLastError();
+}
+
+hipError_t launch_prepare(const float *x, const int32_t *ids, const float *weights, int tokens, Shape shape,
+                          Act xq, RouteOut routes, int mfma_min, int *error, hipStream_t s) {
+    GroupParams p{ids, weights, tokens, shape, routes, mfma_min, error};
+    const size_t q_elements = static_cast<size_t>(tokens) * shape.H;
+    const int W = (tokens + 31) / 32;
+    const size_t small_lds = (static_cast<size_t>(shape.E) * W * 2 + static_cast<size_t>(shape.Ep) * 4 + 1 + 17) * 4;
+    if (tokens <= kSmallGroupTokens && small_lds <= 60 * 1024) {
+        k_prepare_small<<<1 + blocks_for(q_elements, 1024), 1024, small_lds, s>>>(p, x, xq, q_elements);
+        return hipGetLastError();
+    }
+    hipError_t e = launch_fill_u32(routes.bitmap, 0u, static_cast<size_t>(W) * shape.Ep, s);
+    if (e != hipSuccess) return e;
+    const int mark_blocks = static_cast<int>(blocks_for(static_cast<size_t>(tokens), 256));
+    k_mark_quantize<<<mark_blocks + blocks_for(q_elements, 256), 256, 0, s>>>(p, mark_blocks, x, xq, q_elements);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    k_word_prefix<<<blocks_for(static_cast<size_t>(shape.E), 4), 256, 0, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const size_t lds = (static_cast<size_t>(shape.Ep) * 4 + 1 + 17) * 4;
+    k_offsets_items<<<1, 1024, lds, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    k_scatter_pairs<<<blocks_for(static_cast<size_t>(tokens), 256), 256, 0, s>>>(p);
+    return hipGetLastError();
+}
+
+hipError_t launch_single_expert_items(Shape shape, RouteOut routes, int expert, int columns, int use_mfma,
+                                      hipStream_t s) {
+    k_single_items<<<1, 256, 0, s>>>(shape, routes, expert, columns, use_mfma);
+    return hipGetLastError();
+}
+
+namespace {
+unsigned stream_grid(const FfnArgs &a, int slices) {
+    // Upper bound on streaming items: one partial item per nonempty group plus
+    // full items; the persistent loop covers whatever the device produced.
+    const size_t bound = static_cast<size_t>(a.pairs_bound) / kStreamTokens +
+                         static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep));
+    const size_t units = bound * slices;
+    return static_cast<unsigned>(std::min<size_t>(units, 4096));
+}
+}  // namespace
+
+hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s) {
+    if (mfma) return hipErrorNotSupported;
+    const bool dbg = a.middle_f32 || a.gate_dots || a.up_dots;
+    const unsigned grid = stream_grid(a, a.shape.I / 32);
+    if (dbg) k_gate_up_stream<true><<<grid, 512, 0, s>>>(a);
+    else k_gate_up_stream<false><<<grid, 512, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
+    if (mfma) return hipErrorNotSupported;
+    const int nbi = a.shape.I / 32;
+    const unsigned grid = stream_grid(a, a.shape.H / 64);
+    const bool dbg = a.down_dots != nullptr;
+    if (nbi <= 8) {
+        if (dbg) k_down_stream<8, true><<<grid, 512, 0, s>>>(a);
+        else k_down_stream<8, false><<<grid, 512, 0, s>>>(a);
+    } else if (nbi <= 16) {
+        if (dbg) k_down_stream<16, true><<<grid, 512, 0, s>>>(a);
+        else k_down_stream<16, false><<<grid, 512, 0, s>>>(a);
+    } else {
+        if (dbg) k_down_stream<64, true><<<grid, 512, 0, s>>>(a);
+        else k_down_stream<64, false><<<grid, 512, 0, s>>>(a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_fold(const float *contributions, size_t token_stride, const float *weights, int k,
+                       const int32_t *pos_of, const float *shared, size_t shared_stride,
+                       const float *shared_gate, int tokens, int H, float *y, int *error, hipStream_t s) {
+    const size_t n = static_cast<size_t>(tokens) * H;
+    k_fold<<<blocks_for(n, 256), 256, 0, s>>>(contributions, token_stride, weights, k, pos_of, shared,
+                                              shared_stride, shared_gate, tokens, H, y, error);
+    return hipGetLastError();
+}
+
+}  // namespace moe

@@ -1,0 +1,485 @@
+// Layer object and C ABI (include/moe_ffn.h) of the MI355X routed-MoE FFN.
+//
+// Boundary conventions follow the reference launchers (src/hip/linear.cuh:35-45,
+// src/hip/session_ops.cuh:22-45): every argument is checked before the first
+// HIP call, launchers only enqueue on the caller's stream, and only create /
+// destroy / export allocate or synchronise.
+#include "moe_ffn.h"
+#include "moe_internal.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+
+using moe::Act;
+using moe::Item;
+using moe::RouteOut;
+using moe::Shape;
+
+struct moe_ffn_layer {
+    moe_ffn_config cfg{};
+    int device = 0;
+    Shape shape{};
+    void *bank_mem = nullptr;
+    size_t bank_bytes = 0;
+    moe::Bank bank{};
+    uint8_t *gate_codes = nullptr, *up_codes = nullptr, *down_codes = nullptr;
+    uint16_t *gate_scales = nullptr, *up_scales = nullptr, *down_scales = nullptr;
+    void *ws_mem = nullptr;
+    size_t ws_bytes = 0;
+    Act xq{}, mq{};
+    RouteOut routes{};
+    float *contrib = nullptr;
+    int mfma_min = 0;     // smallest group routed to the MFMA path (0 = streaming only)
+    int last_tokens = 0;
+    // Inputs of the last forward (for moe_ffn_replay_stage).
+    const float *last_x = nullptr, *last_weights = nullptr, *last_shared_gate = nullptr;
+    const int32_t *last_ids = nullptr;
+    float *last_y = nullptr;
+    int *last_error = nullptr;
+};
+
+namespace {
+
+constexpr int kInvalid = hipErrorInvalidValue;
+constexpr int kNotSupported = hipErrorNotSupported;
+
+bool aligned(const void *p, size_t a) { return p && reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+bool config_ok(const moe_ffn_config *c) {
+    return c && c->hidden >= 32 && c->hidden <= 16384 && c->hidden % 32 == 0 && c->intermediate >= 32 &&
+           c->intermediate <= 16384 && c->intermediate % 32 == 0 && c->experts >= 1 && c->experts <= 4096 &&
+           c->top_k >= 1 && c->top_k <= 32 && c->top_k <= c->experts && (c->has_shared == 0 || c->has_shared == 1) &&
+           c->max_tokens >= 1 && c->max_tokens <= 65536 && c->hidden % 64 == 0;
+}
+
+Shape shape_of(const moe_ffn_config &c) {
+    return Shape{c.hidden, c.intermediate, c.experts, c.experts + c.has_shared, c.top_k};
+}
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+size_t expert_blocks(const Shape &s) { return static_cast<size_t>(3) * s.H / 32 * s.I; }
+
+// Bank: code planes (16 B/block) then scale planes (2 B/block).
+size_t bank_layout(const Shape &s, size_t off[6]) {
+    const size_t gb = static_cast<size_t>(s.Ep) * s.I * (s.H / 32);   // gate blocks == up blocks == down blocks
+    size_t p = 0;
+    for (int m = 0; m < 3; ++m) { off[m] = p; p = round_up(p + gb * 16, 256); }
+    for (int m = 0; m < 3; ++m) { off[3 + m] = p; p = round_up(p + gb * 2, 256); }
+    return p;
+}
+
+struct WsLayout {
+    size_t xq_codes, xq_heads, mq_codes, mq_heads, pair_token, pair_rank, pos_of, counts, offsets,
+        stream_items, mfma_items, item_counts, bitmap, wprefix, contrib, total;
+};
+
+size_t pairs_capacity(const Shape &s, int N) { return static_cast<size_t>(N) * s.k + (s.Ep > s.E ? N : 0); }
+
+WsLayout ws_layout(const Shape &s, int N) {
+    WsLayout w{};
+    const size_t nbh = s.H / 32, nbi = s.I / 32, P = pairs_capacity(s, N);
+    const size_t W = (static_cast<size_t>(N) + 31) / 32;
+    size_t p = 0;
+    auto take = [&](size_t bytes) { const size_t at = p; p = round_up(p + bytes, 256); return at; };
+    w.xq_codes = take(static_cast<size_t>(N) * nbh * 32);
+    w.xq_heads = take(static_cast<size_t>(N) * nbh * 4);
+    w.mq_codes = take(P * nbi * 32);
+    w.mq_heads = take(P * nbi * 4);
+    w.pair_token = take(P * 4);
+    w.pair_rank = take(P * 4);
+    w.pos_of = take(static_cast<size_t>(N) * s.k * 4);
+    w.counts = take(static_cast<size_t>(s.Ep) * 4);
+    w.offsets = take((static_cast<size_t>(s.Ep) + 1) * 4);
+    w.stream_items = take((P / moe::kStreamTokens + s.Ep + 1) * sizeof(Item));
+    w.mfma_items = take((P / moe::kMfmaTile + s.Ep + 1) * sizeof(Item));
+    w.item_counts = take(16);
+    w.bitmap = take(W * s.Ep * 4);
+    w.wprefix = take(W * s.Ep * 4);
+    w.contrib = take(static_cast<size_t>(N) * (s.k + 1) * s.H * 4);
+    w.total = p;
+    return w;
+}
+
+int finish_create(moe_ffn_layer *L) {
+    // Workspace.
+    const WsLayout w = ws_layout(L->shape, L->cfg.max_tokens);
+    if (hipMalloc(&L->ws_mem, w.total) != hipSuccess) return hipErrorOutOfMemory;
+    L->ws_bytes = w.total;
+    auto *b = static_cast<uint8_t *>(L->ws_mem);
+    L->xq = Act{b + w.xq_codes, reinterpret_cast<uint32_t *>(b + w.xq_heads)};
+    L->mq = Act{b + w.mq_codes, reinterpret_cast<uint32_t *>(b + w.mq_heads)};
+    L->routes.pair_token = reinterpret_cast<int32_t *>(b + w.pair_token);
+    L->routes.pair_rank = reinterpret_cast<int32_t *>(b + w.pair_rank);
+    L->routes.pos_of = reinterpret_cast<int32_t *>(b + w.pos_of);
+    L->routes.counts = reinterpret_cast<int32_t *>(b + w.counts);
+    L->routes.offsets = reinterpret_cast<int32_t *>(b + w.offsets);
+    L->routes.stream_items = reinterpret_cast<Item *>(b + w.stream_items);
+    L->routes.mfma_items = reinterpret_cast<Item *>(b + w.mfma_items);
+    L->routes.item_counts = reinterpret_cast<int32_t *>(b + w.item_counts);
+    L->routes.bitmap = reinterpret_cast<uint32_t *>(b + w.bitmap);
+    L->routes.wprefix = reinterpret_cast<uint32_t *>(b + w.wprefix);
+    L->contrib = reinterpret_cast<float *>(b + w.contrib);
+    if (hipMemset(L->ws_mem, 0, w.total) != hipSuccess) return hipErrorOutOfMemory;
+    if (const char *env = std::getenv("MOE_FFN_MFMA_MIN")) L->mfma_min = std::atoi(env);
+    return hipDeviceSynchronize();
+}
+
+int alloc_bank(moe_ffn_layer *L) {
+    size_t off[6];
+    L->bank_bytes = bank_layout(L->shape, off);
+    if (hipMalloc(&L->bank_mem, L->bank_bytes) != hipSuccess) return hipErrorOutOfMemory;
+    auto *b = static_cast<uint8_t *>(L->bank_mem);
+    L->gate_codes = b + off[0];
+    L->up_codes = b + off[1];
+    L->down_codes = b + off[2];
+    L->gate_scales = reinterpret_cast<uint16_t *>(b + off[3]);
+    L->up_scales = reinterpret_cast<uint16_t *>(b + off[4]);
+    L->down_scales = reinterpret_cast<uint16_t *>(b + off[5]);
+    L->bank = moe::Bank{L->gate_codes, L->up_codes, L->down_codes, L->gate_scales, L->up_scales, L->down_scales};
+    return hipSuccess;
+}
+
+// Repack `count` canonical experts starting at expert `first` from a device
+// staging buffer into the planes.
+int repack_experts(moe_ffn_layer *L, const uint8_t *staging, int first, int count) {
+    const Shape &s = L->shape;
+    const size_t mblocks = static_cast<size_t>(s.I) * (s.H / 32);   // blocks per matrix
+    for (int i = 0; i < count; ++i) {
+        const size_t e = static_cast<size_t>(first + i);
+        const uint8_t *src = staging + static_cast<size_t>(i) * expert_blocks(s) * 18;
+        hipError_t r;
+        if ((r = moe::launch_repack_weights(src, L->gate_codes + e * mblocks * 16, L->gate_scales + e * mblocks,
+                                            mblocks, nullptr)) != hipSuccess) return r;
+        if ((r = moe::launch_repack_weights(src + mblocks * 18, L->up_codes + e * mblocks * 16,
+                                            L->up_scales + e * mblocks, mblocks, nullptr)) != hipSuccess) return r;
+        if ((r = moe::launch_repack_weights(src + 2 * mblocks * 18, L->down_codes + e * mblocks * 16,
+                                            L->down_scales + e * mblocks, mblocks, nullptr)) != hipSuccess) return r;
+    }
+    return hipSuccess;
+}
+
+int create_common(const moe_ffn_config *config, int device, moe_ffn_layer **layer, moe_ffn_layer *&L) {
+    if (!config_ok(config) || !layer) return kInvalid;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return kInvalid;
+    if (hipSetDevice(device) != hipSuccess) return kInvalid;
+    L = new (std::nothrow) moe_ffn_layer();
+    if (!L) return hipErrorOutOfMemory;
+    L->cfg = *config;
+    L->device = device;
+    L->shape = shape_of(*config);
+    const int r = alloc_bank(L);
+    if (r != hipSuccess) { moe_ffn_destroy(L); L = nullptr; return r; }
+    return hipSuccess;
+}
+
+int upload(moe_ffn_layer *L, const void *experts, const void *shared, bool from_device) {
+    const Shape &s = L->shape;
+    const size_t ebytes = expert_blocks(s) * 18;
+    const int chunk = static_cast<int>(std::max<size_t>(1, (size_t{256} << 20) / ebytes));
+    uint8_t *staging = nullptr;
+    if (!from_device && hipMalloc(&staging, static_cast<size_t>(chunk) * ebytes) != hipSuccess)
+        return hipErrorOutOfMemory;
+    int r = hipSuccess;
+    for (int first = 0; first < s.Ep && r == hipSuccess; first += chunk) {
+        const int n = std::min(chunk, s.Ep - first);
+        // Shared expert (index E) comes from its own pointer.
+        const int routed = std::max(0, std::min(n, s.E - first));
+        const uint8_t *src_routed = static_cast<const uint8_t *>(experts) + static_cast<size_t>(first) * ebytes;
+        if (routed > 0) {
+            if (from_device) r = repack_experts(L, src_routed, first, routed);
+            else {
+                r = hipMemcpy(staging, src_routed, routed * ebytes, hipMemcpyHostToDevice);
+                if (r == hipSuccess) r = repack_experts(L, staging, first, routed);
+                if (r == hipSuccess) r = hipDeviceSynchronize();
+            }
+        }
+        if (r == hipSuccess && routed < n) {   // the shared expert
+            if (from_device) r = repack_experts(L, static_cast<const uint8_t *>(shared), s.E, 1);
+            else {
+                r = hipMemcpy(staging, shared, ebytes, hipMemcpyHostToDevice);
+                if (r == hipSuccess) r = repack_experts(L, staging, s.E, 1);
+                if (r == hipSuccess) r = hipDeviceSynchronize();
+            }
+        }
+    }
+    if (r == hipSuccess) r = hipDeviceSynchronize();
+    if (staging) (void)hipFree(staging);
+    return r;
+}
+
+moe::FfnArgs base_args(moe_ffn_layer *L, int tokens, int *error) {
+    moe::FfnArgs a{};
+    a.shape = L->shape;
+    a.bank = L->bank;
+    a.xq = L->xq;
+    a.mq = L->mq;
+    a.routes = L->routes;
+    a.out = L->contrib;
+    a.out_stride_k = L->shape.k + 1;
+    a.tokens = tokens;
+    a.pairs_bound = static_cast<int>(pairs_capacity(L->shape, tokens));
+    a.error = error;
+    return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_ffn_memory_bytes(const moe_ffn_config *config, size_t *weight_bytes, size_t *workspace_bytes) {
+    if (!config_ok(config) || !weight_bytes || !workspace_bytes) return kInvalid;
+    size_t off[6];
+    const Shape s = shape_of(*config);
+    *weight_bytes = bank_layout(s, off);
+    *workspace_bytes = ws_layout(s, config->max_tokens).total;
+    return hipSuccess;
+}
+
+int moe_ffn_create(const moe_ffn_config *config, const void *experts_q4, const void *shared_q4, int device,
+                   moe_ffn_layer **layer) {
+    if (!experts_q4 || (config && config->has_shared && !shared_q4)) return kInvalid;
+    moe_ffn_layer *L = nullptr;
+    int r = create_common(config, device, layer, L);
+    if (r != hipSuccess) return r;
+    r = upload(L, experts_q4, shared_q4, false);
+    if (r == hipSuccess) r = finish_create(L);
+    if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
+    *layer = L;
+    return hipSuccess;
+}
+
+int moe_ffn_create_from_device(const moe_ffn_config *config, const void *experts_q4_device,
+                               const void *shared_q4_device, int device, moe_ffn_layer **layer) {
+    if (!experts_q4_device || !aligned(experts_q4_device, 2) ||
+        (config && config->has_shared && !aligned(shared_q4_device, 2)))
+        return kInvalid;
+    moe_ffn_layer *L = nullptr;
+    int r = create_common(config, device, layer, L);
+    if (r != hipSuccess) return r;
+    r = upload(L, experts_q4_device, shared_q4_device, true);
+    if (r == hipSuccess) r = finish_create(L);
+    if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
+    *layer = L;
+    return hipSuccess;
+}
+
+int moe_ffn_create_synthetic(const moe_ffn_config *config, uint64_t seed, int device, moe_ffn_layer **layer) {
+    moe_ffn_layer *L = nullptr;
+    int r = create_common(config, device, layer, L);
+    if (r != hipSuccess) return r;
+    const size_t blocks = static_cast<size_t>(L->shape.Ep) * L->shape.I * (L->shape.H / 32);
+    uint8_t *codes[3] = {L->gate_codes, L->up_codes, L->down_codes};
+    uint16_t *scales[3] = {L->gate_scales, L->up_scales, L->down_scales};
+    for (int m = 0; m < 3 && r == hipSuccess; ++m)
+        r = moe::launch_synthetic_weights(codes[m], scales[m], blocks, static_cast<size_t>(m) * blocks, seed,
+                                          nullptr);
+    if (r == hipSuccess) r = hipDeviceSynchronize();
+    if (r == hipSuccess) r = finish_create(L);
+    if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
+    *layer = L;
+    return hipSuccess;
+}
+
+int moe_ffn_destroy(moe_ffn_layer *L) {
+    if (!L) return kInvalid;
+    (void)hipSetDevice(L->device);
+    (void)hipDeviceSynchronize();
+    if (L->bank_mem) (void)hipFree(L->bank_mem);
+    if (L->ws_mem) (void)hipFree(L->ws_mem);
+    delete L;
+    return hipSuccess;
+}
+
+int moe_ffn_export_expert(moe_ffn_layer *L, int expert, void *host_q4) {
+    if (!L || !host_q4 || expert < 0 || expert >= L->shape.Ep) return kInvalid;
+    const Shape &s = L->shape;
+    const size_t mblocks = static_cast<size_t>(s.I) * (s.H / 32);
+    uint8_t *staging = nullptr;
+    if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
+    if (hipMalloc(&staging, 3 * mblocks * 18) != hipSuccess) return hipErrorOutOfMemory;
+    const size_t e = static_cast<size_t>(expert);
+    int r = moe::launch_unpack_weights(L->gate_codes + e * mblocks * 16, L->gate_scales + e * mblocks, staging,
+                                       mblocks, nullptr);
+    if (r == hipSuccess)
+        r = moe::launch_unpack_weights(L->up_codes + e * mblocks * 16, L->up_scales + e * mblocks,
+                                       staging + mblocks * 18, mblocks, nullptr);
+    if (r == hipSuccess)
+        r = moe::launch_unpack_weights(L->down_codes + e * mblocks * 16, L->down_scales + e * mblocks,
+                                       staging + 2 * mblocks * 18, mblocks, nullptr);
+    if (r == hipSuccess) r = hipMemcpy(host_q4, staging, 3 * mblocks * 18, hipMemcpyDeviceToHost);
+    (void)hipFree(staging);
+    return r;
+}
+
+namespace {
+int run_stage(moe_ffn_layer *L, int stage, const float *x, const int32_t *ids, const float *weights, int tokens,
+              const float *shared_gate, float *y, int *error, hipStream_t s) {
+    const Shape &sh = L->shape;
+    moe::FfnArgs a = base_args(L, tokens, error);
+    hipError_t r = hipSuccess;
+    switch (stage) {
+    case MOE_STAGE_PREPARE:
+        return moe::launch_prepare(x, ids, weights, tokens, sh, L->xq, L->routes, L->mfma_min, error, s);
+    case MOE_STAGE_GATE_UP:
+        if ((r = moe::launch_gate_up(a, false, s)) != hipSuccess) return r;
+        if (L->mfma_min > 0) r = moe::launch_gate_up(a, true, s);
+        return r;
+    case MOE_STAGE_DOWN:
+        if ((r = moe::launch_down(a, false, s)) != hipSuccess) return r;
+        if (L->mfma_min > 0) r = moe::launch_down(a, true, s);
+        return r;
+    case MOE_STAGE_FOLD: {
+        const size_t stride = static_cast<size_t>(sh.k + 1) * sh.H;
+        return moe::launch_fold(L->contrib, stride, weights, sh.k, L->routes.pos_of,
+                                sh.Ep > sh.E ? L->contrib + static_cast<size_t>(sh.k) * sh.H : nullptr, stride,
+                                shared_gate, tokens, sh.H, y, error, s);
+    }
+    default:
+        return kInvalid;
+    }
+}
+}  // namespace
+
+int moe_ffn_forward(moe_ffn_layer *L, const float *x, const int32_t *ids, const float *weights, int tokens,
+                    const float *shared_gate, float *y, int *error, void *stream) {
+    if (!L || !aligned(x, 4) || !aligned(ids, 4) || !aligned(weights, 4) || !aligned(y, 4) || !aligned(error, 4) ||
+        tokens < 1 || tokens > L->cfg.max_tokens || (shared_gate && !aligned(shared_gate, 4)))
+        return kInvalid;
+    const auto s = static_cast<hipStream_t>(stream);
+    for (int stage = MOE_STAGE_PREPARE; stage <= MOE_STAGE_FOLD; ++stage) {
+        const int r = run_stage(L, stage, x, ids, weights, tokens, shared_gate, y, error, s);
+        if (r != hipSuccess) return r;
+    }
+    L->last_tokens = tokens;
+    L->last_x = x;
+    L->last_ids = ids;
+    L->last_weights = weights;
+    L->last_shared_gate = shared_gate;
+    L->last_y = y;
+    L->last_error = error;
+    return hipSuccess;
+}
+
+int moe_ffn_replay_stage(moe_ffn_layer *L, int stage, void *stream) {
+    if (!L || L->last_tokens < 1 || stage < MOE_STAGE_PREPARE || stage > MOE_STAGE_FOLD) return kInvalid;
+    return run_stage(L, stage, L->last_x, L->last_ids, L->last_weights, L->last_tokens, L->last_shared_gate,
+                     L->last_y, L->last_error, static_cast<hipStream_t>(stream));
+}
+
+int moe_quantize_q8_1(const float *x, void *q8, int width, int columns, int *error, void *stream) {
+    if (!aligned(x, 4) || !aligned(q8, 4) || !aligned(error, 4) || width < 32 || width > 16384 || width % 32 ||
+        columns < 1 || columns > 65536)
+        return kInvalid;
+    return moe::launch_quantize_canonical(x, q8, width, columns, error, static_cast<hipStream_t>(stream));
+}
+
+int moe_ffn_group_routes(moe_ffn_layer *L, const int32_t *ids, const float *weights, int tokens, int32_t *counts,
+                         int32_t *offsets, int32_t *route_token, int32_t *route_rank, int *error, void *stream) {
+    if (!L || !aligned(ids, 4) || !aligned(weights, 4) || !aligned(counts, 4) || !aligned(offsets, 4) ||
+        !aligned(route_token, 4) || !aligned(route_rank, 4) || !aligned(error, 4) || tokens < 1 ||
+        tokens > L->cfg.max_tokens)
+        return kInvalid;
+    const auto s = static_cast<hipStream_t>(stream);
+    const Shape &sh = L->shape;
+    hipError_t r = moe::launch_prepare(nullptr, ids, weights, tokens, sh, L->xq, L->routes, 0, error, s);
+    if (r != hipSuccess) return r;
+    const size_t P = static_cast<size_t>(tokens) * sh.k;
+    if ((r = hipMemcpyAsync(counts, L->routes.counts, sh.E * 4, hipMemcpyDeviceToDevice, s)) != hipSuccess) return r;
+    if ((r = hipMemcpyAsync(offsets, L->routes.offsets, (sh.E + 1) * 4, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return r;
+    if ((r = hipMemcpyAsync(route_token, L->routes.pair_token, P * 4, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return r;
+    return hipMemcpyAsync(route_rank, L->routes.pair_rank, P * 4, hipMemcpyDeviceToDevice, s);
+}
+
+int moe_ffn_expert_gate_up(moe_ffn_layer *L, int expert, const void *x_q8, int columns, float *middle,
+                           void *middle_q8, int32_t *gate_dots, int32_t *up_dots, int path, int *error,
+                           void *stream) {
+    if (!L || expert < 0 || expert >= L->shape.Ep || !aligned(x_q8, 4) || !aligned(middle_q8, 4) ||
+        !aligned(error, 4) || columns < 1 || columns > L->cfg.max_tokens || (middle && !aligned(middle, 4)) ||
+        (gate_dots && !aligned(gate_dots, 4)) || (up_dots && !aligned(up_dots, 4)) || path < 0 || path > 2)
+        return kInvalid;
+    if (path == MOE_PATH_MFMA) return kNotSupported;
+    const auto s = static_cast<hipStream_t>(stream);
+    const Shape &sh = L->shape;
+    hipError_t r = moe::launch_canonical_to_planes(x_q8, L->xq, columns * (sh.H / 32), s);
+    if (r != hipSuccess) return r;
+    if ((r = moe::launch_single_expert_items(sh, L->routes, expert, columns, 0, s)) != hipSuccess) return r;
+    moe::FfnArgs a = base_args(L, columns, error);
+    a.pairs_bound = columns;
+    a.middle_f32 = middle;
+    a.gate_dots = gate_dots;
+    a.up_dots = up_dots;
+    if ((r = moe::launch_gate_up(a, false, s)) != hipSuccess) return r;
+    return moe::launch_planes_to_canonical(L->mq, middle_q8, columns * (sh.I / 32), s);
+}
+
+int moe_ffn_expert_down(moe_ffn_layer *L, int expert, const void *middle_q8, int columns, float *y,
+                        int32_t *down_dots, int path, int *error, void *stream) {
+    if (!L || expert < 0 || expert >= L->shape.Ep || !aligned(middle_q8, 4) || !aligned(y, 4) ||
+        !aligned(error, 4) || columns < 1 || columns > L->cfg.max_tokens || (down_dots && !aligned(down_dots, 4)) ||
+        path < 0 || path > 2)
+        return kInvalid;
+    if (path == MOE_PATH_MFMA) return kNotSupported;
+    const auto s = static_cast<hipStream_t>(stream);
+    const Shape &sh = L->shape;
+    hipError_t r = moe::launch_canonical_to_planes(middle_q8, L->mq, columns * (sh.I / 32), s);
+    if (r != hipSuccess) return r;
+    if ((r = moe::launch_single_expert_items(sh, L->routes, expert, columns, 0, s)) != hipSuccess) return r;
+    moe::FfnArgs a = base_args(L, columns, error);
+    a.pairs_bound = columns;
+    a.out = y;
+    a.out_stride_k = 1;
+    a.down_dots = down_dots;
+    return moe::launch_down(a, false, s);
+}
+
+int moe_combine(const float *contributions, const float *weights, const float *shared, const float *shared_gate,
+                int tokens, int top_k, int hidden, float *y, int *error, void *stream) {
+    if (!aligned(contributions, 4) || !aligned(weights, 4) || !aligned(y, 4) || !aligned(error, 4) || tokens < 1 ||
+        top_k < 1 || top_k > 32 || hidden < 1 || (shared && !aligned(shared, 4)) ||
+        (shared_gate && !aligned(shared_gate, 4)))
+        return kInvalid;
+    return moe::launch_fold(contributions, static_cast<size_t>(top_k) * hidden, weights, top_k, nullptr, shared,
+                            static_cast<size_t>(hidden), shared ? shared_gate : nullptr, tokens, hidden, y, error,
+                            static_cast<hipStream_t>(stream));
+}
+
+int moe_ffn_debug_last(moe_ffn_layer *L, void *x_q8, void *middle_q8, int32_t *route_token, int32_t *route_rank,
+                       void *stream) {
+    if (!L || L->last_tokens < 1) return kInvalid;
+    const auto s = static_cast<hipStream_t>(stream);
+    const Shape &sh = L->shape;
+    const int N = L->last_tokens;
+    hipError_t r = hipSuccess;
+    if (x_q8 && (r = moe::launch_planes_to_canonical(L->xq, x_q8, N * (sh.H / 32), s)) != hipSuccess) return r;
+    const int P = static_cast<int>(pairs_capacity(sh, N));
+    if (middle_q8 && (r = moe::launch_planes_to_canonical(L->mq, middle_q8, P * (sh.I / 32), s)) != hipSuccess)
+        return r;
+    const size_t routed = static_cast<size_t>(N) * sh.k * 4;
+    if (route_token &&
+        (r = hipMemcpyAsync(route_token, L->routes.pair_token, routed, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return r;
+    if (route_rank &&
+        (r = hipMemcpyAsync(route_rank, L->routes.pair_rank, routed, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return r;
+    return hipSuccess;
+}
+
+int moe_ffn_last_stats(moe_ffn_layer *L, int32_t *stream_items, int32_t *mfma_items, int32_t *active_experts) {
+    if (!L) return kInvalid;
+    int32_t c[4] = {0, 0, 0, 0};
+    if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
+    const hipError_t r = hipMemcpy(c, L->routes.item_counts, sizeof(c), hipMemcpyDeviceToHost);
+    if (r != hipSuccess) return r;
+    if (stream_items) *stream_items = c[0];
+    if (mfma_items) *mfma_items = c[1];
+    if (active_experts) *active_experts = c[2];
+    return hipSuccess;
+}
+
+}  // extern "C"

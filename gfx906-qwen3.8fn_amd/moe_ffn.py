@@ -1,0 +1,250 @@
+"""Python binding of the MI355X routed-MoE expert FFN C ABI (include/moe_ffn.h).
+
+This is the host-side operator surface used by the tests and bench.py.  It
+mirrors the reference's expert operator (src/gpu_expert.hpp:7-17, the Experts /
+Layer::ffn path of src/session.hip:976-1078, 1446-1541): token activations,
+top-k expert ids and route weights go in, the routing-weighted FFN output in
+token order comes out.  Every call goes through libmoe_ffn.so; there is no
+CPU or PyTorch fallback -- a missing library raises.
+
+PyTorch is only used to own device memory and streams.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmoe_ffn.so")
+ROOT = os.path.dirname(HERE)
+HEADER = os.path.join(ROOT, "include", "moe_ffn.h")
+
+Q8_BLOCK = 36
+Q4_BLOCK = 18
+PATH_AUTO, PATH_STREAM, PATH_MFMA = 0, 1, 2
+STAGE_PREPARE, STAGE_GATE_UP, STAGE_DOWN, STAGE_FOLD = 0, 1, 2, 3
+
+
+class MoeError(RuntimeError):
+    def __init__(self, what, status):
+        super().__init__(f"{what} failed with status {status}")
+        self.status = status
+
+
+class Config(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("intermediate", ctypes.c_int), ("experts", ctypes.c_int),
+                ("top_k", ctypes.c_int), ("has_shared", ctypes.c_int), ("max_tokens", ctypes.c_int)]
+
+
+_lib = None
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+
+
+def library():
+    """Load libmoe_ffn.so (built in-tree by __graft_entry__.build())."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"HIP extension missing: {LIB_PATH}; run __graft_entry__.build()")
+        lib = ctypes.CDLL(LIB_PATH)
+        lib.moe_ffn_create.argtypes = [ctypes.POINTER(Config), _P, _P, _I, ctypes.POINTER(_P)]
+        lib.moe_ffn_create_from_device.argtypes = [ctypes.POINTER(Config), _P, _P, _I, ctypes.POINTER(_P)]
+        lib.moe_ffn_create_synthetic.argtypes = [ctypes.POINTER(Config), ctypes.c_uint64, _I, ctypes.POINTER(_P)]
+        lib.moe_ffn_destroy.argtypes = [_P]
+        lib.moe_ffn_memory_bytes.argtypes = [ctypes.POINTER(Config), ctypes.POINTER(ctypes.c_size_t),
+                                             ctypes.POINTER(ctypes.c_size_t)]
+        lib.moe_ffn_export_expert.argtypes = [_P, _I, _P]
+        lib.moe_ffn_forward.argtypes = [_P, _P, _P, _P, _I, _P, _P, _P, _P]
+        lib.moe_quantize_q8_1.argtypes = [_P, _P, _I, _I, _P, _P]
+        lib.moe_ffn_group_routes.argtypes = [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P]
+        lib.moe_ffn_expert_gate_up.argtypes = [_P, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P]
+        lib.moe_ffn_expert_down.argtypes = [_P, _I, _P, _I, _P, _P, _I, _P, _P]
+        lib.moe_combine.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P]
+        lib.moe_ffn_debug_last.argtypes = [_P, _P, _P, _P, _P, _P]
+        lib.moe_ffn_replay_stage.argtypes = [_P, _I, _P]
+        lib.moe_ffn_last_stats.argtypes = [_P, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+                                           ctypes.POINTER(ctypes.c_int32)]
+        _lib = lib
+    return _lib
+
+
+def header_symbols():
+    """Function names declared in include/moe_ffn.h."""
+    import re
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^int\s+(moe_\w+)\s*\(", text, flags=re.M)))
+
+
+def _check(status, what):
+    if status != 0:
+        raise MoeError(what, status)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def expert_bytes(hidden, intermediate):
+    return 3 * hidden // 32 * intermediate * Q4_BLOCK
+
+
+class MoeLayer:
+    """One MoE layer resident on the GPU (weights + workspace for max_tokens)."""
+
+    def __init__(self, hidden, intermediate, experts, top_k, has_shared, max_tokens, experts_q4=None,
+                 shared_q4=None, synthetic_seed=None, device=0):
+        self.cfg = Config(hidden, intermediate, experts, top_k, 1 if has_shared else 0, max_tokens)
+        self.H, self.I, self.E, self.k = hidden, intermediate, experts, top_k
+        self.has_shared = bool(has_shared)
+        self.max_tokens = max_tokens
+        self.device = device
+        handle = ctypes.c_void_p()
+        lib = library()
+        if synthetic_seed is not None:
+            st = lib.moe_ffn_create_synthetic(ctypes.byref(self.cfg), ctypes.c_uint64(synthetic_seed), device,
+                                              ctypes.byref(handle))
+        elif isinstance(experts_q4, np.ndarray):
+            experts_q4 = np.ascontiguousarray(experts_q4, dtype=np.uint8)
+            assert experts_q4.size == experts * expert_bytes(hidden, intermediate)
+            sh = None
+            if has_shared:
+                sh = np.ascontiguousarray(shared_q4, dtype=np.uint8)
+                assert sh.size == expert_bytes(hidden, intermediate)
+            st = lib.moe_ffn_create(ctypes.byref(self.cfg), ctypes.c_void_p(experts_q4.ctypes.data),
+                                    None if sh is None else ctypes.c_void_p(sh.ctypes.data), device,
+                                    ctypes.byref(handle))
+        else:   # torch device tensors
+            st = lib.moe_ffn_create_from_device(ctypes.byref(self.cfg), _ptr(experts_q4), _ptr(shared_q4), device,
+                                                ctypes.byref(handle))
+        _check(st, "moe_ffn_create")
+        self.handle = handle
+
+    def close(self):
+        if getattr(self, "handle", None):
+            library().moe_ffn_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------ queries --
+    def export_expert(self, expert):
+        out = np.zeros(expert_bytes(self.H, self.I), np.uint8)
+        _check(library().moe_ffn_export_expert(self.handle, expert, ctypes.c_void_p(out.ctypes.data)),
+               "moe_ffn_export_expert")
+        return out
+
+    def last_stats(self):
+        a, b, c = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        _check(library().moe_ffn_last_stats(self.handle, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c)),
+               "moe_ffn_last_stats")
+        return dict(stream_items=a.value, mfma_items=b.value, active_experts=c.value)
+
+    # ------------------------------------------------------------ forward --
+    def forward(self, x, ids, weights, shared_gate=None, y=None, error=None, stream=None):
+        import torch
+        n = x.shape[0]
+        if y is None:
+            y = torch.empty((n, self.H), dtype=torch.float32, device=x.device)
+        if error is None:
+            error = torch.zeros(1, dtype=torch.int32, device=x.device)
+        _check(library().moe_ffn_forward(self.handle, _ptr(x), _ptr(ids), _ptr(weights), n, _ptr(shared_gate),
+                                         _ptr(y), _ptr(error), _stream(stream)), "moe_ffn_forward")
+        return y, error
+
+    def replay_stage(self, stage, stream=None):
+        _check(library().moe_ffn_replay_stage(self.handle, stage, _stream(stream)), "moe_ffn_replay_stage")
+
+    def debug_last(self, tokens, stream=None):
+        import torch
+        P = tokens * self.k + (tokens if self.has_shared else 0)
+        dev = f"cuda:{self.device}"
+        xq = torch.empty((tokens, self.H // 32 * Q8_BLOCK), dtype=torch.uint8, device=dev)
+        mq = torch.empty((P, self.I // 32 * Q8_BLOCK), dtype=torch.uint8, device=dev)
+        rt = torch.empty(tokens * self.k, dtype=torch.int32, device=dev)
+        rr = torch.empty(tokens * self.k, dtype=torch.int32, device=dev)
+        _check(library().moe_ffn_debug_last(self.handle, _ptr(xq), _ptr(mq), _ptr(rt), _ptr(rr), _stream(stream)),
+               "moe_ffn_debug_last")
+        return dict(x_q8=xq, middle_q8=mq, route_token=rt, route_rank=rr)
+
+    def group_routes(self, ids, weights, stream=None):
+        import torch
+        n = ids.shape[0]
+        dev = ids.device
+        counts = torch.empty(self.E, dtype=torch.int32, device=dev)
+        offsets = torch.empty(self.E + 1, dtype=torch.int32, device=dev)
+        rt = torch.empty(n * self.k, dtype=torch.int32, device=dev)
+        rr = torch.empty(n * self.k, dtype=torch.int32, device=dev)
+        error = torch.zeros(1, dtype=torch.int32, device=dev)
+        _check(library().moe_ffn_group_routes(self.handle, _ptr(ids), _ptr(weights), n, _ptr(counts), _ptr(offsets),
+                                              _ptr(rt), _ptr(rr), _ptr(error), _stream(stream)),
+               "moe_ffn_group_routes")
+        return dict(counts=counts, offsets=offsets, token=rt, rank=rr, error=error)
+
+    def expert_gate_up(self, expert, x_q8, columns, path=PATH_AUTO, dots=False, stream=None):
+        import torch
+        dev = x_q8.device
+        middle = torch.empty((columns, self.I), dtype=torch.float32, device=dev)
+        mq = torch.empty((columns, self.I // 32 * Q8_BLOCK), dtype=torch.uint8, device=dev)
+        gd = ud = None
+        if dots:
+            gd = torch.full((columns, self.I, self.H // 32), -2**31, dtype=torch.int32, device=dev)
+            ud = torch.full((columns, self.I, self.H // 32), -2**31, dtype=torch.int32, device=dev)
+        error = torch.zeros(1, dtype=torch.int32, device=dev)
+        _check(library().moe_ffn_expert_gate_up(self.handle, expert, _ptr(x_q8), columns, _ptr(middle), _ptr(mq),
+                                                _ptr(gd), _ptr(ud), path, _ptr(error), _stream(stream)),
+               "moe_ffn_expert_gate_up")
+        return dict(middle=middle, middle_q8=mq, gate_dots=gd, up_dots=ud, error=error)
+
+    def expert_down(self, expert, middle_q8, columns, path=PATH_AUTO, dots=False, stream=None):
+        import torch
+        dev = middle_q8.device
+        y = torch.empty((columns, self.H), dtype=torch.float32, device=dev)
+        dd = None
+        if dots:
+            dd = torch.full((columns, self.H, self.I // 32), -2**31, dtype=torch.int32, device=dev)
+        error = torch.zeros(1, dtype=torch.int32, device=dev)
+        _check(library().moe_ffn_expert_down(self.handle, expert, _ptr(middle_q8), columns, _ptr(y), _ptr(dd), path,
+                                             _ptr(error), _stream(stream)), "moe_ffn_expert_down")
+        return dict(y=y, down_dots=dd, error=error)
+
+
+def quantize_q8_1(x, error=None, stream=None):
+    """fp32 [cols, width] (device) -> uint8 [cols, width/32*36] canonical Q8_1."""
+    import torch
+    cols, width = x.shape
+    out = torch.empty((cols, width // 32 * Q8_BLOCK), dtype=torch.uint8, device=x.device)
+    if error is None:
+        error = torch.zeros(1, dtype=torch.int32, device=x.device)
+    _check(library().moe_quantize_q8_1(_ptr(x), _ptr(out), width, cols, _ptr(error), _stream(stream)),
+           "moe_quantize_q8_1")
+    return out, error
+
+
+def combine(contributions, weights, shared=None, shared_gate=None, stream=None):
+    import torch
+    n, k, h = contributions.shape
+    y = torch.empty((n, h), dtype=torch.float32, device=contributions.device)
+    error = torch.zeros(1, dtype=torch.int32, device=contributions.device)
+    _check(library().moe_combine(_ptr(contributions), _ptr(weights), _ptr(shared), _ptr(shared_gate), n, k, h,
+                                 _ptr(y), _ptr(error), _stream(stream)), "moe_combine")
+    return y, error
+
+
+def memory_bytes(hidden, intermediate, experts, top_k, has_shared, max_tokens):
+    cfg = Config(hidden, intermediate, experts, top_k, 1 if has_shared else 0, max_tokens)
+    w, s = ctypes.c_size_t(), ctypes.c_size_t()
+    _check(library().moe_ffn_memory_bytes(ctypes.byref(cfg), ctypes.byref(w), ctypes.byref(s)), "memory_bytes")
+    return w.value, s.value

@@ -1,0 +1,173 @@
+/*
+ * moe_ffn.h -- C ABI of the MI355X (gfx950) routed-MoE Q4_0 x Q8_1 expert FFN.
+ *
+ * Drop-in boundary for the routed expert path of 0FL01/gfx906-qwen3.8fn.  It
+ * replaces everything between "token activations + host/device route ids and
+ * weights" and "routed (+shared) FFN aggregate [N][H] fp32" in the reference's
+ * Layer::ffn (src/session.hip:1446-1541, 1384-1410), i.e. the work of
+ *   RouteGroups::prepare / upload_routes     src/routes.cpp:126-182, src/session.hip:393-410
+ *   launch_quantize_q8_1                     src/hip/linear.cuh:107-108
+ *   launch_moe_gather_q8 / launch_moe_scatter src/hip/session_ops.cuh:175-199
+ *   launch_quantized_linear{,_short,_tiled}  src/hip/linear.cuh:70-87
+ *   launch_silu_up_q8_1                      src/hip/linear.cuh:15-17
+ *   launch_routed_fold / launch_scaled_add   src/hip/session_ops.cuh:104-114
+ *   launch_shared_sigmoid_add_rows           src/hip/session_ops.cuh:213-214
+ *   Experts::project/run/run_group/run_chunk src/session.hip:976-1078
+ *
+ * Conventions (kept from src/hip/linear.cuh:35-45, src/hip/session_ops.cuh:22-45):
+ *   - every entry point returns a status (0 = success; otherwise a hipError_t
+ *     value: 1 = invalid value, 2 = out of memory, 801 = not supported);
+ *   - shape / null / alignment checks happen BEFORE any HIP call;
+ *   - launchers only enqueue on the explicit stream (NULL = default stream);
+ *     success means "enqueued", not "completed";
+ *   - no hidden synchronisation, no allocation outside moe_ffn_create;
+ *   - `error` is a caller-owned device int, zeroed by the caller in stream
+ *     order; kernels atomically OR bit 1 (nonfinite / invalid input: bad
+ *     expert id, duplicate id within a token, negative or nonfinite route
+ *     weight) and bit 2 (arithmetic: Q8 not representable, nonfinite result).
+ *     Kernels never clear it; a failing Q8 block is written as all zero.
+ *   - one owner per layer handle; calls on one handle must not overlap.
+ *
+ * Formats (src/quant.hpp:8-18): Q4_0 = 18-byte block {half d; u8 qs[16]},
+ * element j<16 = qs[j]&15, j>=16 = qs[j-16]>>4, value (q-8)*d.  Q8_1 =
+ * 36-byte block {half d; half s; i8 qs[32]} with codes chosen by the FP32
+ * scale amax/127 and s = half of the raw-input XOR-butterfly sum.
+ */
+#ifndef MOE_FFN_H
+#define MOE_FFN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct moe_ffn_config {
+    int hidden;        /* H: multiple of 32, 32..16384 */
+    int intermediate;  /* I: multiple of 32, 32..16384 */
+    int experts;       /* E: routed experts, 1..4096 */
+    int top_k;         /* routes per token, 1..32, <= experts */
+    int has_shared;    /* 1: one shared expert, always routed (src/session.hip:1384-1410) */
+    int max_tokens;    /* capacity of forward(), 1..65536 */
+} moe_ffn_config;
+
+typedef struct moe_ffn_layer moe_ffn_layer;
+
+/* Expert weight bank in the reference's canonical layout: for each expert,
+ * gate [I rows][H/32 blocks], then up [I][H/32], then down [H][I/32], all
+ * 18-byte Q4_0 blocks, rows contiguous (src/session.hip:700-716 expert slots,
+ * src/model.hpp:109-111).  `shared_q4` has the same per-expert layout.
+ *
+ * moe_ffn_create: uploads from HOST memory, repacking on the device into the
+ * MI355X layout (code planes + scale planes); this is the only call that
+ * allocates or synchronises.  Replaces the Experts/GpuExpert constructors
+ * (src/session.hip:689-745, src/gpu_expert.hpp:9, src/hip/expert.hip:205-228). */
+int moe_ffn_create(const moe_ffn_config *config, const void *experts_q4, const void *shared_q4,
+                   int device, moe_ffn_layer **layer);
+
+/* Same, from canonical bytes already resident in device memory (e.g. a
+ * checkpoint loaded straight into HBM). */
+int moe_ffn_create_from_device(const moe_ffn_config *config, const void *experts_q4_device,
+                               const void *shared_q4_device, int device, moe_ffn_layer **layer);
+
+/* Synthetic weight bank generated on the device (for benchmarks of banks too
+ * large to stage through the host): per block d = half(|N(0,0.02)|) and
+ * uniform codes, from a counter-based hash of (seed, block index).  The bytes
+ * are reproducible by moe_ffn_export_expert. */
+int moe_ffn_create_synthetic(const moe_ffn_config *config, uint64_t seed, int device,
+                             moe_ffn_layer **layer);
+
+int moe_ffn_destroy(moe_ffn_layer *layer);
+
+/* Device bytes held by a layer (weights + workspace for max_tokens). */
+int moe_ffn_memory_bytes(const moe_ffn_config *config, size_t *weight_bytes, size_t *workspace_bytes);
+
+/* Copy expert `expert` (0..E-1, or E for the shared expert) back to HOST in
+ * the canonical 18-byte Q4_0 layout (synchronous; test/diagnostic use). */
+int moe_ffn_export_expert(moe_ffn_layer *layer, int expert, void *host_q4);
+
+/* The routed expert FFN of one MoE layer (replaces src/session.hip:1446-1541
+ * plus shared_project/shared_add :1384-1410).  All pointers are DEVICE memory:
+ *   x        [tokens][H] fp32 FFN input
+ *   ids      [tokens][top_k] int32 expert ids (0..E-1, distinct per token)
+ *   weights  [tokens][top_k] fp32 normalised route weights (finite, >= 0)
+ *   shared_gate [tokens] fp32 raw shared-expert gate logits, or NULL for a
+ *            gate of 1.0 (ignored when the layer has no shared expert)
+ *   y        [tokens][H] fp32 output: y = +0; y = y + w_r*expert_r(x) for
+ *            r = 0..top_k-1 in rank order; y = y + sigmoid(g)*shared(x)
+ * tokens in 1..max_tokens.  Enqueue only, no host round trip for routing. */
+int moe_ffn_forward(moe_ffn_layer *layer, const float *x, const int32_t *ids, const float *weights,
+                    int tokens, const float *shared_gate, float *y, int *error, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Stage entry points (parity tests and component timing).
+ * ---------------------------------------------------------------------- */
+
+/* fp32 [columns][width] -> canonical Q8_1 [columns][width/32] (36-byte
+ * blocks).  Replaces launch_quantize_q8_1 (src/hip/linear.cuh:107-108,
+ * kernel src/hip/linear.hip:99-150); width multiple of 32, 32..16384,
+ * columns 1..65536.  Bit-exact with the reference quantize_q8. */
+int moe_quantize_q8_1(const float *x, void *q8, int width, int columns, int *error, void *stream);
+
+/* Route grouping on the device (replaces RouteGroups::prepare,
+ * src/routes.cpp:126-182, and upload_routes src/session.hip:393-410).
+ * Outputs (device): counts [E], offsets [E+1], route_token / route_rank
+ * [tokens*top_k] grouped by ascending expert, then token, then rank. */
+int moe_ffn_group_routes(moe_ffn_layer *layer, const int32_t *ids, const float *weights, int tokens,
+                         int32_t *counts, int32_t *offsets, int32_t *route_token,
+                         int32_t *route_rank, int *error, void *stream);
+
+/* Kernel path selection for the single-expert stages below. */
+enum { MOE_PATH_AUTO = 0, MOE_PATH_STREAM = 1, MOE_PATH_MFMA = 2 };
+
+/* One expert's gate/up projections fused with SiLU(gate)*up and Q8_1
+ * quantization of the middle (replaces Experts::project's gate/up MMVQ +
+ * launch_silu_up_q8_1, src/session.hip:976-991, src/hip/linear.hip:509-525).
+ *   x_q8      [columns][H/32] canonical Q8_1 (device)
+ *   middle    [columns][I] fp32 SiLU(g)*u (device, may be NULL)
+ *   middle_q8 [columns][I/32] canonical Q8_1 (device)
+ *   gate_dots, up_dots [columns][I][H/32] int32 per-block dots (device, may be NULL)
+ * expert in 0..E (E = shared).  columns 1..max_tokens. */
+int moe_ffn_expert_gate_up(moe_ffn_layer *layer, int expert, const void *x_q8, int columns,
+                           float *middle, void *middle_q8, int32_t *gate_dots, int32_t *up_dots,
+                           int path, int *error, void *stream);
+
+/* One expert's down projection of a canonical Q8_1 middle
+ * [columns][I/32] -> y [columns][H] fp32 unweighted (src/session.hip:992-998).
+ * down_dots [columns][H][I/32] int32 (may be NULL). */
+int moe_ffn_expert_down(moe_ffn_layer *layer, int expert, const void *middle_q8, int columns,
+                        float *y, int32_t *down_dots, int path, int *error, void *stream);
+
+/* Rank-order weighted combine (replaces launch_routed_fold +
+ * launch_shared_sigmoid_add_rows, src/hip/session_ops.hip:307-324, 375-391):
+ *   contributions [tokens][top_k][H] unweighted expert outputs
+ *   weights [tokens][top_k], shared [tokens][H] or NULL, shared_gate [tokens] or NULL
+ *   y [tokens][H] = +0 (+ w_r*c_r for r in rank order) (+ sigmoid(g)*shared). */
+int moe_combine(const float *contributions, const float *weights, const float *shared,
+                const float *shared_gate, int tokens, int top_k, int hidden, float *y, int *error,
+                void *stream);
+
+/* Debug view of the last forward() on this layer (device copies, any may be
+ * NULL): x_q8 [tokens][H/32] canonical Q8_1 of the input, middle_q8
+ * [tokens*top_k (+tokens)][I/32] canonical Q8_1 in grouped pair order,
+ * route_token/route_rank [tokens*top_k] grouped order.  Enqueue only. */
+int moe_ffn_debug_last(moe_ffn_layer *layer, void *x_q8, void *middle_q8, int32_t *route_token,
+                       int32_t *route_rank, void *stream);
+
+/* Profiling hook: re-enqueue one stage of the last forward() on `stream`
+ * with the same inputs (which must still be valid): 0 = quantize + group,
+ * 1 = gate/up + SiLU + Q8, 2 = down, 3 = rank-order fold.  Lets a benchmark
+ * time the kernels of one stage alone between events on that stream. */
+enum { MOE_STAGE_PREPARE = 0, MOE_STAGE_GATE_UP = 1, MOE_STAGE_DOWN = 2, MOE_STAGE_FOLD = 3 };
+int moe_ffn_replay_stage(moe_ffn_layer *layer, int stage, void *stream);
+
+/* Last-forward statistics (host, synchronous): work items per path and the
+ * number of experts (incl. shared) that received tokens. */
+int moe_ffn_last_stats(moe_ffn_layer *layer, int32_t *stream_items, int32_t *mfma_items,
+                       int32_t *active_experts);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

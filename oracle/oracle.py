@@ -32,6 +32,15 @@ def _ptr(a):
     return None if a is None else ctypes.c_void_p(a.ctypes.data)
 
 
+def as_q8(a):
+    """View raw canonical Q8_1 bytes (uint8, 36 per block) as Q8_DTYPE records."""
+    a = np.ascontiguousarray(a)
+    if a.dtype == Q8_DTYPE:
+        return a
+    assert a.dtype == np.uint8 and a.size % 36 == 0
+    return a.reshape(-1).view(Q8_DTYPE)
+
+
 def _load_oracle():
     if not os.path.exists(ORACLE_SO):
         raise RuntimeError(f"oracle library missing: {ORACLE_SO} (run make -C oracle)")
@@ -42,6 +51,8 @@ def _load_oracle():
     lib.mo_float_to_half.argtypes = [ctypes.c_float]
     lib.mo_quantize_q8.argtypes = [_P, _SZ, _P]
     lib.mo_block_dot.argtypes = [_P, _P]
+    lib.mo_scaled_dot_q4_0.restype = ctypes.c_float
+    lib.mo_scaled_dot_q4_0.argtypes = [ctypes.c_int32, ctypes.c_uint16, _P]
     lib.mo_block_dots.argtypes = [_P, _I, _I, _P, _I, _P]
     lib.mo_matmul_full.argtypes = [_P, _I, _I, _P, _I, _P]
     lib.mo_matrix_gpu_order.argtypes = [_P, _I, _I, _P, _I, _P]
@@ -113,7 +124,7 @@ def quantize_q8(x):
 
 def block_dots(w, K, M, xq):
     """int32 per-block dots [cols][M][K/32] (src/quant.cpp:48-55)."""
-    xq = np.ascontiguousarray(xq).reshape(-1, K // 32)
+    xq = as_q8(xq).reshape(-1, K // 32)
     cols = xq.shape[0]
     out = np.zeros((cols, M, K // 32), dtype=np.int32)
     lib().mo_block_dots(_ptr(np.ascontiguousarray(w)), K, M, _ptr(xq), cols, _ptr(out))
@@ -121,14 +132,14 @@ def block_dots(w, K, M, xq):
 
 
 def matmul_full(w, K, M, xq):
-    xq = np.ascontiguousarray(xq).reshape(-1, K // 32)
+    xq = as_q8(xq).reshape(-1, K // 32)
     out = np.zeros((xq.shape[0], M), dtype=np.float32)
     lib().mo_matmul_full(_ptr(np.ascontiguousarray(w)), K, M, _ptr(xq), xq.shape[0], _ptr(out))
     return out
 
 
 def matrix_gpu_order(w, K, M, xq, avx2=False):
-    xq = np.ascontiguousarray(xq).reshape(-1, K // 32)
+    xq = as_q8(xq).reshape(-1, K // 32)
     out = np.zeros((xq.shape[0], M), dtype=np.float32)
     f = lib().mo_matrix_gpu_order_avx2 if avx2 else lib().mo_matrix_gpu_order
     rc = f(_ptr(np.ascontiguousarray(w)), K, M, _ptr(xq), xq.shape[0], _ptr(out))
@@ -139,7 +150,7 @@ def matrix_gpu_order(w, K, M, xq, avx2=False):
 
 def expert_forward(gate, up, down, H, I, xq, avx2=False):
     """cpu_expert whole stage.  Returns dict(y, gate, up, middle, middle_q8)."""
-    xq = np.ascontiguousarray(xq).reshape(-1, H // 32)
+    xq = as_q8(xq).reshape(-1, H // 32)
     cols = xq.shape[0]
     y = np.zeros((cols, H), np.float32)
     g = np.zeros((cols, I), np.float32)
@@ -236,7 +247,7 @@ def ref_quantize_q8(x):
 
 
 def ref_matmul(variant, w, K, M, xq):
-    xq = np.ascontiguousarray(xq).reshape(-1, K // 32)
+    xq = as_q8(xq).reshape(-1, K // 32)
     out = np.zeros((xq.shape[0], M), np.float32)
     rc = ref().ref_matmul(variant, _ptr(np.ascontiguousarray(w)), K, M, _ptr(xq), xq.shape[0], _ptr(out))
     if rc:
@@ -245,7 +256,7 @@ def ref_matmul(variant, w, K, M, xq):
 
 
 def ref_cpu_expert(gate, up, down, xq):
-    xq = np.ascontiguousarray(xq).reshape(-1, 80)
+    xq = as_q8(xq).reshape(-1, 80)
     cols = xq.shape[0]
     y = np.zeros((cols, 2560), np.float32)
     g = np.zeros((cols, 640), np.float32)

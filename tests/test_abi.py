@@ -1,0 +1,39 @@
+"""The C-ABI library loads on a machine without a GPU, exports every entry
+point include/moe_ffn.h declares, and rejects bad arguments before any HIP
+call (src/hip/linear.cuh:40-43 convention).  No compute calls here."""
+import ctypes
+import subprocess
+
+import moe_ffn
+
+
+def test_library_exports_every_declared_symbol():
+    lib = moe_ffn.library()
+    declared = moe_ffn.header_symbols()
+    assert len(declared) >= 14
+    for name in declared:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", moe_ffn.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert set(declared) <= exported
+
+
+def test_invalid_arguments_rejected_before_hip():
+    lib = moe_ffn.library()
+    # null / misaligned / bad shapes -> hipErrorInvalidValue (1)
+    assert lib.moe_quantize_q8_1(None, None, 64, 1, None, None) == 1
+    buf = (ctypes.c_float * 64)()
+    assert lib.moe_quantize_q8_1(buf, buf, 33, 1, buf, None) == 1
+    assert lib.moe_quantize_q8_1(buf, buf, 64, 0, buf, None) == 1
+    assert lib.moe_ffn_forward(None, None, None, None, 1, None, None, None, None) == 1
+    assert lib.moe_combine(None, None, None, None, 1, 1, 1, None, None, None) == 1
+    bad = moe_ffn.Config(2048, 500, 512, 10, 1, 8)      # intermediate not a multiple of 32
+    w, s = ctypes.c_size_t(), ctypes.c_size_t()
+    assert lib.moe_ffn_memory_bytes(ctypes.byref(bad), ctypes.byref(w), ctypes.byref(s)) == 1
+
+
+def test_memory_footprint_baseline_shape():
+    w, s = moe_ffn.memory_bytes(2048, 512, 512, 10, True, 16384)
+    # 513 experts x 3 x 1,048,576 weights x 18/32 bytes, plus alignment padding.
+    assert 513 * 1769472 <= w < 513 * 1769472 + 4096
+    assert s > 16384 * 11 * 2048 * 4       # contributions dominate the workspace

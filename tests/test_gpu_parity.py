@@ -1,0 +1,300 @@
+"""GPU parity of the HIP path (libmoe_ffn.so, called through the C ABI) against
+the CPU oracle and the reference-produced golden fixtures.
+
+Bars:
+  * Q8_1 activation / middle codes and headers: bit-exact;
+  * per-block int32 Q4 x Q8 dot sums: bit-exact;
+  * route grouping and the rank-order fold: bit-exact;
+  * fp32 FFN outputs: max |gpu - ref| <= 1e-3 * rms(ref).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import moe_ffn
+import oracle as O
+import workloads as W
+from golden_inputs import expert_weights, route_cases
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+DEV = "cuda:0"
+TOL = 1e-3
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.square(np.asarray(a, np.float64)))))
+
+
+def assert_close(got, ref, tol=TOL, what=""):
+    err = float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))))
+    assert err <= tol * rms(ref), f"{what}: max abs err {err:.3e} > {tol} * rms {rms(ref):.3e}"
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def q8_bytes(q):
+    return np.ascontiguousarray(q).view(np.uint8).reshape(-1)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu_ready():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    print(f"\n[gpu] {torch.cuda.get_device_name(0)}", flush=True)
+    yield
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------- quantizer ---
+def test_quantize_reference_fixture_and_flags():
+    f = np.load(os.path.join(GOLDEN, "quant_q8.npz"), allow_pickle=False)
+    blocks = f["inputs"]
+    q8, err = moe_ffn.quantize_q8_1(dev(blocks.reshape(1, -1)))
+    got = host(q8).reshape(len(blocks), 36)
+    ok = f["status"] == 0
+    assert np.array_equal(got[ok], f["q8"][ok])
+    assert np.all(got[~ok] == 0)
+    assert int(host(err)[0]) != 0
+
+
+def test_quantize_random_bit_exact():
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal((64, 2048)) * np.exp2(rng.integers(-20, 12, (64, 1)))).astype(np.float32)
+    q8, err = moe_ffn.quantize_q8_1(dev(x))
+    assert np.array_equal(host(q8).reshape(-1), q8_bytes(O.quantize_q8(x)))
+    assert int(host(err)[0]) == 0
+
+
+# ------------------------------------------------------ single expert -----
+def _single_expert(H, I, weights, columns):
+    bank = np.concatenate(weights)
+    return moe_ffn.MoeLayer(H, I, 1, 1, False, columns, experts_q4=bank)
+
+
+@pytest.fixture(scope="module")
+def cfg0():
+    """one expert, H 2048, I 512, 8 tokens."""
+    bank = W.q4_bank(1, seed=11)
+    mb = len(bank) // 3
+    g, u, d = bank[:mb], bank[mb:2 * mb], bank[2 * mb:]
+    layer = moe_ffn.MoeLayer(2048, 512, 1, 1, False, 8, experts_q4=bank)
+    x = W.activations(8, seed=12)
+    xq = O.quantize_q8(x)
+    ref = O.expert_forward(g, u, d, 2048, 512, xq, avx2=True)
+    return dict(layer=layer, g=g, u=u, d=d, x=x, xq=xq, ref=ref)
+
+
+def test_cfg0_gate_up_block_dots_bit_exact(cfg0):
+    r = cfg0["layer"].expert_gate_up(0, dev(q8_bytes(cfg0["xq"]).reshape(8, -1)), 8, path=moe_ffn.PATH_STREAM,
+                                     dots=True)
+    assert np.array_equal(host(r["gate_dots"]), O.block_dots(cfg0["g"], 2048, 512, cfg0["xq"]))
+    assert np.array_equal(host(r["up_dots"]), O.block_dots(cfg0["u"], 2048, 512, cfg0["xq"]))
+    assert int(host(r["error"])[0]) == 0
+
+
+def test_cfg0_middle_and_middle_q8(cfg0):
+    r = cfg0["layer"].expert_gate_up(0, dev(q8_bytes(cfg0["xq"]).reshape(8, -1)), 8, path=moe_ffn.PATH_STREAM)
+    middle = host(r["middle"])
+    assert_close(middle, cfg0["ref"]["middle"], what="middle")
+    # The Q8 of the middle is bit-exact given the same fp32 middle.
+    assert np.array_equal(host(r["middle_q8"]).reshape(-1), q8_bytes(O.quantize_q8(middle)))
+
+
+def test_cfg0_down_block_dots_and_projection(cfg0):
+    mq = cfg0["ref"]["middle_q8"]
+    r = cfg0["layer"].expert_down(0, dev(q8_bytes(mq).reshape(8, -1)), 8, path=moe_ffn.PATH_STREAM, dots=True)
+    assert np.array_equal(host(r["down_dots"]), O.block_dots(cfg0["d"], 512, 2048, mq))
+    ref = O.matrix_gpu_order(cfg0["d"], 512, 2048, mq)
+    assert_close(host(r["y"]), ref, tol=1e-5, what="down projection")
+
+
+def test_cfg0_expert_pipeline(cfg0):
+    L = cfg0["layer"]
+    r = L.expert_gate_up(0, dev(q8_bytes(cfg0["xq"]).reshape(8, -1)), 8)
+    y = L.expert_down(0, r["middle_q8"], 8)["y"]
+    assert_close(host(y), cfg0["ref"]["y"], what="expert output")
+
+
+def test_reference_shape_expert_vs_golden():
+    """The reference's own CPU expert output at its fixed 2560/640 shape."""
+    f = np.load(os.path.join(GOLDEN, "cpu_expert_2560x640.npz"), allow_pickle=False)
+    g, u, d = expert_weights(2560, 640)
+    layer = _single_expert(2560, 640, (g, u, d), 3)
+    xq = f["x_q8"].reshape(3, -1)
+    r = layer.expert_gate_up(0, dev(xq), 3, dots=True)
+    assert np.array_equal(host(r["gate_dots"]), O.block_dots(g, 2560, 640, xq))
+    assert_close(host(r["middle"]), f["middle"], what="middle vs reference")
+    y = layer.expert_down(0, r["middle_q8"], 3)["y"]
+    assert_close(host(y), f["y"], what="expert vs reference cpu_expert")
+    layer.close()
+
+
+# ---------------------------------------------------------- grouping -------
+@pytest.fixture(scope="module")
+def router_layer():
+    return moe_ffn.MoeLayer(2048, 512, 512, 10, True, 2048, synthetic_seed=3)
+
+
+def _check_groups(got, ref):
+    assert np.array_equal(host(got["counts"]), ref["counts"])
+    assert np.array_equal(host(got["offsets"]), np.concatenate([[0], np.cumsum(ref["counts"])]))
+    assert np.array_equal(host(got["token"]), ref["token"])
+    assert np.array_equal(host(got["rank"]), ref["rank"])
+
+
+@pytest.mark.parametrize("name", ["pattern_n1", "pattern_n7", "pattern_n64", "pattern_n1024", "random_n300"])
+def test_group_routes_reference_fixture(router_layer, name):
+    f = np.load(os.path.join(GOLDEN, "routes.npz"), allow_pickle=False)
+    ids, w = route_cases()[name]
+    got = router_layer.group_routes(dev(ids), dev(w))
+    ref = {k: f[f"{name}_{k}"] for k in ("token", "rank", "counts")}
+    _check_groups(got, ref)
+    assert int(host(got["error"])[0]) == 0
+
+
+@pytest.mark.parametrize("tokens,kind", [(8, "uniform"), (256, "zipf"), (257, "zipf"), (2048, "zipf")])
+def test_group_routes_vs_oracle(router_layer, tokens, kind):
+    ids, w = W.routes_uniform(tokens, seed=tokens) if kind == "uniform" else W.routes_zipf(tokens, 1.1, seed=tokens)
+    got = router_layer.group_routes(dev(ids), dev(w))
+    _check_groups(got, O.route_groups(ids, w, 512))
+
+
+@pytest.mark.parametrize("name", ["duplicate", "bad_id", "negative_weight"])
+def test_group_routes_invalid_inputs_flag(router_layer, name):
+    ids, w = route_cases()[name]
+    got = router_layer.group_routes(dev(ids), dev(w))
+    assert int(host(got["error"])[0]) & 1
+
+
+# ------------------------------------------------------------- fold --------
+def test_combine_bit_exact():
+    rng = np.random.default_rng(4)
+    c = rng.standard_normal((33, 10, 2048), dtype=np.float32)
+    w = rng.random((33, 10), dtype=np.float32)
+    y, err = moe_ffn.combine(dev(c), dev(w))
+    assert np.array_equal(host(y).view(np.uint32), O.routed_fold(c, w).view(np.uint32))
+    s = rng.standard_normal((33, 2048), dtype=np.float32)
+    y2, _ = moe_ffn.combine(dev(c), dev(w), shared=dev(s))
+    assert np.array_equal(host(y2), (O.routed_fold(c, w) + s).astype(np.float32))
+    g = rng.standard_normal(33, dtype=np.float32)
+    y3, _ = moe_ffn.combine(dev(c), dev(w), shared=dev(s), shared_gate=dev(g))
+    sig = (1.0 / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32)
+    assert_close(host(y3), O.routed_fold(c, w) + sig[:, None] * s, tol=1e-6, what="sigmoid shared add")
+    assert int(host(err)[0]) == 0
+
+
+# -------------------------------------------------------- whole layer ------
+@pytest.fixture(scope="module")
+def moe512():
+    bank = W.q4_bank(512, seed=21)
+    shared = W.q4_bank(1, seed=22)
+    layer = moe_ffn.MoeLayer(2048, 512, 512, 10, True, 4096, experts_q4=bank, shared_q4=shared)
+    return dict(layer=layer, bank=bank, shared=shared)
+
+
+def test_b8_decode_forward(moe512):
+    """8 tokens, uniform top-10 of 512, + shared expert."""
+    x = W.activations(8, seed=31)
+    ids, w = W.routes_uniform(8, seed=32)
+    L = moe512["layer"]
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    ref = O.moe_layer(x, 2048, 512, 512, moe512["bank"], ids, w, shared_q4=moe512["shared"])
+    assert_close(host(y), ref["y"], what="B8 decode layer")
+    assert int(host(err)[0]) == 0
+    dbg = L.debug_last(8)
+    assert np.array_equal(host(dbg["x_q8"]).reshape(-1), q8_bytes(ref["x_q8"]))
+    groups = O.route_groups(ids, w, 512)
+    assert np.array_equal(host(dbg["route_token"]), groups["token"])
+    assert np.array_equal(host(dbg["route_rank"]), groups["rank"])
+
+
+def test_b8_decode_forward_shared_gate(moe512):
+    x = W.activations(8, seed=41)
+    ids, w = W.routes_uniform(8, seed=42)
+    g = np.random.default_rng(43).standard_normal(8).astype(np.float32)
+    y, err = moe512["layer"].forward(dev(x), dev(ids), dev(w), shared_gate=dev(g))
+    ref = O.moe_layer(x, 2048, 512, 512, moe512["bank"], ids, w, shared_q4=moe512["shared"], shared_gate=g)
+    assert_close(host(y), ref["y"], what="B8 with shared sigmoid gate")
+    assert int(host(err)[0]) == 0
+
+
+def test_prefill_4k_zipf_sampled_tokens(moe512):
+    """4096 tokens, Zipf(1.1) top-10.  The whole layer runs
+    on the GPU; the oracle checks a seeded sample of 24 tokens (each token's
+    output depends only on its own routes), plus size-independent properties."""
+    x = W.activations(4096, seed=51)
+    ids, w = W.routes_zipf(4096, 1.1, seed=52)
+    L = moe512["layer"]
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    yh = host(y)
+    assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
+    sample = np.random.default_rng(53).choice(4096, 24, replace=False)
+    mask = np.zeros(4096, np.uint8)
+    mask[sample] = 1
+    ref = O.moe_layer(x, 2048, 512, 512, moe512["bank"], ids, w, shared_q4=moe512["shared"], token_mask=mask)
+    assert_close(yh[sample], ref["y"][sample], what="4K prefill sampled tokens")
+    dbg = L.debug_last(4096)
+    assert np.array_equal(host(dbg["x_q8"]).reshape(4096, -1)[sample],
+                          q8_bytes(ref["x_q8"]).reshape(4096, -1)[sample])
+
+
+def test_forward_reuse_smaller_batch_and_determinism(moe512):
+    L = moe512["layer"]
+    x = W.activations(37, seed=61)
+    ids, w = W.routes_zipf(37, 1.3, seed=62)
+    y1, _ = L.forward(dev(x), dev(ids), dev(w))
+    y1 = host(y1)
+    x5 = x[:5].copy()
+    y5, _ = L.forward(dev(x5), dev(ids[:5]), dev(w[:5]))
+    y2, _ = L.forward(dev(x), dev(ids), dev(w))
+    assert np.array_equal(host(y2), y1)                   # deterministic
+    assert np.array_equal(host(y5), y1[:5])                # per-token independence
+    ref = O.moe_layer(x, 2048, 512, 512, moe512["bank"], ids, w, shared_q4=moe512["shared"])
+    assert_close(y1, ref["y"], what="37-token layer")
+
+
+def test_forward_flags_bad_inputs(moe512):
+    L = moe512["layer"]
+    x = W.activations(8, seed=71)
+    ids, w = W.routes_uniform(8, seed=72)
+    xb = x.copy()
+    xb[3, 100] = np.nan
+    y, err = L.forward(dev(xb), dev(ids), dev(w))
+    assert int(host(err)[0]) & 1
+    ib = ids.copy()
+    ib[2, 4] = 600
+    _, err = L.forward(dev(x), dev(ib), dev(w))
+    assert int(host(err)[0]) & 1
+    ib = ids.copy()
+    ib[2, 4] = ib[2, 0]
+    _, err = L.forward(dev(x), dev(ib), dev(w))
+    assert int(host(err)[0]) & 1
+    # A valid call afterwards is clean (nothing sticky inside the layer).
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    assert int(host(err)[0]) == 0
+
+
+def test_synthetic_bank_export_roundtrip():
+    L = moe_ffn.MoeLayer(2048, 512, 4, 2, True, 8, synthetic_seed=99)
+    e2 = L.export_expert(2)
+    sh = L.export_expert(4)
+    d = e2[:18 * 64 * 512].reshape(-1, 18)[:, :2].copy().view(np.float16).astype(np.float32)
+    assert np.all(np.isfinite(d)) and np.all(d >= 0) and 0.01 < float(np.mean(d)) < 0.025   # |N(0, .02)|
+    x = W.activations(8, seed=81)
+    ids = np.array([[2, 1]] * 8, np.int32)
+    w = np.full((8, 2), 0.5, np.float32)
+    bank = np.concatenate([L.export_expert(e) for e in range(4)])
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    ref = O.moe_layer(x, 2048, 512, 4, bank, ids, w, shared_q4=sh)
+    assert_close(host(y), ref["y"], what="synthetic bank")
+    L.close()

@@ -1,0 +1,289 @@
+"""Pins the CPU oracle (oracle/moe_oracle.c) before it is trusted as the checker.
+
+Sources of truth, in order:
+  * golden fixtures written by the reference's own compiled CPU code
+    (tests/golden/make_golden.py, oracle/_ref): bitwise equality;
+  * literal known answers from the reference's tests
+    (tests/quant_test.cpp:218-300, 338-405, 438-480, 572-603);
+  * closed forms / brute force: IEEE binary16 via numpy, wide-integer dots,
+    one-hot folds.
+"""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from golden_inputs import expert_input, expert_weights, matmul_case, route_cases
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def load(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+def q8_bytes(q):
+    return np.ascontiguousarray(q).view(np.uint8).reshape(-1)
+
+
+# ----------------------------------------------------------------- half ----
+def test_half_to_float_exhaustive_vs_ieee():
+    h = np.arange(65536, dtype=np.uint16)
+    mine = np.array([O.lib().mo_half_to_float(int(v)) for v in h], np.float32)
+    ieee = h.view(np.float16).astype(np.float32)
+    finite = ~np.isnan(ieee)
+    assert np.array_equal(mine[finite].view(np.uint32), ieee[finite].view(np.uint32))
+    # NaNs keep sign and payload and are quieted (quant.cpp:224-227).
+    nan = h[~finite]
+    bits = mine[~finite].view(np.uint32)
+    expect = ((nan.astype(np.uint32) & 0x8000) << 16) | 0x7f800000 | ((nan.astype(np.uint32) & 0x3ff) << 13) | 0x400000
+    assert np.array_equal(bits, expect)
+
+
+def test_float_to_half_rne_vs_numpy():
+    rng = np.random.default_rng(5)
+    bits = rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32)
+    # Concentrate on the half range, subnormal range and rounding boundaries.
+    mags = (rng.standard_normal(200000) * np.exp2(rng.integers(-30, 18, 200000))).astype(np.float32)
+    edges = np.array([65504, 65519.99, 65520, 2.0**-24, 2.0**-25, np.nextafter(2.0**-25, 1), 2.0**-26,
+                      6.1035156e-05, 5.9604645e-08, 1.0 + 2.0**-11, 1.0 + 3 * 2.0**-11], np.float32)
+    vals = np.concatenate([bits.view(np.float32), mags, edges, -edges])
+    vals = vals[~np.isnan(vals)]
+    mine = np.array([O.lib().mo_float_to_half(float(v)) for v in vals], np.uint16)
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(mine, ref)
+
+
+# ------------------------------------------------------------- quantize ----
+def test_quantize_matches_reference_fixture():
+    f = load("quant_q8.npz")
+    for i, block in enumerate(f["inputs"]):
+        if f["status"][i] != 0:
+            with pytest.raises(O.OracleError):
+                O.quantize_q8(block.reshape(1, 32))
+            continue
+        assert np.array_equal(q8_bytes(O.quantize_q8(block.reshape(1, 32))), f["q8"][i]), i
+
+
+def _q(values):
+    return O.quantize_q8(np.asarray(values, np.float32).reshape(1, 32)).reshape(-1)[0]
+
+
+def test_quantize_literal_known_answers():
+    # Ties round away from zero (quant_test.cpp:227-235).
+    v = np.zeros(32, np.float32)
+    v[0] = 127.0
+    v[1:9] = [0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 126.5, -126.5]
+    assert list(_q(v)["qs"][1:9]) == [1, -1, 2, -2, 3, -3, 127, -127]
+    # Raw input sum, not the code reconstruction (quant_test.cpp:244-252).
+    v = np.full(32, 0.4, np.float32)
+    v[0] = 127.0
+    assert _q(v)["s"] == np.float16(np.float32(139.4)).view(np.uint16)
+    # Codes use the original FP32 scale (quant_test.cpp:254-261).
+    v = np.zeros(32, np.float32)
+    v[0] = 1.0
+    v[1] = np.nextafter(np.float32(1.0 / 127.0) * np.float32(0.5), np.float32(0))
+    assert _q(v)["qs"][1] == 0
+    # Ascending XOR butterfly: cancellation gives s = 0 (quant_test.cpp:263-272).
+    v = np.zeros(32, np.float32)
+    v[:4] = [1048576.0, 0.03125, -1048576.0, 0.03125]
+    assert _q(v)["s"] == 0
+    # Minimum surviving half scale keeps codes (quant_test.cpp:274-279).
+    v = np.zeros(32, np.float32)
+    v[0] = np.float32(127.0) * np.nextafter(np.float32(2.0**-25), np.float32(1))
+    v[1] = -v[0]
+    q = _q(v)
+    assert q["d"] == 1 and q["qs"][0] == 127 and q["qs"][1] == -127
+    # Tiny constant: stored half d = 0, codes and raw sum kept (quant_test.cpp:343-353).
+    for sign in (1.0, -1.0):
+        q = _q(np.full(32, sign * 3.4e-6, np.float32))
+        assert q["d"] == 0 and (q["s"] & 0x7fff) != 0 and all(c == int(sign) * 127 for c in q["qs"])
+    # Zero and negative-zero blocks are the exact zero block.
+    v = np.zeros(32, np.float32)
+    v[::2] = -0.0
+    assert q8_bytes(_q(v)).sum() == 0
+
+
+def test_quantize_rejections():
+    for bad in (np.inf, -np.inf, np.nan):
+        v = np.ones(32, np.float32)
+        v[7] = bad
+        with pytest.raises(O.OracleError):
+            _q(v)
+    v = np.zeros(32, np.float32)
+    v[0] = np.float32(1.4e-45)        # FP32 scale underflows to zero
+    with pytest.raises(O.OracleError):
+        _q(v)
+    with pytest.raises(O.OracleError):
+        _q(np.full(32, 3000.0, np.float32))   # raw sum overflows half
+
+
+# ------------------------------------------------------------------ dots ---
+def test_block_dot_full_range_closed_form():
+    L = O.lib()
+    for code in range(16):
+        qs = np.full(16, code * 17, np.uint8)
+        for value in (-128, -127, -1, 0, 1, 126, 127):
+            c = np.full(32, value, np.int8)
+            assert L.mo_block_dot(qs.ctypes.data, c.ctypes.data) == 32 * code * value
+
+
+def test_block_dot_brute_force():
+    rng = np.random.default_rng(3)
+    L = O.lib()
+    for _ in range(500):
+        qs = rng.integers(0, 256, 16, dtype=np.uint8)
+        c = rng.integers(-128, 128, 32, dtype=np.int8)
+        nib = np.concatenate([qs & 15, qs >> 4]).astype(np.int64)
+        assert L.mo_block_dot(qs.ctypes.data, c.ctypes.data) == int((nib * c.astype(np.int64)).sum())
+
+
+def test_scaled_dot_literal():
+    # quant_test.cpp:460-467: d4 = -1, d8 = 0.5, s8 = 3, codes -128, nibbles 0 -> 24.
+    x = np.zeros(1, O.Q8_DTYPE)
+    x["d"], x["s"], x["qs"] = 0x3800, 0x4200, -128
+    assert O.lib().mo_scaled_dot_q4_0(0, 0xbc00, x.ctypes.data) == 24.0
+
+
+def test_matmul_literal_fixture():
+    # quant_test.cpp:572-603: two one-block rows x two columns, column-major out.
+    x = np.zeros(2, O.Q8_DTYPE)
+    x["d"] = 0x3c00
+    x["s"][0], x["s"][1] = 0x4000, 0xc200
+    x["qs"][0, :16], x["qs"][0, 16:], x["qs"][1] = 3, -4, -128
+    w = np.zeros((2, 18), np.uint8)
+    w[:, :2] = np.array([0x3c00], np.uint16).view(np.uint8)
+    w[0, 2:], w[1, 2:] = 0x21, 0x75
+    out = O.matmul_full(w.reshape(-1), 32, 2, x)
+    assert out.reshape(-1).tolist() == [-96.0, -224.0, -6120.0, -24552.0]
+
+
+def test_matmul_matches_reference_fixture():
+    f = load("matmul.npz")
+    for name, (w, K, M, xq) in matmul_case().items():
+        mine = O.matmul_full(w, K, M, xq)
+        for tag in ("scalar", "avx2", "q8ref"):
+            key = f"{name}_{tag}"
+            if key in f:
+                assert np.array_equal(mine.view(np.uint32), f[key].view(np.uint32)), key
+
+
+# ----------------------------------------------------------- cpu_expert ----
+@pytest.fixture(scope="module")
+def expert_fixture():
+    f = load("cpu_expert_2560x640.npz")
+    gate, up, down = expert_weights(2560, 640)
+    assert hashlib.sha256(gate.tobytes() + up.tobytes() + down.tobytes()).hexdigest() == str(f["weights_sha256"])
+    return f, gate, up, down
+
+
+def test_expert_input_quantization_matches_reference(expert_fixture):
+    f, *_ = expert_fixture
+    x = expert_input(3, 2560)
+    assert np.array_equal(x, f["x"])
+    assert np.array_equal(q8_bytes(O.quantize_q8(x)), f["x_q8"].reshape(-1))
+
+
+@pytest.mark.parametrize("avx2", [False, True])
+def test_expert_forward_bitwise_vs_reference(expert_fixture, avx2):
+    f, gate, up, down = expert_fixture
+    out = O.expert_forward(gate, up, down, 2560, 640, f["x_q8"], avx2=avx2)
+    for key in ("gate", "up", "middle", "y"):
+        assert np.array_equal(out[key].view(np.uint32), f[key].view(np.uint32)), key
+    assert np.array_equal(q8_bytes(out["middle_q8"]), f["middle_q8"].reshape(-1))
+
+
+def test_expert_columns_are_independent(expert_fixture):
+    f, gate, up, down = expert_fixture
+    xq = O.as_q8(f["x_q8"]).reshape(3, 80)
+    grouped = O.expert_forward(gate, up, down, 2560, 640, xq)["y"]
+    for c in range(3):
+        single = O.expert_forward(gate, up, down, 2560, 640, xq[c:c + 1])["y"]
+        assert np.array_equal(single.view(np.uint32), grouped[c:c + 1].view(np.uint32))
+
+
+def test_gpu_order_differs_from_serial_order(expert_fixture):
+    # The two reference orders are distinct: a test that mixed them up fails.
+    f, gate, *_ = expert_fixture
+    xq = O.as_q8(f["x_q8"]).reshape(3, 80)
+    a = O.matrix_gpu_order(gate, 2560, 640, xq)
+    b = O.matmul_full(gate, 2560, 640, xq)
+    assert not np.array_equal(a, b)
+    assert np.max(np.abs(a - b)) < 1e-3 * np.sqrt(np.mean(b * b))
+
+
+# ---------------------------------------------------------------- routes ---
+def test_routes_match_reference_fixture():
+    f = load("routes.npz")
+    for name, (ids, w) in route_cases().items():
+        if int(f[f"{name}_status"]) != 0:
+            with pytest.raises(O.OracleError):
+                O.route_groups(ids, w, 512)
+            continue
+        g = O.route_groups(ids, w, 512)
+        for key in ("token", "rank", "expert", "counts"):
+            assert np.array_equal(g[key], f[f"{name}_{key}"]), (name, key)
+        assert np.array_equal(g["weight"].view(np.uint32), f[f"{name}_weight_bits"]), name
+        assert np.array_equal(g["offsets"][1:], np.cumsum(g["counts"]))
+
+
+def test_routes_brute_force_stable_sort():
+    rng = np.random.default_rng(9)
+    ids = np.array([rng.permutation(64)[:6] for _ in range(40)], np.int32)
+    w = rng.random((40, 6), dtype=np.float32)
+    g = O.route_groups(ids, w, 64)
+    keys = sorted((int(ids[t, r]), t, r) for t in range(40) for r in range(6))
+    assert [(int(e), int(t), int(r)) for e, t, r in zip(g["expert"], g["token"], g["rank"])] == keys
+
+
+# ------------------------------------------------------------------ fold ---
+def test_fold_rank_order_and_rounding():
+    # Left fold from +0 in rank order with separately rounded products: the
+    # cancellation case distinguishes it from pairwise or reversed sums.
+    c = np.array([[[1e8], [1.0], [-1e8]]], np.float32)
+    w = np.ones((1, 3), np.float32)
+    assert O.routed_fold(c, w)[0, 0] == 0.0          # (1e8 + 1) - 1e8 in fp32
+    c3 = np.array([[[1e8], [-1e8], [1.0]]], np.float32)
+    assert O.routed_fold(c3, w)[0, 0] == 1.0
+    # One-hot weights copy a contribution exactly; a scaled product rounds once.
+    rng = np.random.default_rng(1)
+    c = rng.standard_normal((4, 10, 16), dtype=np.float32)
+    for r in range(10):
+        w = np.zeros((4, 10), np.float32)
+        w[:, r] = 1.0
+        assert np.array_equal(O.routed_fold(c, w), c[:, r])
+    w = np.zeros((4, 10), np.float32)
+    w[:, 3] = 0.3
+    assert np.array_equal(O.routed_fold(c, w), (np.float32(0.3) * c[:, 3]).astype(np.float32))
+
+
+# ------------------------------------------------------------ composition --
+def test_moe_layer_composes_expert_and_fold():
+    H, I, E, k, N = 256, 64, 8, 3, 5
+    rng = np.random.default_rng(2)
+    bank = np.concatenate([np.concatenate(expert_weights(H, I, seed=700 + 3 * e)) for e in range(E)])
+    shared = np.concatenate(expert_weights(H, I, seed=990))
+    x = rng.standard_normal((N, H), dtype=np.float32)
+    ids = np.array([rng.permutation(E)[:k] for _ in range(N)], np.int32)
+    w = rng.random((N, k), dtype=np.float32)
+    out = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, want_contrib=True)
+    xq = O.quantize_q8(x)
+    eb = 3 * H // 32 * I * 18
+    mb = eb // 3
+    for t in range(N):
+        for r in range(k):
+            e = ids[t, r]
+            b = bank[e * eb:(e + 1) * eb]
+            y = O.expert_forward(b[:mb], b[mb:2 * mb], b[2 * mb:], H, I, xq[t:t + 1])["y"][0]
+            assert np.array_equal(y, out["contrib"][t, r])
+    folded = O.routed_fold(out["contrib"], w)
+    s = np.stack([O.expert_forward(shared[:mb], shared[mb:2 * mb], shared[2 * mb:], H, I, xq[t:t + 1])["y"][0]
+                  for t in range(N)])
+    assert np.array_equal(out["y"], (folded + s).astype(np.float32))
+    # Baseline pool computes the same bits.
+    sec, workers, yb = O.baseline_layer(x, H, I, E, bank, ids, w, shared_q4=shared, workers=2, repeats=1)
+    assert workers >= 1 and sec > 0
+    assert np.array_equal(yb, out["y"])
