@@ -760,7 +760,9 @@ hipError_t launch_fill_u32(uint32_t *p, uint32_t value, size_t count, hipStream_
 hipError_t launch_prepare(const float *x, const int32_t *ids, const float *weights, int tokens, Shape shape,
                           Act xq, RouteOut routes, int mfma_min, int *error, hipStream_t s) {
     GroupParams p{ids, weights, tokens, shape, routes, mfma_min, error};
-    const size_t q_elements = static_cast<size_t>(tokens) * shape.H;
+    // Grouping alone (x == nullptr, as moe_ffn_group_routes calls it) launches
+    // no quantization blocks: they would read x.
+    const size_t q_elements = x ? static_cast<size_t>(tokens) * shape.H : 0;
     const int W = (tokens + 31) / 32;
     const size_t small_lds = (static_cast<size_t>(shape.E) * W * 2 + static_cast<size_t>(shape.Ep) * 4 + 1 + 17) * 4;
     if (tokens <= kSmallGroupTokens && small_lds <= 60 * 1024) {
