@@ -32,15 +32,17 @@ def log(*a):
 
 def time_forward(layer, x, ids, w, steps, warmup):
     import torch
+    y = torch.empty((x.shape[0], layer.H), dtype=torch.float32, device=x.device)
+    err = torch.zeros(1, dtype=torch.int32, device=x.device)
     for _ in range(warmup):
-        layer.forward(x, ids, w)
+        layer.forward(x, ids, w, y=y, error=err)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
     for _ in range(steps):
-        y, err = layer.forward(x, ids, w)
+        layer.forward(x, ids, w, y=y, error=err)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
@@ -85,7 +87,18 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device-to-device copy x5 (FETCH_SIZE/WRITE_SIZE scale for rocprofv3 --pmc)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[bench] copy calibration: 5 x 1 GiB device copies")
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the MoE layer on one GPU only; --gpus must be 1", file=sys.stderr)
         sys.exit(2)
@@ -144,6 +157,7 @@ def main():
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": None, "bytes_per_launch": gate_bytes, "us_per_launch": t_gate * 1e6},
         "stages_us": {"prepare": t_prep * 1e6, "gate_up": t_gate * 1e6, "down": t_down * 1e6, "fold": t_fold * 1e6},
+        "down_stage_hbm_frac": units * DOWN_BYTES_PER_EXPERT / t_down / 1e9 / HBM_PEAK_GBS,
     }
 
     # ---- 4K Zipf prefill (reported beside) --------------------------------

@@ -29,9 +29,13 @@ struct Bank {
 };
 
 // A work item: one expert group slice of <= kStreamTokens (stream path) or
-// <= kMfmaTile (MFMA path) consecutive grouped pairs.
+// <= kMfmaTile (MFMA path) consecutive grouped pairs.  Streaming items carry
+// their pairs' tokens and ranks inline so a kernel can issue activation loads
+// straight after the (scalar) item load.
 struct Item {
     int expert, first, ncols, pad;
+    int token[kStreamTokens];
+    int rank[kStreamTokens];
 };
 
 struct Shape {
@@ -46,7 +50,7 @@ struct RouteOut {
     int32_t *pos_of;       // [N*k] grouped position of (t, r) or -1
     Item *stream_items;    // [<= P'/kStreamTokens + Ep]
     Item *mfma_items;      // [<= P'/kMfmaTile + Ep]
-    int32_t *item_counts;  // [0] stream, [1] mfma, [2] active experts
+    int32_t *item_counts;  // [0] stream items, [1] mfma items, [2] active groups, [3] grouped pairs
     uint32_t *bitmap;      // large path: [W][Ep] token bitmaps
     uint32_t *wprefix;     // large path: [W][Ep] per-word exclusive popcount prefix
 };
@@ -97,6 +101,7 @@ struct FfnArgs {
     float *middle_f32; // optional [pairs][I]
     int32_t *gate_dots, *up_dots, *down_dots;  // optional per-block dots [pair][rows][blocks]
     int *error;
+    int cu_count;      // compute units of the device (persistent grids)
 };
 
 hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s);

@@ -266,8 +266,10 @@ struct GroupParams {
 // Items from group counts/offsets: groups below mfma_min (or all groups when
 // mfma_min == 0) become streaming items of <= kStreamTokens pairs, larger
 // groups become MFMA items of <= kMfmaTile pairs.  cnt/off may live in LDS.
+// With fill, the grouped pair arrays are already written (by this block) and
+// streaming items get their tokens and ranks inline.
 __device__ void build_items(const GroupParams &p, const int32_t *cnt, const int32_t *off, int32_t *ns,
-                            int32_t *nm, int32_t *tmp) {
+                            int32_t *nm, int32_t *tmp, bool fill) {
     const int Ep = p.shape.Ep;
     for (int e = threadIdx.x; e < Ep; e += blockDim.x) {
         const int n = cnt[e];
@@ -287,15 +289,25 @@ __device__ void build_items(const GroupParams &p, const int32_t *cnt, const int3
         for (int c = 0, f = 0; f < n; ++c, f += size) {
             Item it;
             it.expert = e; it.first = off[e] + f; it.ncols = min(size, n - f); it.pad = 0;
+            for (int j = 0; j < kStreamTokens; ++j) {
+                const bool in = fill && !big && j < it.ncols;
+                it.token[j] = in ? p.r.pair_token[it.first + j] : 0;
+                it.rank[j] = in ? p.r.pair_rank[it.first + j] : 0;
+            }
             dst[c] = it;
         }
     }
+    // Active groups: counted with one LDS atomic per nonempty group.
+    if (threadIdx.x == 0) tmp[0] = 0;
+    __syncthreads();
+    for (int e = threadIdx.x; e < Ep; e += blockDim.x)
+        if (cnt[e] > 0) atomicAdd(&tmp[0], 1);
+    __syncthreads();
     if (threadIdx.x == 0) {
-        int active = 0;
-        for (int e = 0; e < Ep; ++e) active += cnt[e] > 0;
         p.r.item_counts[0] = total_s;
         p.r.item_counts[1] = total_m;
-        p.r.item_counts[2] = active;
+        p.r.item_counts[2] = tmp[0];
+        p.r.item_counts[3] = off[Ep];   // grouped pairs incl. shared
     }
 }
 
@@ -325,14 +337,25 @@ __global__ __launch_bounds__(1024) void k_prepare_small(GroupParams p, const flo
     int32_t *ns = off + Ep + 1;                                         // [Ep]
     int32_t *nm = ns + Ep;                                              // [Ep]
     int32_t *tmp = nm + Ep;                                             // [17]
+    int32_t *eid = tmp + 17;                                            // [N*k] expert or -1
     for (int i = threadIdx.x; i < E * W; i += blockDim.x) bits[i] = 0;
+    for (int i = threadIdx.x; i < N * k; i += blockDim.x) eid[i] = p.ids[i];
     __syncthreads();
+    // Validate (src/routes.cpp:145-157) from LDS.  Thread tid owns entries
+    // tid + m*blockDim (m < 32, N*k <= 32*blockDim); bit m of `valid` records
+    // entry m's validity for the scatter below.
     int flags = 0;
-    for (int t = threadIdx.x; t < N; t += blockDim.x)
-        for (int r = 0; r < k; ++r) {
-            const int e = route_entry(p.ids, p.weights, t, r, k, E, flags);
-            if (e >= 0) atomicOr(&bits[e * W + (t >> 5)], 1u << (t & 31));
-        }
+    uint32_t valid = 0;
+    for (int i = threadIdx.x, m = 0; i < N * k; i += blockDim.x, ++m) {
+        const int t = i / k, r = i % k, e = eid[i];
+        const float w = p.weights[i];
+        if (!isfinite(w) || w < 0.0f) flags |= 1;
+        bool ok = e >= 0 && e < E;
+        for (int q = 0; ok && q < r; ++q) ok = eid[t * k + q] != e;
+        if (!ok) { flags |= 1; continue; }
+        valid |= 1u << m;
+        atomicOr(&bits[e * W + (t >> 5)], 1u << (t & 31));
+    }
     __syncthreads();
     for (int e = threadIdx.x; e < Ep; e += blockDim.x) {
         if (e >= E) { cnt[e] = N; continue; }   // shared expert: every token
@@ -344,25 +367,23 @@ __global__ __launch_bounds__(1024) void k_prepare_small(GroupParams p, const flo
     const int total = block_exclusive_scan(cnt, off, Ep, tmp);
     if (threadIdx.x == 0) off[Ep] = total;
     __syncthreads();
-    for (int t = threadIdx.x; t < N; t += blockDim.x) {
-        for (int r = 0; r < k; ++r) {
-            int dummy = 0;
-            const int e = route_entry(p.ids, p.weights, t, r, k, E, dummy);
-            int pos = -1;
-            if (e >= 0) {
-                const uint32_t word = bits[e * W + (t >> 5)];
-                pos = off[e] + static_cast<int>(wpre[e * W + (t >> 5)]) +
-                      __popc(word & ((1u << (t & 31)) - 1u));
-                p.r.pair_token[pos] = t;
-                p.r.pair_rank[pos] = r;
-            }
-            p.r.pos_of[static_cast<size_t>(t) * k + r] = pos;
+    for (int i = threadIdx.x, m = 0; i < N * k; i += blockDim.x, ++m) {
+        const int t = i / k, r = i % k, e = eid[i];
+        int pos = -1;
+        if (valid & (1u << m)) {
+            const uint32_t word = bits[e * W + (t >> 5)];
+            pos = off[e] + static_cast<int>(wpre[e * W + (t >> 5)]) + __popc(word & ((1u << (t & 31)) - 1u));
+            p.r.pair_token[pos] = t;
+            p.r.pair_rank[pos] = r;
         }
-        if (Ep > E) { p.r.pair_token[off[E] + t] = t; p.r.pair_rank[off[E] + t] = k; }
+        p.r.pos_of[i] = pos;
     }
+    if (Ep > E)
+        for (int t = threadIdx.x; t < N; t += blockDim.x) { p.r.pair_token[off[E] + t] = t; p.r.pair_rank[off[E] + t] = k; }
     for (int e = threadIdx.x; e < Ep; e += blockDim.x) { p.r.counts[e] = cnt[e]; p.r.offsets[e] = off[e]; }
     if (threadIdx.x == 0) p.r.offsets[Ep] = off[Ep];
-    build_items(p, cnt, off, ns, nm, tmp);
+    __syncthreads();   // pair arrays complete before build_items copies them into items
+    build_items(p, cnt, off, ns, nm, tmp, true);
     if (flags) atomicOr(p.error, flags);
 }
 
@@ -432,7 +453,7 @@ __global__ __launch_bounds__(1024) void k_offsets_items(GroupParams p) {
     __syncthreads();
     for (int e = threadIdx.x; e < Ep; e += blockDim.x) { p.r.counts[e] = cnt[e]; p.r.offsets[e] = off[e]; }
     if (threadIdx.x == 0) p.r.offsets[Ep] = off[Ep];
-    build_items(p, cnt, off, ns, nm, tmp);
+    build_items(p, cnt, off, ns, nm, tmp, false);   // tokens filled by k_item_tokens
 }
 
 // Step 4: one thread per token places its pairs.
@@ -460,6 +481,18 @@ __global__ __launch_bounds__(256) void k_scatter_pairs(GroupParams p) {
     }
 }
 
+// Copies each streaming item's pair tokens and ranks into the item (runs
+// after the grouped pair arrays are complete).
+__global__ __launch_bounds__(256) void k_item_tokens(RouteOut r) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= r.item_counts[0]) return;
+    Item &it = r.stream_items[i];
+    for (int j = 0; j < it.ncols; ++j) {
+        it.token[j] = r.pair_token[it.first + j];
+        it.rank[j] = r.pair_rank[it.first + j];
+    }
+}
+
 // Single-expert stage setup (one block).
 __global__ void k_single_items(Shape shape, RouteOut r, int expert, int columns, int use_mfma) {
     for (int j = threadIdx.x; j < columns; j += blockDim.x) { r.pair_token[j] = j; r.pair_rank[j] = 0; }
@@ -470,11 +503,13 @@ __global__ void k_single_items(Shape shape, RouteOut r, int expert, int columns,
         for (int f = 0; f < columns; f += size, ++c) {
             Item it;
             it.expert = expert; it.first = f; it.ncols = min(size, columns - f); it.pad = 0;
+            for (int j = 0; j < kStreamTokens; ++j) { it.token[j] = f + j; it.rank[j] = 0; }
             dst[c] = it;
         }
         r.item_counts[0] = use_mfma ? 0 : c;
         r.item_counts[1] = use_mfma ? c : 0;
         r.item_counts[2] = 1;
+        r.item_counts[3] = columns;
         (void)shape;
     }
 }
@@ -482,13 +517,13 @@ __global__ void k_single_items(Shape shape, RouteOut r, int expert, int columns,
 // ------------------------------------------------ streaming (decode) path ---
 // gate/up + SiLU + Q8.  One work unit = (item, slice of 32 intermediate rows).
 // 8 waves: waves 0-3 take gate rows slice*32 + 8w .. +7, waves 4-7 the same
-// up rows.  Lane l takes blocks l, l+64, ...: each row is one coalesced
-// 16-byte-per-lane wave load of the code plane.  After the K loop the 8 row
-// sums of each token are reduced across the wave by a transposing butterfly
-// (xor 32/16/8 halve the row set, xor 4/2/1 finish the sum), the 64 sums go
-// through LDS, and wave j quantizes token j's 32 SiLU(g)*u values into one
-// Q8_1 block of the middle.
-template<bool Dbg>
+// up rows.  Lane l takes blocks l, l+64, ... (NBL of them): each row is one
+// coalesced 16-byte-per-lane wave load of the code plane, held in registers
+// while the item's tokens are processed one at a time.  Each token's 8 row
+// sums are reduced across the wave by a transposing butterfly (xor 32/16/8
+// halve the row set, xor 4/2/1 finish the sum), the 64 sums go through LDS,
+// and wave j quantizes token j's 32 SiLU(g)*u values into one Q8_1 block.
+template<int NBL, bool Dbg>
 __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
     constexpr int T = kStreamTokens;
     __shared__ float gu[2][32][T];
@@ -496,6 +531,8 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
     const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32, S = I / 32;
     const int units = a.routes.item_counts[0] * S;
     const int mat = wave >> 2;
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+    const int rho = (b5 ? 4 : 0) + (b4 ? 2 : 0) + (b3 ? 1 : 0);
     for (int u = blockIdx.x; u < units; u += gridDim.x) {
         const Item it = a.routes.stream_items[u / S];
         const int s = u % S;
@@ -503,52 +540,62 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
         const size_t mrow = static_cast<size_t>(it.expert) * I + row0;
         const uint8_t *codes = (mat ? a.bank.up_codes : a.bank.gate_codes) + mrow * nbh * 16;
         const uint16_t *scales = (mat ? a.bank.up_scales : a.bank.gate_scales) + mrow * nbh;
-        int tok[T];
+        // NBL <= 2: the item's weight rows stay in registers across its
+        // tokens.  NBL == 0 (H > 4096): rows are re-read per token (L1/L2 hits).
+        constexpr int HOLD = NBL > 0 ? NBL : 1;
+        uint4 w[HOLD][8];
+        float d4[HOLD][8];
 #pragma unroll
-        for (int j = 0; j < T; ++j) tok[j] = a.routes.pair_token[it.first + min(j, it.ncols - 1)];
-        float acc[8][T];
-#pragma unroll
-        for (int r = 0; r < 8; ++r)
-#pragma unroll
-            for (int j = 0; j < T; ++j) acc[r][j] = 0.0f;
-        for (int kb = lane; kb < nbh; kb += 64) {
-            uint4 w[8];
-            float d4[8];
+        for (int nb = 0; nb < NBL; ++nb) {
+            const int kb = lane + 64 * nb;
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
-                w[r] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbh + kb) * 16);
-                d4[r] = h2f(scales[static_cast<size_t>(r) * nbh + kb]);
+                if (kb < nbh) {
+                    w[nb][r] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbh + kb) * 16);
+                    d4[nb][r] = h2f(scales[static_cast<size_t>(r) * nbh + kb]);
+                } else {
+                    w[nb][r] = make_uint4(0, 0, 0, 0);
+                    d4[nb][r] = 0.0f;
+                }
             }
+        }
+#pragma unroll 1
+        for (int j = 0; j < it.ncols; ++j) {
+            const int tok = a.routes.pair_token[it.first + j];
+            float acc[8];
 #pragma unroll
-            for (int j = 0; j < T; ++j) {
-                if (j >= it.ncols) break;
-                const size_t xb = static_cast<size_t>(tok[j]) * nbh + kb;
+            for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+#pragma unroll
+            for (int nb = 0; nb < (NBL > 0 ? NBL : 1); ++nb)
+            for (int kb = lane + 64 * nb; kb < nbh; kb += (NBL > 0 ? nbh : 64)) {
+                if constexpr (NBL == 0) {
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) {
+                        w[0][r] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbh + kb) * 16);
+                        d4[0][r] = h2f(scales[static_cast<size_t>(r) * nbh + kb]);
+                    }
+                }
+                const size_t xb = static_cast<size_t>(tok) * nbh + kb;
                 const uint4 x0 = *reinterpret_cast<const uint4 *>(a.xq.codes + xb * 32);
                 const uint4 x1 = *reinterpret_cast<const uint4 *>(a.xq.codes + xb * 32 + 16);
                 const uint32_t hd = a.xq.heads[xb];
                 const float d8 = h2f(hd), c8 = -8.0f * h2f(hd >> 16);
 #pragma unroll
                 for (int r = 0; r < 8; ++r) {
-                    const int dot = dot_block(w[r], x0, x1);
+                    const int dot = dot_block(w[nb][r], x0, x1);
                     if constexpr (Dbg) {
                         int32_t *dots = mat ? a.up_dots : a.gate_dots;
                         if (dots) dots[(static_cast<size_t>(it.first + j) * I + row0 + r) * nbh + kb] = dot;
                     }
-                    acc[r][j] = fmaf(d4[r], fmaf(static_cast<float>(dot), d8, c8), acc[r][j]);
+                    acc[r] = fmaf(d4[nb][r], fmaf(static_cast<float>(dot), d8, c8), acc[r]);
                 }
             }
-        }
-        // Transposing reduction: lane ends with the sum of row rho(lane).
-        const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
-        const int rho = (b5 ? 4 : 0) + (b4 ? 2 : 0) + (b3 ? 1 : 0);
-#pragma unroll
-        for (int j = 0; j < T; ++j) {
-            if (j >= it.ncols) break;
+            // Transposing reduction: lane ends with the sum of row rho(lane).
             float v4[4], v2[2];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float send = b5 ? acc[i][j] : acc[i + 4][j];
-                const float keep = b5 ? acc[i + 4][j] : acc[i][j];
+                const float send = b5 ? acc[i] : acc[i + 4];
+                const float keep = b5 ? acc[i + 4] : acc[i];
                 v4[i] = keep + __shfl_xor(send, 32, 64);
             }
 #pragma unroll
@@ -580,6 +627,99 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
             }
         }
         __syncthreads();
+    }
+}
+
+// High-occupancy form of k_gate_up_stream for H <= 2048 (one block per lane,
+// one unit per workgroup).  Decode streaming is bound by bytes in flight per
+// CU: each wave keeps its 8 weight rows (8 KB) in flight with a small register
+// footprint, so 4 workgroups (32 waves, 256 KB of loads) fit on a CU.  Same
+// arithmetic and outputs as k_gate_up_stream.
+template<bool Dbg>
+__global__ __launch_bounds__(512, 8) void k_gate_up_lean(FfnArgs a) {
+    constexpr int T = kStreamTokens;
+    __shared__ float gu[2][32][T];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32, S = I / 32;
+    const int u = blockIdx.x;
+    if (u >= a.routes.item_counts[0] * S) return;    // uniform per workgroup
+    const int mat = wave >> 2;
+    const bool has = lane < nbh;
+    // Item fields are read through the pointer (uniform scalar loads): a
+    // local copy indexed by the runtime token slot would live in scratch.
+    const Item *itp = a.routes.stream_items + u / S;
+    const Item it{itp->expert, itp->first, itp->ncols, 0};
+    const int s = u % S;
+    const int row0 = s * 32 + (wave & 3) * 8;
+    const size_t b0 = (static_cast<size_t>(it.expert) * I + row0) * nbh + lane;
+    const uint8_t *codes = (mat ? a.bank.up_codes : a.bank.gate_codes) + b0 * 16;
+    const uint16_t *scales = (mat ? a.bank.up_scales : a.bank.gate_scales) + b0;
+    uint4 w[8];
+    uint32_t d4[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        w[r] = has ? *reinterpret_cast<const uint4 *>(codes + static_cast<size_t>(r) * nbh * 16) : make_uint4(0, 0, 0, 0);
+        d4[r] = has ? scales[static_cast<size_t>(r) * nbh] : 0u;
+    }
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+    const int rho = (b5 ? 4 : 0) + (b4 ? 2 : 0) + (b3 ? 1 : 0);
+#pragma unroll 1
+    for (int j = 0; j < it.ncols; ++j) {
+        // Token ids come from the item (scalar loads issued with the item),
+        // so these loads go out right behind the weight loads.
+        const size_t xb = static_cast<size_t>(itp->token[j]) * nbh + lane;
+        const uint4 x0 = has ? *reinterpret_cast<const uint4 *>(a.xq.codes + xb * 32) : make_uint4(0, 0, 0, 0);
+        const uint4 x1 = has ? *reinterpret_cast<const uint4 *>(a.xq.codes + xb * 32 + 16) : make_uint4(0, 0, 0, 0);
+        const uint32_t hx = has ? a.xq.heads[xb] : 0u;
+        const float d8 = h2f(hx), c8 = -8.0f * h2f(hx >> 16);
+        // Keep the nibble masking inside the token loop: hoisting it would
+        // hold 64 unpacked words per lane and halve the occupancy.
+#pragma unroll
+        for (int r = 0; r < 8; ++r) asm volatile("" : "+v"(w[r].x), "+v"(w[r].y), "+v"(w[r].z), "+v"(w[r].w));
+        float acc[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int dot = dot_block(w[r], x0, x1);
+            if constexpr (Dbg) {
+                int32_t *dots = mat ? a.up_dots : a.gate_dots;
+                if (dots && has) dots[(static_cast<size_t>(it.first + j) * I + row0 + r) * nbh + lane] = dot;
+            }
+            acc[r] = h2f(d4[r]) * fmaf(static_cast<float>(dot), d8, c8);
+        }
+        float v4[4], v2[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float send = b5 ? acc[i] : acc[i + 4];
+            const float keep = b5 ? acc[i + 4] : acc[i];
+            v4[i] = keep + __shfl_xor(send, 32, 64);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float send = b4 ? v4[i] : v4[i + 2];
+            const float keep = b4 ? v4[i + 2] : v4[i];
+            v2[i] = keep + __shfl_xor(send, 16, 64);
+        }
+        float v = (b3 ? v2[1] : v2[0]) + __shfl_xor(b3 ? v2[0] : v2[1], 8, 64);
+        v = xor_sum(v, 4);
+        v = xor_sum(v, 2);
+        v = xor_sum(v, 1);
+        if ((lane & 7) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
+    }
+    __syncthreads();
+    if (wave < it.ncols) {
+        const int j = wave, i = lane & 31;
+        int flags = 0;
+        const float m = silu_mul(gu[0][i][j], gu[1][i][j], flags);
+        const Q8Lane q = quantize32(m);
+        if (lane < 32) {
+            const size_t pair = static_cast<size_t>(it.first + j);
+            const size_t mb = pair * nbi + s;
+            a.mq.codes[mb * 32 + i] = static_cast<uint8_t>(q.code);
+            if (i == 0) a.mq.heads[mb] = q.head;
+            if (Dbg && a.middle_f32) a.middle_f32[pair * I + s * 32 + i] = m;
+            const int f = flags | (i == 0 ? q.flags : 0);
+            if (f) atomicOr(a.error, f);
+        }
     }
 }
 
@@ -647,6 +787,82 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
                 for (int m = LPR / 2; m >= 1; m >>= 1) v = xor_sum(v, m);
                 if (kb0 == 0) a.out[orow * H + row0 + l * RPL + sub] = v;
             }
+        }
+    }
+}
+
+// High-occupancy streaming down projection for I <= 512 (a row of I/32 <= 16
+// blocks is <= 256 code bytes, 16 lanes; one wave load covers 4 rows).  Work
+// unit = (item, slice of 64 output rows); a 2-wave workgroup gives each wave
+// 32 rows = 8 independent 16-byte loads per lane in flight.  Row sums of the
+// item's pairs are written unweighted to their contribution rows
+// (token * out_stride_k + rank), like the reference's scatter
+// (src/hip/session_ops.hip:357-373).
+// NBI = 16 specialises I = 512 (every lane holds a block); NBI = 0 reads
+// I/32 <= 16 at run time.
+template<int NBI, bool Dbg>
+__global__ __launch_bounds__(128, NBI ? 8 : 7) void k_down_lean(FfnArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int H = a.shape.H, nbi = NBI ? NBI : a.shape.I / 32, S = H / 64;
+    const int u = blockIdx.x;
+    if (u >= a.routes.item_counts[0] * S) return;   // uniform per workgroup
+    const Item *itp = a.routes.stream_items + u / S;   // fields via pointer: no scratch copy
+    const Item it{itp->expert, itp->first, itp->ncols, 0};
+    const int slice = u % S;
+    const int row0 = slice * 64 + wave * 32;
+    const int sub = lane >> 4, kb = lane & 15;
+    const bool has = NBI == 16 || kb < nbi;
+    const size_t b0 = (static_cast<size_t>(it.expert) * H + row0 + sub) * nbi + kb;
+    uint4 w[8];
+    uint32_t d4[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+        const size_t b = b0 + static_cast<size_t>(4 * l) * nbi;
+        w[l] = has ? *reinterpret_cast<const uint4 *>(a.bank.down_codes + b * 16) : make_uint4(0, 0, 0, 0);
+        d4[l] = has ? a.bank.down_scales[b] : 0u;
+    }
+    // Transposing reduction over the 16 lanes of a row: xor 8/4/2 halve the
+    // 8 load-rows, xor 1 finishes; lane ends with load-row lr(lane).
+    const bool c3 = lane & 8, c2 = lane & 4, c1 = lane & 2;
+    const int lr = (c3 ? 4 : 0) + (c2 ? 2 : 0) + (c1 ? 1 : 0);
+#pragma unroll 1
+    for (int j = 0; j < it.ncols; ++j) {
+        const int pair = it.first + j;
+        const size_t xb = static_cast<size_t>(pair) * nbi + kb;
+        const uint4 x0 = has ? *reinterpret_cast<const uint4 *>(a.mq.codes + xb * 32) : make_uint4(0, 0, 0, 0);
+        const uint4 x1 = has ? *reinterpret_cast<const uint4 *>(a.mq.codes + xb * 32 + 16) : make_uint4(0, 0, 0, 0);
+        const uint32_t hx = has ? a.mq.heads[xb] : 0u;
+        const float d8 = h2f(hx), c8 = -8.0f * h2f(hx >> 16);
+#pragma unroll
+        for (int l = 0; l < 8; ++l) asm volatile("" : "+v"(w[l].x), "+v"(w[l].y), "+v"(w[l].z), "+v"(w[l].w));
+        float acc[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const int dot = dot_block(w[l], x0, x1);
+            if constexpr (Dbg) {
+                if (a.down_dots && has)
+                    a.down_dots[(static_cast<size_t>(pair) * H + row0 + 4 * l + sub) * nbi + kb] = dot;
+            }
+            acc[l] = h2f(d4[l]) * fmaf(static_cast<float>(dot), d8, c8);
+        }
+        float v4[4], v2[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float send = c3 ? acc[i] : acc[i + 4];
+            const float keep = c3 ? acc[i + 4] : acc[i];
+            v4[i] = keep + __shfl_xor(send, 8, 64);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float send = c2 ? v4[i] : v4[i + 2];
+            const float keep = c2 ? v4[i + 2] : v4[i];
+            v2[i] = keep + __shfl_xor(send, 4, 64);
+        }
+        float v = (c1 ? v2[1] : v2[0]) + __shfl_xor(c1 ? v2[0] : v2[1], 2, 64);
+        v = xor_sum(v, 1);
+        if ((lane & 1) == 0) {
+            const size_t orow = static_cast<size_t>(itp->token[j]) * a.out_stride_k + itp->rank[j];
+            a.out[orow * H + row0 + 4 * lr + sub] = v;
         }
     }
 }
@@ -764,8 +980,9 @@ hipError_t launch_prepare(const float *x, const int32_t *ids, const float *weigh
     // no quantization blocks: they would read x.
     const size_t q_elements = x ? static_cast<size_t>(tokens) * shape.H : 0;
     const int W = (tokens + 31) / 32;
-    const size_t small_lds = (static_cast<size_t>(shape.E) * W * 2 + static_cast<size_t>(shape.Ep) * 4 + 1 + 17) * 4;
-    if (tokens <= kSmallGroupTokens && small_lds <= 60 * 1024) {
+    const size_t small_lds = (static_cast<size_t>(shape.E) * W * 2 + static_cast<size_t>(shape.Ep) * 4 + 1 + 17 +
+                              static_cast<size_t>(tokens) * shape.k) * 4;
+    if (tokens <= kSmallGroupTokens && small_lds <= 60 * 1024 && tokens * shape.k <= 32 * 1024) {
         k_prepare_small<<<1 + blocks_for(q_elements, 1024), 1024, small_lds, s>>>(p, x, xq, q_elements);
         return hipGetLastError();
     }
@@ -780,6 +997,10 @@ hipError_t launch_prepare(const float *x, const int32_t *ids, const float *weigh
     k_offsets_items<<<1, 1024, lds, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     k_scatter_pairs<<<blocks_for(static_cast<size_t>(tokens), 256), 256, 0, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const size_t pairs = static_cast<size_t>(tokens) * (shape.k + (shape.Ep > shape.E ? 1 : 0));
+    const size_t item_bound = pairs / kStreamTokens + std::min<size_t>(pairs, shape.Ep);
+    k_item_tokens<<<blocks_for(item_bound, 256), 256, 0, s>>>(routes);
     return hipGetLastError();
 }
 
@@ -800,12 +1021,26 @@ unsigned stream_grid(const FfnArgs &a, int slices) {
 }
 }  // namespace
 
+template<int NBL>
+void gate_up_stream(const FfnArgs &a, bool dbg, unsigned grid, hipStream_t s) {
+    if (dbg) k_gate_up_stream<NBL, true><<<grid, 512, 0, s>>>(a);
+    else k_gate_up_stream<NBL, false><<<grid, 512, 0, s>>>(a);
+}
+
 hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s) {
     if (mfma) return hipErrorNotSupported;
     const bool dbg = a.middle_f32 || a.gate_dots || a.up_dots;
     const unsigned grid = stream_grid(a, a.shape.I / 32);
-    if (dbg) k_gate_up_stream<true><<<grid, 512, 0, s>>>(a);
-    else k_gate_up_stream<false><<<grid, 512, 0, s>>>(a);
+    const int nbl = (a.shape.H / 32 + 63) / 64;
+    if (nbl <= 1) {
+        // One unit per workgroup; grid = upper bound on units (extra groups exit).
+        const size_t bound = (static_cast<size_t>(a.pairs_bound) / kStreamTokens +
+                              static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep))) * (a.shape.I / 32);
+        const unsigned lgrid = static_cast<unsigned>(bound);
+        if (dbg) k_gate_up_lean<true><<<lgrid, 512, 0, s>>>(a);
+        else k_gate_up_lean<false><<<lgrid, 512, 0, s>>>(a);
+    } else if (nbl <= 2) gate_up_stream<2>(a, dbg, grid, s);
+    else gate_up_stream<0>(a, dbg, grid, s);
     return hipGetLastError();
 }
 
@@ -814,7 +1049,14 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
     const int nbi = a.shape.I / 32;
     const unsigned grid = stream_grid(a, a.shape.H / 64);
     const bool dbg = a.down_dots != nullptr;
-    if (nbi <= 8) {
+    if (nbi <= 16) {
+        const size_t bound = (static_cast<size_t>(a.pairs_bound) / kStreamTokens +
+                              static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep))) * (a.shape.H / 64);
+        const unsigned g = static_cast<unsigned>(bound);
+        if (dbg) k_down_lean<0, true><<<g, 128, 0, s>>>(a);
+        else if (nbi == 16) k_down_lean<16, false><<<g, 128, 0, s>>>(a);
+        else k_down_lean<0, false><<<g, 128, 0, s>>>(a);
+    } else if (nbi <= 8) {
         if (dbg) k_down_stream<8, true><<<grid, 512, 0, s>>>(a);
         else k_down_stream<8, false><<<grid, 512, 0, s>>>(a);
     } else if (nbi <= 16) {

@@ -32,6 +32,7 @@ struct moe_ffn_layer {
     RouteOut routes{};
     float *contrib = nullptr;
     int mfma_min = 0;     // smallest group routed to the MFMA path (0 = streaming only)
+    int cu_count = 256;   // compute units of the device
     int last_tokens = 0;
     // Inputs of the last forward (for moe_ffn_replay_stage).
     const float *last_x = nullptr, *last_weights = nullptr, *last_shared_gate = nullptr;
@@ -124,6 +125,9 @@ int finish_create(moe_ffn_layer *L) {
     L->contrib = reinterpret_cast<float *>(b + w.contrib);
     if (hipMemset(L->ws_mem, 0, w.total) != hipSuccess) return hipErrorOutOfMemory;
     if (const char *env = std::getenv("MOE_FFN_MFMA_MIN")) L->mfma_min = std::atoi(env);
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, L->device) == hipSuccess && cus > 0)
+        L->cu_count = cus;
     return hipDeviceSynchronize();
 }
 
@@ -223,6 +227,7 @@ moe::FfnArgs base_args(moe_ffn_layer *L, int tokens, int *error) {
     a.tokens = tokens;
     a.pairs_bound = static_cast<int>(pairs_capacity(L->shape, tokens));
     a.error = error;
+    a.cu_count = L->cu_count;
     return a;
 }
 
