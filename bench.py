@@ -67,6 +67,18 @@ def time_stage(layer, stage, reps):
     return e0.elapsed_time(e1) / 1e3 / reps
 
 
+def pmc_traffic(kernel, units):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc record
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a 1 GiB copy calibration),
+    or None when no record for this kernel and unit count exists."""
+    path = os.path.join(ROOT, "profiles", "pmc_b8_decode.json")
+    try:
+        rec = json.load(open(path))["kernels"][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    return rec["traffic_bytes"] if rec.get("units") == units else None
+
+
 def cpu_baseline(x, bank, shared, ids, w, target_seconds):
     import oracle as O
     cpus = O.physical_cpus()
@@ -153,9 +165,10 @@ def main():
                    "top_k": 10, "shared_experts": 1, "touched_experts": touched,
                    "gpu_event_us_per_layer": gpu * 1e6,
                    "layer_hbm_frac": layer_bytes / gpu / 1e9 / HBM_PEAK_GBS},
-        "roofline": {"kernel": "k_gate_up_stream (gate/up + SiLU + Q8 of the middle)", "bound": "hbm",
+        "roofline": {"kernel": "k_gate_up_lean (gate/up + SiLU + Q8 of the middle)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None, "bytes_per_launch": gate_bytes, "us_per_launch": t_gate * 1e6},
+                     "traffic": pmc_traffic("k_gate_up_lean<false>", units),
+                     "bytes_per_launch": gate_bytes, "us_per_launch": t_gate * 1e6},
         "stages_us": {"prepare": t_prep * 1e6, "gate_up": t_gate * 1e6, "down": t_down * 1e6, "fold": t_fold * 1e6},
         "down_stage_hbm_frac": units * DOWN_BYTES_PER_EXPERT / t_down / 1e9 / HBM_PEAK_GBS,
     }

@@ -211,20 +211,6 @@ __global__ __launch_bounds__(256) void k_fill_u32(uint32_t *p, uint32_t v, size_
 // computed without any ordering between threads.  The shared expert is group
 // E, holding every token once (rank = k).
 
-// Validates entry (t, r) (src/routes.cpp:145-157); returns the expert or -1 if
-// the entry cannot be grouped (bad id or duplicate of an earlier rank).
-__device__ __forceinline__ int route_entry(const int32_t *ids, const float *weights, int t, int r, int k,
-                                           int E, int &flags) {
-    const size_t base = static_cast<size_t>(t) * k;
-    const int e = ids[base + r];
-    const float w = weights[base + r];
-    if (!isfinite(w) || w < 0.0f) flags |= 1;
-    if (e < 0 || e >= E) { flags |= 1; return -1; }
-    for (int q = 0; q < r; ++q)
-        if (ids[base + q] == e) { flags |= 1; return -1; }
-    return e;
-}
-
 // Block-wide exclusive scan of n ints (any n) by a 1024-thread block.
 __device__ int block_exclusive_scan(const int32_t *in, int32_t *out, int n, int32_t *tmp) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
@@ -280,22 +266,29 @@ __device__ void build_items(const GroupParams &p, const int32_t *cnt, const int3
     __syncthreads();
     const int total_s = block_exclusive_scan(ns, ns, Ep, tmp);
     const int total_m = block_exclusive_scan(nm, nm, Ep, tmp);
-    for (int e = threadIdx.x; e < Ep; e += blockDim.x) {
-        const int n = cnt[e];
-        if (n == 0) continue;
-        const bool big = p.mfma_min > 0 && n >= p.mfma_min;
-        const int size = big ? kMfmaTile : kStreamTokens;
-        Item *dst = big ? p.r.mfma_items + nm[e] : p.r.stream_items + ns[e];
-        for (int c = 0, f = 0; f < n; ++c, f += size) {
-            Item it;
-            it.expert = e; it.first = off[e] + f; it.ncols = min(size, n - f); it.pad = 0;
-            for (int j = 0; j < kStreamTokens; ++j) {
-                const bool in = fill && !big && j < it.ncols;
-                it.token[j] = in ? p.r.pair_token[it.first + j] : 0;
-                it.rank[j] = in ? p.r.pair_rank[it.first + j] : 0;
-            }
-            dst[c] = it;
+    // One thread per item.  Item i of a path belongs to the last group e with
+    // first_item[e] <= i (groups without items of that path share the next
+    // group's first index, so the last such e is the owner).
+    for (int i = threadIdx.x; i < total_s + total_m; i += blockDim.x) {
+        const bool big = i >= total_s;
+        const int li = big ? i - total_s : i;
+        const int32_t *first = big ? nm : ns;
+        int lo = 0, hi = Ep;   // first e with first[e] > li
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (first[mid] <= li) lo = mid + 1; else hi = mid;
         }
+        const int e = lo - 1;
+        const int size = big ? kMfmaTile : kStreamTokens;
+        const int f = (li - first[e]) * size;
+        Item it;
+        it.expert = e; it.first = off[e] + f; it.ncols = min(size, cnt[e] - f); it.pad = 0;
+        for (int j = 0; j < kStreamTokens; ++j) {
+            const bool in = fill && !big && j < it.ncols;
+            it.token[j] = in ? p.r.pair_token[it.first + j] : 0;
+            it.rank[j] = in ? p.r.pair_rank[it.first + j] : 0;
+        }
+        (big ? p.r.mfma_items : p.r.stream_items)[li] = it;
     }
     // Active groups: counted with one LDS atomic per nonempty group.
     if (threadIdx.x == 0) tmp[0] = 0;
@@ -387,18 +380,47 @@ __global__ __launch_bounds__(1024) void k_prepare_small(GroupParams p, const flo
     if (flags) atomicOr(p.error, flags);
 }
 
-// Large path, step 1: blocks [0, mark_blocks) set bitmap bits (one thread per
-// token), the rest quantize x.  The bitmap is [W][Ep] (word-major) so the
+// Large path.  Mark and scatter blocks take 256 tokens each and stage their
+// ids in LDS ([256][k] ints, dynamic), so the duplicate checks of
+// src/routes.cpp:145-157 read LDS rather than chains of global loads.
+// Validates entry (t, r) (src/routes.cpp:145-157) and returns its expert, or
+// -1 when it cannot be grouped (bad id, duplicate of an earlier rank); bad
+// ids, duplicates and negative or nonfinite weights set flag bit 1.
+__device__ __forceinline__ int staged_entry(const int32_t *sid, const float *weights, int t, int tl, int r,
+                                            int k, int E, int &flags) {
+    const int e = sid[tl * k + r];
+    const float w = weights[static_cast<size_t>(t) * k + r];
+    if (!isfinite(w) || w < 0.0f) flags |= 1;
+    if (e < 0 || e >= E) { flags |= 1; return -1; }
+    for (int q = 0; q < r; ++q)
+        if (sid[tl * k + q] == e) { flags |= 1; return -1; }
+    return e;
+}
+
+__device__ void stage_ids(const GroupParams &p, int t0, int32_t *sid) {
+    const int k = p.shape.k;
+    const int n = min(256, p.tokens - t0) * k;
+    const int32_t *src = p.ids + static_cast<size_t>(t0) * k;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) sid[i] = src[i];
+    __syncthreads();
+}
+
+// Step 1: blocks [0, mark_blocks) set bitmap bits (one thread per token),
+// the rest quantize x.  The bitmap is [W][Ep] (word-major) so the
 // per-expert prefix kernel reads it coalesced.
 __global__ __launch_bounds__(256) void k_mark_quantize(GroupParams p, int mark_blocks,
                                                        const float *__restrict__ x, Act xq,
                                                        size_t q_elements) {
+    extern __shared__ uint32_t lds[];
     if (static_cast<int>(blockIdx.x) < mark_blocks) {
-        const int t = blockIdx.x * blockDim.x + threadIdx.x;
+        int32_t *sid = reinterpret_cast<int32_t *>(lds);
+        const int t0 = blockIdx.x * 256;
+        stage_ids(p, t0, sid);
+        const int t = t0 + threadIdx.x;
         if (t >= p.tokens) return;
         int flags = 0;
         for (int r = 0; r < p.shape.k; ++r) {
-            const int e = route_entry(p.ids, p.weights, t, r, p.shape.k, p.shape.E, flags);
+            const int e = staged_entry(sid, p.weights, t, threadIdx.x, r, p.shape.k, p.shape.E, flags);
             if (e >= 0) atomicOr(&p.r.bitmap[static_cast<size_t>(t >> 5) * p.shape.Ep + e], 1u << (t & 31));
         }
         if (flags) atomicOr(p.error, flags);
@@ -458,12 +480,16 @@ __global__ __launch_bounds__(1024) void k_offsets_items(GroupParams p) {
 
 // Step 4: one thread per token places its pairs.
 __global__ __launch_bounds__(256) void k_scatter_pairs(GroupParams p) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    extern __shared__ uint32_t lds[];
+    int32_t *sid = reinterpret_cast<int32_t *>(lds);
+    const int t0 = blockIdx.x * 256;
+    stage_ids(p, t0, sid);
+    const int t = t0 + threadIdx.x;
     if (t >= p.tokens) return;
     const int k = p.shape.k, E = p.shape.E, Ep = p.shape.Ep;
     for (int r = 0; r < k; ++r) {
         int dummy = 0;
-        const int e = route_entry(p.ids, p.weights, t, r, k, E, dummy);
+        const int e = staged_entry(sid, p.weights, t, threadIdx.x, r, k, E, dummy);
         int pos = -1;
         if (e >= 0) {
             const size_t wi = static_cast<size_t>(t >> 5) * Ep + e;
@@ -883,16 +909,31 @@ __global__ __launch_bounds__(256) void k_fold(const float *__restrict__ c, size_
     const size_t t = i / H, h = i % H;
     int flags = 0;
     float v = 0.0f;
-    for (int r = 0; r < k; ++r) {
-        if (pos_of && pos_of[t * k + r] < 0) continue;
-        float x = c[t * token_stride + static_cast<size_t>(r) * H + h];
-        float s = w[t * k + r];
-        if (!isfinite(x)) { flags |= 1; x = 0.0f; }
-        if (!isfinite(s)) { flags |= 1; s = 0.0f; }
-        float p = s * x;
-        if (!isfinite(p)) { flags |= 2; p = 0.0f; }
-        v = v + p;
-        if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+    // Ranks are taken 8 at a time: all loads of a chunk are issued before the
+    // sequential (rank-order) accumulation.  Rows of ungrouped pairs are read
+    // but not used.
+    for (int r0 = 0; r0 < k; r0 += 8) {
+        float xs[8], ws[8];
+        bool use[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int r = r0 + q;
+            const bool in = r < k;
+            use[q] = in && (!pos_of || pos_of[t * k + r] >= 0);
+            xs[q] = in ? c[t * token_stride + static_cast<size_t>(r) * H + h] : 0.0f;
+            ws[q] = in ? w[t * k + r] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            if (!use[q]) continue;
+            float x = xs[q], s = ws[q];
+            if (!isfinite(x)) { flags |= 1; x = 0.0f; }
+            if (!isfinite(s)) { flags |= 1; s = 0.0f; }
+            float p = s * x;
+            if (!isfinite(p)) { flags |= 2; p = 0.0f; }
+            v = v + p;
+            if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+        }
     }
     if (shared) {
         float x = shared[t * shared_stride + h];
@@ -989,14 +1030,15 @@ hipError_t launch_prepare(const float *x, const int32_t *ids, const float *weigh
     hipError_t e = launch_fill_u32(routes.bitmap, 0u, static_cast<size_t>(W) * shape.Ep, s);
     if (e != hipSuccess) return e;
     const int mark_blocks = static_cast<int>(blocks_for(static_cast<size_t>(tokens), 256));
-    k_mark_quantize<<<mark_blocks + blocks_for(q_elements, 256), 256, 0, s>>>(p, mark_blocks, x, xq, q_elements);
+    const size_t id_lds = static_cast<size_t>(256) * shape.k * 4;
+    k_mark_quantize<<<mark_blocks + blocks_for(q_elements, 256), 256, id_lds, s>>>(p, mark_blocks, x, xq, q_elements);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     k_word_prefix<<<blocks_for(static_cast<size_t>(shape.E), 4), 256, 0, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const size_t lds = (static_cast<size_t>(shape.Ep) * 4 + 1 + 17) * 4;
     k_offsets_items<<<1, 1024, lds, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    k_scatter_pairs<<<blocks_for(static_cast<size_t>(tokens), 256), 256, 0, s>>>(p);
+    k_scatter_pairs<<<blocks_for(static_cast<size_t>(tokens), 256), 256, id_lds, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const size_t pairs = static_cast<size_t>(tokens) * (shape.k + (shape.Ep > shape.E ? 1 : 0));
     const size_t item_bound = pairs / kStreamTokens + std::min<size_t>(pairs, shape.Ep);

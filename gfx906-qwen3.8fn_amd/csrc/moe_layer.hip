@@ -215,6 +215,40 @@ int upload(moe_ffn_layer *L, const void *experts, const void *shared, bool from_
     return r;
 }
 
+// Upload from three per-matrix host tensors [E][rows][blocks] (the GGUF
+// routed-expert tensors) plus the shared expert's three matrices.  Each
+// matrix's planes have the same expert-major order, so a chunk of experts is
+// one copy and one repack launch.
+int upload_tensors(moe_ffn_layer *L, const void *const routed[3], const void *const shared[3]) {
+    const Shape &s = L->shape;
+    const size_t mblocks = static_cast<size_t>(s.I) * (s.H / 32);   // blocks per expert matrix
+    const size_t mbytes = mblocks * 18;
+    const int chunk = static_cast<int>(std::max<size_t>(1, (size_t{256} << 20) / mbytes));
+    uint8_t *staging = nullptr;
+    if (hipMalloc(&staging, static_cast<size_t>(chunk) * mbytes) != hipSuccess) return hipErrorOutOfMemory;
+    uint8_t *codes[3] = {L->gate_codes, L->up_codes, L->down_codes};
+    uint16_t *scales[3] = {L->gate_scales, L->up_scales, L->down_scales};
+    int r = hipSuccess;
+    for (int m = 0; m < 3 && r == hipSuccess; ++m) {
+        for (int first = 0; first < s.Ep && r == hipSuccess; first += chunk) {
+            const int n = std::min(chunk, s.Ep - first);
+            const int nr = std::max(0, std::min(n, s.E - first));   // routed experts in this chunk
+            if (nr > 0)
+                r = hipMemcpy(staging, static_cast<const uint8_t *>(routed[m]) + static_cast<size_t>(first) * mbytes,
+                              static_cast<size_t>(nr) * mbytes, hipMemcpyHostToDevice);
+            if (r == hipSuccess && nr < n)   // the shared expert follows the routed ones
+                r = hipMemcpy(staging + static_cast<size_t>(nr) * mbytes, shared[m], mbytes, hipMemcpyHostToDevice);
+            if (r == hipSuccess)
+                r = moe::launch_repack_weights(staging, codes[m] + static_cast<size_t>(first) * mblocks * 16,
+                                               scales[m] + static_cast<size_t>(first) * mblocks,
+                                               static_cast<size_t>(n) * mblocks, nullptr);
+            if (r == hipSuccess) r = hipDeviceSynchronize();
+        }
+    }
+    (void)hipFree(staging);
+    return r;
+}
+
 moe::FfnArgs base_args(moe_ffn_layer *L, int tokens, int *error) {
     moe::FfnArgs a{};
     a.shape = L->shape;
@@ -266,6 +300,23 @@ int moe_ffn_create_from_device(const moe_ffn_config *config, const void *experts
     int r = create_common(config, device, layer, L);
     if (r != hipSuccess) return r;
     r = upload(L, experts_q4_device, shared_q4_device, true);
+    if (r == hipSuccess) r = finish_create(L);
+    if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
+    *layer = L;
+    return hipSuccess;
+}
+
+int moe_ffn_create_tensors(const moe_ffn_config *config, const void *gate_exps, const void *up_exps,
+                           const void *down_exps, const void *shared_gate, const void *shared_up,
+                           const void *shared_down, int device, moe_ffn_layer **layer) {
+    if (!gate_exps || !up_exps || !down_exps) return kInvalid;
+    if (config && config->has_shared && (!shared_gate || !shared_up || !shared_down)) return kInvalid;
+    moe_ffn_layer *L = nullptr;
+    int r = create_common(config, device, layer, L);
+    if (r != hipSuccess) return r;
+    const void *const routed[3] = {gate_exps, up_exps, down_exps};
+    const void *const shared[3] = {shared_gate, shared_up, shared_down};
+    r = upload_tensors(L, routed, shared);
     if (r == hipSuccess) r = finish_create(L);
     if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
     *layer = L;

@@ -52,6 +52,8 @@ def library():
         lib = ctypes.CDLL(LIB_PATH)
         lib.moe_ffn_create.argtypes = [ctypes.POINTER(Config), _P, _P, _I, ctypes.POINTER(_P)]
         lib.moe_ffn_create_from_device.argtypes = [ctypes.POINTER(Config), _P, _P, _I, ctypes.POINTER(_P)]
+        lib.moe_ffn_create_tensors.argtypes = [ctypes.POINTER(Config), _P, _P, _P, _P, _P, _P, _I,
+                                               ctypes.POINTER(_P)]
         lib.moe_ffn_create_synthetic.argtypes = [ctypes.POINTER(Config), ctypes.c_uint64, _I, ctypes.POINTER(_P)]
         lib.moe_ffn_destroy.argtypes = [_P]
         lib.moe_ffn_memory_bytes.argtypes = [ctypes.POINTER(Config), ctypes.POINTER(ctypes.c_size_t),
@@ -101,7 +103,7 @@ class MoeLayer:
     """One MoE layer resident on the GPU (weights + workspace for max_tokens)."""
 
     def __init__(self, hidden, intermediate, experts, top_k, has_shared, max_tokens, experts_q4=None,
-                 shared_q4=None, synthetic_seed=None, device=0):
+                 shared_q4=None, synthetic_seed=None, device=0, tensors=None, shared_tensors=None):
         self.cfg = Config(hidden, intermediate, experts, top_k, 1 if has_shared else 0, max_tokens)
         self.H, self.I, self.E, self.k = hidden, intermediate, experts, top_k
         self.has_shared = bool(has_shared)
@@ -109,7 +111,18 @@ class MoeLayer:
         self.device = device
         handle = ctypes.c_void_p()
         lib = library()
-        if synthetic_seed is not None:
+        if tensors is not None:   # (gate_exps, up_exps, down_exps) host arrays, reference tensor layout
+            ts = [np.ascontiguousarray(t, dtype=np.uint8) for t in tensors]
+            mb = hidden // 32 * intermediate * 18
+            assert all(t.size == experts * mb for t in ts)
+            ss = [None, None, None]
+            if has_shared:
+                ss = [np.ascontiguousarray(t, dtype=np.uint8) for t in shared_tensors]
+                assert all(t.size == mb for t in ss)
+            ptr = lambda a: None if a is None else ctypes.c_void_p(a.ctypes.data)
+            st = lib.moe_ffn_create_tensors(ctypes.byref(self.cfg), *[ptr(t) for t in ts], *[ptr(t) for t in ss],
+                                            device, ctypes.byref(handle))
+        elif synthetic_seed is not None:
             st = lib.moe_ffn_create_synthetic(ctypes.byref(self.cfg), ctypes.c_uint64(synthetic_seed), device,
                                               ctypes.byref(handle))
         elif isinstance(experts_q4, np.ndarray):

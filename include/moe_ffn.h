@@ -71,6 +71,16 @@ int moe_ffn_create(const moe_ffn_config *config, const void *experts_q4, const v
 int moe_ffn_create_from_device(const moe_ffn_config *config, const void *experts_q4_device,
                                const void *shared_q4_device, int device, moe_ffn_layer **layer);
 
+/* Same, from the routed-expert tensors as the reference holds them: three
+ * host tensors gate_exps [E][I][H/32], up_exps [E][I][H/32], down_exps
+ * [E][H][I/32] of 18-byte Q4_0 blocks (GGUF ffn_{gate,up,down}_exps, rank 3
+ * [input, output, expert]; Experts::ram, src/session.hip:700-716,
+ * src/model.hpp:109-111), plus the shared expert's three matrices (NULL when
+ * the layer has none).  Lets Experts' loaded tensors be handed over as is. */
+int moe_ffn_create_tensors(const moe_ffn_config *config, const void *gate_exps, const void *up_exps,
+                           const void *down_exps, const void *shared_gate, const void *shared_up,
+                           const void *shared_down, int device, moe_ffn_layer **layer);
+
 /* Synthetic weight bank generated on the device (for benchmarks of banks too
  * large to stage through the host): per block d = half(|N(0,0.02)|) and
  * uniform codes, from a counter-based hash of (seed, block index).  The bytes

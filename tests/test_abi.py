@@ -27,6 +27,11 @@ def test_invalid_arguments_rejected_before_hip():
     assert lib.moe_quantize_q8_1(buf, buf, 64, 0, buf, None) == 1
     assert lib.moe_ffn_forward(None, None, None, None, 1, None, None, None, None) == 1
     assert lib.moe_combine(None, None, None, None, 1, 1, 1, None, None, None) == 1
+    ok = moe_ffn.Config(2048, 512, 512, 10, 1, 8)
+    h = ctypes.c_void_p()
+    assert lib.moe_ffn_create_tensors(ctypes.byref(ok), buf, None, buf, buf, buf, buf, 0, ctypes.byref(h)) == 1
+    assert lib.moe_ffn_create_tensors(ctypes.byref(ok), buf, buf, buf, None, buf, buf, 0, ctypes.byref(h)) == 1
+    assert lib.moe_ffn_create(ctypes.byref(ok), None, buf, 0, ctypes.byref(h)) == 1
     bad = moe_ffn.Config(2048, 500, 512, 10, 1, 8)      # intermediate not a multiple of 32
     w, s = ctypes.c_size_t(), ctypes.c_size_t()
     assert lib.moe_ffn_memory_bytes(ctypes.byref(bad), ctypes.byref(w), ctypes.byref(s)) == 1

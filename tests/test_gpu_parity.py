@@ -298,3 +298,33 @@ def test_synthetic_bank_export_roundtrip():
     ref = O.moe_layer(x, 2048, 512, 4, bank, ids, w, shared_q4=sh)
     assert_close(host(y), ref["y"], what="synthetic bank")
     L.close()
+
+
+def _split_tensors(bank, E, H, I):
+    """Canonical per-expert bank [E][gate|up|down] -> the reference's three
+    routed-expert tensors [E][rows][blocks] (src/session.hip:700-716)."""
+    mb = H // 32 * I * 18
+    per = bank.reshape(E, 3, mb)
+    return [np.ascontiguousarray(per[:, m, :]).reshape(-1) for m in range(3)]
+
+
+def test_create_from_reference_tensors(moe512):
+    """moe_ffn_create_tensors at the bench shape: 512 experts + shared span two
+    staging chunks (455 expert matrices each); every expert on either side of
+    the boundary and the shared one export to the canonical bytes, and the
+    forward matches the canonical-upload layer bit for bit."""
+    bank, shared = moe512["bank"], moe512["shared"]
+    ts = _split_tensors(bank, 512, 2048, 512)
+    ss = _split_tensors(shared, 1, 2048, 512)
+    L = moe_ffn.MoeLayer(2048, 512, 512, 10, True, 64, tensors=ts, shared_tensors=ss)
+    eb = len(bank) // 512
+    for e in (0, 1, 454, 455, 456, 511):
+        assert np.array_equal(L.export_expert(e), bank[e * eb:(e + 1) * eb]), e
+    assert np.array_equal(L.export_expert(512), shared)
+    x = W.activations(8, seed=91)
+    ids, w = W.routes_uniform(8, seed=92)
+    y1, e1 = L.forward(dev(x), dev(ids), dev(w))
+    y2, e2 = moe512["layer"].forward(dev(x), dev(ids), dev(w))
+    assert np.array_equal(host(y1), host(y2))
+    assert int(host(e1)[0]) == 0 and int(host(e2)[0]) == 0
+    L.close()

@@ -287,3 +287,32 @@ def test_moe_layer_composes_expert_and_fold():
     sec, workers, yb = O.baseline_layer(x, H, I, E, bank, ids, w, shared_q4=shared, workers=2, repeats=1)
     assert workers >= 1 and sec > 0
     assert np.array_equal(yb, out["y"])
+
+
+def test_shared_sigmoid_gate_closed_forms():
+    # y = fold + sigmoid(g) * shared (src/hip/session_ops.hip:375-391).  g = 0
+    # gives scale 0.5 exactly (a power-of-two product rounds nowhere); g = 30
+    # gives 1/(1+expf(-30)) == 1.0f in fp32, i.e. the ungated sum; a negative
+    # gate scales below 1 and differs from both.
+    H, I, E, k, N = 128, 64, 6, 2, 3
+    rng = np.random.default_rng(4)
+    bank = np.concatenate([np.concatenate(expert_weights(H, I, seed=800 + 3 * e)) for e in range(E)])
+    shared = np.concatenate(expert_weights(H, I, seed=991))
+    x = rng.standard_normal((N, H), dtype=np.float32)
+    ids = np.array([rng.permutation(E)[:k] for _ in range(N)], np.int32)
+    w = rng.random((N, k), dtype=np.float32)
+    base = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, want_contrib=True)
+    folded = O.routed_fold(base["contrib"], w)
+    s = (base["y"] - folded).astype(np.float32)     # exact: y = folded + s, recovered below
+    assert np.array_equal((folded + s).astype(np.float32), base["y"])
+    half = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, shared_gate=np.zeros(N, np.float32))["y"]
+    mb = 3 * H // 32 * I * 18 // 3
+    sh = np.stack([O.expert_forward(shared[:mb], shared[mb:2 * mb], shared[2 * mb:], H, I,
+                                    O.quantize_q8(x[t:t + 1]))["y"][0] for t in range(N)])
+    assert np.array_equal(half, (folded + np.float32(0.5) * sh).astype(np.float32))
+    one = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, shared_gate=np.full(N, 30.0, np.float32))["y"]
+    assert np.array_equal(one, base["y"])
+    neg = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, shared_gate=np.full(N, -2.0, np.float32))["y"]
+    scale = np.float32(1.0) / (np.float32(1.0) + np.exp(np.float32(2.0), dtype=np.float32))
+    assert np.allclose(neg, folded + scale * sh, rtol=0, atol=1e-6 * float(np.abs(sh).max()))
+    assert not np.array_equal(neg, half) and not np.array_equal(neg, one)
