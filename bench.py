@@ -30,19 +30,22 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_forward(layer, x, ids, w, steps, warmup):
+def time_forward(layer, x, sets, steps, warmup):
+    """Wall and GPU-event time per forward; step i uses route set i % len(sets),
+    so consecutive steps touch different experts (weights are not left hot in
+    the 256 MB Infinity Cache by a repeated identical step)."""
     import torch
     y = torch.empty((x.shape[0], layer.H), dtype=torch.float32, device=x.device)
     err = torch.zeros(1, dtype=torch.int32, device=x.device)
-    for _ in range(warmup):
-        layer.forward(x, ids, w, y=y, error=err)
+    for i in range(warmup):
+        layer.forward(x, *sets[i % len(sets)], y=y, error=err)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
-    for _ in range(steps):
-        layer.forward(x, ids, w, y=y, error=err)
+    for i in range(steps):
+        layer.forward(x, *sets[i % len(sets)], y=y, error=err)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
@@ -52,31 +55,35 @@ def time_forward(layer, x, ids, w, steps, warmup):
     return wall, gpu, y
 
 
-def time_stage(layer, stage, reps):
-    """Average duration of one stage's launch, HIP events on its stream."""
+def time_stages(layer, x, sets, steps):
+    """Per-stage durations of real forwards (same rotation as time_forward):
+    the library records timing events (no system-scope fence) on the forward's
+    stream before the first and after every stage; read once at the end.
+    Returns the summed seconds per stage."""
     import torch
-    stream = torch.cuda.current_stream()
-    layer.replay_stage(stage)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        layer.replay_stage(stage)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / 1e3 / reps
+    y = torch.empty((x.shape[0], layer.H), dtype=torch.float32, device=x.device)
+    err = torch.zeros(1, dtype=torch.int32, device=x.device)
+    layer.profile(steps)
+    for i in range(steps):
+        layer.forward(x, *sets[i % len(sets)], y=y, error=err)
+    total, n = layer.profile_read()
+    layer.profile(0)
+    assert n == steps
+    return np.array(total)
 
 
 def pmc_traffic(kernel, units):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc record
     (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a 1 GiB copy calibration),
-    or None when no record for this kernel and unit count exists."""
+    at `units` expert units per launch; None when no record exists."""
     path = os.path.join(ROOT, "profiles", "pmc_b8_decode.json")
     try:
         rec = json.load(open(path))["kernels"][kernel]
     except (OSError, KeyError, ValueError):
         return None
-    return rec["traffic_bytes"] if rec.get("units") == units else None
+    # The record holds the mean bytes per launch at its mean unit count; the
+    # traffic of this kernel is linear in units (one weight set per unit).
+    return rec["traffic_bytes"] / rec["units"] * units
 
 
 def cpu_baseline(x, bank, shared, ids, w, target_seconds):
@@ -127,24 +134,25 @@ def main():
     layer = moe_ffn.MoeLayer(2048, 512, 512, 10, True, max_tokens, experts_q4=bank, shared_q4=shared)
 
     # ---- B8 decode (headline) -------------------------------------------
-    N = 8
+    N, R = 8, 64
     xh = W.activations(N, seed=1002)
-    idh, wh = W.routes_uniform(N, seed=1003)
-    x, ids, w = dev(xh), dev(idh), dev(wh)
-    hist = W.group_histogram(idh)
-    log(f"[bench] b8 decode: {hist}")
-    wall, gpu, _ = time_forward(layer, x, ids, w, args.steps, args.warmup)
+    route_sets = [W.routes_uniform(N, seed=1003 + r) for r in range(R)]
+    x = dev(xh)
+    sets = [(dev(i), dev(w)) for i, w in route_sets]
+    touched = np.array([W.group_histogram(i)["touched"] for i, _ in route_sets])
+    log(f"[bench] b8 decode: {R} route sets, touched experts mean {touched.mean():.1f} "
+        f"(min {touched.min()}, max {touched.max()})")
+    wall, gpu, _ = time_forward(layer, x, sets, args.steps, args.warmup)
     stats = layer.last_stats()
-    touched = hist["touched"]
-    reps = max(50, args.steps)
-    t_gate = time_stage(layer, moe_ffn.STAGE_GATE_UP, reps)
-    t_down = time_stage(layer, moe_ffn.STAGE_DOWN, reps)
-    t_prep = time_stage(layer, moe_ffn.STAGE_PREPARE, reps)
-    t_fold = time_stage(layer, moe_ffn.STAGE_FOLD, reps)
-    units = touched + 1
-    gate_bytes = units * GATE_UP_BYTES_PER_EXPERT
-    achieved = gate_bytes / t_gate / 1e9
-    layer_bytes = W.algorithmic_bytes(N, touched)
+    # Stage durations over the same rotation; step i touched[i % R] + 1 units.
+    n_stage = max(R, args.steps)
+    t_stage = time_stages(layer, x, sets, n_stage)
+    units = touched[np.arange(n_stage) % R] + 1
+    gate_bytes = float(np.sum(units)) * GATE_UP_BYTES_PER_EXPERT
+    down_bytes = float(np.sum(units)) * DOWN_BYTES_PER_EXPERT
+    t_prep, t_gate, t_down, t_fold = (t_stage / n_stage).tolist()
+    achieved = gate_bytes / float(t_stage[1]) / 1e9
+    layer_bytes = float(np.mean([W.algorithmic_bytes(N, int(t)) for t in touched]))
     log(f"[bench] b8 wall {wall*1e6:.1f} us gpu {gpu*1e6:.1f} us; stages prep {t_prep*1e6:.1f} gate/up "
         f"{t_gate*1e6:.1f} down {t_down*1e6:.1f} fold {t_fold*1e6:.1f} us; items {stats}")
 
@@ -160,17 +168,19 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8xint4->int32, fp32 accumulate",
-        "data": "synthetic (seeded Q4_0 weights d=|N(0,.02)|, x~N(0,1), uniform top-10 routing)",
+        "data": "synthetic (seeded Q4_0 weights d=|N(0,.02)|, x~N(0,1), uniform top-10 routing, "
+                f"{R} route sets rotated per step)",
         "config": {"workload": "b8_decode", "tokens": N, "hidden": 2048, "intermediate": 512, "experts": 512,
-                   "top_k": 10, "shared_experts": 1, "touched_experts": touched,
+                   "top_k": 10, "shared_experts": 1, "route_sets": R,
+                   "touched_experts_mean": float(touched.mean()),
                    "gpu_event_us_per_layer": gpu * 1e6,
                    "layer_hbm_frac": layer_bytes / gpu / 1e9 / HBM_PEAK_GBS},
         "roofline": {"kernel": "k_gate_up_lean (gate/up + SiLU + Q8 of the middle)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": pmc_traffic("k_gate_up_lean<false>", units),
-                     "bytes_per_launch": gate_bytes, "us_per_launch": t_gate * 1e6},
+                     "traffic": pmc_traffic("k_gate_up_lean<false>", float(touched.mean()) + 1),
+                     "bytes_per_launch": gate_bytes / n_stage, "us_per_launch": t_gate * 1e6},
         "stages_us": {"prepare": t_prep * 1e6, "gate_up": t_gate * 1e6, "down": t_down * 1e6, "fold": t_fold * 1e6},
-        "down_stage_hbm_frac": units * DOWN_BYTES_PER_EXPERT / t_down / 1e9 / HBM_PEAK_GBS,
+        "down_stage_hbm_frac": down_bytes / float(t_stage[2]) / 1e9 / HBM_PEAK_GBS,
     }
 
     # ---- 4K Zipf prefill (reported beside) --------------------------------
@@ -180,7 +190,7 @@ def main():
         idp, wp = W.routes_zipf(NP, 1.1, seed=2003)
         hp = W.group_histogram(idp)
         log(f"[bench] 4k prefill: {hp}")
-        wall_p, gpu_p, _ = time_forward(layer, dev(xph), dev(idp), dev(wp), args.prefill_steps, 3)
+        wall_p, gpu_p, _ = time_forward(layer, dev(xph), [(dev(idp), dev(wp))], args.prefill_steps, 3)
         ops = W.int8_ops(NP)
         pbytes = W.algorithmic_bytes(NP, hp["touched"])
         result["prefill_4k"] = {
@@ -192,6 +202,7 @@ def main():
 
     # ---- CPU baseline (same weights and inputs) ----------------------------
     if not args.no_cpu:
+        idh, wh = route_sets[0]
         sec, used, repeats = cpu_baseline(xh, bank, shared, idh, wh, args.cpu_seconds)
         result["cpu_baseline"] = {
             "value": N / sec, "unit": "tokens/s per MoE layer", "cores": used, "kind": "port",

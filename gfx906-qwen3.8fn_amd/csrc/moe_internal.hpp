@@ -23,6 +23,20 @@ inline constexpr int kStreamTokens = 4;     // tokens per streaming (decode) wor
 inline constexpr int kMfmaTile = 128;       // tokens per MFMA work item (4 waves x 32)
 inline constexpr int kSmallGroupTokens = 256;  // single-workgroup grouping limit
 
+// Scale-plane order.  Scales are grouped so that one 16-byte load gives a
+// lane the 8 scales the streaming kernels need for its block:
+//   gate/up (kScaleGroupGateUp):  [rows/8][blocks][8]    row r at slot r % 8
+//   down    (kScaleGroupDown):    [rows/32][blocks][32]  row r at slot (r % 4) * 8 + (r % 32) / 4
+// `row` counts rows across experts (expert * rows_per_expert + r); rows per
+// expert are multiples of 32, so groups never straddle experts.
+inline constexpr int kScaleGroupGateUp = 8;
+inline constexpr int kScaleGroupDown = 32;
+__host__ __device__ inline size_t scale_index(size_t row, int kb, int blocks_per_row, int group) {
+    if (group == kScaleGroupGateUp)
+        return ((row / 8) * blocks_per_row + kb) * 8 + row % 8;
+    return ((row / 32) * blocks_per_row + kb) * 32 + (row % 4) * 8 + (row % 32) / 4;
+}
+
 struct Bank {
     const uint8_t *gate_codes, *up_codes, *down_codes;
     const uint16_t *gate_scales, *up_scales, *down_scales;
@@ -70,12 +84,16 @@ hipError_t launch_quantize_planes(const float *x, Act out, int width, int column
 hipError_t launch_canonical_to_planes(const void *q8, Act out, int blocks, hipStream_t s);
 hipError_t launch_planes_to_canonical(Act in, void *q8, int blocks, hipStream_t s);
 
-hipError_t launch_repack_weights(const uint8_t *canonical, uint8_t *codes, uint16_t *scales,
-                                 size_t blocks, hipStream_t s);
-hipError_t launch_unpack_weights(const uint8_t *codes, const uint16_t *scales, uint8_t *canonical,
-                                 size_t blocks, hipStream_t s);
-hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, size_t blocks, size_t block0,
-                                    uint64_t seed, hipStream_t s);
+// Weight planes of one matrix kind (codes / scales = plane bases).  The call
+// covers plane blocks [block0, block0 + blocks); rows hold `blocks_per_row`
+// blocks and scales use scale group `group`.
+hipError_t launch_repack_weights(const uint8_t *canonical, uint8_t *codes, uint16_t *scales, size_t blocks,
+                                 size_t block0, int blocks_per_row, int group, hipStream_t s);
+hipError_t launch_unpack_weights(const uint8_t *codes, const uint16_t *scales, uint8_t *canonical, size_t blocks,
+                                 size_t block0, int blocks_per_row, int group, hipStream_t s);
+// Synthetic blocks: hashed from (seed, hash0 + plane block index).
+hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, size_t blocks, size_t hash0,
+                                    int blocks_per_row, int group, uint64_t seed, hipStream_t s);
 
 // Quantize x into `xq` and group routes (tokens <= kSmallGroupTokens path or
 // the multi-kernel path).  mfma_min = smallest group that goes to MFMA (0 = never).

@@ -146,26 +146,30 @@ __global__ __launch_bounds__(256) void k_planes_to_canonical(const uint8_t *code
 // ---------------------------------------------------------- weight planes ---
 // Canonical blocks are 18 bytes with 2-byte alignment: read them as 9 u16.
 __global__ __launch_bounds__(256) void k_repack(const uint16_t *canonical, uint32_t *codes,
-                                                uint16_t *scales, size_t blocks) {
+                                                uint16_t *scales, size_t blocks, size_t block0, int nb,
+                                                int group) {
     const size_t b = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= blocks) return;
+    const size_t g = block0 + b;
     const uint16_t *src = canonical + b * 9;
-    scales[b] = src[0];
+    scales[scale_index(g / nb, static_cast<int>(g % nb), nb, group)] = src[0];
     uint4 c;
     c.x = src[1] | (static_cast<uint32_t>(src[2]) << 16);
     c.y = src[3] | (static_cast<uint32_t>(src[4]) << 16);
     c.z = src[5] | (static_cast<uint32_t>(src[6]) << 16);
     c.w = src[7] | (static_cast<uint32_t>(src[8]) << 16);
-    reinterpret_cast<uint4 *>(codes)[b] = c;
+    reinterpret_cast<uint4 *>(codes)[g] = c;
 }
 
 __global__ __launch_bounds__(256) void k_unpack(const uint32_t *codes, const uint16_t *scales,
-                                                uint16_t *canonical, size_t blocks) {
+                                                uint16_t *canonical, size_t blocks, size_t block0, int nb,
+                                                int group) {
     const size_t b = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= blocks) return;
-    const uint4 c = reinterpret_cast<const uint4 *>(codes)[b];
+    const size_t g = block0 + b;
+    const uint4 c = reinterpret_cast<const uint4 *>(codes)[g];
     uint16_t *dst = canonical + b * 9;
-    dst[0] = scales[b];
+    dst[0] = scales[scale_index(g / nb, static_cast<int>(g % nb), nb, group)];
     dst[1] = c.x & 0xffffu; dst[2] = c.x >> 16;
     dst[3] = c.y & 0xffffu; dst[4] = c.y >> 16;
     dst[5] = c.z & 0xffffu; dst[6] = c.z >> 16;
@@ -182,10 +186,10 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
 // Synthetic Q4_0 blocks: codes uniform 0..15 (16 random bytes), d =
 // half(|N(0, 0.02)|) by Box-Muller, all from a counter hash of (seed, block).
 __global__ __launch_bounds__(256) void k_synthetic(uint32_t *codes, uint16_t *scales, size_t blocks,
-                                                   size_t block0, uint64_t seed) {
+                                                   size_t hash0, int nb, int group, uint64_t seed) {
     const size_t b = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= blocks) return;
-    const uint64_t g = block0 + b;
+    const uint64_t g = hash0 + b;
     const uint64_t h0 = mix64(seed ^ mix64(4 * g + 0)), h1 = mix64(seed ^ mix64(4 * g + 1));
     const uint64_t h2 = mix64(seed ^ mix64(4 * g + 2));
     uint4 c;
@@ -195,12 +199,29 @@ __global__ __launch_bounds__(256) void k_synthetic(uint32_t *codes, uint16_t *sc
     const float u1 = (static_cast<float>(h2 >> 40) + 1.0f) * 0x1p-24f;          // (0, 1]
     const float u2 = static_cast<float>((h2 >> 16) & 0xffffffu) * 0x1p-24f;      // [0, 1)
     const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
-    scales[b] = static_cast<uint16_t>(f2h(fabsf(z) * 0.02f));
+    scales[scale_index(b / nb, static_cast<int>(b % nb), nb, group)] = static_cast<uint16_t>(f2h(fabsf(z) * 0.02f));
 }
 
 __global__ __launch_bounds__(256) void k_fill_u32(uint32_t *p, uint32_t v, size_t n) {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
+}
+
+// -------------------------------------------------------- buffer loads ---
+// Raw buffer loads: a uniform base in a buffer resource (SGPRs), a 32-bit
+// per-lane offset and a uniform SGPR offset.  A wave's row loads then share
+// one offset VGPR and are all issued before the first is waited for.  The
+// resource covers `bytes` from `base` (dword 3 = 32-bit data format, the gfx9
+// raw-buffer setting).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, off, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, lane_off, off, 0);
 }
 
 // ------------------------------------------------------------- grouping ----
@@ -565,7 +586,7 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
         const int row0 = s * 32 + (wave & 3) * 8;
         const size_t mrow = static_cast<size_t>(it.expert) * I + row0;
         const uint8_t *codes = (mat ? a.bank.up_codes : a.bank.gate_codes) + mrow * nbh * 16;
-        const uint16_t *scales = (mat ? a.bank.up_scales : a.bank.gate_scales) + mrow * nbh;
+        const uint16_t *scales = mat ? a.bank.up_scales : a.bank.gate_scales;
         // NBL <= 2: the item's weight rows stay in registers across its
         // tokens.  NBL == 0 (H > 4096): rows are re-read per token (L1/L2 hits).
         constexpr int HOLD = NBL > 0 ? NBL : 1;
@@ -578,7 +599,7 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
             for (int r = 0; r < 8; ++r) {
                 if (kb < nbh) {
                     w[nb][r] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbh + kb) * 16);
-                    d4[nb][r] = h2f(scales[static_cast<size_t>(r) * nbh + kb]);
+                    d4[nb][r] = h2f(scales[scale_index(mrow + r, kb, nbh, kScaleGroupGateUp)]);
                 } else {
                     w[nb][r] = make_uint4(0, 0, 0, 0);
                     d4[nb][r] = 0.0f;
@@ -598,7 +619,7 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
 #pragma unroll
                     for (int r = 0; r < 8; ++r) {
                         w[0][r] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbh + kb) * 16);
-                        d4[0][r] = h2f(scales[static_cast<size_t>(r) * nbh + kb]);
+                        d4[0][r] = h2f(scales[scale_index(mrow + r, kb, nbh, kScaleGroupGateUp)]);
                     }
                 }
                 const size_t xb = static_cast<size_t>(tok) * nbh + kb;
@@ -659,65 +680,82 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
 // High-occupancy form of k_gate_up_stream for H <= 2048 (one block per lane,
 // one unit per workgroup).  Decode streaming is bound by bytes in flight per
 // CU: each wave keeps its 8 weight rows (8 KB) in flight with a small register
-// footprint, so 4 workgroups (32 waves, 256 KB of loads) fit on a CU.  Same
-// arithmetic and outputs as k_gate_up_stream.
+// footprint, so 4 workgroups (32 waves, 256 KB of loads) fit on a CU.  Grid =
+// (item bound, I/32 slices); same arithmetic and outputs as k_gate_up_stream.
 template<bool Dbg>
 __global__ __launch_bounds__(512, 8) void k_gate_up_lean(FfnArgs a) {
     constexpr int T = kStreamTokens;
     __shared__ float gu[2][32][T];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32, S = I / 32;
-    const int u = blockIdx.x;
-    if (u >= a.routes.item_counts[0] * S) return;    // uniform per workgroup
+    // The wave index is uniform: as a scalar it keeps row bases in SGPRs.
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32;
+    const int item = blockIdx.x, s = blockIdx.y;
+    // Item header, its tokens and the item count are independent loads
+    // (the item array is sized for the grid), issued together.
+    const int4 hdr = *reinterpret_cast<const int4 *>(a.routes.stream_items + item);
+    const int4 tok = *reinterpret_cast<const int4 *>(a.routes.stream_items[item].token);
+    const int count = a.routes.item_counts[0];
+    // Keeps the compiler from deferring the item loads behind the count check.
+    asm volatile("" ::"s"(hdr.x), "s"(hdr.y), "s"(hdr.z), "s"(tok.x), "s"(tok.y), "s"(tok.z), "s"(tok.w), "s"(count));
+    if (item >= count) return;   // uniform per workgroup
+    const int expert = hdr.x, first = hdr.y, ncols = hdr.z;
     const int mat = wave >> 2;
-    const bool has = lane < nbh;
-    // Item fields are read through the pointer (uniform scalar loads): a
-    // local copy indexed by the runtime token slot would live in scratch.
-    const Item *itp = a.routes.stream_items + u / S;
-    const Item it{itp->expert, itp->first, itp->ncols, 0};
-    const int s = u % S;
     const int row0 = s * 32 + (wave & 3) * 8;
-    const size_t b0 = (static_cast<size_t>(it.expert) * I + row0) * nbh + lane;
-    const uint8_t *codes = (mat ? a.bank.up_codes : a.bank.gate_codes) + b0 * 16;
-    const uint16_t *scales = (mat ? a.bank.up_scales : a.bank.gate_scales) + b0;
-    uint4 w[8];
-    uint32_t d4[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        w[r] = has ? *reinterpret_cast<const uint4 *>(codes + static_cast<size_t>(r) * nbh * 16) : make_uint4(0, 0, 0, 0);
-        d4[r] = has ? scales[static_cast<size_t>(r) * nbh] : 0u;
-    }
+    // Lanes past the row end (H < 2048) read block 0 and drop their products:
+    // every load is unconditional, so a wave's 8 row loads are all in flight
+    // at once (a guarded load would be waited for before the next is issued).
+    const bool has = lane < nbh;
+    const int kb = has ? lane : 0;
+    // The wave's 8 rows are one buffer (uniform base, per-row SGPR offset, one
+    // lane-offset VGPR); the lane's 8 scales (rows row0..row0+7 of its block)
+    // are one 16-byte load.
+    const size_t mrow = static_cast<size_t>(expert) * I + row0;    // row0 % 8 == 0
+    const uint32_t row_bytes = static_cast<uint32_t>(nbh) * 16u;
+    const auto wr = buffer_rsrc((mat ? a.bank.up_codes : a.bank.gate_codes) + mrow * row_bytes, 8 * row_bytes);
+    const auto sr = buffer_rsrc((mat ? a.bank.up_scales : a.bank.gate_scales) + mrow * nbh, row_bytes);
+    const uint32_t lane_off = static_cast<uint32_t>(kb) * 16u;
     const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
     const int rho = (b5 ? 4 : 0) + (b4 ? 2 : 0) + (b3 ? 1 : 0);
+    // Weights are loaded per token together with that token's activations:
+    // the first token streams them from HBM, further tokens of the item hit
+    // L2.  Nothing but the token ids stays live across iterations.
 #pragma unroll 1
-    for (int j = 0; j < it.ncols; ++j) {
-        // Token ids come from the item (scalar loads issued with the item),
-        // so these loads go out right behind the weight loads.
-        const size_t xb = static_cast<size_t>(itp->token[j]) * nbh + lane;
-        const uint4 x0 = has ? *reinterpret_cast<const uint4 *>(a.xq.codes + xb * 32) : make_uint4(0, 0, 0, 0);
-        const uint4 x1 = has ? *reinterpret_cast<const uint4 *>(a.xq.codes + xb * 32 + 16) : make_uint4(0, 0, 0, 0);
-        const uint32_t hx = has ? a.xq.heads[xb] : 0u;
+    for (int j = 0; j < ncols; ++j) {
+        const int t = j == 0 ? tok.x : j == 1 ? tok.y : j == 2 ? tok.z : tok.w;
+        const size_t xrow = static_cast<size_t>(t) * nbh;
+        const auto xr = buffer_rsrc(a.xq.codes + xrow * 32, static_cast<uint32_t>(nbh) * 32u);
+        const auto hr = buffer_rsrc(a.xq.heads + xrow, static_cast<uint32_t>(nbh) * 4u);
+        uint4 w[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) w[r] = buffer_load16(wr, lane_off, r * row_bytes);
+        const uint4 d4p = buffer_load16(sr, lane_off, 0);
+        const uint4 x0 = buffer_load16(xr, 2 * lane_off, 0);
+        const uint4 x1 = buffer_load16(xr, 2 * lane_off, 16);
+        const uint32_t hx = buffer_load4(hr, lane_off / 4, 0);
         const float d8 = h2f(hx), c8 = -8.0f * h2f(hx >> 16);
-        // Keep the nibble masking inside the token loop: hoisting it would
-        // hold 64 unpacked words per lane and halve the occupancy.
-#pragma unroll
-        for (int r = 0; r < 8; ++r) asm volatile("" : "+v"(w[r].x), "+v"(w[r].y), "+v"(w[r].z), "+v"(w[r].w));
-        float acc[8];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int dot = dot_block(w[r], x0, x1);
-            if constexpr (Dbg) {
-                int32_t *dots = mat ? a.up_dots : a.gate_dots;
-                if (dots && has) dots[(static_cast<size_t>(it.first + j) * I + row0 + r) * nbh + lane] = dot;
-            }
-            acc[r] = h2f(d4[r]) * fmaf(static_cast<float>(dot), d8, c8);
-        }
+        // Rows i and i+4 are computed together and folded at once (xor 32),
+        // so at most 4 partial sums are live.
         float v4[4], v2[2];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float send = b5 ? acc[i] : acc[i + 4];
-            const float keep = b5 ? acc[i + 4] : acc[i];
+            float pr[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int r = i + 4 * h;
+                const int dot = dot_block(w[r], x0, x1);
+                if constexpr (Dbg) {
+                    int32_t *dots = mat ? a.up_dots : a.gate_dots;
+                    if (dots && has) dots[(static_cast<size_t>(first + j) * I + row0 + r) * nbh + lane] = dot;
+                }
+                const uint32_t d4 = (&d4p.x)[r >> 1] >> (16 * (r & 1));
+                pr[h] = has ? h2f(d4) * fmaf(static_cast<float>(dot), d8, c8) : 0.0f;
+            }
+            const float send = b5 ? pr[0] : pr[1];
+            const float keep = b5 ? pr[1] : pr[0];
             v4[i] = keep + __shfl_xor(send, 32, 64);
+            // One row pair at a time: without this fence the scheduler starts
+            // every row's nibble unpack as soon as its load lands and spills.
+            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -732,13 +770,13 @@ __global__ __launch_bounds__(512, 8) void k_gate_up_lean(FfnArgs a) {
         if ((lane & 7) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
     }
     __syncthreads();
-    if (wave < it.ncols) {
+    if (wave < ncols) {
         const int j = wave, i = lane & 31;
         int flags = 0;
         const float m = silu_mul(gu[0][i][j], gu[1][i][j], flags);
         const Q8Lane q = quantize32(m);
         if (lane < 32) {
-            const size_t pair = static_cast<size_t>(it.first + j);
+            const size_t pair = static_cast<size_t>(first + j);
             const size_t mb = pair * nbi + s;
             a.mq.codes[mb * 32 + i] = static_cast<uint8_t>(q.code);
             if (i == 0) a.mq.heads[mb] = q.head;
@@ -766,7 +804,7 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
         const int row0 = (u % S) * 64 + wave * 8;
         const size_t mrow = static_cast<size_t>(it.expert) * H + row0;
         const uint8_t *codes = a.bank.down_codes + mrow * nbi * 16;
-        const uint16_t *scales = a.bank.down_scales + mrow * nbi;
+        const uint16_t *scales = a.bank.down_scales;
         float acc[LOADS][T];
 #pragma unroll
         for (int l = 0; l < LOADS; ++l)
@@ -779,7 +817,7 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
             for (int l = 0; l < LOADS; ++l) {
                 const int r = l * RPL + sub;
                 w[l] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbi + kb) * 16);
-                d4[l] = h2f(scales[static_cast<size_t>(r) * nbi + kb]);
+                d4[l] = h2f(scales[scale_index(mrow + r, kb, nbi, kScaleGroupDown)]);
             }
 #pragma unroll
             for (int j = 0; j < T; ++j) {
@@ -819,64 +857,79 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
 
 // High-occupancy streaming down projection for I <= 512 (a row of I/32 <= 16
 // blocks is <= 256 code bytes, 16 lanes; one wave load covers 4 rows).  Work
-// unit = (item, slice of 64 output rows); a 2-wave workgroup gives each wave
-// 32 rows = 8 independent 16-byte loads per lane in flight.  Row sums of the
-// item's pairs are written unweighted to their contribution rows
-// (token * out_stride_k + rank), like the reference's scatter
-// (src/hip/session_ops.hip:357-373).
+// unit = (item, slice of 64 output rows), grid = (item bound, H/64); a 2-wave
+// workgroup gives each wave 32 rows = 8 independent 16-byte loads per lane in
+// flight.  Row sums of the item's pairs are written unweighted to their
+// contribution rows (token * out_stride_k + rank), like the reference's
+// scatter (src/hip/session_ops.hip:357-373).
 // NBI = 16 specialises I = 512 (every lane holds a block); NBI = 0 reads
 // I/32 <= 16 at run time.
 template<int NBI, bool Dbg>
 __global__ __launch_bounds__(128, NBI ? 8 : 7) void k_down_lean(FfnArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int H = a.shape.H, nbi = NBI ? NBI : a.shape.I / 32, S = H / 64;
-    const int u = blockIdx.x;
-    if (u >= a.routes.item_counts[0] * S) return;   // uniform per workgroup
-    const Item *itp = a.routes.stream_items + u / S;   // fields via pointer: no scratch copy
-    const Item it{itp->expert, itp->first, itp->ncols, 0};
-    const int slice = u % S;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int H = a.shape.H, nbi = NBI ? NBI : a.shape.I / 32;
+    const int item = blockIdx.x, slice = blockIdx.y;
+    const int4 hdr = *reinterpret_cast<const int4 *>(a.routes.stream_items + item);
+    const int4 tok = *reinterpret_cast<const int4 *>(a.routes.stream_items[item].token);
+    const int4 rnk = *reinterpret_cast<const int4 *>(a.routes.stream_items[item].rank);
+    const int count = a.routes.item_counts[0];
+    asm volatile("" ::"s"(hdr.x), "s"(hdr.y), "s"(hdr.z), "s"(tok.x), "s"(tok.y), "s"(tok.z), "s"(tok.w),
+                 "s"(rnk.x), "s"(rnk.y), "s"(rnk.z), "s"(rnk.w), "s"(count));
+    if (item >= count) return;   // uniform per workgroup
+    const int expert = hdr.x, first = hdr.y, ncols = hdr.z;
     const int row0 = slice * 64 + wave * 32;
-    const int sub = lane >> 4, kb = lane & 15;
-    const bool has = NBI == 16 || kb < nbi;
-    const size_t b0 = (static_cast<size_t>(it.expert) * H + row0 + sub) * nbi + kb;
-    uint4 w[8];
-    uint32_t d4[8];
-#pragma unroll
-    for (int l = 0; l < 8; ++l) {
-        const size_t b = b0 + static_cast<size_t>(4 * l) * nbi;
-        w[l] = has ? *reinterpret_cast<const uint4 *>(a.bank.down_codes + b * 16) : make_uint4(0, 0, 0, 0);
-        d4[l] = has ? a.bank.down_scales[b] : 0u;
-    }
+    const int sub = lane >> 4, kl = lane & 15;
+    // Lanes past the row end (I < 512) read block 0 and drop their products,
+    // so all loads are unconditional and in flight together.
+    const bool has = NBI == 16 || kl < nbi;
+    const int kb = has ? kl : 0;
+    // The wave's 32 rows are one buffer (per-load SGPR offset, one lane-offset
+    // VGPR); the lane's 8 scales (rows row0 + sub + 4l of its block) are one
+    // 16-byte load.
+    const size_t mrow = static_cast<size_t>(expert) * H + row0;     // row0 % 32 == 0
+    const uint32_t row_bytes = static_cast<uint32_t>(nbi) * 16u;
+    const auto wr = buffer_rsrc(a.bank.down_codes + mrow * row_bytes, 32 * row_bytes);
+    const auto sr = buffer_rsrc(a.bank.down_scales + mrow * nbi, 4 * row_bytes);
+    const uint32_t lane_off = static_cast<uint32_t>(sub * nbi + kb) * 16u;
     // Transposing reduction over the 16 lanes of a row: xor 8/4/2 halve the
     // 8 load-rows, xor 1 finishes; lane ends with load-row lr(lane).
     const bool c3 = lane & 8, c2 = lane & 4, c1 = lane & 2;
     const int lr = (c3 ? 4 : 0) + (c2 ? 2 : 0) + (c1 ? 1 : 0);
+    // Weights are loaded per pair together with its middle activations (the
+    // first pair streams them from HBM, further pairs hit L2).
 #pragma unroll 1
-    for (int j = 0; j < it.ncols; ++j) {
-        const int pair = it.first + j;
-        const size_t xb = static_cast<size_t>(pair) * nbi + kb;
-        const uint4 x0 = has ? *reinterpret_cast<const uint4 *>(a.mq.codes + xb * 32) : make_uint4(0, 0, 0, 0);
-        const uint4 x1 = has ? *reinterpret_cast<const uint4 *>(a.mq.codes + xb * 32 + 16) : make_uint4(0, 0, 0, 0);
-        const uint32_t hx = has ? a.mq.heads[xb] : 0u;
+    for (int j = 0; j < ncols; ++j) {
+        const int pair = first + j;
+        const size_t xrow = static_cast<size_t>(pair) * nbi;
+        const auto xr = buffer_rsrc(a.mq.codes + xrow * 32, static_cast<uint32_t>(nbi) * 32u);
+        const auto hr = buffer_rsrc(a.mq.heads + xrow, static_cast<uint32_t>(nbi) * 4u);
+        uint4 w[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) w[l] = buffer_load16(wr, lane_off, 4 * l * row_bytes);
+        const uint4 d4p = buffer_load16(sr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
+        const uint4 x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
+        const uint4 x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
+        const uint32_t hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
         const float d8 = h2f(hx), c8 = -8.0f * h2f(hx >> 16);
-#pragma unroll
-        for (int l = 0; l < 8; ++l) asm volatile("" : "+v"(w[l].x), "+v"(w[l].y), "+v"(w[l].z), "+v"(w[l].w));
-        float acc[8];
-#pragma unroll
-        for (int l = 0; l < 8; ++l) {
-            const int dot = dot_block(w[l], x0, x1);
-            if constexpr (Dbg) {
-                if (a.down_dots && has)
-                    a.down_dots[(static_cast<size_t>(pair) * H + row0 + 4 * l + sub) * nbi + kb] = dot;
-            }
-            acc[l] = h2f(d4[l]) * fmaf(static_cast<float>(dot), d8, c8);
-        }
         float v4[4], v2[2];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float send = c3 ? acc[i] : acc[i + 4];
-            const float keep = c3 ? acc[i + 4] : acc[i];
+            float pr[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int l = i + 4 * h;
+                const int dot = dot_block(w[l], x0, x1);
+                if constexpr (Dbg) {
+                    if (a.down_dots && has)
+                        a.down_dots[(static_cast<size_t>(pair) * H + row0 + 4 * l + sub) * nbi + kl] = dot;
+                }
+                const uint32_t d4 = (&d4p.x)[l >> 1] >> (16 * (l & 1));
+                pr[h] = has ? h2f(d4) * fmaf(static_cast<float>(dot), d8, c8) : 0.0f;
+            }
+            const float send = c3 ? pr[0] : pr[1];
+            const float keep = c3 ? pr[1] : pr[0];
             v4[i] = keep + __shfl_xor(send, 8, 64);
+            __builtin_amdgcn_sched_barrier(0);   // one row pair at a time (register pressure)
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -887,7 +940,9 @@ __global__ __launch_bounds__(128, NBI ? 8 : 7) void k_down_lean(FfnArgs a) {
         float v = (c1 ? v2[1] : v2[0]) + __shfl_xor(c1 ? v2[0] : v2[1], 2, 64);
         v = xor_sum(v, 1);
         if ((lane & 1) == 0) {
-            const size_t orow = static_cast<size_t>(itp->token[j]) * a.out_stride_k + itp->rank[j];
+            const int t = j == 0 ? tok.x : j == 1 ? tok.y : j == 2 ? tok.z : tok.w;
+            const int rk = j == 0 ? rnk.x : j == 1 ? rnk.y : j == 2 ? rnk.z : rnk.w;
+            const size_t orow = static_cast<size_t>(t) * a.out_stride_k + rk;
             a.out[orow * H + row0 + 4 * lr + sub] = v;
         }
     }
@@ -988,23 +1043,25 @@ hipError_t launch_planes_to_canonical(Act in, void *q8, int blocks, hipStream_t 
 }
 
 hipError_t launch_repack_weights(const uint8_t *canonical, uint8_t *codes, uint16_t *scales, size_t blocks,
-                                 hipStream_t s) {
+                                 size_t block0, int blocks_per_row, int group, hipStream_t s) {
     k_repack<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<const uint16_t *>(canonical),
-                                                      reinterpret_cast<uint32_t *>(codes), scales, blocks);
+                                                      reinterpret_cast<uint32_t *>(codes), scales, blocks, block0,
+                                                      blocks_per_row, group);
     return hipGetLastError();
 }
 
-hipError_t launch_unpack_weights(const uint8_t *codes, const uint16_t *scales, uint8_t *canonical,
-                                 size_t blocks, hipStream_t s) {
+hipError_t launch_unpack_weights(const uint8_t *codes, const uint16_t *scales, uint8_t *canonical, size_t blocks,
+                                 size_t block0, int blocks_per_row, int group, hipStream_t s) {
     k_unpack<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<const uint32_t *>(codes), scales,
-                                                      reinterpret_cast<uint16_t *>(canonical), blocks);
+                                                      reinterpret_cast<uint16_t *>(canonical), blocks, block0,
+                                                      blocks_per_row, group);
     return hipGetLastError();
 }
 
-hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, size_t blocks, size_t block0,
-                                    uint64_t seed, hipStream_t s) {
+hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, size_t blocks, size_t hash0,
+                                    int blocks_per_row, int group, uint64_t seed, hipStream_t s) {
     k_synthetic<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<uint32_t *>(codes), scales, blocks,
-                                                         block0, seed);
+                                                         hash0, blocks_per_row, group, seed);
     return hipGetLastError();
 }
 
@@ -1053,6 +1110,13 @@ hipError_t launch_single_expert_items(Shape shape, RouteOut routes, int expert, 
 }
 
 namespace {
+// Upper bound on streaming items (the size the item array is allocated for):
+// one partial item per nonempty group plus full items.
+unsigned stream_item_bound(const FfnArgs &a) {
+    return static_cast<unsigned>(static_cast<size_t>(a.pairs_bound) / kStreamTokens +
+                                 static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep)));
+}
+
 unsigned stream_grid(const FfnArgs &a, int slices) {
     // Upper bound on streaming items: one partial item per nonempty group plus
     // full items; the persistent loop covers whatever the device produced.
@@ -1075,10 +1139,8 @@ hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s) {
     const unsigned grid = stream_grid(a, a.shape.I / 32);
     const int nbl = (a.shape.H / 32 + 63) / 64;
     if (nbl <= 1) {
-        // One unit per workgroup; grid = upper bound on units (extra groups exit).
-        const size_t bound = (static_cast<size_t>(a.pairs_bound) / kStreamTokens +
-                              static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep))) * (a.shape.I / 32);
-        const unsigned lgrid = static_cast<unsigned>(bound);
+        // One unit per workgroup; grid = (item bound, slices), extra items exit.
+        const dim3 lgrid(stream_item_bound(a), a.shape.I / 32);
         if (dbg) k_gate_up_lean<true><<<lgrid, 512, 0, s>>>(a);
         else k_gate_up_lean<false><<<lgrid, 512, 0, s>>>(a);
     } else if (nbl <= 2) gate_up_stream<2>(a, dbg, grid, s);
@@ -1092,9 +1154,7 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
     const unsigned grid = stream_grid(a, a.shape.H / 64);
     const bool dbg = a.down_dots != nullptr;
     if (nbi <= 16) {
-        const size_t bound = (static_cast<size_t>(a.pairs_bound) / kStreamTokens +
-                              static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep))) * (a.shape.H / 64);
-        const unsigned g = static_cast<unsigned>(bound);
+        const dim3 g(stream_item_bound(a), a.shape.H / 64);
         if (dbg) k_down_lean<0, true><<<g, 128, 0, s>>>(a);
         else if (nbi == 16) k_down_lean<16, false><<<g, 128, 0, s>>>(a);
         else k_down_lean<0, false><<<g, 128, 0, s>>>(a);

@@ -39,6 +39,10 @@ struct moe_ffn_layer {
     const int32_t *last_ids = nullptr;
     float *last_y = nullptr;
     int *last_error = nullptr;
+    // Stage profiler (moe_ffn_profile): a ring of events, one set per forward.
+    static constexpr int kStageMarks = MOE_STAGE_FOLD + 2;
+    hipEvent_t *prof_events = nullptr;
+    int prof_capacity = 0, prof_used = 0;
 };
 
 namespace {
@@ -146,6 +150,20 @@ int alloc_bank(moe_ffn_layer *L) {
     return hipSuccess;
 }
 
+// One matrix kind's planes: gate (m = 0), up (1), down (2).
+struct Plane {
+    uint8_t *codes;
+    uint16_t *scales;
+    int blocks_per_row, group;
+};
+
+Plane plane(const moe_ffn_layer *L, int m) {
+    const int nbh = L->shape.H / 32, nbi = L->shape.I / 32;
+    if (m == 0) return Plane{L->gate_codes, L->gate_scales, nbh, moe::kScaleGroupGateUp};
+    if (m == 1) return Plane{L->up_codes, L->up_scales, nbh, moe::kScaleGroupGateUp};
+    return Plane{L->down_codes, L->down_scales, nbi, moe::kScaleGroupDown};
+}
+
 // Repack `count` canonical experts starting at expert `first` from a device
 // staging buffer into the planes.
 int repack_experts(moe_ffn_layer *L, const uint8_t *staging, int first, int count) {
@@ -154,13 +172,12 @@ int repack_experts(moe_ffn_layer *L, const uint8_t *staging, int first, int coun
     for (int i = 0; i < count; ++i) {
         const size_t e = static_cast<size_t>(first + i);
         const uint8_t *src = staging + static_cast<size_t>(i) * expert_blocks(s) * 18;
-        hipError_t r;
-        if ((r = moe::launch_repack_weights(src, L->gate_codes + e * mblocks * 16, L->gate_scales + e * mblocks,
-                                            mblocks, nullptr)) != hipSuccess) return r;
-        if ((r = moe::launch_repack_weights(src + mblocks * 18, L->up_codes + e * mblocks * 16,
-                                            L->up_scales + e * mblocks, mblocks, nullptr)) != hipSuccess) return r;
-        if ((r = moe::launch_repack_weights(src + 2 * mblocks * 18, L->down_codes + e * mblocks * 16,
-                                            L->down_scales + e * mblocks, mblocks, nullptr)) != hipSuccess) return r;
+        for (int m = 0; m < 3; ++m) {
+            const Plane pl = plane(L, m);
+            const hipError_t r = moe::launch_repack_weights(src + m * mblocks * 18, pl.codes, pl.scales, mblocks,
+                                                            e * mblocks, pl.blocks_per_row, pl.group, nullptr);
+            if (r != hipSuccess) return r;
+        }
     }
     return hipSuccess;
 }
@@ -226,10 +243,9 @@ int upload_tensors(moe_ffn_layer *L, const void *const routed[3], const void *co
     const int chunk = static_cast<int>(std::max<size_t>(1, (size_t{256} << 20) / mbytes));
     uint8_t *staging = nullptr;
     if (hipMalloc(&staging, static_cast<size_t>(chunk) * mbytes) != hipSuccess) return hipErrorOutOfMemory;
-    uint8_t *codes[3] = {L->gate_codes, L->up_codes, L->down_codes};
-    uint16_t *scales[3] = {L->gate_scales, L->up_scales, L->down_scales};
     int r = hipSuccess;
     for (int m = 0; m < 3 && r == hipSuccess; ++m) {
+        const Plane pl = plane(L, m);
         for (int first = 0; first < s.Ep && r == hipSuccess; first += chunk) {
             const int n = std::min(chunk, s.Ep - first);
             const int nr = std::max(0, std::min(n, s.E - first));   // routed experts in this chunk
@@ -239,14 +255,21 @@ int upload_tensors(moe_ffn_layer *L, const void *const routed[3], const void *co
             if (r == hipSuccess && nr < n)   // the shared expert follows the routed ones
                 r = hipMemcpy(staging + static_cast<size_t>(nr) * mbytes, shared[m], mbytes, hipMemcpyHostToDevice);
             if (r == hipSuccess)
-                r = moe::launch_repack_weights(staging, codes[m] + static_cast<size_t>(first) * mblocks * 16,
-                                               scales[m] + static_cast<size_t>(first) * mblocks,
-                                               static_cast<size_t>(n) * mblocks, nullptr);
+                r = moe::launch_repack_weights(staging, pl.codes, pl.scales, static_cast<size_t>(n) * mblocks,
+                                               static_cast<size_t>(first) * mblocks, pl.blocks_per_row, pl.group,
+                                               nullptr);
             if (r == hipSuccess) r = hipDeviceSynchronize();
         }
     }
     (void)hipFree(staging);
     return r;
+}
+
+void profile_free(moe_ffn_layer *L) {
+    for (int i = 0; i < L->prof_capacity * moe_ffn_layer::kStageMarks; ++i) (void)hipEventDestroy(L->prof_events[i]);
+    delete[] L->prof_events;
+    L->prof_events = nullptr;
+    L->prof_capacity = L->prof_used = 0;
 }
 
 moe::FfnArgs base_args(moe_ffn_layer *L, int tokens, int *error) {
@@ -328,11 +351,11 @@ int moe_ffn_create_synthetic(const moe_ffn_config *config, uint64_t seed, int de
     int r = create_common(config, device, layer, L);
     if (r != hipSuccess) return r;
     const size_t blocks = static_cast<size_t>(L->shape.Ep) * L->shape.I * (L->shape.H / 32);
-    uint8_t *codes[3] = {L->gate_codes, L->up_codes, L->down_codes};
-    uint16_t *scales[3] = {L->gate_scales, L->up_scales, L->down_scales};
-    for (int m = 0; m < 3 && r == hipSuccess; ++m)
-        r = moe::launch_synthetic_weights(codes[m], scales[m], blocks, static_cast<size_t>(m) * blocks, seed,
-                                          nullptr);
+    for (int m = 0; m < 3 && r == hipSuccess; ++m) {
+        const Plane pl = plane(L, m);
+        r = moe::launch_synthetic_weights(pl.codes, pl.scales, blocks, static_cast<size_t>(m) * blocks,
+                                          pl.blocks_per_row, pl.group, seed, nullptr);
+    }
     if (r == hipSuccess) r = hipDeviceSynchronize();
     if (r == hipSuccess) r = finish_create(L);
     if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
@@ -344,6 +367,7 @@ int moe_ffn_destroy(moe_ffn_layer *L) {
     if (!L) return kInvalid;
     (void)hipSetDevice(L->device);
     (void)hipDeviceSynchronize();
+    profile_free(L);
     if (L->bank_mem) (void)hipFree(L->bank_mem);
     if (L->ws_mem) (void)hipFree(L->ws_mem);
     delete L;
@@ -358,14 +382,12 @@ int moe_ffn_export_expert(moe_ffn_layer *L, int expert, void *host_q4) {
     if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
     if (hipMalloc(&staging, 3 * mblocks * 18) != hipSuccess) return hipErrorOutOfMemory;
     const size_t e = static_cast<size_t>(expert);
-    int r = moe::launch_unpack_weights(L->gate_codes + e * mblocks * 16, L->gate_scales + e * mblocks, staging,
-                                       mblocks, nullptr);
-    if (r == hipSuccess)
-        r = moe::launch_unpack_weights(L->up_codes + e * mblocks * 16, L->up_scales + e * mblocks,
-                                       staging + mblocks * 18, mblocks, nullptr);
-    if (r == hipSuccess)
-        r = moe::launch_unpack_weights(L->down_codes + e * mblocks * 16, L->down_scales + e * mblocks,
-                                       staging + 2 * mblocks * 18, mblocks, nullptr);
+    int r = hipSuccess;
+    for (int m = 0; m < 3 && r == hipSuccess; ++m) {
+        const Plane pl = plane(L, m);
+        r = moe::launch_unpack_weights(pl.codes, pl.scales, staging + m * mblocks * 18, mblocks, e * mblocks,
+                                       pl.blocks_per_row, pl.group, nullptr);
+    }
     if (r == hipSuccess) r = hipMemcpy(host_q4, staging, 3 * mblocks * 18, hipMemcpyDeviceToHost);
     (void)hipFree(staging);
     return r;
@@ -406,9 +428,13 @@ int moe_ffn_forward(moe_ffn_layer *L, const float *x, const int32_t *ids, const 
         tokens < 1 || tokens > L->cfg.max_tokens || (shared_gate && !aligned(shared_gate, 4)))
         return kInvalid;
     const auto s = static_cast<hipStream_t>(stream);
+    hipEvent_t *marks = nullptr;
+    if (L->prof_used < L->prof_capacity) marks = L->prof_events + (L->prof_used++) * moe_ffn_layer::kStageMarks;
+    if (marks && hipEventRecord(marks[0], s) != hipSuccess) return kInvalid;
     for (int stage = MOE_STAGE_PREPARE; stage <= MOE_STAGE_FOLD; ++stage) {
         const int r = run_stage(L, stage, x, ids, weights, tokens, shared_gate, y, error, s);
         if (r != hipSuccess) return r;
+        if (marks && hipEventRecord(marks[stage + 1], s) != hipSuccess) return kInvalid;
     }
     L->last_tokens = tokens;
     L->last_x = x;
@@ -418,6 +444,47 @@ int moe_ffn_forward(moe_ffn_layer *L, const float *x, const int32_t *ids, const 
     L->last_y = y;
     L->last_error = error;
     return hipSuccess;
+}
+
+int moe_ffn_profile(moe_ffn_layer *L, int forwards) {
+    if (!L || forwards < 0 || forwards > 65536) return kInvalid;
+    profile_free(L);
+    if (forwards == 0) return hipSuccess;
+    const int n = forwards * moe_ffn_layer::kStageMarks;
+    L->prof_events = new (std::nothrow) hipEvent_t[n]();
+    if (!L->prof_events) return hipErrorOutOfMemory;
+    for (int i = 0; i < n; ++i) {
+        // Timing markers without the system-scope release of a default event,
+        // so recording them does not add cache writebacks between stages.
+        if (hipEventCreateWithFlags(&L->prof_events[i], hipEventDisableSystemFence) != hipSuccess) {
+            for (int j = 0; j < i; ++j) (void)hipEventDestroy(L->prof_events[j]);
+            delete[] L->prof_events;
+            L->prof_events = nullptr;
+            return hipErrorOutOfMemory;
+        }
+    }
+    L->prof_capacity = forwards;
+    L->prof_used = 0;
+    return hipSuccess;
+}
+
+int moe_ffn_profile_read(moe_ffn_layer *L, double *stage_ms, int *forwards) {
+    if (!L || !stage_ms || !forwards) return kInvalid;
+    for (int st = 0; st <= MOE_STAGE_FOLD; ++st) stage_ms[st] = 0.0;
+    *forwards = L->prof_used;
+    if (L->prof_used == 0) return hipSuccess;
+    hipEvent_t *last = L->prof_events + (L->prof_used - 1) * moe_ffn_layer::kStageMarks;
+    hipError_t r = hipEventSynchronize(last[moe_ffn_layer::kStageMarks - 1]);
+    for (int f = 0; f < L->prof_used && r == hipSuccess; ++f) {
+        hipEvent_t *m = L->prof_events + f * moe_ffn_layer::kStageMarks;
+        for (int st = 0; st <= MOE_STAGE_FOLD && r == hipSuccess; ++st) {
+            float ms = 0.0f;
+            r = hipEventElapsedTime(&ms, m[st], m[st + 1]);
+            stage_ms[st] += ms;
+        }
+    }
+    L->prof_used = 0;
+    return r;
 }
 
 int moe_ffn_replay_stage(moe_ffn_layer *L, int stage, void *stream) {

@@ -67,6 +67,8 @@ def library():
         lib.moe_combine.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P]
         lib.moe_ffn_debug_last.argtypes = [_P, _P, _P, _P, _P, _P]
         lib.moe_ffn_replay_stage.argtypes = [_P, _I, _P]
+        lib.moe_ffn_profile.argtypes = [_P, _I]
+        lib.moe_ffn_profile_read.argtypes = [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]
         lib.moe_ffn_last_stats.argtypes = [_P, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
                                            ctypes.POINTER(ctypes.c_int32)]
         _lib = lib
@@ -179,6 +181,17 @@ class MoeLayer:
 
     def replay_stage(self, stage, stream=None):
         _check(library().moe_ffn_replay_stage(self.handle, stage, _stream(stream)), "moe_ffn_replay_stage")
+
+    def profile(self, forwards):
+        """Record stage timing events for the next `forwards` forward() calls."""
+        _check(library().moe_ffn_profile(self.handle, forwards), "moe_ffn_profile")
+
+    def profile_read(self):
+        """(seconds per stage summed over the recorded forwards, count)."""
+        ms = (ctypes.c_double * (STAGE_FOLD + 1))()
+        n = ctypes.c_int()
+        _check(library().moe_ffn_profile_read(self.handle, ms, ctypes.byref(n)), "moe_ffn_profile_read")
+        return [v / 1e3 for v in ms], n.value
 
     def debug_last(self, tokens, stream=None):
         import torch

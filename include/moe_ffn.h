@@ -172,6 +172,17 @@ int moe_ffn_debug_last(moe_ffn_layer *layer, void *x_q8, void *middle_q8, int32_
 enum { MOE_STAGE_PREPARE = 0, MOE_STAGE_GATE_UP = 1, MOE_STAGE_DOWN = 2, MOE_STAGE_FOLD = 3 };
 int moe_ffn_replay_stage(moe_ffn_layer *layer, int stage, void *stream);
 
+/* Stage profiler.  moe_ffn_profile(layer, n) creates timing events for the
+ * next n forward() calls (n = 0 releases them; this call allocates host-side
+ * event objects and may synchronise).  Each profiled forward records an event
+ * before its first stage and after every stage on its own stream.
+ * moe_ffn_profile_read waits for the last recorded forward and returns the
+ * summed milliseconds per stage (MOE_STAGE_* order, 4 values) over the
+ * forwards recorded since the last read, and their count; it then rearms the
+ * same events for the next n forwards. */
+int moe_ffn_profile(moe_ffn_layer *layer, int forwards);
+int moe_ffn_profile_read(moe_ffn_layer *layer, double *stage_ms, int *forwards);
+
 /* Last-forward statistics (host, synchronous): work items per path and the
  * number of experts (incl. shared) that received tokens. */
 int moe_ffn_last_stats(moe_ffn_layer *layer, int32_t *stream_items, int32_t *mfma_items,
