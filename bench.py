@@ -175,9 +175,9 @@ def main():
                    "touched_experts_mean": float(touched.mean()),
                    "gpu_event_us_per_layer": gpu * 1e6,
                    "layer_hbm_frac": layer_bytes / gpu / 1e9 / HBM_PEAK_GBS},
-        "roofline": {"kernel": "k_gate_up_lean (gate/up + SiLU + Q8 of the middle)", "bound": "hbm",
+        "roofline": {"kernel": "k_decode_gate_up (x Q8 + gate/up + SiLU + middle Q8)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": pmc_traffic("k_gate_up_lean<false>", float(touched.mean()) + 1),
+                     "traffic": pmc_traffic("k_decode_gate_up", float(touched.mean()) + 1),
                      "bytes_per_launch": gate_bytes / n_stage, "us_per_launch": t_gate * 1e6},
         "stages_us": {"prepare": t_prep * 1e6, "gate_up": t_gate * 1e6, "down": t_down * 1e6, "fold": t_fold * 1e6},
         "down_stage_hbm_frac": down_bytes / float(t_stage[2]) / 1e9 / HBM_PEAK_GBS,

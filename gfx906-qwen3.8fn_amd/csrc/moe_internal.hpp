@@ -122,6 +122,30 @@ struct FfnArgs {
     int cu_count;      // compute units of the device (persistent grids)
 };
 
+// Ungrouped decode path (few tokens, mostly one token per expert): work is
+// indexed by (token, rank) directly, so no grouping runs.  The middle Q8 row
+// of pair (t, r) is t * (k + has_shared) + r.
+struct DecodeArgs {
+    FfnArgs f;
+    const float *x;            // [tokens][H]
+    const int32_t *ids;        // [tokens][k]
+    const float *weights;      // [tokens][k]
+    const float *shared_gate;  // [tokens] or nullptr
+    float *y;                  // [tokens][H]
+};
+inline constexpr int kDecodeMaxBlocksH = 64;   // H/32 <= 64: one block per lane
+inline constexpr int kDecodeMaxBlocksI = 16;   // I/32 <= 16: 16 lanes per down row
+inline constexpr int kDecodeMaxPairs = 16;     // k + has_shared <= 16: one wave per rank in the fold
+// gate/up + SiLU + Q8 (quantizes each token's x on the fly; rank 0 / slice 0
+// also writes the token's x Q8 planes for debugging).
+hipError_t launch_decode_gate_up(const DecodeArgs &d, hipStream_t s);
+// down + rank-order fold + shared add into y.
+hipError_t launch_decode_down_fold(const DecodeArgs &d, hipStream_t s);
+// Debug view: the decode-layout middle Q8 rows in grouped pair order, as
+// canonical 36-byte blocks (routes must hold the grouping of the same batch).
+hipError_t launch_decode_middle_grouped(Act mq, RouteOut routes, Shape shape, int tokens, void *q8,
+                                        hipStream_t s);
+
 hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s);
 hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s);
 

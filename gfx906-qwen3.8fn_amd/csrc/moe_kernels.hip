@@ -93,6 +93,74 @@ __device__ __forceinline__ Q8Lane quantize32(float x) {
     return q;
 }
 
+// One Q8_1 block from P lanes (P = 2 or 4): lane l holds elements
+// (32/P) * part .. +32/P-1 of its block, part = l / (64/P); the partners are
+// lanes l ^ 32 (and l ^ 16 for P = 4).  Same bits as quantize32: max is
+// order-free, and each part's pairwise sum is an aligned subtree of the XOR
+// butterfly 1..16, whose last stages combine the parts in the same order.
+// codes[] gets the lane's 32/P codes (4 per word, element order); head and
+// flags are valid in every lane of the block.
+template<int P>
+struct Q8Part {
+    uint32_t codes[8 / P];
+    uint32_t head;
+    int flags;
+};
+
+template<int P>
+__device__ __forceinline__ Q8Part<P> quantize_part(float (&v)[32 / P]) {
+    constexpr int n = 32 / P;
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < n; ++i)
+        if (!isfinite(v[i])) { bad = 1; v[i] = 0.0f; }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < n; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    float t[n];
+#pragma unroll
+    for (int i = 0; i < n; ++i) t[i] = v[i];
+#pragma unroll
+    for (int w = n / 2; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) t[i] = t[2 * i] + t[2 * i + 1];
+    float sum = t[0];
+    if constexpr (P == 4) {
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        bad |= __shfl_xor(bad, 16, 64);
+        sum = sum + __shfl_xor(sum, 16, 64);
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    bad |= __shfl_xor(bad, 32, 64);
+    sum = sum + __shfl_xor(sum, 32, 64);   // commutative: every lane of the block agrees
+    const float d = amax / 127.0f;
+    const uint32_t hd = f2h(d), hs = f2h(sum);
+    const bool representable = isfinite(sum) && (hs & 0x7c00u) != 0x7c00u &&
+                               (hd & 0x7c00u) != 0x7c00u && (amax == 0.0f || d > 0.0f);
+    const bool quant = !bad && representable && amax != 0.0f;
+    int bad_code = 0;
+    Q8Part<P> q;
+#pragma unroll
+    for (int w = 0; w < n / 4; ++w) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const float c = quant ? roundf(v[4 * w + b] / d) : 0.0f;
+            bad_code |= !isfinite(c) || c < -127.0f || c > 127.0f;
+            word |= (static_cast<uint32_t>(static_cast<int>(c)) & 0xffu) << (8 * b);
+        }
+        q.codes[w] = word;
+    }
+    if constexpr (P == 4) bad_code |= __shfl_xor(bad_code, 16, 64);
+    bad_code |= __shfl_xor(bad_code, 32, 64);
+    const bool valid = !bad && representable && !bad_code;
+#pragma unroll
+    for (int w = 0; w < n / 4; ++w) q.codes[w] = valid ? q.codes[w] : 0u;
+    q.head = (valid && amax != 0.0f) ? (hd | (hs << 16)) : 0u;
+    q.flags = (bad ? 1 : 0) | ((representable && !bad_code) ? 0 : 2);
+    return q;
+}
+
 // SiLU(g)*u with the reference's sanitisation (src/hip/linear.hip:106-120).
 __device__ __forceinline__ float silu_mul(float g, float u, int &flags) {
     if (!isfinite(g)) { flags |= 1; g = 0.0f; }
@@ -948,6 +1016,273 @@ __global__ __launch_bounds__(128, NBI ? 8 : 7) void k_down_lean(FfnArgs a) {
     }
 }
 
+// ----------------------------------------------------- ungrouped decode ---
+// Route (t, r) of a decode batch, validated as RouteGroups::prepare does
+// (src/routes.cpp:145-157): returns the expert (E = shared for r == k) or -1
+// for a bad id or a duplicate of an earlier rank.  `flags` gets bit 1 for a
+// bad id, a duplicate, or a negative / nonfinite weight.
+__device__ __forceinline__ int decode_route(const DecodeArgs &d, int t, int r, int &flags) {
+    const int k = d.f.shape.k, E = d.f.shape.E;
+    if (r == k) return E;
+    const int32_t *row = d.ids + static_cast<size_t>(t) * k;
+    const int e = row[r];
+    const float w = d.weights[static_cast<size_t>(t) * k + r];
+    if (!isfinite(w) || w < 0.0f) flags |= 1;
+    bool ok = e >= 0 && e < E;
+    for (int q = 0; q < r; ++q) ok = ok && row[q] != e;
+    if (!ok) { flags |= 1; return -1; }
+    return e;
+}
+
+// gate/up + SiLU + Q8 for one (token, rank) pair and one slice of 32
+// intermediate rows; grid = (k + shared, tokens, I/32).  The 8 waves take
+// 8 gate / up rows each as in k_gate_up_lean.  The token's x row is quantized
+// by the whole workgroup into LDS (the same quantize32 as the quantize
+// kernels) while the weight loads are in flight.
+__global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
+    __shared__ uint32_t xs[kDecodeMaxBlocksH * 8];   // Q8 codes of the token, [blocks][32 B]
+    __shared__ uint32_t xh[kDecodeMaxBlocksH];       // heads
+    __shared__ float gu[2][32];
+    const FfnArgs &a = d.f;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32;
+    // XCD-aware order: workgroup id i runs on XCD i % 8.  Ids are laid out so
+    // that the tokens of one (rank, slice) are consecutive on one XCD: the
+    // shared expert's rows of a slice (and an expert two tokens share, at the
+    // same rank) are then fetched from HBM once into that XCD's L2.
+    const int N = a.tokens, P1 = a.shape.k + (a.shape.Ep > a.shape.E ? 1 : 0), S = I / 32;
+    const int id = blockIdx.x, j = id >> 3;
+    const int t = j % N, r = (j / N) % P1, s = (id & 7) + 8 * (j / (N * P1));
+    if (s >= S) return;
+    int flags = 0;
+    const int expert = decode_route(d, t, r, flags);
+    if (s == 0 && flags && threadIdx.x == 0) atomicOr(a.error, flags);
+    // Rank 0 / slice 0 reports the token's input flags and writes its x Q8,
+    // so it quantizes even when its own route is invalid.
+    const bool report = r == 0 && s == 0;
+    if (expert < 0 && !report) return;   // uniform per workgroup
+    // Waves 0-3 quantize the token row, 4 lanes per block (wave w, lane l:
+    // block 16w + l % 16, elements 8 * (l / 16) .. +7).  They issue their x
+    // loads before their weight loads, so waiting for x never waits behind
+    // the weights.
+    const bool quant_wave = wave < 4;
+    const int qblk = wave * 16 + (lane & 15), qpart = lane >> 4;
+    float xv[8];
+    if (quant_wave) {
+        const auto xr = buffer_rsrc(d.x + static_cast<size_t>(t) * H, static_cast<uint32_t>(H) * 4u);
+        const uint32_t off = static_cast<uint32_t>(qblk * 32 + qpart * 8) * 4u;   // past H: reads 0
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint4 v = buffer_load16(xr, off, q * 16);
+            xv[4 * q] = __uint_as_float(v.x); xv[4 * q + 1] = __uint_as_float(v.y);
+            xv[4 * q + 2] = __uint_as_float(v.z); xv[4 * q + 3] = __uint_as_float(v.w);
+        }
+    }
+    // Weights of this wave's 8 rows (as k_gate_up_lean).
+    const int mat = wave >> 2;
+    const int row0 = s * 32 + (wave & 3) * 8;
+    const bool has = lane < nbh;
+    const int kb = has ? lane : 0;
+    const size_t mrow = static_cast<size_t>(expert < 0 ? 0 : expert) * I + row0;
+    const uint32_t row_bytes = static_cast<uint32_t>(nbh) * 16u;
+    const auto wr = buffer_rsrc((mat ? a.bank.up_codes : a.bank.gate_codes) + mrow * row_bytes, 8 * row_bytes);
+    const auto sr = buffer_rsrc((mat ? a.bank.up_scales : a.bank.gate_scales) + mrow * nbh, row_bytes);
+    const uint32_t lane_off = static_cast<uint32_t>(kb) * 16u;
+    uint4 w[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) w[q] = buffer_load16(wr, lane_off, q * row_bytes);
+    const uint4 d4p = buffer_load16(sr, lane_off, 0);
+    if (quant_wave) {
+        const Q8Part<4> qp = quantize_part<4>(xv);
+        if (qblk < nbh) {
+            reinterpret_cast<uint2 *>(xs)[qblk * 4 + qpart] = make_uint2(qp.codes[0], qp.codes[1]);
+            if (qpart == 0) xh[qblk] = qp.head;
+            if (report) {
+                const size_t gb = static_cast<size_t>(t) * nbh + qblk;
+                reinterpret_cast<uint2 *>(a.xq.codes)[gb * 4 + qpart] = make_uint2(qp.codes[0], qp.codes[1]);
+                if (qpart == 0) {
+                    a.xq.heads[gb] = qp.head;
+                    if (qp.flags) atomicOr(a.error, qp.flags);
+                }
+            }
+        }
+    }
+    if (expert < 0) return;   // the reporting workgroup of an invalid route
+    __syncthreads();
+    const uint4 x0 = reinterpret_cast<const uint4 *>(xs)[kb * 2];
+    const uint4 x1 = reinterpret_cast<const uint4 *>(xs)[kb * 2 + 1];
+    const uint32_t hx = xh[kb];
+    const float d8 = h2f(hx), c8 = -8.0f * h2f(hx >> 16);
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+    const int rho = (b5 ? 4 : 0) + (b4 ? 2 : 0) + (b3 ? 1 : 0);
+    float v4[4], v2[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float pr[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int q = i + 4 * h;
+            const int dot = dot_block(w[q], x0, x1);
+            const uint32_t d4 = (&d4p.x)[q >> 1] >> (16 * (q & 1));
+            pr[h] = has ? h2f(d4) * fmaf(static_cast<float>(dot), d8, c8) : 0.0f;
+        }
+        const float send = b5 ? pr[0] : pr[1];
+        const float keep = b5 ? pr[1] : pr[0];
+        v4[i] = keep + __shfl_xor(send, 32, 64);
+        __builtin_amdgcn_sched_barrier(0);   // one row pair at a time (register pressure)
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float send = b4 ? v4[i] : v4[i + 2];
+        const float keep = b4 ? v4[i + 2] : v4[i];
+        v2[i] = keep + __shfl_xor(send, 16, 64);
+    }
+    float v = (b3 ? v2[1] : v2[0]) + __shfl_xor(b3 ? v2[0] : v2[1], 8, 64);
+    v = xor_sum(v, 4);
+    v = xor_sum(v, 2);
+    v = xor_sum(v, 1);
+    if ((lane & 7) == 0) gu[mat][(wave & 3) * 8 + rho] = v;
+    __syncthreads();
+    if (wave == 0) {
+        const int i = lane & 31;
+        int f = 0;
+        const float m = silu_mul(gu[0][i], gu[1][i], f);
+        const Q8Lane q = quantize32(m);
+        if (lane < 32) {
+            const size_t mb = (static_cast<size_t>(t) * P1 + r) * nbi + s;
+            a.mq.codes[mb * 32 + i] = static_cast<uint8_t>(q.code);
+            if (i == 0) a.mq.heads[mb] = q.head;
+            f |= i == 0 ? q.flags : 0;
+            if (f) atomicOr(a.error, f);
+        }
+    }
+}
+
+// down + fold for one token and 32 output rows; grid = (tokens, H/32), one
+// wave per rank (block = 64 * (k + shared) threads).  Wave r computes the 32
+// unweighted row sums of its pair (lane (sub, kb): rows sub + 4l, l < 8, as in
+// k_down_lean), then 32 threads fold the ranks in order and add the shared
+// expert -- the separately rounded fold of k_fold, with no contribution
+// buffer and no second kernel.
+__global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
+    __shared__ float part[kDecodeMaxPairs][32];
+    __shared__ int valid[kDecodeMaxPairs];
+    const FfnArgs &a = d.f;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int H = a.shape.H, nbi = a.shape.I / 32, k = a.shape.k;
+    const int P1 = blockDim.x >> 6;
+    // XCD-aware order (workgroup i runs on XCD i % 8): the tokens of one row
+    // slice are consecutive on one XCD, so the rows of the shared expert (and
+    // of an expert two tokens share) are fetched from HBM once per slice.
+    const int N = a.tokens, S = H / 32;
+    const int id = blockIdx.x, j = id >> 3;
+    const int t = j % N, slice = (id & 7) + 8 * (j / N);
+    if (slice >= S) return;
+    const int row0 = slice * 32, r = wave;
+    int dummy = 0;
+    const int expert = decode_route(d, t, r, dummy);
+    if (lane == 0) valid[r] = expert >= 0;
+    if (expert >= 0) {
+        const int sub = lane >> 4, kl = lane & 15;
+        const bool has = kl < nbi;
+        const int kb = has ? kl : 0;
+        const size_t mrow = static_cast<size_t>(expert) * H + row0;     // row0 % 32 == 0
+        const uint32_t row_bytes = static_cast<uint32_t>(nbi) * 16u;
+        const auto wr = buffer_rsrc(a.bank.down_codes + mrow * row_bytes, 32 * row_bytes);
+        const auto sr = buffer_rsrc(a.bank.down_scales + mrow * nbi, 4 * row_bytes);
+        const uint32_t lane_off = static_cast<uint32_t>(sub * nbi + kb) * 16u;
+        const size_t xrow = (static_cast<size_t>(t) * P1 + r) * nbi;
+        const auto xr = buffer_rsrc(a.mq.codes + xrow * 32, static_cast<uint32_t>(nbi) * 32u);
+        const auto hr = buffer_rsrc(a.mq.heads + xrow, static_cast<uint32_t>(nbi) * 4u);
+        uint4 w[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) w[l] = buffer_load16(wr, lane_off, 4 * l * row_bytes);
+        const uint4 d4p = buffer_load16(sr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
+        const uint4 x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
+        const uint4 x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
+        const uint32_t hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
+        const float d8 = h2f(hx), c8 = -8.0f * h2f(hx >> 16);
+        const bool c3 = lane & 8, c2 = lane & 4, c1 = lane & 2;
+        const int lr = (c3 ? 4 : 0) + (c2 ? 2 : 0) + (c1 ? 1 : 0);
+        float v4[4], v2[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float pr[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int l = i + 4 * h;
+                const int dot = dot_block(w[l], x0, x1);
+                const uint32_t d4 = (&d4p.x)[l >> 1] >> (16 * (l & 1));
+                pr[h] = has ? h2f(d4) * fmaf(static_cast<float>(dot), d8, c8) : 0.0f;
+            }
+            const float send = c3 ? pr[0] : pr[1];
+            const float keep = c3 ? pr[1] : pr[0];
+            v4[i] = keep + __shfl_xor(send, 8, 64);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float send = c2 ? v4[i] : v4[i + 2];
+            const float keep = c2 ? v4[i + 2] : v4[i];
+            v2[i] = keep + __shfl_xor(send, 4, 64);
+        }
+        float v = (c1 ? v2[1] : v2[0]) + __shfl_xor(c1 ? v2[0] : v2[1], 2, 64);
+        v = xor_sum(v, 1);
+        if ((lane & 1) == 0) part[r][4 * lr + sub] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 32) {
+        const int row = threadIdx.x;
+        const float *wt = d.weights + static_cast<size_t>(t) * k;
+        int flags = 0;
+        float v = 0.0f;
+        for (int q = 0; q < k; ++q) {
+            if (!valid[q]) continue;
+            float x = part[q][row];
+            float s = wt[q];
+            if (!isfinite(x)) { flags |= 1; x = 0.0f; }
+            if (!isfinite(s)) { flags |= 1; s = 0.0f; }
+            float p = s * x;
+            if (!isfinite(p)) { flags |= 2; p = 0.0f; }
+            v = v + p;
+            if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+        }
+        if (P1 > k) {
+            float x = part[k][row];
+            if (!isfinite(x)) { flags |= 1; x = 0.0f; }
+            float scale = 1.0f;
+            if (d.shared_gate) {
+                float g = d.shared_gate[t];
+                if (!isfinite(g)) { flags |= 1; g = 0.0f; }
+                scale = 1.0f / (1.0f + expf(-g));
+                if (!isfinite(scale)) { flags |= 2; scale = 0.0f; }
+            }
+            float p = scale * x;
+            if (!isfinite(p)) { flags |= 2; p = 0.0f; }
+            v = v + p;
+            if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+        }
+        d.y[static_cast<size_t>(t) * H + row0 + row] = flags ? 0.0f : v;
+        if (flags) atomicOr(a.error, flags);
+    }
+}
+
+// One thread per (pair, block, word): canonical Q8_1 block words of decode
+// row t * P1 + r written at the pair's grouped position.
+__global__ __launch_bounds__(256) void k_decode_middle_grouped(Act mq, RouteOut routes, Shape sh, int tokens,
+                                                               uint32_t *q8) {
+    const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0), nbi = sh.I / 32;
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<size_t>(tokens) * P1 * nbi * 9) return;
+    const size_t word = i % 9, blk = (i / 9) % nbi, pair = i / 9 / nbi;
+    const int t = static_cast<int>(pair / P1), r = static_cast<int>(pair % P1);
+    const int pos = r < sh.k ? routes.pos_of[static_cast<size_t>(t) * sh.k + r] : routes.offsets[sh.E] + t;
+    if (pos < 0) return;
+    const size_t src = pair * nbi + blk;
+    const uint32_t v = word == 0 ? mq.heads[src] : reinterpret_cast<const uint32_t *>(mq.codes)[src * 8 + word - 1];
+    q8[(static_cast<size_t>(pos) * nbi + blk) * 9 + word] = v;
+}
+
 // ------------------------------------------------------------------ fold ---
 // y = +0; y = y + (w_r * c_r) for r = 0..k-1 (separately rounded, rank
 // order); then y = y + scale * shared with scale = 1/(1+expf(-g)) or 1.
@@ -1145,6 +1480,31 @@ hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s) {
         else k_gate_up_lean<false><<<lgrid, 512, 0, s>>>(a);
     } else if (nbl <= 2) gate_up_stream<2>(a, dbg, grid, s);
     else gate_up_stream<0>(a, dbg, grid, s);
+    return hipGetLastError();
+}
+
+// Grids cover 8 XCD lanes x ceil(slices / 8) x the other dimensions (the
+// kernels map a linear id to (token, rank, slice) and skip slices past the end).
+hipError_t launch_decode_gate_up(const DecodeArgs &d, hipStream_t s) {
+    const Shape &sh = d.f.shape;
+    const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0);
+    const unsigned groups = static_cast<unsigned>((sh.I / 32 + 7) / 8);
+    k_decode_gate_up<<<8u * groups * P1 * d.f.tokens, 512, 0, s>>>(d);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_down_fold(const DecodeArgs &d, hipStream_t s) {
+    const Shape &sh = d.f.shape;
+    const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0);
+    const unsigned groups = static_cast<unsigned>((sh.H / 32 + 7) / 8);
+    k_decode_down_fold<<<8u * groups * d.f.tokens, 64 * P1, 0, s>>>(d);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_middle_grouped(Act mq, RouteOut routes, Shape shape, int tokens, void *q8, hipStream_t s) {
+    const int P1 = shape.k + (shape.Ep > shape.E ? 1 : 0);
+    const size_t n = static_cast<size_t>(tokens) * P1 * (shape.I / 32) * 9;
+    k_decode_middle_grouped<<<blocks_for(n, 256), 256, 0, s>>>(mq, routes, shape, tokens, static_cast<uint32_t *>(q8));
     return hipGetLastError();
 }
 

@@ -32,6 +32,8 @@ struct moe_ffn_layer {
     RouteOut routes{};
     float *contrib = nullptr;
     int mfma_min = 0;     // smallest group routed to the MFMA path (0 = streaming only)
+    int decode_mode = -1; // ungrouped decode path: -1 auto, 0 never, 1 whenever shapes allow
+    bool last_decode = false;
     int cu_count = 256;   // compute units of the device
     int last_tokens = 0;
     // Inputs of the last forward (for moe_ffn_replay_stage).
@@ -129,6 +131,7 @@ int finish_create(moe_ffn_layer *L) {
     L->contrib = reinterpret_cast<float *>(b + w.contrib);
     if (hipMemset(L->ws_mem, 0, w.total) != hipSuccess) return hipErrorOutOfMemory;
     if (const char *env = std::getenv("MOE_FFN_MFMA_MIN")) L->mfma_min = std::atoi(env);
+    if (const char *env = std::getenv("MOE_FFN_DECODE")) L->decode_mode = std::atoi(env) ? 1 : 0;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, L->device) == hipSuccess && cus > 0)
         L->cu_count = cus;
@@ -394,11 +397,29 @@ int moe_ffn_export_expert(moe_ffn_layer *L, int expert, void *host_q4) {
 }
 
 namespace {
+// The ungrouped decode path: shapes its kernels cover, and (in auto mode)
+// few enough routes per expert that re-reading an expert shared by two tokens
+// costs less than grouping (tokens * k <= E / 4).
+bool use_decode(const moe_ffn_layer *L, int tokens) {
+    const Shape &sh = L->shape;
+    const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0);
+    const bool fits = sh.H / 32 <= moe::kDecodeMaxBlocksH && sh.I / 32 <= moe::kDecodeMaxBlocksI &&
+                      P1 <= moe::kDecodeMaxPairs;
+    if (!fits || L->decode_mode == 0) return false;
+    return L->decode_mode == 1 || static_cast<long>(tokens) * sh.k * 4 <= sh.E;
+}
+
 int run_stage(moe_ffn_layer *L, int stage, const float *x, const int32_t *ids, const float *weights, int tokens,
-              const float *shared_gate, float *y, int *error, hipStream_t s) {
+              const float *shared_gate, float *y, int *error, hipStream_t s, bool decode) {
     const Shape &sh = L->shape;
     moe::FfnArgs a = base_args(L, tokens, error);
     hipError_t r = hipSuccess;
+    if (decode) {
+        const moe::DecodeArgs d{a, x, ids, weights, shared_gate, y};
+        if (stage == MOE_STAGE_GATE_UP) return moe::launch_decode_gate_up(d, s);
+        if (stage == MOE_STAGE_DOWN) return moe::launch_decode_down_fold(d, s);
+        return stage >= MOE_STAGE_PREPARE && stage <= MOE_STAGE_FOLD ? hipSuccess : kInvalid;
+    }
     switch (stage) {
     case MOE_STAGE_PREPARE:
         return moe::launch_prepare(x, ids, weights, tokens, sh, L->xq, L->routes, L->mfma_min, error, s);
@@ -428,14 +449,16 @@ int moe_ffn_forward(moe_ffn_layer *L, const float *x, const int32_t *ids, const 
         tokens < 1 || tokens > L->cfg.max_tokens || (shared_gate && !aligned(shared_gate, 4)))
         return kInvalid;
     const auto s = static_cast<hipStream_t>(stream);
+    const bool decode = use_decode(L, tokens);
     hipEvent_t *marks = nullptr;
     if (L->prof_used < L->prof_capacity) marks = L->prof_events + (L->prof_used++) * moe_ffn_layer::kStageMarks;
     if (marks && hipEventRecord(marks[0], s) != hipSuccess) return kInvalid;
     for (int stage = MOE_STAGE_PREPARE; stage <= MOE_STAGE_FOLD; ++stage) {
-        const int r = run_stage(L, stage, x, ids, weights, tokens, shared_gate, y, error, s);
+        const int r = run_stage(L, stage, x, ids, weights, tokens, shared_gate, y, error, s, decode);
         if (r != hipSuccess) return r;
         if (marks && hipEventRecord(marks[stage + 1], s) != hipSuccess) return kInvalid;
     }
+    L->last_decode = decode;
     L->last_tokens = tokens;
     L->last_x = x;
     L->last_ids = ids;
@@ -490,7 +513,7 @@ int moe_ffn_profile_read(moe_ffn_layer *L, double *stage_ms, int *forwards) {
 int moe_ffn_replay_stage(moe_ffn_layer *L, int stage, void *stream) {
     if (!L || L->last_tokens < 1 || stage < MOE_STAGE_PREPARE || stage > MOE_STAGE_FOLD) return kInvalid;
     return run_stage(L, stage, L->last_x, L->last_ids, L->last_weights, L->last_tokens, L->last_shared_gate,
-                     L->last_y, L->last_error, static_cast<hipStream_t>(stream));
+                     L->last_y, L->last_error, static_cast<hipStream_t>(stream), L->last_decode);
 }
 
 int moe_quantize_q8_1(const float *x, void *q8, int width, int columns, int *error, void *stream) {
@@ -581,7 +604,15 @@ int moe_ffn_debug_last(moe_ffn_layer *L, void *x_q8, void *middle_q8, int32_t *r
     hipError_t r = hipSuccess;
     if (x_q8 && (r = moe::launch_planes_to_canonical(L->xq, x_q8, N * (sh.H / 32), s)) != hipSuccess) return r;
     const int P = static_cast<int>(pairs_capacity(sh, N));
-    if (middle_q8 && (r = moe::launch_planes_to_canonical(L->mq, middle_q8, P * (sh.I / 32), s)) != hipSuccess)
+    if (L->last_decode) {
+        // The decode path does not group: group the same routes now (the last
+        // inputs must still be valid) and reorder its middle rows to match.
+        if ((r = moe::launch_prepare(nullptr, L->last_ids, L->last_weights, N, sh, L->xq, L->routes, L->mfma_min,
+                                     L->last_error, s)) != hipSuccess)
+            return r;
+        if (middle_q8 && (r = moe::launch_decode_middle_grouped(L->mq, L->routes, sh, N, middle_q8, s)) != hipSuccess)
+            return r;
+    } else if (middle_q8 && (r = moe::launch_planes_to_canonical(L->mq, middle_q8, P * (sh.I / 32), s)) != hipSuccess)
         return r;
     const size_t routed = static_cast<size_t>(N) * sh.k * 4;
     if (route_token &&
@@ -597,6 +628,11 @@ int moe_ffn_last_stats(moe_ffn_layer *L, int32_t *stream_items, int32_t *mfma_it
     if (!L) return kInvalid;
     int32_t c[4] = {0, 0, 0, 0};
     if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
+    if (L->last_decode && L->last_tokens > 0) {   // group the last batch's routes (not done by the decode path)
+        const hipError_t g = moe::launch_prepare(nullptr, L->last_ids, L->last_weights, L->last_tokens, L->shape,
+                                                 L->xq, L->routes, L->mfma_min, L->last_error, nullptr);
+        if (g != hipSuccess) return g;
+    }
     const hipError_t r = hipMemcpy(c, L->routes.item_counts, sizeof(c), hipMemcpyDeviceToHost);
     if (r != hipSuccess) return r;
     if (stream_items) *stream_items = c[0];

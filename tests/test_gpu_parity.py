@@ -328,3 +328,100 @@ def test_create_from_reference_tensors(moe512):
     assert np.array_equal(host(y1), host(y2))
     assert int(host(e1)[0]) == 0 and int(host(e2)[0]) == 0
     L.close()
+
+
+def _layer_with_path(decode, *args, **kw):
+    """A layer whose forward path is forced: MOE_FFN_DECODE is read at creation."""
+    old = os.environ.get("MOE_FFN_DECODE")
+    os.environ["MOE_FFN_DECODE"] = "1" if decode else "0"
+    try:
+        return moe_ffn.MoeLayer(*args, **kw)
+    finally:
+        if old is None:
+            del os.environ["MOE_FFN_DECODE"]
+        else:
+            os.environ["MOE_FFN_DECODE"] = old
+
+
+@pytest.mark.parametrize("gate", [False, True])
+def test_decode_and_grouped_paths_agree(gate):
+    """The ungrouped decode path (work per (token, rank), fold inside the down
+    kernel) and the grouped path give the same bits, including for an invalid
+    id and a duplicate id (both contribute nothing and set bit 1), and match
+    the oracle, where an invalid route equals a weight-0 route to an unused
+    expert."""
+    H, I, E, K, N = 2048, 512, 24, 6, 5
+    bank = W.q4_bank(E, seed=301)
+    shared = W.q4_bank(1, seed=302)
+    x = W.activations(N, seed=303)
+    ids, w = W.routes_uniform(N, experts=E, k=K, seed=304)
+    g = np.random.default_rng(305).standard_normal(N).astype(np.float32) if gate else None
+    ids_bad = ids.copy()
+    ids_bad[0, 0] = E + 5           # bad id (rank 0: the token's reporting workgroup)
+    ids_bad[3, 2] = ids_bad[3, 1]   # duplicate
+    outs = {}
+    for decode in (True, False):
+        L = _layer_with_path(decode, H, I, E, K, True, N, experts_q4=bank, shared_q4=shared)
+        for name, i_ in (("ok", ids), ("bad", ids_bad)):
+            y, err = L.forward(dev(x), dev(i_), dev(w), shared_gate=None if g is None else dev(g))
+            outs[(decode, name)] = (host(y), int(host(err)[0]))
+        dbg = L.debug_last(N)
+        assert np.array_equal(host(dbg["x_q8"]).reshape(-1), q8_bytes(O.quantize_q8(x)))
+        L.close()
+    for name in ("ok", "bad"):
+        (yd, ed), (yg, eg) = outs[(True, name)], outs[(False, name)]
+        assert np.array_equal(yd, yg), name
+        assert ed == eg == (0 if name == "ok" else 1), (name, ed, eg)
+    ref = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, shared_gate=g)["y"]
+    assert_close(outs[(True, "ok")][0], ref, what="decode path")
+    rid, rw = ids_bad.copy(), w.copy()
+    for t, r in ((0, 0), (3, 2)):
+        rid[t, r] = next(e for e in range(E) if e not in ids_bad[t])
+        rw[t, r] = 0.0
+    ref_bad = O.moe_layer(x, H, I, E, bank, rid, rw, shared_q4=shared, shared_gate=g)["y"]
+    assert_close(outs[(True, "bad")][0], ref_bad, what="decode path, invalid routes")
+
+
+def test_decode_path_middle_debug_view(moe512):
+    """debug_last on a decode-path forward returns the middle Q8 rows in
+    grouped order, bit-identical to the single-expert gate/up stage of the
+    same expert on the same token (same per-row arithmetic)."""
+    L = moe512["layer"]
+    x = W.activations(8, seed=311)
+    ids, w = W.routes_uniform(8, seed=312)
+    L.forward(dev(x), dev(ids), dev(w))
+    dbg = L.debug_last(8)
+    groups = O.route_groups(ids, w, 512)
+    mid = host(dbg["middle_q8"]).reshape(8 * 11, -1)
+    xq = dev(q8_bytes(O.quantize_q8(x)).reshape(8, -1))
+    for pos in (0, 17, 45, 79):
+        t, e = int(groups["token"][pos]), int(groups["expert"][pos])
+        r = L.expert_gate_up(e, xq[t:t + 1].contiguous(), 1)
+        assert np.array_equal(mid[pos], host(r["middle_q8"]).reshape(-1)), pos
+    # shared expert rows follow the routed ones, one per token
+    r = L.expert_gate_up(512, xq, 8)
+    assert np.array_equal(mid[80:], host(r["middle_q8"]).reshape(8, -1))
+
+
+def test_decode_quantizer_reference_fixture():
+    """The decode path quantizes x inside its gate/up kernel (4 lanes per
+    block); the x Q8 it writes must equal the reference quantizer's bytes on
+    the reference fixture's blocks (ties, tiny and huge scales, zero blocks),
+    with failing blocks zeroed and flagged, like the standalone quantizer."""
+    f = np.load(os.path.join(GOLDEN, "quant_q8.npz"), allow_pickle=False)
+    blocks = f["inputs"]
+    rows = -(-len(blocks) // 64)
+    x = np.zeros((rows * 64, 32), np.float32)
+    x[:len(blocks)] = blocks
+    x = x.reshape(rows, 2048)
+    bank = W.q4_bank(4, seed=321)
+    L = _layer_with_path(True, 2048, 512, 4, 1, False, rows, experts_q4=bank)
+    ids = np.zeros((rows, 1), np.int32)
+    w = np.ones((rows, 1), np.float32)
+    _, err = L.forward(dev(x), dev(ids), dev(w))
+    got = host(L.debug_last(rows)["x_q8"]).reshape(-1, 36)[:len(blocks)]
+    ok = f["status"] == 0
+    assert np.array_equal(got[ok], f["q8"][ok])
+    assert np.all(got[~ok] == 0)
+    assert int(host(err)[0]) != 0
+    L.close()
