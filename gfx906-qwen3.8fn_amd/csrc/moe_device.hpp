@@ -1,0 +1,314 @@
+// Device primitives shared by the kernel translation units (moe_kernels.hip,
+// moe_mfma.hip): fp16 conversions, the Q4_0 x Q8 block dot, the Q8_1
+// quantizers with the reference's XOR-butterfly raw sum, SiLU(g)*u with the
+// reference's sanitisation, and raw buffer loads.  gfx950 (CDNA4), wave64.
+#pragma once
+
+#include "moe_expf.h"
+#include "moe_internal.hpp"
+
+#include <hip/hip_fp16.h>
+
+#if defined(__FAST_MATH__)
+#error "moe kernels require strict IEEE fp32 (correctly rounded division for Q8 scales)"
+#endif
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "moe kernels are written for gfx950 (CDNA4)"
+#endif
+
+#pragma clang fp contract(off)
+
+namespace moe {
+namespace {
+
+// ------------------------------------------------------------ primitives ---
+__device__ __forceinline__ float h2f(uint32_t bits) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(bits & 0xffffu)));
+}
+__device__ __forceinline__ uint32_t f2h(float v) {
+    return __half_as_ushort(__float2half_rn(v));
+}
+
+// Integer block dot over one Q4_0 code chunk (16 bytes: byte j holds element j
+// in its low nibble and element j+16 in its high nibble) and 32 Q8 codes
+// (x0 = codes 0..15, x1 = codes 16..31).  Nibbles are 0..15, so v_dot4_i32_i8
+// on the masked bytes is the exact unsigned-nibble x signed-code sum.
+__device__ __forceinline__ int dot_block(uint4 w, uint4 x0, uint4 x1) {
+    constexpr uint32_t m = 0x0f0f0f0fu;
+    int s = 0;
+    s = __builtin_amdgcn_sdot4(static_cast<int>(w.x & m), static_cast<int>(x0.x), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>(w.y & m), static_cast<int>(x0.y), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>(w.z & m), static_cast<int>(x0.z), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>(w.w & m), static_cast<int>(x0.w), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((w.x >> 4) & m), static_cast<int>(x1.x), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((w.y >> 4) & m), static_cast<int>(x1.y), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((w.z >> 4) & m), static_cast<int>(x1.z), s, false);
+    s = __builtin_amdgcn_sdot4(static_cast<int>((w.w >> 4) & m), static_cast<int>(x1.w), s, false);
+    return s;
+}
+
+__device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
+
+// The two fragment dots of one block in the reference CPU/MMVQ order
+// (src/cpu_expert.cpp:156-213): fragment f covers code bytes 8f..8f+7, i.e.
+// elements 8f..8f+7 (low nibbles, codes x0) and 16+8f..16+8f+7 (high
+// nibbles, codes x1).  dot_block(w, x0, x1) is their sum.
+__device__ __forceinline__ void fragment_dots(uint4 w, uint4 x0, uint4 x1, int &f0, int &f1) {
+    constexpr uint32_t m = 0x0f0f0f0fu;
+    f0 = __builtin_amdgcn_sdot4(static_cast<int>(w.x & m), static_cast<int>(x0.x), 0, false);
+    f0 = __builtin_amdgcn_sdot4(static_cast<int>(w.y & m), static_cast<int>(x0.y), f0, false);
+    f0 = __builtin_amdgcn_sdot4(static_cast<int>((w.x >> 4) & m), static_cast<int>(x1.x), f0, false);
+    f0 = __builtin_amdgcn_sdot4(static_cast<int>((w.y >> 4) & m), static_cast<int>(x1.y), f0, false);
+    f1 = __builtin_amdgcn_sdot4(static_cast<int>(w.z & m), static_cast<int>(x0.z), 0, false);
+    f1 = __builtin_amdgcn_sdot4(static_cast<int>(w.w & m), static_cast<int>(x0.w), f1, false);
+    f1 = __builtin_amdgcn_sdot4(static_cast<int>((w.z >> 4) & m), static_cast<int>(x1.z), f1, false);
+    f1 = __builtin_amdgcn_sdot4(static_cast<int>((w.w >> 4) & m), static_cast<int>(x1.w), f1, false);
+}
+
+// fma(d4, t, +0) with d4 given as the lo / hi fp16 half of a word.
+__device__ __forceinline__ float mul_half_lo(uint32_t h2, float t) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(t));
+    return r;
+}
+__device__ __forceinline__ float mul_half_hi(uint32_t h2, float t) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(t));
+    return r;
+}
+
+// Down projection form (K = I/32 <= 16 blocks): 16 lanes per row group, lane
+// kl = block kl, eight rows per lane (row index l of w[l], scale half l of
+// d4p).  The reference's order for K <= 16 blocks (src/cpu_expert.cpp:156-213)
+// is: z = fma(d4, fma(float(I_f), d8, -4 s8), +0) per block and fragment;
+// the 128-lane fold first adds +0 (lanes k + 32 are empty), then the two
+// fragments, then the blocks pairwise in index order (XOR 1, 2, 4, 8), and
+// finally +0 again (the empty upper half).  (z0 + 0) + (z1 + 0) equals
+// (z0 + z1) + 0 for every pair of floats, so each +0 is done once.  Rows are
+// traded during the first three stages: lane l ends with the total of row
+// 4*(l & 1) + 2*(l>>1 & 1) + (l>>2 & 1); lanes l and l ^ 8 agree.
+__device__ __forceinline__ float rows8_down_exact(const uint4 (&w)[8], uint4 d4p, uint4 x0, uint4 x1, uint32_t head,
+                                                  bool has, int lane) {
+    const float d8 = h2f(head), c4 = -4.0f * h2f(head >> 16);
+    const bool c0 = lane & 1, c1 = lane & 2, c2 = lane & 4;
+    float v4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float z[2];   // rows i, i + 4
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int q = i + 4 * h;
+            int f0, f1;
+            fragment_dots(w[q], x0, x1, f0, f1);
+            const uint32_t d4w = (&d4p.x)[q >> 1];
+            const float t0 = fmaf(static_cast<float>(f0), d8, c4), t1 = fmaf(static_cast<float>(f1), d8, c4);
+            const float z0 = (q & 1) ? mul_half_hi(d4w, t0) : mul_half_lo(d4w, t0);
+            const float z1 = (q & 1) ? mul_half_hi(d4w, t1) : mul_half_lo(d4w, t1);
+            z[h] = has ? (z0 + z1) + 0.0f : 0.0f;
+        }
+        const float send = c0 ? z[0] : z[1];
+        const float keep = c0 ? z[1] : z[0];
+        v4[i] = keep + __shfl_xor(send, 1, 64);
+        __builtin_amdgcn_sched_barrier(0);   // one row pair at a time (register pressure)
+    }
+    float v2[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float send = c1 ? v4[i] : v4[i + 2];
+        const float keep = c1 ? v4[i + 2] : v4[i];
+        v2[i] = keep + __shfl_xor(send, 2, 64);
+    }
+    float v = (c2 ? v2[1] : v2[0]) + __shfl_xor(c2 ? v2[0] : v2[1], 4, 64);
+    v = xor_sum(v, 8);
+    return v + 0.0f;
+}
+
+// Eight weight rows (w[q], scales d4p: row q at half q) against one token's
+// Q8 block per lane (lane = block, H/32 <= 64), summed in the reference's
+// exact fp32 order (src/cpu_expert.cpp:156-213, the gfx906 MMVQ reduction):
+// per block and fragment z = fma(d4, fma(float(I_f), d8, -4 s8), +0); the
+// reference's 128-lane fold adds lane k' and k'+32 per fragment, then the two
+// fragments, then the blocks pairwise in index order (XOR 1, 2, 4, 8, 16).
+// Rows are traded between lanes during the first stages so every lane ends
+// with one row's total: lane l holds row 4*(l>>5 & 1) + 2*(l & 1) + (l>>1 & 1).
+// Lanes with `has` false (blocks past H) contribute +0, as the reference's
+// unused lanes do.
+__device__ __forceinline__ float rows8_exact(const uint4 (&w)[8], uint4 d4p, uint4 x0, uint4 x1, uint32_t head,
+                                             bool has, int lane) {
+    const float d8 = h2f(head), c4 = -4.0f * h2f(head >> 16);
+    const bool b5 = lane & 32, b0 = lane & 1, b1 = lane & 2;
+    float v4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float z[2][2];   // [row i / i + 4][fragment]
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int q = i + 4 * h;
+            int f0, f1;
+            fragment_dots(w[q], x0, x1, f0, f1);
+            const uint32_t d4w = (&d4p.x)[q >> 1];
+            const float t0 = fmaf(static_cast<float>(f0), d8, c4), t1 = fmaf(static_cast<float>(f1), d8, c4);
+            z[h][0] = has ? ((q & 1) ? mul_half_hi(d4w, t0) : mul_half_lo(d4w, t0)) : 0.0f;
+            z[h][1] = has ? ((q & 1) ? mul_half_hi(d4w, t1) : mul_half_lo(d4w, t1)) : 0.0f;
+        }
+        float u[2];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const float send = b5 ? z[0][f] : z[1][f];
+            const float keep = b5 ? z[1][f] : z[0][f];
+            u[f] = keep + __shfl_xor(send, 32, 64);
+        }
+        v4[i] = u[0] + u[1];
+        __builtin_amdgcn_sched_barrier(0);   // one row pair at a time (register pressure)
+    }
+    float v2[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float send = b0 ? v4[i] : v4[i + 2];
+        const float keep = b0 ? v4[i + 2] : v4[i];
+        v2[i] = keep + __shfl_xor(send, 1, 64);
+    }
+    float v = (b1 ? v2[1] : v2[0]) + __shfl_xor(b1 ? v2[0] : v2[1], 2, 64);
+    v = xor_sum(v, 4);
+    v = xor_sum(v, 8);
+    return xor_sum(v, 16);
+}
+
+// One Q8_1 block from 32 lanes (lane32 = element index).  Semantics of the
+// reference GPU quantizer (src/hip/linear.hip:121-149): a nonfinite element
+// poisons its block (bit 1), an unrepresentable scale/sum/code sets bit 2,
+// and a failing block is written as all zero.  The raw sum is the ascending
+// XOR butterfly 1,2,4,8,16 of the (sanitised) inputs -- each stage adds the
+// partner's value, so both partners hold the same sum as in the reference.
+struct Q8Lane {
+    int8_t code;
+    uint32_t head;   // half d | half s << 16 (valid in every lane)
+    int flags;       // per-block flags (valid in every lane)
+};
+
+__device__ __forceinline__ Q8Lane quantize32(float x) {
+    int bad = !isfinite(x);
+    if (bad) x = 0.0f;
+    float amax = fabsf(x);
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+        bad |= __shfl_xor(bad, m, 32);
+    }
+    float sum = x;
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) sum = sum + __shfl_xor(sum, m, 32);
+    const float d = amax / 127.0f;
+    const uint32_t hd = f2h(d), hs = f2h(sum);
+    const bool representable = isfinite(sum) && (hs & 0x7c00u) != 0x7c00u &&
+                               (hd & 0x7c00u) != 0x7c00u && (amax == 0.0f || d > 0.0f);
+    const float code = (!bad && representable && amax != 0.0f) ? roundf(x / d) : 0.0f;
+    int bad_code = !isfinite(code) || code < -127.0f || code > 127.0f;
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) bad_code |= __shfl_xor(bad_code, m, 32);
+    const bool valid = !bad && representable && !bad_code;
+    Q8Lane q;
+    q.code = valid ? static_cast<int8_t>(code) : int8_t{0};
+    q.head = (valid && amax != 0.0f) ? (hd | (hs << 16)) : 0u;
+    q.flags = (bad ? 1 : 0) | ((representable && !bad_code) ? 0 : 2);
+    return q;
+}
+
+// One Q8_1 block from P lanes (P = 2 or 4): lane l holds elements
+// (32/P) * part .. +32/P-1 of its block, part = l / (64/P); the partners are
+// lanes l ^ 32 (and l ^ 16 for P = 4).  Same bits as quantize32: max is
+// order-free, and each part's pairwise sum is an aligned subtree of the XOR
+// butterfly 1..16, whose last stages combine the parts in the same order.
+// codes[] gets the lane's 32/P codes (4 per word, element order); head and
+// flags are valid in every lane of the block.
+template<int P>
+struct Q8Part {
+    uint32_t codes[8 / P];
+    uint32_t head;
+    int flags;
+};
+
+template<int P>
+__device__ __forceinline__ Q8Part<P> quantize_part(float (&v)[32 / P]) {
+    constexpr int n = 32 / P;
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < n; ++i)
+        if (!isfinite(v[i])) { bad = 1; v[i] = 0.0f; }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < n; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    float t[n];
+#pragma unroll
+    for (int i = 0; i < n; ++i) t[i] = v[i];
+#pragma unroll
+    for (int w = n / 2; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) t[i] = t[2 * i] + t[2 * i + 1];
+    float sum = t[0];
+    if constexpr (P == 4) {
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        bad |= __shfl_xor(bad, 16, 64);
+        sum = sum + __shfl_xor(sum, 16, 64);
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    bad |= __shfl_xor(bad, 32, 64);
+    sum = sum + __shfl_xor(sum, 32, 64);   // commutative: every lane of the block agrees
+    const float d = amax / 127.0f;
+    const uint32_t hd = f2h(d), hs = f2h(sum);
+    const bool representable = isfinite(sum) && (hs & 0x7c00u) != 0x7c00u &&
+                               (hd & 0x7c00u) != 0x7c00u && (amax == 0.0f || d > 0.0f);
+    const bool quant = !bad && representable && amax != 0.0f;
+    int bad_code = 0;
+    Q8Part<P> q;
+#pragma unroll
+    for (int w = 0; w < n / 4; ++w) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const float c = quant ? roundf(v[4 * w + b] / d) : 0.0f;
+            bad_code |= !isfinite(c) || c < -127.0f || c > 127.0f;
+            word |= (static_cast<uint32_t>(static_cast<int>(c)) & 0xffu) << (8 * b);
+        }
+        q.codes[w] = word;
+    }
+    if constexpr (P == 4) bad_code |= __shfl_xor(bad_code, 16, 64);
+    bad_code |= __shfl_xor(bad_code, 32, 64);
+    const bool valid = !bad && representable && !bad_code;
+#pragma unroll
+    for (int w = 0; w < n / 4; ++w) q.codes[w] = valid ? q.codes[w] : 0u;
+    q.head = (valid && amax != 0.0f) ? (hd | (hs << 16)) : 0u;
+    q.flags = (bad ? 1 : 0) | ((representable && !bad_code) ? 0 : 2);
+    return q;
+}
+
+// SiLU(g)*u with the reference's sanitisation (src/hip/linear.hip:106-120).
+__device__ __forceinline__ float silu_mul(float g, float u, int &flags) {
+    if (!isfinite(g)) { flags |= 1; g = 0.0f; }
+    if (!isfinite(u)) { flags |= 1; u = 0.0f; }
+    float a = g / (1.0f + moe_expf(-g));
+    if (!isfinite(a)) { flags |= 2; a = 0.0f; }
+    float v = a * u;
+    if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+    return flags ? 0.0f : v;
+}
+
+// -------------------------------------------------------- buffer loads ---
+// Raw buffer loads: a uniform base in a buffer resource (SGPRs), a 32-bit
+// per-lane offset and a uniform SGPR offset.  A wave's row loads then share
+// one offset VGPR and are all issued before the first is waited for.  The
+// resource covers `bytes` from `base` (dword 3 = 32-bit data format, the gfx9
+// raw-buffer setting).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, off, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, lane_off, off, 0);
+}
+
+}  // namespace
+}  // namespace moe

@@ -1,0 +1,102 @@
+/*
+ * moe_expf.h -- single-precision exp with the bits of the host C library.
+ *
+ * The reference's CPU expert computes SiLU with the host's expf
+ * (src/cpu_expert.cpp:251, std::exp on a float) and its GPU kernels with the
+ * device expf (src/hip/linear.hip:113); it records device/host expf parity as
+ * unqualified (src/cpu_expert.hpp:73-74).  A 1-ulp difference there can move a
+ * middle value across a Q8 rounding boundary, and one changed middle code of
+ * the shared expert moves its token's output by ~1e-2 rms.  So the device
+ * evaluates expf exactly as the host library on the target image does
+ * (glibc 2.35, x86-64 FMA build), restated from the published method:
+ *
+ *   k = round(x * 32/ln2), r = x * 32/ln2 - k          (double, via 1.5*2^52 shift)
+ *   2^(k/32) = table[k % 32] with k/32 added to the exponent field
+ *   2^(r/32) ~ C2' r + 1 + (C0' r + C1') r^2           (cubic, Horner with FMAs)
+ *   result = (float)(2^(k/32) * 2^(r/32))
+ *
+ * where table[i] = bits(2^(i/32)) - (i << 47), computed here from the
+ * mathematics, and the FMA build fuses x * 32/ln2 into both the shift and the
+ * reduction.  The host build of this function (moe_expf_host) was compared
+ * with the host expf over all 2^32 inputs (0 mismatches) and is compared on a
+ * dense sample by the CPU tests; the device build performs the same IEEE
+ * double operations and is compared on the GPU (moe_expf_device).
+ */
+#ifndef MOE_EXPF_H
+#define MOE_EXPF_H
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define MOE_EXPF_FN __host__ __device__ __forceinline__
+#else
+#define MOE_EXPF_FN static inline
+#endif
+
+MOE_EXPF_FN double moe_expf_asdouble(uint64_t u) {
+    double d;
+    __builtin_memcpy(&d, &u, sizeof d);
+    return d;
+}
+MOE_EXPF_FN uint64_t moe_expf_asuint64(double d) {
+    uint64_t u;
+    __builtin_memcpy(&u, &d, sizeof u);
+    return u;
+}
+MOE_EXPF_FN uint32_t moe_expf_asuint(float f) {
+    uint32_t u;
+    __builtin_memcpy(&u, &f, sizeof u);
+    return u;
+}
+
+/* bits(2^(i/32)) - (i << 47): adding k << 47 to entry k % 32 scales by 2^(k/32). */
+MOE_EXPF_FN uint64_t moe_expf_table(int i) {
+    switch (i & 31) {
+    case 0: return 0x3ff0000000000000ull;  case 1: return 0x3fefd9b0d3158574ull;
+    case 2: return 0x3fefb5586cf9890full;  case 3: return 0x3fef9301d0125b51ull;
+    case 4: return 0x3fef72b83c7d517bull;  case 5: return 0x3fef54873168b9aaull;
+    case 6: return 0x3fef387a6e756238ull;  case 7: return 0x3fef1e9df51fdee1ull;
+    case 8: return 0x3fef06fe0a31b715ull;  case 9: return 0x3feef1a7373aa9cbull;
+    case 10: return 0x3feedea64c123422ull; case 11: return 0x3feece086061892dull;
+    case 12: return 0x3feebfdad5362a27ull; case 13: return 0x3feeb42b569d4f82ull;
+    case 14: return 0x3feeab07dd485429ull; case 15: return 0x3feea47eb03a5585ull;
+    case 16: return 0x3feea09e667f3bcdull; case 17: return 0x3fee9f75e8ec5f74ull;
+    case 18: return 0x3feea11473eb0187ull; case 19: return 0x3feea589994cce13ull;
+    case 20: return 0x3feeace5422aa0dbull; case 21: return 0x3feeb737b0cdc5e5ull;
+    case 22: return 0x3feec49182a3f090ull; case 23: return 0x3feed503b23e255dull;
+    case 24: return 0x3feee89f995ad3adull; case 25: return 0x3feeff76f2fb5e47ull;
+    case 26: return 0x3fef199bdd85529cull; case 27: return 0x3fef3720dcef9069ull;
+    case 28: return 0x3fef5818dcfba487ull; case 29: return 0x3fef7c97337b9b5full;
+    case 30: return 0x3fefa4afa2a490daull; default: return 0x3fefd0765b6e4540ull;
+    }
+}
+
+MOE_EXPF_FN float moe_expf(float x) {
+    const uint32_t abstop = (moe_expf_asuint(x) >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {                                   /* |x| >= 88 (top bits of 88.0f) */
+        if (moe_expf_asuint(x) == 0xff800000u) return 0.0f;   /* -inf */
+        if (abstop >= 0x7f8u) return x + x;                   /* +inf, nan */
+        if (x > 0x1.62e42ep6f) return __builtin_inff();       /* overflow */
+        if (x < -0x1.9fe368p6f) return 0.0f;                  /* underflow */
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    const uint64_t ki = moe_expf_asuint64(kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    const double s = moe_expf_asdouble(moe_expf_table((int)(ki & 31u)) + (ki << 47));
+    const double z = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+#endif /* MOE_EXPF_H */

@@ -148,6 +148,9 @@ hipError_t launch_decode_middle_grouped(Act mq, RouteOut routes, Shape shape, in
 
 hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s);
 hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s);
+// Int8-MFMA kernels over the MFMA items (moe_mfma.hip).
+hipError_t launch_gate_up_mfma(const FfnArgs &a, hipStream_t s);
+hipError_t launch_down_mfma(const FfnArgs &a, hipStream_t s);
 
 hipError_t launch_fold(const float *contributions, size_t token_stride, const float *weights, int k,
                        const int32_t *pos_of, const float *shared, size_t shared_stride,
@@ -155,5 +158,6 @@ hipError_t launch_fold(const float *contributions, size_t token_stride, const fl
                        hipStream_t s);
 
 hipError_t launch_fill_u32(uint32_t *p, uint32_t value, size_t count, hipStream_t s);
+hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s);
 
 }  // namespace moe

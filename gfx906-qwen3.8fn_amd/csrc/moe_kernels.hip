@@ -4,173 +4,18 @@
 //   Q8_1 quantization  src/quant.cpp:275-325, GPU form src/hip/linear.hip:99-150
 //   Q4_0 block dot     src/quant.cpp:48-55   (unsigned nibbles x signed codes)
 //   block scaling      src/quant.cpp:88-93   d4 * (I*d8 - 8*s8)
-//   SiLU(gate)*up      src/hip/linear.hip:106-120 (sanitised, device expf)
+//   SiLU(gate)*up      src/hip/linear.hip:106-120 (sanitised; expf with the host libm bits, moe_expf.h)
 //   rank-order fold    src/hip/session_ops.hip:307-324, shared add :375-391
 // The per-block int32 dots and the Q8 codes are bit-exact with the reference;
 // the fp32 accumulation order across blocks is this implementation's own.
-#include "moe_internal.hpp"
-
-#include <hip/hip_fp16.h>
+#include "moe_device.hpp"
 
 #include <algorithm>
 
-#if defined(__FAST_MATH__)
-#error "moe kernels require strict IEEE fp32 (correctly rounded division for Q8 scales)"
-#endif
-#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
-#error "moe kernels are written for gfx950 (CDNA4)"
-#endif
 #pragma clang fp contract(off)
 
 namespace moe {
 namespace {
-
-// ------------------------------------------------------------ primitives ---
-__device__ __forceinline__ float h2f(uint32_t bits) {
-    return __half2float(__ushort_as_half(static_cast<unsigned short>(bits & 0xffffu)));
-}
-__device__ __forceinline__ uint32_t f2h(float v) {
-    return __half_as_ushort(__float2half_rn(v));
-}
-
-// Integer block dot over one Q4_0 code chunk (16 bytes: byte j holds element j
-// in its low nibble and element j+16 in its high nibble) and 32 Q8 codes
-// (x0 = codes 0..15, x1 = codes 16..31).  Nibbles are 0..15, so v_dot4_i32_i8
-// on the masked bytes is the exact unsigned-nibble x signed-code sum.
-__device__ __forceinline__ int dot_block(uint4 w, uint4 x0, uint4 x1) {
-    constexpr uint32_t m = 0x0f0f0f0fu;
-    int s = 0;
-    s = __builtin_amdgcn_sdot4(static_cast<int>(w.x & m), static_cast<int>(x0.x), s, false);
-    s = __builtin_amdgcn_sdot4(static_cast<int>(w.y & m), static_cast<int>(x0.y), s, false);
-    s = __builtin_amdgcn_sdot4(static_cast<int>(w.z & m), static_cast<int>(x0.z), s, false);
-    s = __builtin_amdgcn_sdot4(static_cast<int>(w.w & m), static_cast<int>(x0.w), s, false);
-    s = __builtin_amdgcn_sdot4(static_cast<int>((w.x >> 4) & m), static_cast<int>(x1.x), s, false);
-    s = __builtin_amdgcn_sdot4(static_cast<int>((w.y >> 4) & m), static_cast<int>(x1.y), s, false);
-    s = __builtin_amdgcn_sdot4(static_cast<int>((w.z >> 4) & m), static_cast<int>(x1.z), s, false);
-    s = __builtin_amdgcn_sdot4(static_cast<int>((w.w >> 4) & m), static_cast<int>(x1.w), s, false);
-    return s;
-}
-
-__device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
-
-// One Q8_1 block from 32 lanes (lane32 = element index).  Semantics of the
-// reference GPU quantizer (src/hip/linear.hip:121-149): a nonfinite element
-// poisons its block (bit 1), an unrepresentable scale/sum/code sets bit 2,
-// and a failing block is written as all zero.  The raw sum is the ascending
-// XOR butterfly 1,2,4,8,16 of the (sanitised) inputs -- each stage adds the
-// partner's value, so both partners hold the same sum as in the reference.
-struct Q8Lane {
-    int8_t code;
-    uint32_t head;   // half d | half s << 16 (valid in every lane)
-    int flags;       // per-block flags (valid in every lane)
-};
-
-__device__ __forceinline__ Q8Lane quantize32(float x) {
-    int bad = !isfinite(x);
-    if (bad) x = 0.0f;
-    float amax = fabsf(x);
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-        bad |= __shfl_xor(bad, m, 32);
-    }
-    float sum = x;
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) sum = sum + __shfl_xor(sum, m, 32);
-    const float d = amax / 127.0f;
-    const uint32_t hd = f2h(d), hs = f2h(sum);
-    const bool representable = isfinite(sum) && (hs & 0x7c00u) != 0x7c00u &&
-                               (hd & 0x7c00u) != 0x7c00u && (amax == 0.0f || d > 0.0f);
-    const float code = (!bad && representable && amax != 0.0f) ? roundf(x / d) : 0.0f;
-    int bad_code = !isfinite(code) || code < -127.0f || code > 127.0f;
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) bad_code |= __shfl_xor(bad_code, m, 32);
-    const bool valid = !bad && representable && !bad_code;
-    Q8Lane q;
-    q.code = valid ? static_cast<int8_t>(code) : int8_t{0};
-    q.head = (valid && amax != 0.0f) ? (hd | (hs << 16)) : 0u;
-    q.flags = (bad ? 1 : 0) | ((representable && !bad_code) ? 0 : 2);
-    return q;
-}
-
-// One Q8_1 block from P lanes (P = 2 or 4): lane l holds elements
-// (32/P) * part .. +32/P-1 of its block, part = l / (64/P); the partners are
-// lanes l ^ 32 (and l ^ 16 for P = 4).  Same bits as quantize32: max is
-// order-free, and each part's pairwise sum is an aligned subtree of the XOR
-// butterfly 1..16, whose last stages combine the parts in the same order.
-// codes[] gets the lane's 32/P codes (4 per word, element order); head and
-// flags are valid in every lane of the block.
-template<int P>
-struct Q8Part {
-    uint32_t codes[8 / P];
-    uint32_t head;
-    int flags;
-};
-
-template<int P>
-__device__ __forceinline__ Q8Part<P> quantize_part(float (&v)[32 / P]) {
-    constexpr int n = 32 / P;
-    int bad = 0;
-#pragma unroll
-    for (int i = 0; i < n; ++i)
-        if (!isfinite(v[i])) { bad = 1; v[i] = 0.0f; }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < n; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    float t[n];
-#pragma unroll
-    for (int i = 0; i < n; ++i) t[i] = v[i];
-#pragma unroll
-    for (int w = n / 2; w >= 1; w >>= 1)
-#pragma unroll
-        for (int i = 0; i < w; ++i) t[i] = t[2 * i] + t[2 * i + 1];
-    float sum = t[0];
-    if constexpr (P == 4) {
-        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-        bad |= __shfl_xor(bad, 16, 64);
-        sum = sum + __shfl_xor(sum, 16, 64);
-    }
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    bad |= __shfl_xor(bad, 32, 64);
-    sum = sum + __shfl_xor(sum, 32, 64);   // commutative: every lane of the block agrees
-    const float d = amax / 127.0f;
-    const uint32_t hd = f2h(d), hs = f2h(sum);
-    const bool representable = isfinite(sum) && (hs & 0x7c00u) != 0x7c00u &&
-                               (hd & 0x7c00u) != 0x7c00u && (amax == 0.0f || d > 0.0f);
-    const bool quant = !bad && representable && amax != 0.0f;
-    int bad_code = 0;
-    Q8Part<P> q;
-#pragma unroll
-    for (int w = 0; w < n / 4; ++w) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const float c = quant ? roundf(v[4 * w + b] / d) : 0.0f;
-            bad_code |= !isfinite(c) || c < -127.0f || c > 127.0f;
-            word |= (static_cast<uint32_t>(static_cast<int>(c)) & 0xffu) << (8 * b);
-        }
-        q.codes[w] = word;
-    }
-    if constexpr (P == 4) bad_code |= __shfl_xor(bad_code, 16, 64);
-    bad_code |= __shfl_xor(bad_code, 32, 64);
-    const bool valid = !bad && representable && !bad_code;
-#pragma unroll
-    for (int w = 0; w < n / 4; ++w) q.codes[w] = valid ? q.codes[w] : 0u;
-    q.head = (valid && amax != 0.0f) ? (hd | (hs << 16)) : 0u;
-    q.flags = (bad ? 1 : 0) | ((representable && !bad_code) ? 0 : 2);
-    return q;
-}
-
-// SiLU(g)*u with the reference's sanitisation (src/hip/linear.hip:106-120).
-__device__ __forceinline__ float silu_mul(float g, float u, int &flags) {
-    if (!isfinite(g)) { flags |= 1; g = 0.0f; }
-    if (!isfinite(u)) { flags |= 1; u = 0.0f; }
-    float a = g / (1.0f + expf(-g));
-    if (!isfinite(a)) { flags |= 2; a = 0.0f; }
-    float v = a * u;
-    if (!isfinite(v)) { flags |= 2; v = 0.0f; }
-    return flags ? 0.0f : v;
-}
 
 // ------------------------------------------------------------ quantizers ---
 // One thread per element; 32-lane groups are whole Q8 blocks.
@@ -270,26 +115,14 @@ __global__ __launch_bounds__(256) void k_synthetic(uint32_t *codes, uint16_t *sc
     scales[scale_index(b / nb, static_cast<int>(b % nb), nb, group)] = static_cast<uint16_t>(f2h(fabsf(z) * 0.02f));
 }
 
+__global__ __launch_bounds__(256) void k_expf(const float *x, float *y, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = moe_expf(x[i]);
+}
+
 __global__ __launch_bounds__(256) void k_fill_u32(uint32_t *p, uint32_t v, size_t n) {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
-}
-
-// -------------------------------------------------------- buffer loads ---
-// Raw buffer loads: a uniform base in a buffer resource (SGPRs), a 32-bit
-// per-lane offset and a uniform SGPR offset.  A wave's row loads then share
-// one offset VGPR and are all issued before the first is waited for.  The
-// resource covers `bytes` from `base` (dword 3 = 32-bit data format, the gfx9
-// raw-buffer setting).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), 0x00020000);
-}
-__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, uint32_t off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, off, 0);
-    return make_uint4(v[0], v[1], v[2], v[3]);
-}
-__device__ __forceinline__ uint32_t buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, lane_off, off, 0);
 }
 
 // ------------------------------------------------------------- grouping ----
@@ -782,8 +615,7 @@ __global__ __launch_bounds__(512, 8) void k_gate_up_lean(FfnArgs a) {
     const auto wr = buffer_rsrc((mat ? a.bank.up_codes : a.bank.gate_codes) + mrow * row_bytes, 8 * row_bytes);
     const auto sr = buffer_rsrc((mat ? a.bank.up_scales : a.bank.gate_scales) + mrow * nbh, row_bytes);
     const uint32_t lane_off = static_cast<uint32_t>(kb) * 16u;
-    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
-    const int rho = (b5 ? 4 : 0) + (b4 ? 2 : 0) + (b3 ? 1 : 0);
+    const int rho = 4 * ((lane >> 5) & 1) + 2 * (lane & 1) + ((lane >> 1) & 1);   // row rows8_exact leaves in this lane
     // Weights are loaded per token together with that token's activations:
     // the first token streams them from HBM, further tokens of the item hit
     // L2.  Nothing but the token ids stays live across iterations.
@@ -800,42 +632,15 @@ __global__ __launch_bounds__(512, 8) void k_gate_up_lean(FfnArgs a) {
         const uint4 x0 = buffer_load16(xr, 2 * lane_off, 0);
         const uint4 x1 = buffer_load16(xr, 2 * lane_off, 16);
         const uint32_t hx = buffer_load4(hr, lane_off / 4, 0);
-        const float d8 = h2f(hx), c8 = -8.0f * h2f(hx >> 16);
-        // Rows i and i+4 are computed together and folded at once (xor 32),
-        // so at most 4 partial sums are live.
-        float v4[4], v2[2];
+        if constexpr (Dbg) {
+            int32_t *dots = mat ? a.up_dots : a.gate_dots;
+            if (dots && has)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float pr[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int r = i + 4 * h;
-                const int dot = dot_block(w[r], x0, x1);
-                if constexpr (Dbg) {
-                    int32_t *dots = mat ? a.up_dots : a.gate_dots;
-                    if (dots && has) dots[(static_cast<size_t>(first + j) * I + row0 + r) * nbh + lane] = dot;
-                }
-                const uint32_t d4 = (&d4p.x)[r >> 1] >> (16 * (r & 1));
-                pr[h] = has ? h2f(d4) * fmaf(static_cast<float>(dot), d8, c8) : 0.0f;
-            }
-            const float send = b5 ? pr[0] : pr[1];
-            const float keep = b5 ? pr[1] : pr[0];
-            v4[i] = keep + __shfl_xor(send, 32, 64);
-            // One row pair at a time: without this fence the scheduler starts
-            // every row's nibble unpack as soon as its load lands and spills.
-            __builtin_amdgcn_sched_barrier(0);
+                for (int r = 0; r < 8; ++r)
+                    dots[(static_cast<size_t>(first + j) * I + row0 + r) * nbh + lane] = dot_block(w[r], x0, x1);
         }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float send = b4 ? v4[i] : v4[i + 2];
-            const float keep = b4 ? v4[i + 2] : v4[i];
-            v2[i] = keep + __shfl_xor(send, 16, 64);
-        }
-        float v = (b3 ? v2[1] : v2[0]) + __shfl_xor(b3 ? v2[0] : v2[1], 8, 64);
-        v = xor_sum(v, 4);
-        v = xor_sum(v, 2);
-        v = xor_sum(v, 1);
-        if ((lane & 7) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
+        const float v = rows8_exact(w, d4p, x0, x1, hx, has, lane);
+        if ((lane & 28) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
     }
     __syncthreads();
     if (wave < ncols) {
@@ -961,8 +766,7 @@ __global__ __launch_bounds__(128, NBI ? 8 : 7) void k_down_lean(FfnArgs a) {
     const uint32_t lane_off = static_cast<uint32_t>(sub * nbi + kb) * 16u;
     // Transposing reduction over the 16 lanes of a row: xor 8/4/2 halve the
     // 8 load-rows, xor 1 finishes; lane ends with load-row lr(lane).
-    const bool c3 = lane & 8, c2 = lane & 4, c1 = lane & 2;
-    const int lr = (c3 ? 4 : 0) + (c2 ? 2 : 0) + (c1 ? 1 : 0);
+    const int lr = 4 * (lane & 1) + 2 * ((lane >> 1) & 1) + ((lane >> 2) & 1);   // row rows8_down_exact leaves here
     // Weights are loaded per pair together with its middle activations (the
     // first pair streams them from HBM, further pairs hit L2).
 #pragma unroll 1
@@ -978,36 +782,14 @@ __global__ __launch_bounds__(128, NBI ? 8 : 7) void k_down_lean(FfnArgs a) {
         const uint4 x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
         const uint4 x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
         const uint32_t hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
-        const float d8 = h2f(hx), c8 = -8.0f * h2f(hx >> 16);
-        float v4[4], v2[2];
+        if constexpr (Dbg) {
+            if (a.down_dots && has)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float pr[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int l = i + 4 * h;
-                const int dot = dot_block(w[l], x0, x1);
-                if constexpr (Dbg) {
-                    if (a.down_dots && has)
-                        a.down_dots[(static_cast<size_t>(pair) * H + row0 + 4 * l + sub) * nbi + kl] = dot;
-                }
-                const uint32_t d4 = (&d4p.x)[l >> 1] >> (16 * (l & 1));
-                pr[h] = has ? h2f(d4) * fmaf(static_cast<float>(dot), d8, c8) : 0.0f;
-            }
-            const float send = c3 ? pr[0] : pr[1];
-            const float keep = c3 ? pr[1] : pr[0];
-            v4[i] = keep + __shfl_xor(send, 8, 64);
-            __builtin_amdgcn_sched_barrier(0);   // one row pair at a time (register pressure)
+                for (int l = 0; l < 8; ++l)
+                    a.down_dots[(static_cast<size_t>(pair) * H + row0 + 4 * l + sub) * nbi + kl] = dot_block(w[l], x0, x1);
         }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float send = c2 ? v4[i] : v4[i + 2];
-            const float keep = c2 ? v4[i + 2] : v4[i];
-            v2[i] = keep + __shfl_xor(send, 4, 64);
-        }
-        float v = (c1 ? v2[1] : v2[0]) + __shfl_xor(c1 ? v2[0] : v2[1], 2, 64);
-        v = xor_sum(v, 1);
-        if ((lane & 1) == 0) {
+        const float v = rows8_down_exact(w, d4p, x0, x1, hx, has, lane);
+        if ((lane & 8) == 0) {
             const int t = j == 0 ? tok.x : j == 1 ? tok.y : j == 2 ? tok.z : tok.w;
             const int rk = j == 0 ? rnk.x : j == 1 ? rnk.y : j == 2 ? rnk.z : rnk.w;
             const size_t orow = static_cast<size_t>(t) * a.out_stride_k + rk;
@@ -1111,37 +893,9 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
     __syncthreads();
     const uint4 x0 = reinterpret_cast<const uint4 *>(xs)[kb * 2];
     const uint4 x1 = reinterpret_cast<const uint4 *>(xs)[kb * 2 + 1];
-    const uint32_t hx = xh[kb];
-    const float d8 = h2f(hx), c8 = -8.0f * h2f(hx >> 16);
-    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
-    const int rho = (b5 ? 4 : 0) + (b4 ? 2 : 0) + (b3 ? 1 : 0);
-    float v4[4], v2[2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float pr[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int q = i + 4 * h;
-            const int dot = dot_block(w[q], x0, x1);
-            const uint32_t d4 = (&d4p.x)[q >> 1] >> (16 * (q & 1));
-            pr[h] = has ? h2f(d4) * fmaf(static_cast<float>(dot), d8, c8) : 0.0f;
-        }
-        const float send = b5 ? pr[0] : pr[1];
-        const float keep = b5 ? pr[1] : pr[0];
-        v4[i] = keep + __shfl_xor(send, 32, 64);
-        __builtin_amdgcn_sched_barrier(0);   // one row pair at a time (register pressure)
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const float send = b4 ? v4[i] : v4[i + 2];
-        const float keep = b4 ? v4[i + 2] : v4[i];
-        v2[i] = keep + __shfl_xor(send, 16, 64);
-    }
-    float v = (b3 ? v2[1] : v2[0]) + __shfl_xor(b3 ? v2[0] : v2[1], 8, 64);
-    v = xor_sum(v, 4);
-    v = xor_sum(v, 2);
-    v = xor_sum(v, 1);
-    if ((lane & 7) == 0) gu[mat][(wave & 3) * 8 + rho] = v;
+    const float v = rows8_exact(w, d4p, x0, x1, xh[kb], has, lane);
+    const int rho = 4 * ((lane >> 5) & 1) + 2 * (lane & 1) + ((lane >> 1) & 1);
+    if ((lane & 28) == 0) gu[mat][(wave & 3) * 8 + rho] = v;
     __syncthreads();
     if (wave == 0) {
         const int i = lane & 31;
@@ -1201,34 +955,9 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
         const uint4 x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
         const uint4 x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
         const uint32_t hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
-        const float d8 = h2f(hx), c8 = -8.0f * h2f(hx >> 16);
-        const bool c3 = lane & 8, c2 = lane & 4, c1 = lane & 2;
-        const int lr = (c3 ? 4 : 0) + (c2 ? 2 : 0) + (c1 ? 1 : 0);
-        float v4[4], v2[2];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float pr[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int l = i + 4 * h;
-                const int dot = dot_block(w[l], x0, x1);
-                const uint32_t d4 = (&d4p.x)[l >> 1] >> (16 * (l & 1));
-                pr[h] = has ? h2f(d4) * fmaf(static_cast<float>(dot), d8, c8) : 0.0f;
-            }
-            const float send = c3 ? pr[0] : pr[1];
-            const float keep = c3 ? pr[1] : pr[0];
-            v4[i] = keep + __shfl_xor(send, 8, 64);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float send = c2 ? v4[i] : v4[i + 2];
-            const float keep = c2 ? v4[i + 2] : v4[i];
-            v2[i] = keep + __shfl_xor(send, 4, 64);
-        }
-        float v = (c1 ? v2[1] : v2[0]) + __shfl_xor(c1 ? v2[0] : v2[1], 2, 64);
-        v = xor_sum(v, 1);
-        if ((lane & 1) == 0) part[r][4 * lr + sub] = v;
+        const float v = rows8_down_exact(w, d4p, x0, x1, hx, has, lane);
+        const int lr = 4 * (lane & 1) + 2 * ((lane >> 1) & 1) + ((lane >> 2) & 1);
+        if ((lane & 8) == 0) part[r][4 * lr + sub] = v;
     }
     __syncthreads();
     if (threadIdx.x < 32) {
@@ -1254,7 +983,7 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
             if (d.shared_gate) {
                 float g = d.shared_gate[t];
                 if (!isfinite(g)) { flags |= 1; g = 0.0f; }
-                scale = 1.0f / (1.0f + expf(-g));
+                scale = 1.0f / (1.0f + moe_expf(-g));
                 if (!isfinite(scale)) { flags |= 2; scale = 0.0f; }
             }
             float p = scale * x;
@@ -1285,7 +1014,7 @@ __global__ __launch_bounds__(256) void k_decode_middle_grouped(Act mq, RouteOut 
 
 // ------------------------------------------------------------------ fold ---
 // y = +0; y = y + (w_r * c_r) for r = 0..k-1 (separately rounded, rank
-// order); then y = y + scale * shared with scale = 1/(1+expf(-g)) or 1.
+// order); then y = y + scale * shared with scale = 1/(1+expf(-g)) or 1 (moe_expf).
 // Nonfinite operands set bit 1, nonfinite results bit 2, and zero the output
 // element (src/hip/session_ops.hip:307-324, 375-391).  Pairs that could not
 // be grouped (pos_of < 0: bad id / duplicate, already flagged) contribute 0.
@@ -1332,7 +1061,7 @@ __global__ __launch_bounds__(256) void k_fold(const float *__restrict__ c, size_
         if (shared_gate) {
             float g = shared_gate[t];
             if (!isfinite(g)) { flags |= 1; g = 0.0f; }
-            scale = 1.0f / (1.0f + expf(-g));
+            scale = 1.0f / (1.0f + moe_expf(-g));
             if (!isfinite(scale)) { flags |= 2; scale = 0.0f; }
         }
         float p = scale * x;
@@ -1397,6 +1126,11 @@ hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, size_t blo
                                     int blocks_per_row, int group, uint64_t seed, hipStream_t s) {
     k_synthetic<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<uint32_t *>(codes), scales, blocks,
                                                          hash0, blocks_per_row, group, seed);
+    return hipGetLastError();
+}
+
+hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s) {
+    k_expf<<<blocks_for(static_cast<size_t>(n), 256), 256, 0, s>>>(x, y, n);
     return hipGetLastError();
 }
 
@@ -1469,7 +1203,7 @@ void gate_up_stream(const FfnArgs &a, bool dbg, unsigned grid, hipStream_t s) {
 }
 
 hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s) {
-    if (mfma) return hipErrorNotSupported;
+    if (mfma) return launch_gate_up_mfma(a, s);
     const bool dbg = a.middle_f32 || a.gate_dots || a.up_dots;
     const unsigned grid = stream_grid(a, a.shape.I / 32);
     const int nbl = (a.shape.H / 32 + 63) / 64;
@@ -1509,7 +1243,7 @@ hipError_t launch_decode_middle_grouped(Act mq, RouteOut routes, Shape shape, in
 }
 
 hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
-    if (mfma) return hipErrorNotSupported;
+    if (mfma) return launch_down_mfma(a, s);
     const int nbi = a.shape.I / 32;
     const unsigned grid = stream_grid(a, a.shape.H / 64);
     const bool dbg = a.down_dots != nullptr;

@@ -4,6 +4,7 @@
 // src/hip/session_ops.cuh:22-45): every argument is checked before the first
 // HIP call, launchers only enqueue on the caller's stream, and only create /
 // destroy / export allocate or synchronise.
+#include "moe_expf.h"
 #include "moe_ffn.h"
 #include "moe_internal.hpp"
 
@@ -31,7 +32,7 @@ struct moe_ffn_layer {
     Act xq{}, mq{};
     RouteOut routes{};
     float *contrib = nullptr;
-    int mfma_min = 0;     // smallest group routed to the MFMA path (0 = streaming only)
+    int mfma_min = 1;     // smallest group routed to the MFMA path (0 = streaming only)
     int decode_mode = -1; // ungrouped decode path: -1 auto, 0 never, 1 whenever shapes allow
     bool last_decode = false;
     int cu_count = 256;   // compute units of the device
@@ -50,7 +51,6 @@ struct moe_ffn_layer {
 namespace {
 
 constexpr int kInvalid = hipErrorInvalidValue;
-constexpr int kNotSupported = hipErrorNotSupported;
 
 bool aligned(const void *p, size_t a) { return p && reinterpret_cast<uintptr_t>(p) % a == 0; }
 
@@ -423,12 +423,14 @@ int run_stage(moe_ffn_layer *L, int stage, const float *x, const int32_t *ids, c
     switch (stage) {
     case MOE_STAGE_PREPARE:
         return moe::launch_prepare(x, ids, weights, tokens, sh, L->xq, L->routes, L->mfma_min, error, s);
+    // With mfma_min == 1 every nonempty group is an MFMA item and the
+    // streaming launch would only start empty workgroups.
     case MOE_STAGE_GATE_UP:
-        if ((r = moe::launch_gate_up(a, false, s)) != hipSuccess) return r;
+        if (L->mfma_min != 1 && (r = moe::launch_gate_up(a, false, s)) != hipSuccess) return r;
         if (L->mfma_min > 0) r = moe::launch_gate_up(a, true, s);
         return r;
     case MOE_STAGE_DOWN:
-        if ((r = moe::launch_down(a, false, s)) != hipSuccess) return r;
+        if (L->mfma_min != 1 && (r = moe::launch_down(a, false, s)) != hipSuccess) return r;
         if (L->mfma_min > 0) r = moe::launch_down(a, true, s);
         return r;
     case MOE_STAGE_FOLD: {
@@ -549,18 +551,18 @@ int moe_ffn_expert_gate_up(moe_ffn_layer *L, int expert, const void *x_q8, int c
         !aligned(error, 4) || columns < 1 || columns > L->cfg.max_tokens || (middle && !aligned(middle, 4)) ||
         (gate_dots && !aligned(gate_dots, 4)) || (up_dots && !aligned(up_dots, 4)) || path < 0 || path > 2)
         return kInvalid;
-    if (path == MOE_PATH_MFMA) return kNotSupported;
+    const bool mfma = path != MOE_PATH_STREAM;
     const auto s = static_cast<hipStream_t>(stream);
     const Shape &sh = L->shape;
     hipError_t r = moe::launch_canonical_to_planes(x_q8, L->xq, columns * (sh.H / 32), s);
     if (r != hipSuccess) return r;
-    if ((r = moe::launch_single_expert_items(sh, L->routes, expert, columns, 0, s)) != hipSuccess) return r;
+    if ((r = moe::launch_single_expert_items(sh, L->routes, expert, columns, mfma, s)) != hipSuccess) return r;
     moe::FfnArgs a = base_args(L, columns, error);
     a.pairs_bound = columns;
     a.middle_f32 = middle;
     a.gate_dots = gate_dots;
     a.up_dots = up_dots;
-    if ((r = moe::launch_gate_up(a, false, s)) != hipSuccess) return r;
+    if ((r = moe::launch_gate_up(a, mfma, s)) != hipSuccess) return r;
     return moe::launch_planes_to_canonical(L->mq, middle_q8, columns * (sh.I / 32), s);
 }
 
@@ -570,18 +572,19 @@ int moe_ffn_expert_down(moe_ffn_layer *L, int expert, const void *middle_q8, int
         !aligned(error, 4) || columns < 1 || columns > L->cfg.max_tokens || (down_dots && !aligned(down_dots, 4)) ||
         path < 0 || path > 2)
         return kInvalid;
-    if (path == MOE_PATH_MFMA) return kNotSupported;
+    const bool mfma = path != MOE_PATH_STREAM;
+    if (mfma && !aligned(y, 16)) return kInvalid;   // the MFMA down kernel stores float4 rows
     const auto s = static_cast<hipStream_t>(stream);
     const Shape &sh = L->shape;
     hipError_t r = moe::launch_canonical_to_planes(middle_q8, L->mq, columns * (sh.I / 32), s);
     if (r != hipSuccess) return r;
-    if ((r = moe::launch_single_expert_items(sh, L->routes, expert, columns, 0, s)) != hipSuccess) return r;
+    if ((r = moe::launch_single_expert_items(sh, L->routes, expert, columns, mfma, s)) != hipSuccess) return r;
     moe::FfnArgs a = base_args(L, columns, error);
     a.pairs_bound = columns;
     a.out = y;
     a.out_stride_k = 1;
     a.down_dots = down_dots;
-    return moe::launch_down(a, false, s);
+    return moe::launch_down(a, mfma, s);
 }
 
 int moe_combine(const float *contributions, const float *weights, const float *shared, const float *shared_gate,
@@ -638,6 +641,17 @@ int moe_ffn_last_stats(moe_ffn_layer *L, int32_t *stream_items, int32_t *mfma_it
     if (stream_items) *stream_items = c[0];
     if (mfma_items) *mfma_items = c[1];
     if (active_experts) *active_experts = c[2];
+    return hipSuccess;
+}
+
+int moe_expf_device(const float *x, float *y, int n, void *stream) {
+    if (!aligned(x, 4) || !aligned(y, 4) || n < 1) return kInvalid;
+    return moe::launch_expf(x, y, n, static_cast<hipStream_t>(stream));
+}
+
+int moe_expf_host(const float *x, float *y, size_t n) {
+    if (!x || !y) return kInvalid;
+    for (size_t i = 0; i < n; ++i) y[i] = moe_expf(x[i]);
     return hipSuccess;
 }
 

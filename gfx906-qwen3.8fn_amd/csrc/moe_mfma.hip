@@ -1,0 +1,591 @@
+// Int8-MFMA grouped expert projections for prefill-width groups (gfx950).
+//
+// Replaces the reference's MMQ path (src/hip/mmq.hip:139-381, mmq<Q4_0,J>) and
+// the Session's MMVQ expert projections for wide groups
+// (src/hip/linear.hip:156-490), with the same arithmetic contract:
+//   per-block int32 dot  I = sum (qs&15)*c[i] + (qs>>4)*c[i+16]  src/quant.cpp:48-55
+//   block value          d4 * (I*d8 - 8*s8)                       src/quant.cpp:88-93
+//   SiLU(g)*u + Q8_1     src/hip/linear.hip:99-150, :509-525
+//
+// One v_mfma_i32_32x32x32_i8 is one Q4_0 block (K = 32) of a 32-row x
+// 32-token tile, so its int32 results are exactly the reference's per-block
+// dots.  The per-block scaling cannot be chained through the MFMA, so every
+// result needs a vector epilogue; it is kept to two VALU instructions:
+//   * the MFMA accumulates onto the constant 0x4B400000 (1.5 * 2^23), so the
+//     result bits read as the float F = 12582912 + I exactly (|I| <= 61440);
+//   * t = fma(F, d8, -12582912*d8) = round(I*d8)  (12582912*d8 is exact: d8 is
+//     an fp16 value, 3*2^22 times it needs at most 13 significand bits);
+//   * acc = fma(d4, t, acc) with d4 taken straight from its fp16 plane
+//     (v_fma_mix_f32).
+// The -8*d4*s8 terms form a [rows x blocks] x [blocks x tokens] product of
+// fp16 values; one v_mfma_f32_32x32x16_f16 covers 16 blocks of it (fp16
+// products are exact in fp32), and it seeds the accumulators.
+//
+// Work unit = (MFMA item of <= 128 grouped pairs of one expert, row slice).
+// Units are ordered item-major, and XCD x (workgroups x, x+8, ...) walks the
+// x-th contiguous eighth of them, so items of one expert (which read the same
+// weight rows) share an XCD's L2.
+#include "moe_device.hpp"
+
+#include <algorithm>
+
+#pragma clang fp contract(off)
+
+namespace moe {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+constexpr int kSub = 32;                   // tokens per MFMA tile (N)
+constexpr int kSubs = kMfmaTile / kSub;    // tiles per item
+constexpr int kMagic = 0x4B400000;         // bits of 12582912.0f
+constexpr float kMagicF = 12582912.0f;
+constexpr uint32_t kNibbles = 0x0f0f0f0fu;
+
+struct Unit {
+    int item, slice;
+    bool ok;
+};
+
+// blockIdx -> (item, slice) with the XCD-contiguous order described above.
+__device__ __forceinline__ Unit mfma_unit(int count, int slices) {
+    const int units = count * slices;
+    const int per = (units + 7) >> 3;
+    const int n = static_cast<int>(blockIdx.x >> 3);
+    const int u = static_cast<int>(blockIdx.x & 7) * per + n;
+    Unit r;
+    r.ok = n < per && u < units;
+    r.item = r.ok ? u / slices : 0;
+    r.slice = r.ok ? u % slices : 0;
+    return r;
+}
+
+__device__ __forceinline__ float half_lo(uint32_t w) { return h2f(w); }
+__device__ __forceinline__ float half_hi(uint32_t w) { return h2f(w >> 16); }
+
+// 8 fp16 values as an MFMA operand.
+__device__ __forceinline__ v8h pack8(const uint32_t (&w)[4]) {
+    v4i v = {static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]), static_cast<int>(w[3])};
+    return __builtin_bit_cast(v8h, v);
+}
+
+// The fp16 hi halves (s of a Q8_1 head) of 8 heads, zero for blocks >= nb.
+__device__ __forceinline__ v8h head_sums(uint4 h0, uint4 h1, int kb0, int nb) {
+    const uint32_t hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = kb0 + 2 * e < nb ? hv[2 * e] >> 16 : 0u;
+        const uint32_t hi = kb0 + 2 * e + 1 < nb ? hv[2 * e + 1] & 0xffff0000u : 0u;
+        w[e] = lo | hi;
+    }
+    return pack8(w);
+}
+
+// acc[v] += d4[v] * round(I[v] * d8) for one MFMA result (see the file comment).
+__device__ __forceinline__ void scale_block(float (&acc)[16], v16i r, uint32_t head, const uint32_t (&d4)[8]) {
+    const v16f f = __builtin_bit_cast(v16f, r);
+    const float d8 = half_lo(head);
+    const float nk = -kMagicF * d8;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const float t = fmaf(f[v], d8, nk);
+        const float s = (v & 1) ? half_hi(d4[v >> 1]) : half_lo(d4[v >> 1]);
+        acc[v] = fmaf(s, t, acc[v]);
+    }
+}
+
+// What one wave needs to project its 32 weight rows against up to kSubs
+// token tiles.  Offsets are per lane; per-block steps are uniform.
+struct TileArgs {
+    __amdgpu_buffer_rsrc_t wr, sr, xr, hr;   // weight codes, weight scales, activation codes, activation heads
+    uint32_t w_off;                          // lane's A row (block b at + 16 b)
+    uint32_t s_off0, s_off1, s_step;         // lane's two 16-byte scale groups (block b at + b s_step)
+    uint32_t x_off[kSubs], h_off[kSubs];     // lane's token rows (block b at + 32 b / + 4 b)
+    const uint16_t *cscale;                  // lane's A-row scale of block kb at cscale[kb * cstride]
+    int cstride;
+    int nb;                                  // blocks per row (K / 32)
+    int shift;                               // 0: low nibbles (lane half 0), 4: high nibbles
+    int32_t *dots;                           // debug: per-block dots [pair][rows][nb] or null
+    size_t dot_rows;                         // rows per pair in `dots`
+    int dot_row0, dot_pair0, ncols, m, h;
+};
+
+// Debug-dot row of accumulator register v in lane half h.
+template<bool Down>
+__device__ __forceinline__ int acc_row(int v, int h) {
+    return Down ? 4 * (v & 7) + 2 * h + (v >> 3) : 16 * h + v;
+}
+
+struct Loads {
+    uint4 w, d0, d1;
+    uint4 x[kSubs];
+    uint32_t hd[kSubs];
+};
+
+template<int NS>
+__device__ __forceinline__ Loads tile_loads(const TileArgs &t, int b) {
+    Loads l;
+    const uint32_t ub = static_cast<uint32_t>(b);
+    l.w = buffer_load16(t.wr, t.w_off, ub * 16u);
+    l.d0 = buffer_load16(t.sr, t.s_off0, ub * t.s_step);
+    l.d1 = buffer_load16(t.sr, t.s_off1, ub * t.s_step);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        l.x[s] = buffer_load16(t.xr, t.x_off[s], ub * 32u);
+        l.hd[s] = buffer_load4(t.hr, t.h_off[s], ub * 4u);
+    }
+    return l;
+}
+
+// acc[s] = -8 * sum_b d4 s8 + sum_b d4 round(I d8) for the NS token tiles.
+// The loads of block b + 1 are issued before block b is computed.
+template<int NS, bool Dbg, bool Down>
+__device__ __forceinline__ void tile_project(const TileArgs &t, float (&acc)[kSubs][16]) {
+    v16f corr[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) corr[s] = v16f{};
+    for (int c = 0; c < t.nb; c += 16) {
+        const int kb0 = c + 8 * t.h;
+        uint32_t dw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int k0 = kb0 + 2 * e, k1 = k0 + 1;
+            const uint32_t lo = t.cscale[std::min(k0, t.nb - 1) * t.cstride];
+            const uint32_t hi = t.cscale[std::min(k1, t.nb - 1) * t.cstride];
+            dw[e] = (k0 < t.nb ? lo : 0u) | (k1 < t.nb ? hi << 16 : 0u);
+        }
+        const v8h da = pack8(dw);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const uint4 h0 = buffer_load16(t.hr, t.h_off[s] + 4u * kb0, 0);
+            const uint4 h1 = buffer_load16(t.hr, t.h_off[s] + 4u * kb0, 16);
+            corr[s] = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, head_sums(h0, h1, kb0, t.nb), corr[s], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[s][v] = -8.0f * corr[s][v];
+
+    v16i magic;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) magic[v] = kMagic;
+    Loads cur = tile_loads<NS>(t, 0);
+#pragma unroll 1
+    for (int b = 0; b < t.nb; ++b) {
+        const Loads nxt = tile_loads<NS>(t, std::min(b + 1, t.nb - 1));
+        const uint32_t d4[8] = {cur.d0.x, cur.d0.y, cur.d0.z, cur.d0.w, cur.d1.x, cur.d1.y, cur.d1.z, cur.d1.w};
+        const v4i A = {static_cast<int>((cur.w.x >> t.shift) & kNibbles), static_cast<int>((cur.w.y >> t.shift) & kNibbles),
+                       static_cast<int>((cur.w.z >> t.shift) & kNibbles), static_cast<int>((cur.w.w >> t.shift) & kNibbles)};
+        v16i r[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const v4i B = {static_cast<int>(cur.x[s].x), static_cast<int>(cur.x[s].y), static_cast<int>(cur.x[s].z),
+                           static_cast<int>(cur.x[s].w)};
+            r[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, magic, 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            scale_block(acc[s], r[s], cur.hd[s], d4);
+            if constexpr (Dbg) {
+                const int j = kSub * s + t.m;
+                if (t.dots && j < t.ncols)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        t.dots[(static_cast<size_t>(t.dot_pair0 + j) * t.dot_rows + t.dot_row0 + acc_row<Down>(v, t.h)) *
+                                   t.nb + b] = r[s][v] - kMagic;
+            }
+        }
+        cur = nxt;
+    }
+}
+
+template<bool Dbg, bool Down>
+__device__ __forceinline__ void tile_dispatch(const TileArgs &t, int nsub, float (&acc)[kSubs][16]) {
+    switch (nsub) {
+    case 1: tile_project<1, Dbg, Down>(t, acc); break;
+    case 2: tile_project<2, Dbg, Down>(t, acc); break;
+    case 3: tile_project<3, Dbg, Down>(t, acc); break;
+    default: tile_project<4, Dbg, Down>(t, acc); break;
+    }
+}
+
+// ------------------------------------------------------------- gate / up ---
+// The gate and up projections feed SiLU and the middle Q8, and one middle
+// code that rounds differently moves its token's output by ~1e-2 rms, so they
+// reproduce the reference's fp32 arithmetic exactly (cpu_expert's
+// matrix_gpu_order, src/cpu_expert.cpp:156-213, the order of the gfx906
+// MMVQ kernel src/hip/linear.hip:156-281):
+//   fragment f of block k: bytes 8f..8f+7 of the code chunk, i.e. elements
+//     8f..8f+7 (low nibbles) and 16+8f..16+8f+7 (high nibbles);
+//   lane L = 2*(k%64) + f:  acc[L] = fma(d4, fma(float(I_f), d8, -4*s8), acc[L])
+//     over k = L/2, L/2 + 64, ... in increasing k;
+//   u_f(k') = acc[2k'+f] + acc[2(k'+32)+f],  v(k') = u_0(k') + u_1(k')  (k' < 32);
+//   result = pairwise tree of v(0..31) in index order (XOR butterfly 1..32).
+// Every add and fma is the same IEEE fp32 operation, so the gate and up
+// values are bit-identical to the reference's, and with moe_expf so is the
+// middle.  Fragment dots come from two MFMAs per block whose A operands keep
+// only that fragment's bytes (the other half zero); both MFMAs start from 0.
+
+// acc[v] = fma(d4[v], fma(float(I[v]), d8, c4), acc[v]); d4 read as fp16 by
+// v_fma_mix_f32 (lo / hi half of each word).
+__device__ __forceinline__ float fma_mix_lo(uint32_t h2, float t, float acc) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(t), "v"(acc));
+    return r;
+}
+__device__ __forceinline__ float fma_mix_hi(uint32_t h2, float t, float acc) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(t), "v"(acc));
+    return r;
+}
+
+__device__ __forceinline__ void fragment_scale(float (&acc)[16], v16i I, float d8, float c4, const uint32_t (&d4)[8]) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const float t = fmaf(static_cast<float>(I[v]), d8, c4);
+        acc[v] = (v & 1) ? fma_mix_hi(d4[v >> 1], t, acc[v]) : fma_mix_lo(d4[v >> 1], t, acc[v]);
+    }
+}
+
+struct GuTile {
+    __amdgpu_buffer_rsrc_t wr, sr, xr, hr;
+    uint32_t w_off, s_off0, s_off1, x_off, h_off;
+    int nb, shift;
+    int32_t *dots;     // debug: [pair][I][nb] or null
+    size_t dot_base;   // dots index of (pair of this lane, row R0 + 16h, block 0)
+    bool dot_ok;
+};
+
+struct BlockLoads {
+    uint4 w, d0, d1, x;
+    uint32_t hd;
+};
+
+__device__ __forceinline__ BlockLoads block_loads(const GuTile &t, int b) {
+    const uint32_t ub = static_cast<uint32_t>(b);
+    BlockLoads l;
+    l.w = buffer_load16(t.wr, t.w_off, ub * 16u);
+    l.d0 = buffer_load16(t.sr, t.s_off0, ub * 16u);
+    l.d1 = buffer_load16(t.sr, t.s_off1, ub * 16u);
+    l.x = buffer_load16(t.xr, t.x_off, ub * 32u);
+    l.hd = buffer_load4(t.hr, t.h_off, ub * 4u);
+    return l;
+}
+
+// Fragment f's dots of one block for the wave's 32 rows x 32 tokens.
+template<int F>
+__device__ __forceinline__ v16i fragment_dots(const GuTile &t, const BlockLoads &l) {
+    const v16i zero = {};
+    const v4i B = {static_cast<int>(l.x.x), static_cast<int>(l.x.y), static_cast<int>(l.x.z), static_cast<int>(l.x.w)};
+    const v4i A = F == 0 ? v4i{static_cast<int>((l.w.x >> t.shift) & kNibbles), static_cast<int>((l.w.y >> t.shift) & kNibbles), 0, 0}
+                         : v4i{0, 0, static_cast<int>((l.w.z >> t.shift) & kNibbles), static_cast<int>((l.w.w >> t.shift) & kNibbles)};
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, zero, 0, 0, 0);
+}
+
+template<bool Dbg>
+__device__ __forceinline__ void store_dots(const GuTile &t, int b, v16i I0, v16i I1) {
+    if constexpr (Dbg) {
+        if (t.dot_ok)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) t.dots[t.dot_base + static_cast<size_t>(v) * t.nb + b] = I0[v] + I1[v];
+    }
+}
+
+// acc[2j+f] of the reference lane array for the wave's 16 outputs per lane:
+// sequential fmas over blocks j, j+64, ... (< nb).
+template<bool Dbg>
+__device__ __forceinline__ void lane_sums(const GuTile &t, int j, float (&a0)[16], float (&a1)[16]) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) { a0[v] = 0.0f; a1[v] = 0.0f; }
+    for (int b = j; b < t.nb; b += 64) {
+        const BlockLoads l = block_loads(t, b);
+        const uint32_t d4[8] = {l.d0.x, l.d0.y, l.d0.z, l.d0.w, l.d1.x, l.d1.y, l.d1.z, l.d1.w};
+        const v16i I0 = fragment_dots<0>(t, l), I1 = fragment_dots<1>(t, l);
+        const float d8 = half_lo(l.hd), c4 = -4.0f * half_hi(l.hd);
+        fragment_scale(a0, I0, d8, c4, d4);
+        fragment_scale(a1, I1, d8, c4, d4);
+        store_dots<Dbg>(t, b, I0, I1);
+    }
+}
+
+// v(k') = (acc[2k'] + acc[2(k'+32)]) + (acc[2k'+1] + acc[2(k'+32)+1]).
+// Single: nb <= 64, so each lane of the reference holds at most one block
+// and acc = fma(d4, t, +0).
+template<bool Single, bool Dbg>
+__device__ __forceinline__ void fold_leaf(const GuTile &t, int kp, float (&v)[16]) {
+    if constexpr (Single) {
+        const int kb = kp + 32;
+        const bool has_a = kp < t.nb, has_b = kb < t.nb;   // uniform
+        const BlockLoads la = block_loads(t, has_a ? kp : 0);
+        const BlockLoads lb = block_loads(t, has_b ? kb : 0);
+        const uint32_t da[8] = {la.d0.x, la.d0.y, la.d0.z, la.d0.w, la.d1.x, la.d1.y, la.d1.z, la.d1.w};
+        const uint32_t db[8] = {lb.d0.x, lb.d0.y, lb.d0.z, lb.d0.w, lb.d1.x, lb.d1.y, lb.d1.z, lb.d1.w};
+        const float d8a = half_lo(la.hd), c4a = -4.0f * half_hi(la.hd);
+        const float d8b = half_lo(lb.hd), c4b = -4.0f * half_hi(lb.hd);
+        float u[2][16];
+        v16i keep_a0, keep_b0;
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const v16i Ia = f ? fragment_dots<1>(t, la) : fragment_dots<0>(t, la);
+            const v16i Ib = f ? fragment_dots<1>(t, lb) : fragment_dots<0>(t, lb);
+            float za[16], zb[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) { za[i] = 0.0f; zb[i] = 0.0f; }
+            if (has_a) fragment_scale(za, Ia, d8a, c4a, da);
+            if (has_b) fragment_scale(zb, Ib, d8b, c4b, db);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) u[f][i] = za[i] + zb[i];
+            if constexpr (Dbg) {
+                if (f == 0) { keep_a0 = Ia; keep_b0 = Ib; }
+                else {
+                    if (has_a) store_dots<Dbg>(t, kp, keep_a0, Ia);
+                    if (has_b) store_dots<Dbg>(t, kb, keep_b0, Ib);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = u[0][i] + u[1][i];
+    } else {
+        float a0[16], a1[16], b0[16], b1[16];
+        lane_sums<Dbg>(t, kp, a0, a1);
+        lane_sums<Dbg>(t, kp + 32, b0, b1);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = (a0[i] + b0[i]) + (a1[i] + b1[i]);
+    }
+    // One leaf at a time: hoisting the next leaf's loads and MFMAs above this
+    // point multiplies the live registers.
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The pairwise tree over v(0..31) in index order.  Leaves are taken two at a
+// time (a level-1 node) and merged upward like a binary counter: each level
+// holds at most one pending left operand.  Level 1 stays in registers;
+// levels 2-4 (touched every 4, 8, 16 leaves) wait in LDS (`park`, 3 x 16
+// floats per lane of this wave).
+template<bool Single, bool Dbg>
+__device__ __forceinline__ void fold_tree(const GuTile &t, float (*park)[16][64], int lane, float (&res)[16]) {
+    float l1[16];
+#pragma unroll 1
+    for (int p = 0; p < 16; ++p) {
+        float w[16], x[16];
+        fold_leaf<Single, Dbg>(t, 2 * p, w);
+        fold_leaf<Single, Dbg>(t, 2 * p + 1, x);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
+        if ((p & 1) == 0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) l1[i] = w[i];
+            continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = l1[i] + w[i];
+        int lvl = 0;
+        // Levels 2..4: node index p >> (lvl + 1); odd nodes merge with the parked left operand.
+        for (; lvl < 3; ++lvl) {
+            if (((p >> (lvl + 1)) & 1) == 0) break;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) w[i] = park[lvl][i][lane] + w[i];
+        }
+        if (lvl < 3) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) park[lvl][i][lane] = w[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) res[i] = w[i];
+        }
+    }
+}
+
+// Workgroup = 2 waves: wave 0 gate rows R0..R0+31, wave 1 the same up rows,
+// both for token tile `sub` (32 pairs) of an MFMA item.  A-row m of the MFMA
+// is physical row 16*((m>>2)&1) + 4*(m>>3) + (m&3), so accumulator register v
+// of lane half h is row 16h + v: the lane's 16 scales per block are two
+// 16-byte groups of the [rows/8][blocks][8] plane, and its 16 middle values
+// are elements 16h..16h+15 of one Q8_1 block.  Units are ordered
+// (item, slice, sub) so the 4 tiles of an item that read the same weight rows
+// are adjacent on one XCD.
+template<bool Dbg>
+__global__ __launch_bounds__(128) void k_gate_up_mfma(FfnArgs a) {
+    __shared__ float xch[16][64];
+    __shared__ float park[2][3][16][64];   // pending tree levels 2-4, per wave
+    const int lane = threadIdx.x & 63;
+    const int mat = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int H = a.shape.H, I = a.shape.I, nb = H / 32, nbi = I / 32;
+    const int slices = nbi * kSubs;
+    const Unit un = mfma_unit(a.routes.item_counts[1], slices);
+    if (!un.ok) return;   // uniform per workgroup
+    const Item *itp = a.routes.mfma_items + un.item;
+    const int expert = itp->expert, first = itp->first, ncols = itp->ncols;
+    const int sub = un.slice % kSubs;
+    const int R0 = (un.slice / kSubs) * 32;
+    if (kSub * sub >= ncols) return;   // uniform per workgroup: no tokens in this tile
+    const int m = lane & 31, h = lane >> 5;
+    const int prow = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
+    const int j = kSub * sub + m;
+    const int pair = first + std::min(j, ncols - 1);
+
+    const size_t rbase = static_cast<size_t>(expert) * I + R0;
+    const uint32_t row_bytes = static_cast<uint32_t>(nb) * 16u;
+    GuTile t;
+    t.wr = buffer_rsrc((mat ? a.bank.up_codes : a.bank.gate_codes) + rbase * row_bytes, 32u * row_bytes);
+    t.sr = buffer_rsrc((mat ? a.bank.up_scales : a.bank.gate_scales) + rbase * nb, 32u * static_cast<uint32_t>(nb) * 2u);
+    t.xr = buffer_rsrc(a.xq.codes, static_cast<uint32_t>(a.tokens) * static_cast<uint32_t>(nb) * 32u);
+    t.hr = buffer_rsrc(a.xq.heads, static_cast<uint32_t>(a.tokens) * static_cast<uint32_t>(nb) * 4u);
+    t.w_off = static_cast<uint32_t>(prow) * row_bytes;
+    t.s_off0 = static_cast<uint32_t>(2 * h * nb) * 16u;
+    t.s_off1 = t.s_off0 + static_cast<uint32_t>(nb) * 16u;
+    const uint32_t tok = static_cast<uint32_t>(a.routes.pair_token[pair]);
+    t.x_off = tok * static_cast<uint32_t>(nb) * 32u + 16u * h;
+    t.h_off = tok * static_cast<uint32_t>(nb) * 4u;
+    t.nb = nb;
+    t.shift = 4 * h;
+    t.dots = Dbg ? (mat ? a.up_dots : a.gate_dots) : nullptr;
+    t.dot_base = (static_cast<size_t>(pair) * I + R0 + 16 * h) * nb;
+    t.dot_ok = Dbg && t.dots && j < ncols;
+
+    float res[16];
+    if (nb <= 64) fold_tree<true, Dbg>(t, park[mat], lane, res);
+    else fold_tree<false, Dbg>(t, park[mat], lane, res);
+    if (mat == 1) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) xch[v][lane] = res[v];
+    }
+    __syncthreads();
+    if (mat != 0) return;
+    int flags = 0;
+    float mid[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mid[v] = silu_mul(res[v], xch[v][lane], flags);
+    float keep[16];
+    if constexpr (Dbg) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) keep[v] = mid[v];
+    }
+    const Q8Part<2> q8 = quantize_part<2>(mid);
+    if (j < ncols) {
+        const size_t mb = static_cast<size_t>(pair) * nbi + R0 / 32;
+        *reinterpret_cast<uint4 *>(a.mq.codes + mb * 32 + 16 * h) =
+            make_uint4(q8.codes[0], q8.codes[1], q8.codes[2], q8.codes[3]);
+        if (h == 0) a.mq.heads[mb] = q8.head;
+        if constexpr (Dbg) {
+            if (a.middle_f32)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) a.middle_f32[static_cast<size_t>(pair) * I + R0 + 16 * h + v] = keep[v];
+        }
+        const int f = flags | (h == 0 ? q8.flags : 0);
+        if (f) atomicOr(a.error, f);
+    }
+}
+
+// ------------------------------------------------------------------ down ---
+// Workgroup = 4 waves x 32 output rows = 128 rows of H.  A-row m maps to
+// physical row rho = 4*(v&7) + 2*hh + (v>>3) with v = 4*(m>>3) + (m&3) and
+// hh = (m>>2)&1, so accumulator register v of lane half h is row
+// 4*(v&7) + 2h + (v>>3), whose scale sits at slot 16h + v of the
+// [rows/32][blocks][32] plane (slot (r%4)*8 + (r%32)/4): one 32-byte load per
+// lane and block.  Before the stores, lanes l and l^32 trade 8 values so each
+// lane holds 16 consecutive rows (4 float4 stores per tile).
+template<bool Dbg>
+__global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int H = a.shape.H, nbi = a.shape.I / 32;
+    const int slices = (H + 127) / 128;
+    const Unit un = mfma_unit(a.routes.item_counts[1], slices);
+    if (!un.ok) return;
+    const Item *itp = a.routes.mfma_items + un.item;
+    const int expert = itp->expert, first = itp->first, ncols = itp->ncols;
+    const int R0 = un.slice * 128 + wave * 32;
+    if (R0 >= H) return;   // no barrier in this kernel
+    const int nsub = (ncols + kSub - 1) / kSub;
+    const int m = lane & 31, h = lane >> 5;
+    const int mv = 4 * (m >> 3) + (m & 3);
+    const int prow = 4 * (mv & 7) + 2 * ((m >> 2) & 1) + (mv >> 3);
+    const int pslot = (prow & 3) * 8 + (prow >> 2);
+
+    const size_t rbase = static_cast<size_t>(expert) * H + R0;
+    const uint32_t row_bytes = static_cast<uint32_t>(nbi) * 16u;
+    const uint16_t *scales = a.bank.down_scales + rbase * nbi;        // [nbi][32] halfs of this 32-row group
+    const uint32_t pairs = static_cast<uint32_t>(a.pairs_bound);
+    TileArgs t;
+    t.wr = buffer_rsrc(a.bank.down_codes + rbase * row_bytes, 32u * row_bytes);
+    t.sr = buffer_rsrc(scales, static_cast<uint32_t>(nbi) * 64u);
+    t.xr = buffer_rsrc(a.mq.codes, pairs * static_cast<uint32_t>(nbi) * 32u);
+    t.hr = buffer_rsrc(a.mq.heads, pairs * static_cast<uint32_t>(nbi) * 4u);
+    t.w_off = static_cast<uint32_t>(prow) * row_bytes;
+    t.s_off0 = 32u * h;
+    t.s_off1 = 32u * h + 16u;
+    t.s_step = 64u;
+#pragma unroll
+    for (int s = 0; s < kSubs; ++s) {
+        const uint32_t p = static_cast<uint32_t>(first + std::min(kSub * s + m, ncols - 1));
+        t.x_off[s] = p * static_cast<uint32_t>(nbi) * 32u + 16u * h;
+        t.h_off[s] = p * static_cast<uint32_t>(nbi) * 4u;
+    }
+    t.cscale = scales + pslot;
+    t.cstride = 32;
+    t.nb = nbi;
+    t.shift = 4 * h;
+    t.dots = Dbg ? a.down_dots : nullptr;
+    t.dot_rows = static_cast<size_t>(H);
+    t.dot_row0 = R0;
+    t.dot_pair0 = first;
+    t.ncols = ncols;
+    t.m = m;
+    t.h = h;
+    float acc[kSubs][16];
+    tile_dispatch<Dbg, true>(t, nsub, acc);
+
+    // Lane half h holds rows 4q + 2h (v = q) and 4q + 2h + 1 (v = 8 + q),
+    // q = 0..7.  After the trade lane half h holds rows 16h .. 16h + 15.
+#pragma unroll
+    for (int s = 0; s < kSubs; ++s) {
+        if (s >= nsub) break;
+        const int j = kSub * s + m;
+        const bool valid = j < ncols;
+        const int p = first + std::min(j, ncols - 1);
+        const size_t orow = static_cast<size_t>(a.routes.pair_token[p]) * a.out_stride_k + a.routes.pair_rank[p];
+        float *dst = a.out + orow * H + R0 + 16 * h;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float send0 = h ? acc[s][q] : acc[s][4 + q];
+            const float send1 = h ? acc[s][8 + q] : acc[s][12 + q];
+            const float recv0 = __shfl_xor(send0, 32, 64);
+            const float recv1 = __shfl_xor(send1, 32, 64);
+            const float4 o = h ? make_float4(recv0, recv1, acc[s][4 + q], acc[s][12 + q])
+                               : make_float4(acc[s][q], acc[s][8 + q], recv0, recv1);
+            if (valid) *reinterpret_cast<float4 *>(dst + 4 * q) = o;
+        }
+    }
+}
+
+unsigned mfma_grid(const FfnArgs &a, int slices) {
+    const size_t bound = static_cast<size_t>(a.pairs_bound) / kMfmaTile +
+                         static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep));
+    const size_t units = bound * static_cast<size_t>(slices);
+    return static_cast<unsigned>((units + 7) / 8 * 8);
+}
+
+}  // namespace
+
+hipError_t launch_gate_up_mfma(const FfnArgs &a, hipStream_t s) {
+    const bool dbg = a.middle_f32 || a.gate_dots || a.up_dots;
+    const unsigned grid = mfma_grid(a, a.shape.I / 32 * kSubs);
+    if (dbg) k_gate_up_mfma<true><<<grid, 128, 0, s>>>(a);
+    else k_gate_up_mfma<false><<<grid, 128, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_down_mfma(const FfnArgs &a, hipStream_t s) {
+    const unsigned grid = mfma_grid(a, (a.shape.H + 127) / 128);
+    if (a.down_dots) k_down_mfma<true><<<grid, 256, 0, s>>>(a);
+    else k_down_mfma<false><<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace moe

@@ -69,6 +69,8 @@ def library():
         lib.moe_ffn_replay_stage.argtypes = [_P, _I, _P]
         lib.moe_ffn_profile.argtypes = [_P, _I]
         lib.moe_ffn_profile_read.argtypes = [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]
+        lib.moe_expf_device.argtypes = [_P, _P, _I, _P]
+        lib.moe_expf_host.argtypes = [_P, _P, ctypes.c_size_t]
         lib.moe_ffn_last_stats.argtypes = [_P, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
                                            ctypes.POINTER(ctypes.c_int32)]
         _lib = lib
@@ -245,6 +247,23 @@ class MoeLayer:
         _check(library().moe_ffn_expert_down(self.handle, expert, _ptr(middle_q8), columns, _ptr(y), _ptr(dd), path,
                                              _ptr(error), _stream(stream)), "moe_ffn_expert_down")
         return dict(y=y, down_dots=dd, error=error)
+
+
+def expf_host(x):
+    """The kernels' expf (moe_expf.h) run on the CPU: float32 array in, out."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    _check(library().moe_expf_host(ctypes.c_void_p(x.ctypes.data), ctypes.c_void_p(y.ctypes.data), x.size),
+           "moe_expf_host")
+    return y
+
+
+def expf_device(x, stream=None):
+    """The kernels' expf on the GPU: float32 device tensor in, out."""
+    import torch
+    y = torch.empty_like(x)
+    _check(library().moe_expf_device(_ptr(x), _ptr(y), x.numel(), _stream(stream)), "moe_expf_device")
+    return y
 
 
 def quantize_q8_1(x, error=None, stream=None):

@@ -128,7 +128,9 @@ int moe_ffn_group_routes(moe_ffn_layer *layer, const int32_t *ids, const float *
                          int32_t *counts, int32_t *offsets, int32_t *route_token,
                          int32_t *route_rank, int *error, void *stream);
 
-/* Kernel path selection for the single-expert stages below. */
+/* Kernel path selection for the single-expert stages below: MFMA = the
+ * int8-MFMA kernels of the grouped forward (AUTO selects them); STREAM = the
+ * per-token streaming-dot kernels. */
 enum { MOE_PATH_AUTO = 0, MOE_PATH_STREAM = 1, MOE_PATH_MFMA = 2 };
 
 /* One expert's gate/up projections fused with SiLU(gate)*up and Q8_1
@@ -187,6 +189,16 @@ int moe_ffn_profile_read(moe_ffn_layer *layer, double *stage_ms, int *forwards);
  * number of experts (incl. shared) that received tokens. */
 int moe_ffn_last_stats(moe_ffn_layer *layer, int32_t *stream_items, int32_t *mfma_items,
                        int32_t *active_experts);
+
+/* SiLU exponential checks.  The kernels evaluate expf(-g) of SiLU and of the
+ * shared-expert sigmoid gate with the bits of the host C library's expf (the
+ * function src/cpu_expert.cpp:251 calls), so the middle matches the CPU
+ * reference bit for bit; the reference's device expf (src/hip/linear.hip:113)
+ * does not.  moe_expf_device enqueues y[i] = expf(x[i]) on the GPU with the
+ * kernels' function; moe_expf_host runs the same code on the CPU.  No
+ * counterpart in the reference: they exist for parity tests. */
+int moe_expf_device(const float *x, float *y, int n, void *stream);
+int moe_expf_host(const float *x, float *y, size_t n);
 
 #ifdef __cplusplus
 }

@@ -656,3 +656,9 @@ done:
     free(st.offsets); free(st.contrib); free(st.shared_out); free(st.jobs);
     return rc;
 }
+
+/* The C library's expf over an array (the function the reference's CPU SiLU
+ * calls, src/cpu_expert.cpp:251): the checker for the kernels' expf. */
+void mo_expf_libm(const float *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = expf(x[i]);
+}

@@ -134,6 +134,9 @@ int mo_baseline_layer(const float *x, int tokens, int H, int I, int E, int top_k
 /* Physical-core representatives (first allowed sibling per (package,core)). */
 int mo_allowed_physical_cpus(int *cpus, int capacity, int *count);
 
+/* The C library's expf over an array (checker for the kernels' expf). */
+void mo_expf_libm(const float *x, float *y, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

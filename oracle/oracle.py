@@ -50,6 +50,8 @@ def _load_oracle():
     lib.mo_float_to_half.restype = ctypes.c_uint16
     lib.mo_float_to_half.argtypes = [ctypes.c_float]
     lib.mo_quantize_q8.argtypes = [_P, _SZ, _P]
+    lib.mo_expf_libm.restype = None
+    lib.mo_expf_libm.argtypes = [_P, _P, _SZ]
     lib.mo_block_dot.argtypes = [_P, _P]
     lib.mo_scaled_dot_q4_0.restype = ctypes.c_float
     lib.mo_scaled_dot_q4_0.argtypes = [ctypes.c_int32, ctypes.c_uint16, _P]
@@ -120,6 +122,14 @@ def quantize_q8(x):
     out = np.zeros(x.shape[:-1] + (x.shape[-1] // 32,), dtype=Q8_DTYPE)
     _check(lib().mo_quantize_q8(_ptr(x), x.size, _ptr(out)), "quantize_q8")
     return out
+
+
+def expf_libm(x):
+    """The C library's expf, elementwise (float32 in, float32 out)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().mo_expf_libm(_ptr(x), _ptr(y), x.size)
+    return y
 
 
 def block_dots(w, K, M, xq):

@@ -46,6 +46,45 @@ def q8_bytes(q):
     return np.ascontiguousarray(q).view(np.uint8).reshape(-1)
 
 
+def layer_parity(L, x, ids, w, bank, shared, y_gpu, sample, what, H=2048, I=512):
+    """Parity of a whole-layer forward on the tokens `sample`:
+      1. x Q8 bytes equal to the reference quantizer's;
+      2. every middle Q8 row (grouped order, from debug_last) equal byte for
+         byte to the oracle's cpu_expert middle of that (token, expert) --
+         the gate/up kernels follow the reference's fp32 order and expf, so
+         this is exact, not a tolerance;
+      3. the output within 1e-5 rms of the oracle's whole layer (the down
+         projection sums its blocks in the kernel's own order; the north_star
+         bar is 1e-3 rms)."""
+    N, E = x.shape[0], L.E
+    nbi = I // 32
+    dbg = L.debug_last(N)
+    mid = host(dbg["middle_q8"]).reshape(-1, nbi, 36)
+    mask = np.zeros(N, np.uint8)
+    mask[sample] = 1
+    ref = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, token_mask=mask)
+    assert np.array_equal(host(dbg["x_q8"]).reshape(N, -1)[sample], q8_bytes(ref["x_q8"]).reshape(N, -1)[sample])
+    groups = O.route_groups(ids, w, E)
+    P = int(groups["offsets"][-1])
+    eb = len(bank) // E
+    mb = eb // 3
+    xq = O.quantize_q8(x[sample])
+    pos = {int(t): i for i, t in enumerate(sample)}
+
+    def oracle_middle(e_bytes, t):
+        ro = O.expert_forward(e_bytes[:mb], e_bytes[mb:2 * mb], e_bytes[2 * mb:], H, I, xq[pos[t]:pos[t] + 1])
+        return q8_bytes(ro["middle_q8"]).reshape(nbi, 36)
+
+    for p in range(P):
+        t = int(groups["token"][p])
+        if t in pos:
+            e = int(groups["expert"][p])
+            assert np.array_equal(mid[p], oracle_middle(bank[e * eb:(e + 1) * eb], t)), f"{what}: middle of pair {p}"
+    for t in sample:
+        assert np.array_equal(mid[P + int(t)], oracle_middle(shared, int(t))), f"{what}: shared middle of {t}"
+    assert_close(y_gpu[sample], ref["y"][sample], tol=1e-5, what=what)
+
+
 @pytest.fixture(scope="module", autouse=True)
 def gpu_ready():
     if not torch.cuda.is_available():
@@ -103,11 +142,12 @@ def test_cfg0_gate_up_block_dots_bit_exact(cfg0):
 
 
 def test_cfg0_middle_and_middle_q8(cfg0):
+    """Streaming path (H <= 2048): gate/up in the reference's fp32 order and
+    expf, so the middle and its Q8 are bit-identical to the CPU reference's."""
     r = cfg0["layer"].expert_gate_up(0, dev(q8_bytes(cfg0["xq"]).reshape(8, -1)), 8, path=moe_ffn.PATH_STREAM)
     middle = host(r["middle"])
-    assert_close(middle, cfg0["ref"]["middle"], what="middle")
-    # The Q8 of the middle is bit-exact given the same fp32 middle.
-    assert np.array_equal(host(r["middle_q8"]).reshape(-1), q8_bytes(O.quantize_q8(middle)))
+    assert np.array_equal(middle.view(np.uint32), cfg0["ref"]["middle"].view(np.uint32))
+    assert np.array_equal(host(r["middle_q8"]).reshape(-1), q8_bytes(cfg0["ref"]["middle_q8"]))
 
 
 def test_cfg0_down_block_dots_and_projection(cfg0):
@@ -131,10 +171,12 @@ def test_reference_shape_expert_vs_golden():
     g, u, d = expert_weights(2560, 640)
     layer = _single_expert(2560, 640, (g, u, d), 3)
     xq = f["x_q8"].reshape(3, -1)
-    r = layer.expert_gate_up(0, dev(xq), 3, dots=True)
+    # H = 2560 > 2048: the wide streaming kernel (per-block dots bit-exact,
+    # its own fp32 order across blocks).
+    r = layer.expert_gate_up(0, dev(xq), 3, path=moe_ffn.PATH_STREAM, dots=True)
     assert np.array_equal(host(r["gate_dots"]), O.block_dots(g, 2560, 640, xq))
     assert_close(host(r["middle"]), f["middle"], what="middle vs reference")
-    y = layer.expert_down(0, r["middle_q8"], 3)["y"]
+    y = layer.expert_down(0, r["middle_q8"], 3, path=moe_ffn.PATH_STREAM)["y"]
     assert_close(host(y), f["y"], what="expert vs reference cpu_expert")
     layer.close()
 
@@ -209,7 +251,9 @@ def test_b8_decode_forward(moe512):
     L = moe512["layer"]
     y, err = L.forward(dev(x), dev(ids), dev(w))
     ref = O.moe_layer(x, 2048, 512, 512, moe512["bank"], ids, w, shared_q4=moe512["shared"])
-    assert_close(host(y), ref["y"], what="B8 decode layer")
+    # The decode path follows the reference's fp32 order in every projection
+    # and its fold: the layer output is bit-identical to the CPU reference's.
+    assert np.array_equal(host(y).view(np.uint32), ref["y"].view(np.uint32))
     assert int(host(err)[0]) == 0
     dbg = L.debug_last(8)
     assert np.array_equal(host(dbg["x_q8"]).reshape(-1), q8_bytes(ref["x_q8"]))
@@ -224,7 +268,7 @@ def test_b8_decode_forward_shared_gate(moe512):
     g = np.random.default_rng(43).standard_normal(8).astype(np.float32)
     y, err = moe512["layer"].forward(dev(x), dev(ids), dev(w), shared_gate=dev(g))
     ref = O.moe_layer(x, 2048, 512, 512, moe512["bank"], ids, w, shared_q4=moe512["shared"], shared_gate=g)
-    assert_close(host(y), ref["y"], what="B8 with shared sigmoid gate")
+    assert np.array_equal(host(y).view(np.uint32), ref["y"].view(np.uint32))
     assert int(host(err)[0]) == 0
 
 
@@ -239,13 +283,7 @@ def test_prefill_4k_zipf_sampled_tokens(moe512):
     yh = host(y)
     assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
     sample = np.random.default_rng(53).choice(4096, 24, replace=False)
-    mask = np.zeros(4096, np.uint8)
-    mask[sample] = 1
-    ref = O.moe_layer(x, 2048, 512, 512, moe512["bank"], ids, w, shared_q4=moe512["shared"], token_mask=mask)
-    assert_close(yh[sample], ref["y"][sample], what="4K prefill sampled tokens")
-    dbg = L.debug_last(4096)
-    assert np.array_equal(host(dbg["x_q8"]).reshape(4096, -1)[sample],
-                          q8_bytes(ref["x_q8"]).reshape(4096, -1)[sample])
+    layer_parity(L, x, ids, w, moe512["bank"], moe512["shared"], yh, sample, "4K prefill")
 
 
 def test_forward_reuse_smaller_batch_and_determinism(moe512):
@@ -258,9 +296,11 @@ def test_forward_reuse_smaller_batch_and_determinism(moe512):
     y5, _ = L.forward(dev(x5), dev(ids[:5]), dev(w[:5]))
     y2, _ = L.forward(dev(x), dev(ids), dev(w))
     assert np.array_equal(host(y2), y1)                   # deterministic
-    assert np.array_equal(host(y5), y1[:5])                # per-token independence
+    # 5 tokens take the decode path (reference order throughout), 37 the
+    # grouped MFMA path (its down projection sums blocks in its own order).
     ref = O.moe_layer(x, 2048, 512, 512, moe512["bank"], ids, w, shared_q4=moe512["shared"])
-    assert_close(y1, ref["y"], what="37-token layer")
+    assert np.array_equal(host(y5).view(np.uint32), ref["y"][:5].view(np.uint32))
+    assert_close(y1, ref["y"], tol=1e-5, what="37-token layer")
 
 
 def test_forward_flags_bad_inputs(moe512):
@@ -346,10 +386,12 @@ def _layer_with_path(decode, *args, **kw):
 @pytest.mark.parametrize("gate", [False, True])
 def test_decode_and_grouped_paths_agree(gate):
     """The ungrouped decode path (work per (token, rank), fold inside the down
-    kernel) and the grouped path give the same bits, including for an invalid
-    id and a duplicate id (both contribute nothing and set bit 1), and match
-    the oracle, where an invalid route equals a weight-0 route to an unused
-    expert."""
+    kernel) and the grouped streaming path both follow the reference's fp32
+    order, so they give the same bits as each other and as the oracle,
+    including for an invalid id and a duplicate id (both contribute nothing
+    and set bit 1; the oracle sees a weight-0 route to an unused expert).
+    The grouped MFMA path (the default for grouped batches) has the same
+    middle and sums its down blocks in its own order: within 1e-5 rms."""
     H, I, E, K, N = 2048, 512, 24, 6, 5
     bank = W.q4_bank(E, seed=301)
     shared = W.q4_bank(1, seed=302)
@@ -360,26 +402,28 @@ def test_decode_and_grouped_paths_agree(gate):
     ids_bad[0, 0] = E + 5           # bad id (rank 0: the token's reporting workgroup)
     ids_bad[3, 2] = ids_bad[3, 1]   # duplicate
     outs = {}
-    for decode in (True, False):
-        L = _layer_with_path(decode, H, I, E, K, True, N, experts_q4=bank, shared_q4=shared)
+    paths = {"decode": {"MOE_FFN_DECODE": 1}, "stream": {"MOE_FFN_DECODE": 0, "MOE_FFN_MFMA_MIN": 0},
+             "mfma": {"MOE_FFN_DECODE": 0, "MOE_FFN_MFMA_MIN": 1}}
+    for path, env in paths.items():
+        L = _layer_env(env, H, I, E, K, True, N, experts_q4=bank, shared_q4=shared)
         for name, i_ in (("ok", ids), ("bad", ids_bad)):
             y, err = L.forward(dev(x), dev(i_), dev(w), shared_gate=None if g is None else dev(g))
-            outs[(decode, name)] = (host(y), int(host(err)[0]))
+            outs[(path, name)] = (host(y), int(host(err)[0]))
         dbg = L.debug_last(N)
         assert np.array_equal(host(dbg["x_q8"]).reshape(-1), q8_bytes(O.quantize_q8(x)))
         L.close()
-    for name in ("ok", "bad"):
-        (yd, ed), (yg, eg) = outs[(True, name)], outs[(False, name)]
-        assert np.array_equal(yd, yg), name
-        assert ed == eg == (0 if name == "ok" else 1), (name, ed, eg)
-    ref = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, shared_gate=g)["y"]
-    assert_close(outs[(True, "ok")][0], ref, what="decode path")
     rid, rw = ids_bad.copy(), w.copy()
     for t, r in ((0, 0), (3, 2)):
         rid[t, r] = next(e for e in range(E) if e not in ids_bad[t])
         rw[t, r] = 0.0
-    ref_bad = O.moe_layer(x, H, I, E, bank, rid, rw, shared_q4=shared, shared_gate=g)["y"]
-    assert_close(outs[(True, "bad")][0], ref_bad, what="decode path, invalid routes")
+    refs = {"ok": O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, shared_gate=g)["y"],
+            "bad": O.moe_layer(x, H, I, E, bank, rid, rw, shared_q4=shared, shared_gate=g)["y"]}
+    for name in ("ok", "bad"):
+        (yd, ed), (ys, es), (ym, em) = outs[("decode", name)], outs[("stream", name)], outs[("mfma", name)]
+        assert ed == es == em == (0 if name == "ok" else 1), (name, ed, es, em)
+        assert np.array_equal(yd.view(np.uint32), refs[name].view(np.uint32)), name
+        assert np.array_equal(ys.view(np.uint32), refs[name].view(np.uint32)), name
+        assert_close(ym, refs[name], tol=1e-5, what=f"MFMA path, {name} routes")
 
 
 def test_decode_path_middle_debug_view(moe512):
@@ -425,3 +469,166 @@ def test_decode_quantizer_reference_fixture():
     assert np.all(got[~ok] == 0)
     assert int(host(err)[0]) != 0
     L.close()
+
+
+# ------------------------------------------------------- int8-MFMA path ----
+def _layer_env(env, *args, **kw):
+    """A layer created with the given MOE_FFN_* settings (read at creation)."""
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    try:
+        return moe_ffn.MoeLayer(*args, **kw)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+@pytest.fixture(scope="module")
+def mfma_expert():
+    bank = W.q4_bank(1, seed=401)
+    mb = len(bank) // 3
+    layer = moe_ffn.MoeLayer(2048, 512, 1, 1, False, 200, experts_q4=bank)
+    return dict(layer=layer, g=bank[:mb], u=bank[mb:2 * mb], d=bank[2 * mb:])
+
+
+@pytest.mark.parametrize("columns", [1, 8, 33, 128, 200])
+def test_mfma_expert_stages_bit_exact_dots(mfma_expert, columns):
+    """Single-expert stages on the int8-MFMA path: per-block int32 dots of
+    gate, up and down bit-exact (partial token tiles, one and two 128-pair
+    items), middle within 1e-3 rms of the oracle and its Q8 bytes equal to
+    the reference quantizer of the GPU middle, down within 1e-5 rms of the
+    reference cpu_expert order on a shared middle."""
+    L, g, u, d = mfma_expert["layer"], mfma_expert["g"], mfma_expert["u"], mfma_expert["d"]
+    x = W.activations(columns, seed=410 + columns)
+    xq = O.quantize_q8(x)
+    r = L.expert_gate_up(0, dev(q8_bytes(xq).reshape(columns, -1)), columns, path=moe_ffn.PATH_MFMA, dots=True)
+    assert np.array_equal(host(r["gate_dots"]), O.block_dots(g, 2048, 512, xq))
+    assert np.array_equal(host(r["up_dots"]), O.block_dots(u, 2048, 512, xq))
+    ref = O.expert_forward(g, u, d, 2048, 512, xq, avx2=True)
+    middle = host(r["middle"])
+    # The MFMA gate/up follows the reference's fp32 order and expf: the
+    # middle and its Q8 are bit-identical to the CPU reference's.
+    assert np.array_equal(middle.view(np.uint32), ref["middle"].view(np.uint32))
+    assert np.array_equal(host(r["middle_q8"]).reshape(-1), q8_bytes(ref["middle_q8"]))
+    assert int(host(r["error"])[0]) == 0
+    mq = ref["middle_q8"]
+    rd = L.expert_down(0, dev(q8_bytes(mq).reshape(columns, -1)), columns, path=moe_ffn.PATH_MFMA, dots=True)
+    assert np.array_equal(host(rd["down_dots"]), O.block_dots(d, 512, 2048, mq))
+    assert_close(host(rd["y"]), O.matrix_gpu_order(d, 512, 2048, mq), tol=1e-5, what="MFMA down projection")
+    # The non-debug kernels give the same bits as the debug ones.
+    r2 = L.expert_gate_up(0, dev(q8_bytes(xq).reshape(columns, -1)), columns, path=moe_ffn.PATH_MFMA)
+    assert np.array_equal(host(r2["middle_q8"]), host(r["middle_q8"]))
+    rd2 = L.expert_down(0, dev(q8_bytes(mq).reshape(columns, -1)), columns, path=moe_ffn.PATH_MFMA)
+    assert np.array_equal(host(rd2["y"]), host(rd["y"]))
+
+
+def test_mfma_reference_shape_expert_vs_golden():
+    """The reference's own CPU expert output at 2560/640 on the MFMA path
+    (80 and 20 blocks per row: partial 16-block chunks of the s8 term)."""
+    f = np.load(os.path.join(GOLDEN, "cpu_expert_2560x640.npz"), allow_pickle=False)
+    g, u, d = expert_weights(2560, 640)
+    layer = _single_expert(2560, 640, (g, u, d), 3)
+    xq = f["x_q8"].reshape(3, -1)
+    r = layer.expert_gate_up(0, dev(xq), 3, path=moe_ffn.PATH_MFMA, dots=True)
+    assert np.array_equal(host(r["gate_dots"]), O.block_dots(g, 2560, 640, xq))
+    assert np.array_equal(host(r["up_dots"]), O.block_dots(u, 2560, 640, xq))
+    # bit-identical to the compiled reference cpu_expert's middle (80 blocks:
+    # reference lanes holding two blocks each)
+    assert np.array_equal(host(r["middle"]).view(np.uint32), f["middle"].view(np.uint32))
+    rd = layer.expert_down(0, r["middle_q8"], 3, path=moe_ffn.PATH_MFMA, dots=True)
+    mq = host(r["middle_q8"]).reshape(3, -1)
+    assert np.array_equal(host(rd["down_dots"]), O.block_dots(d, 640, 2560, mq))
+    assert_close(host(rd["y"]), f["y"], what="MFMA expert vs reference cpu_expert")
+    layer.close()
+
+
+def test_mfma_layer_4k_zipf(moe512):
+    """BASELINE configs[2] with every group on the MFMA path: sampled tokens
+    against the oracle, and every token against the streaming path."""
+    x = W.activations(4096, seed=501)
+    ids, w = W.routes_zipf(4096, 1.1, seed=502)
+    L = _layer_env({"MOE_FFN_MFMA_MIN": 1}, 2048, 512, 512, 10, True, 4096, experts_q4=moe512["bank"],
+                   shared_q4=moe512["shared"])
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    yh = host(y)
+    assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
+    st = L.last_stats()
+    assert st["stream_items"] == 0 and st["mfma_items"] > 0
+    sample = np.random.default_rng(503).choice(4096, 24, replace=False)
+    layer_parity(L, x, ids, w, moe512["bank"], moe512["shared"], yh, sample, "MFMA 4K prefill")
+    # Every token against the streaming kernels (k_gate_up_lean / k_down_lean):
+    # both gate/up paths follow the reference's fp32 order, so the middles
+    # are identical; the two down kernels sum their blocks in different
+    # orders.
+    S = _layer_env({"MOE_FFN_MFMA_MIN": 0}, 2048, 512, 512, 10, True, 4096, experts_q4=moe512["bank"],
+                   shared_q4=moe512["shared"])
+    ys, es = S.forward(dev(x), dev(ids), dev(w))
+    assert int(host(es)[0]) == 0 and S.last_stats()["mfma_items"] == 0
+    assert np.array_equal(host(S.debug_last(4096)["middle_q8"]), host(L.debug_last(4096)["middle_q8"]))
+    assert_close(yh, host(ys), tol=1e-5, what="MFMA vs streaming path, all 4096 tokens")
+    S.close()
+    y2, _ = L.forward(dev(x), dev(ids), dev(w))
+    assert np.array_equal(host(y2), yh)   # deterministic
+    L.close()
+
+
+@pytest.mark.parametrize("mfma_min", [1, 16, 0])
+def test_mfma_layer_small_batches(moe512, mfma_min):
+    """Grouped path (decode path off) with MFMA for groups >= mfma_min (0:
+    streaming kernels only): 37 and 300 Zipf tokens fully against the oracle;
+    per-token independence (bit-exact on a single path; with mixed paths the
+    down projection of a group depends on the path its size selects)."""
+    L = _layer_env({"MOE_FFN_MFMA_MIN": mfma_min, "MOE_FFN_DECODE": 0}, 2048, 512, 512, 10, True, 300,
+                   experts_q4=moe512["bank"], shared_q4=moe512["shared"])
+    for n, seed in ((37, 511), (300, 512)):
+        x = W.activations(n, seed=seed)
+        ids, w = W.routes_zipf(n, 1.3, seed=seed + 100)
+        y, err = L.forward(dev(x), dev(ids), dev(w))
+        yh = host(y)
+        assert int(host(err)[0]) == 0
+        layer_parity(L, x, ids, w, moe512["bank"], moe512["shared"], yh, np.arange(n),
+                     f"{n}-token layer, mfma_min {mfma_min}")
+        y5, _ = L.forward(dev(x[:5].copy()), dev(ids[:5]), dev(w[:5]))
+        if mfma_min in (0, 1):
+            assert np.array_equal(host(y5), yh[:5])
+        else:
+            assert_close(host(y5), yh[:5], tol=1e-5, what="mixed paths, 5-token batch")
+    L.close()
+
+
+def test_mfma_layer_invalid_routes_flag():
+    """A bad id and a duplicate id on the MFMA path contribute nothing and set
+    bit 1; the rest matches the oracle with those routes at weight 0."""
+    H, I, E, K, N = 2048, 512, 24, 6, 40
+    bank = W.q4_bank(E, seed=601)
+    shared = W.q4_bank(1, seed=602)
+    x = W.activations(N, seed=603)
+    ids, w = W.routes_uniform(N, experts=E, k=K, seed=604)
+    ids[0, 0] = E + 5
+    ids[3, 2] = ids[3, 1]
+    L = _layer_env({"MOE_FFN_MFMA_MIN": 1, "MOE_FFN_DECODE": 0}, H, I, E, K, True, N, experts_q4=bank,
+                   shared_q4=shared)
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    assert int(host(err)[0]) == 1
+    rid, rw = ids.copy(), w.copy()
+    for t, r in ((0, 0), (3, 2)):
+        rid[t, r] = next(e for e in range(E) if e not in ids[t])
+        rw[t, r] = 0.0
+    ref = O.moe_layer(x, H, I, E, bank, rid, rw, shared_q4=shared)["y"]
+    assert_close(host(y), ref, what="MFMA path, invalid routes")
+    L.close()
+
+
+def test_expf_device_matches_libm():
+    """The kernels' expf on the GPU equals the C library's expf bit for bit
+    (the function the reference's CPU SiLU calls, src/cpu_expert.cpp:251)."""
+    from test_abi import _expf_sample
+    x = _expf_sample()
+    got = host(moe_ffn.expf_device(dev(x)))
+    ref = O.expf_libm(x)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
