@@ -21,10 +21,8 @@
 // fp16 values; one v_mfma_f32_32x32x16_f16 covers 16 blocks of it (fp16
 // products are exact in fp32), and it seeds the accumulators.
 //
-// Work unit = (MFMA item of <= 128 grouped pairs of one expert, row slice).
-// Units are ordered item-major, and XCD x (workgroups x, x+8, ...) walks the
-// x-th contiguous eighth of them, so items of one expert (which read the same
-// weight rows) share an XCD's L2.
+// Work unit = (MFMA item of <= 128 grouped pairs of one expert, row slice),
+// ordered item-major and dealt to the XCDs in chunks (see mfma_unit).
 #include "moe_device.hpp"
 
 #include <algorithm>
@@ -50,14 +48,18 @@ struct Unit {
     bool ok;
 };
 
-// blockIdx -> (item, slice) with the XCD-contiguous order described above.
+// blockIdx -> (item, slice).  Workgroup i runs on XCD i % 8; XCD x takes
+// chunks of kUnitChunk consecutive units round-robin (chunk c goes to XCD
+// c % 8), so the units of one item slice share an XCD while the work of the
+// popular experts is spread over all XCDs.
+constexpr int kUnitChunk = 4;
+
 __device__ __forceinline__ Unit mfma_unit(int count, int slices) {
     const int units = count * slices;
-    const int per = (units + 7) >> 3;
-    const int n = static_cast<int>(blockIdx.x >> 3);
-    const int u = static_cast<int>(blockIdx.x & 7) * per + n;
+    const int n = static_cast<int>(blockIdx.x >> 3), x = static_cast<int>(blockIdx.x & 7);
+    const int u = ((n / kUnitChunk) * 8 + x) * kUnitChunk + n % kUnitChunk;
     Unit r;
-    r.ok = n < per && u < units;
+    r.ok = u < units;
     r.item = r.ok ? u / slices : 0;
     r.slice = r.ok ? u % slices : 0;
     return r;
@@ -313,68 +315,162 @@ __device__ __forceinline__ void lane_sums(const GuTile &t, int j, float (&a0)[16
     }
 }
 
-// v(k') = (acc[2k'] + acc[2(k'+32)]) + (acc[2k'+1] + acc[2(k'+32)+1]).
-// Single: nb <= 64, so each lane of the reference holds at most one block
-// and acc = fma(d4, t, +0).
-template<bool Single, bool Dbg>
-__device__ __forceinline__ void fold_leaf(const GuTile &t, int kp, float (&v)[16]) {
-    if constexpr (Single) {
-        const int kb = kp + 32;
-        const bool has_a = kp < t.nb, has_b = kb < t.nb;   // uniform
-        const BlockLoads la = block_loads(t, has_a ? kp : 0);
-        const BlockLoads lb = block_loads(t, has_b ? kb : 0);
-        const uint32_t da[8] = {la.d0.x, la.d0.y, la.d0.z, la.d0.w, la.d1.x, la.d1.y, la.d1.z, la.d1.w};
-        const uint32_t db[8] = {lb.d0.x, lb.d0.y, lb.d0.z, lb.d0.w, lb.d1.x, lb.d1.y, lb.d1.z, lb.d1.w};
-        const float d8a = half_lo(la.hd), c4a = -4.0f * half_hi(la.hd);
-        const float d8b = half_lo(lb.hd), c4b = -4.0f * half_hi(lb.hd);
-        float u[2][16];
-        v16i keep_a0, keep_b0;
+// ---- H <= 2048 (one block per reference lane): staged scales and heads,
+// weights and activations prefetched one leaf pair ahead.
+constexpr int kGuMaxBlocks = 64;
+
+struct GuStage {
+    const uint32_t *d4;   // LDS [nb][32 halfs] of this wave's rows (row 16h + v at half 16h + v)
+    const uint32_t *hd;   // unused
+};
+
+struct Blk {
+    uint4 w, x;           // code chunk of the lane's A row, Q8 codes of its token (16 bytes each)
+};
+
+__device__ __forceinline__ Blk blk_load(const GuTile &t, int b) {
+    const uint32_t ub = static_cast<uint32_t>(b);
+    return Blk{buffer_load16(t.wr, t.w_off, ub * 16u), buffer_load16(t.xr, t.x_off, ub * 32u)};
+}
+
+// Fragment F's dots of one block with v_mfma_i32_32x32x16_i8 (K = 16 = one
+// fragment): lane half h supplies the fragment's 8 nibbles of elements
+// 16h + 8F .. +7 and the same 8 Q8 codes.
+template<int F>
+__device__ __forceinline__ v16i frag_mfma(const Blk &k, int shift) {
+    const uint32_t w0 = F ? k.w.z : k.w.x, w1 = F ? k.w.w : k.w.y;
+    const uint32_t x0 = F ? k.x.z : k.x.x, x1 = F ? k.x.w : k.x.y;
+    const long A = static_cast<long>((static_cast<uint64_t>((w1 >> shift) & kNibbles) << 32) | ((w0 >> shift) & kNibbles));
+    const long B = static_cast<long>((static_cast<uint64_t>(x1) << 32) | x0);
+    return __builtin_amdgcn_mfma_i32_32x32x16_i8(A, B, v16i{}, 0, 0, 0);
+}
+
+// fma(d4[v], fma(float(I), d8, c4), +0): the reference's lane value of one
+// block and fragment for output register v.
+__device__ __forceinline__ float frag_value(int I, float d8, float c4, const uint32_t (&d4)[8], int v) {
+    const float t = fmaf(static_cast<float>(I), d8, c4);
+    return (v & 1) ? mul_half_hi(d4[v >> 1], t) : mul_half_lo(d4[v >> 1], t);
+}
+
+// v(k') = (acc[2k'] + acc[2(k'+32)]) + (acc[2k'+1] + acc[2(k'+32)+1]) with
+// acc[2j+f] the fragment-f value of block j (+0 past nb).  Full: nb == 64.
+// Blocks k' and k'+32 are loaded here; the fragment-0 pair is finished before
+// the fragment-1 MFMAs so only two MFMA results are live.
+template<bool Full, bool Dbg>
+__device__ __forceinline__ void leaf_staged(const GuTile &t, const GuStage &g, int kp, int m, int h, float (&v)[16]) {
+    const int jb = kp + 32;
+    const bool has_a = Full || kp < t.nb, has_b = Full || jb < t.nb;   // uniform
+    const int ja = has_a ? kp : 0, jc = has_b ? jb : 0;
+    const Blk ka = blk_load(t, ja), kb = blk_load(t, jc);
+    const uint32_t ha = buffer_load4(t.hr, t.h_off, static_cast<uint32_t>(ja) * 4u);
+    const uint32_t hb = buffer_load4(t.hr, t.h_off, static_cast<uint32_t>(jc) * 4u);
+    const uint4 *da4 = reinterpret_cast<const uint4 *>(g.d4 + ja * 16 + 8 * h);
+    const uint4 *db4 = reinterpret_cast<const uint4 *>(g.d4 + jc * 16 + 8 * h);
+    const uint4 a0 = da4[0], a1 = da4[1], b0 = db4[0], b1 = db4[1];
+    const uint32_t da[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const uint32_t db[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const float d8a = half_lo(ha), c4a = -4.0f * half_hi(ha);
+    const float d8b = half_lo(hb), c4b = -4.0f * half_hi(hb);
+    float u0[16];
+    v16i keep_a0, keep_b0;
+    {
+        const v16i Ia = frag_mfma<0>(ka, t.shift), Ib = frag_mfma<0>(kb, t.shift);
 #pragma unroll
-        for (int f = 0; f < 2; ++f) {
-            const v16i Ia = f ? fragment_dots<1>(t, la) : fragment_dots<0>(t, la);
-            const v16i Ib = f ? fragment_dots<1>(t, lb) : fragment_dots<0>(t, lb);
-            float za[16], zb[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) { za[i] = 0.0f; zb[i] = 0.0f; }
-            if (has_a) fragment_scale(za, Ia, d8a, c4a, da);
-            if (has_b) fragment_scale(zb, Ib, d8b, c4b, db);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) u[f][i] = za[i] + zb[i];
-            if constexpr (Dbg) {
-                if (f == 0) { keep_a0 = Ia; keep_b0 = Ib; }
-                else {
-                    if (has_a) store_dots<Dbg>(t, kp, keep_a0, Ia);
-                    if (has_b) store_dots<Dbg>(t, kb, keep_b0, Ib);
-                }
-            }
+        for (int i = 0; i < 16; ++i) {
+            float za = frag_value(Ia[i], d8a, c4a, da, i), zb = frag_value(Ib[i], d8b, c4b, db, i);
+            if (!Full) { za = has_a ? za : 0.0f; zb = has_b ? zb : 0.0f; }
+            u0[i] = za + zb;
         }
+        if constexpr (Dbg) { keep_a0 = Ia; keep_b0 = Ib; }
+    }
+    {
+        const v16i Ia = frag_mfma<1>(ka, t.shift), Ib = frag_mfma<1>(kb, t.shift);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = u[0][i] + u[1][i];
-    } else {
-        float a0[16], a1[16], b0[16], b1[16];
-        lane_sums<Dbg>(t, kp, a0, a1);
-        lane_sums<Dbg>(t, kp + 32, b0, b1);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = (a0[i] + b0[i]) + (a1[i] + b1[i]);
+        for (int i = 0; i < 16; ++i) {
+            float za = frag_value(Ia[i], d8a, c4a, da, i), zb = frag_value(Ib[i], d8b, c4b, db, i);
+            if (!Full) { za = has_a ? za : 0.0f; zb = has_b ? zb : 0.0f; }
+            v[i] = u0[i] + (za + zb);
+        }
+        if constexpr (Dbg) {
+            if (has_a) store_dots<Dbg>(t, kp, keep_a0, Ia);
+            if (has_b) store_dots<Dbg>(t, jb, keep_b0, Ib);
+        }
     }
     // One leaf at a time: hoisting the next leaf's loads and MFMAs above this
     // point multiplies the live registers.
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// The pairwise tree over v(0..31) in index order.  Leaves are taken two at a
-// time (a level-1 node) and merged upward like a binary counter: each level
-// holds at most one pending left operand.  Level 1 stays in registers;
-// levels 2-4 (touched every 4, 8, 16 leaves) wait in LDS (`park`, 3 x 16
-// floats per lane of this wave).
-template<bool Single, bool Dbg>
-__device__ __forceinline__ void fold_tree(const GuTile &t, float (*park)[16][64], int lane, float (&res)[16]) {
-    float l1[16];
+// Leaves 2p and 2p+1 and their merge into the pairwise tree over v(0..31):
+// leaves are taken two at a time (a level-1 node) and merged upward like a
+// binary counter, so each level holds at most one pending left operand.
+// Levels 1-2 stay in registers; levels 3-4 (touched every 8, 16 leaves) wait
+// in LDS (`park`, 2 x 16 floats per lane of this wave).
+template<bool Full, bool Dbg>
+__device__ __forceinline__ void tree_step(const GuTile &t, const GuStage &g, float (*park)[16][64], int lane, int p,
+                                          float (&l1)[16], float (&l2)[16], float (&res)[16]) {
+    const int m = lane & 31, h = lane >> 5;
+    float w[16], x[16];
+    leaf_staged<Full, Dbg>(t, g, 2 * p, m, h, w);
+    leaf_staged<Full, Dbg>(t, g, 2 * p + 1, m, h, x);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
+    if ((p & 1) == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) l1[i] = w[i];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = l1[i] + w[i];
+    if ((p & 2) == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) l2[i] = w[i];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = l2[i] + w[i];
+    int lvl = 0;
+    for (; lvl < 2; ++lvl) {
+        if (((p >> (lvl + 2)) & 1) == 0) break;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = park[lvl][i][lane] + w[i];
+    }
+    if (lvl < 2) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) park[lvl][i][lane] = w[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) res[i] = w[i];
+    }
+}
+
+template<bool Full, bool Dbg>
+__device__ __forceinline__ void fold_tree_staged(const GuTile &t, const GuStage &g, float (*park)[16][64], int lane,
+                                                 float (&res)[16]) {
+    float l1[16], l2[16];
+#pragma unroll 1
+    for (int p = 0; p < 16; ++p) tree_step<Full, Dbg>(t, g, park, lane, p, l1, l2, res);
+}
+
+// ---- H > 2048 (reference lanes holding several blocks): per-block loads.
+template<bool Dbg>
+__device__ __forceinline__ void fold_leaf_multi(const GuTile &t, int kp, float (&v)[16]) {
+    float a0[16], a1[16], b0[16], b1[16];
+    lane_sums<Dbg>(t, kp, a0, a1);
+    lane_sums<Dbg>(t, kp + 32, b0, b1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = (a0[i] + b0[i]) + (a1[i] + b1[i]);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template<bool Dbg>
+__device__ __forceinline__ void fold_tree_multi(const GuTile &t, float (*park)[16][64], int lane, float (&res)[16]) {
+    float l1[16], l2[16];
 #pragma unroll 1
     for (int p = 0; p < 16; ++p) {
         float w[16], x[16];
-        fold_leaf<Single, Dbg>(t, 2 * p, w);
-        fold_leaf<Single, Dbg>(t, 2 * p + 1, x);
+        fold_leaf_multi<Dbg>(t, 2 * p, w);
+        fold_leaf_multi<Dbg>(t, 2 * p + 1, x);
 #pragma unroll
         for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
         if ((p & 1) == 0) {
@@ -384,14 +480,20 @@ __device__ __forceinline__ void fold_tree(const GuTile &t, float (*park)[16][64]
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) w[i] = l1[i] + w[i];
+        if ((p & 2) == 0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) l2[i] = w[i];
+            continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = l2[i] + w[i];
         int lvl = 0;
-        // Levels 2..4: node index p >> (lvl + 1); odd nodes merge with the parked left operand.
-        for (; lvl < 3; ++lvl) {
-            if (((p >> (lvl + 1)) & 1) == 0) break;
+        for (; lvl < 2; ++lvl) {
+            if (((p >> (lvl + 2)) & 1) == 0) break;
 #pragma unroll
             for (int i = 0; i < 16; ++i) w[i] = park[lvl][i][lane] + w[i];
         }
-        if (lvl < 3) {
+        if (lvl < 2) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) park[lvl][i][lane] = w[i];
         } else {
@@ -410,9 +512,12 @@ __device__ __forceinline__ void fold_tree(const GuTile &t, float (*park)[16][64]
 // (item, slice, sub) so the 4 tiles of an item that read the same weight rows
 // are adjacent on one XCD.
 template<bool Dbg>
-__global__ __launch_bounds__(128) void k_gate_up_mfma(FfnArgs a) {
-    __shared__ float xch[16][64];
-    __shared__ float park[2][3][16][64];   // pending tree levels 2-4, per wave
+__global__ __launch_bounds__(128, 3) void k_gate_up_mfma(FfnArgs a) {
+    // Pending tree levels 3-4 per wave; after the tree the up wave's area
+    // carries its result to the gate wave.
+    __shared__ float park[2][2][16][64];
+    __shared__ uint4 d4_lds[2][kGuMaxBlocks][4];          // [mat][block][32 halfs]
+    float (*xch)[64] = park[1][0];
     const int lane = threadIdx.x & 63;
     const int mat = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, I = a.shape.I, nb = H / 32, nbi = I / 32;
@@ -449,13 +554,27 @@ __global__ __launch_bounds__(128) void k_gate_up_mfma(FfnArgs a) {
     t.dot_ok = Dbg && t.dots && j < ncols;
 
     float res[16];
-    if (nb <= 64) fold_tree<true, Dbg>(t, park[mat], lane, res);
-    else fold_tree<false, Dbg>(t, park[mat], lane, res);
+    if (nb <= kGuMaxBlocks) {
+        // Stage the tile's scales (both matrices) and its tokens' Q8 heads.
+        // Scale group g (rows 8g..8g+7) of block b is one 16-byte chunk of the
+        // [rows/8][blocks][8] plane and lands at halfs 8g..8g+7 of [mat][b].
+        for (int c = threadIdx.x; c < 8 * nb; c += blockDim.x) {
+            const int mm = c / (4 * nb), rem = c % (4 * nb), gi = rem / nb, b = rem % nb;
+            const uint16_t *plane = mm ? a.bank.up_scales : a.bank.gate_scales;
+            d4_lds[mm][b][gi] = *reinterpret_cast<const uint4 *>(plane + (rbase + 8 * gi) * nb + b * 8);
+        }
+        __syncthreads();
+        const GuStage g{reinterpret_cast<const uint32_t *>(&d4_lds[mat][0][0]), nullptr};
+        if (nb == kGuMaxBlocks) fold_tree_staged<true, Dbg>(t, g, park[mat], lane, res);
+        else fold_tree_staged<false, Dbg>(t, g, park[mat], lane, res);
+    } else {
+        fold_tree_multi<Dbg>(t, park[mat], lane, res);
+    }
     if (mat == 1) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) xch[v][lane] = res[v];
     }
-    __syncthreads();
+    __syncthreads();   // (the up wave's tree is done with park[1]; the gate wave's with park[0])
     if (mat != 0) return;
     int flags = 0;
     float mid[16];
@@ -487,11 +606,87 @@ __global__ __launch_bounds__(128) void k_gate_up_mfma(FfnArgs a) {
 // physical row rho = 4*(v&7) + 2*hh + (v>>3) with v = 4*(m>>3) + (m&3) and
 // hh = (m>>2)&1, so accumulator register v of lane half h is row
 // 4*(v&7) + 2h + (v>>3), whose scale sits at slot 16h + v of the
-// [rows/32][blocks][32] plane (slot (r%4)*8 + (r%32)/4): one 32-byte load per
+// [rows/32][blocks][32] plane (slot (r%4)*8 + (r%32)/4): one 32-byte read per
 // lane and block.  Before the stores, lanes l and l^32 trade 8 values so each
 // lane holds 16 consecutive rows (4 float4 stores per tile).
+//
+// I <= 512 (16 blocks): the four waves read the same middle rows, so the
+// item's middle codes and heads are staged once in LDS; each wave issues all
+// 16 weight-block loads up front and stages its 32-row scale tile in LDS.
+constexpr int kDnMaxBlocks = 16;
+
+struct DownStage {
+    uint4 x[kDnMaxBlocks][kMfmaTile][2];     // middle codes [block][pair][32 bytes]
+    uint32_t hd[kDnMaxBlocks][kMfmaTile];    // middle heads [block][pair]
+    uint4 d4[4][kDnMaxBlocks][4];            // per wave: scales [block][32 slots]
+};
+
+template<int NS, bool Dbg>
+__device__ __forceinline__ void down_staged(const FfnArgs &a, const DownStage &st, int wave, const uint4 (&wa)[kDnMaxBlocks],
+                                            int nbi, int first, int ncols, int R0, int prow, int pslot, float (&acc)[kSubs][16]) {
+    const int lane = threadIdx.x & 63, m = lane & 31, h = lane >> 5, shift = 4 * h;
+    const uint16_t *d4h = reinterpret_cast<const uint16_t *>(&st.d4[wave][0][0]);
+    // Seed: -8 * sum_b d4 s8, 16 blocks in one f16 MFMA.
+    uint32_t dw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int k0 = 8 * h + 2 * e, k1 = k0 + 1;
+        const uint32_t lo = k0 < nbi ? d4h[k0 * 32 + pslot] : 0u;
+        const uint32_t hi = k1 < nbi ? d4h[k1 * 32 + pslot] : 0u;
+        dw[e] = lo | (hi << 16);
+    }
+    const v8h da = pack8(dw);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        uint32_t sw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int k0 = 8 * h + 2 * e, k1 = k0 + 1;
+            const uint32_t lo = k0 < nbi ? st.hd[k0][kSub * s + m] >> 16 : 0u;
+            const uint32_t hi = k1 < nbi ? st.hd[k1][kSub * s + m] & 0xffff0000u : 0u;
+            sw[e] = lo | hi;
+        }
+        const v16f corr = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, pack8(sw), v16f{}, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[s][v] = -8.0f * corr[v];
+    }
+    v16i magic;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) magic[v] = kMagic;
+#pragma unroll
+    for (int b = 0; b < kDnMaxBlocks; ++b) {
+        if (b < nbi) {   // uniform; a guard rather than a break keeps the loop unrolled
+        const uint4 w = wa[b];
+        const uint4 d0 = st.d4[wave][b][2 * h], d1 = st.d4[wave][b][2 * h + 1];
+        const uint32_t d4[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+        const v4i A = {static_cast<int>((w.x >> shift) & kNibbles), static_cast<int>((w.y >> shift) & kNibbles),
+                       static_cast<int>((w.z >> shift) & kNibbles), static_cast<int>((w.w >> shift) & kNibbles)};
+        v16i r[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const uint4 xb = st.x[b][kSub * s + m][h];
+            const v4i B = {static_cast<int>(xb.x), static_cast<int>(xb.y), static_cast<int>(xb.z), static_cast<int>(xb.w)};
+            r[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, magic, 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            scale_block(acc[s], r[s], st.hd[b][kSub * s + m], d4);
+            if constexpr (Dbg) {
+                const int j = kSub * s + m;
+                if (a.down_dots && j < ncols)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        a.down_dots[(static_cast<size_t>(first + j) * a.shape.H + R0 + 4 * (v & 7) + 2 * h + (v >> 3)) * nbi + b] =
+                            r[s][v] - kMagic;
+            }
+        }
+        }
+    }
+}
+
 template<bool Dbg>
 __global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
+    __shared__ DownStage st;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = a.shape.I / 32;
@@ -501,45 +696,77 @@ __global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
     const Item *itp = a.routes.mfma_items + un.item;
     const int expert = itp->expert, first = itp->first, ncols = itp->ncols;
     const int R0 = un.slice * 128 + wave * 32;
-    if (R0 >= H) return;   // no barrier in this kernel
+    const bool active = R0 < H;      // wave-uniform
     const int nsub = (ncols + kSub - 1) / kSub;
     const int m = lane & 31, h = lane >> 5;
     const int mv = 4 * (m >> 3) + (m & 3);
     const int prow = 4 * (mv & 7) + 2 * ((m >> 2) & 1) + (mv >> 3);
     const int pslot = (prow & 3) * 8 + (prow >> 2);
 
-    const size_t rbase = static_cast<size_t>(expert) * H + R0;
+    const size_t rbase = static_cast<size_t>(expert) * H + (active ? R0 : 0);
     const uint32_t row_bytes = static_cast<uint32_t>(nbi) * 16u;
     const uint16_t *scales = a.bank.down_scales + rbase * nbi;        // [nbi][32] halfs of this 32-row group
-    const uint32_t pairs = static_cast<uint32_t>(a.pairs_bound);
-    TileArgs t;
-    t.wr = buffer_rsrc(a.bank.down_codes + rbase * row_bytes, 32u * row_bytes);
-    t.sr = buffer_rsrc(scales, static_cast<uint32_t>(nbi) * 64u);
-    t.xr = buffer_rsrc(a.mq.codes, pairs * static_cast<uint32_t>(nbi) * 32u);
-    t.hr = buffer_rsrc(a.mq.heads, pairs * static_cast<uint32_t>(nbi) * 4u);
-    t.w_off = static_cast<uint32_t>(prow) * row_bytes;
-    t.s_off0 = 32u * h;
-    t.s_off1 = 32u * h + 16u;
-    t.s_step = 64u;
-#pragma unroll
-    for (int s = 0; s < kSubs; ++s) {
-        const uint32_t p = static_cast<uint32_t>(first + std::min(kSub * s + m, ncols - 1));
-        t.x_off[s] = p * static_cast<uint32_t>(nbi) * 32u + 16u * h;
-        t.h_off[s] = p * static_cast<uint32_t>(nbi) * 4u;
-    }
-    t.cscale = scales + pslot;
-    t.cstride = 32;
-    t.nb = nbi;
-    t.shift = 4 * h;
-    t.dots = Dbg ? a.down_dots : nullptr;
-    t.dot_rows = static_cast<size_t>(H);
-    t.dot_row0 = R0;
-    t.dot_pair0 = first;
-    t.ncols = ncols;
-    t.m = m;
-    t.h = h;
     float acc[kSubs][16];
-    tile_dispatch<Dbg, true>(t, nsub, acc);
+    if (nbi <= kDnMaxBlocks) {
+        // Weight blocks first (their HBM latency overlaps the staging).
+        const auto wr = buffer_rsrc(a.bank.down_codes + rbase * row_bytes, 32u * row_bytes);
+        const uint32_t w_off = static_cast<uint32_t>(prow) * row_bytes;
+        uint4 wa[kDnMaxBlocks];
+#pragma unroll
+        for (int b = 0; b < kDnMaxBlocks; ++b) wa[b] = buffer_load16(wr, w_off, static_cast<uint32_t>(b < nbi ? b : 0) * 16u);
+        // Middle codes and heads of the item's pairs (zero past ncols).
+        const int cols = nsub * kSub;
+        for (int c = threadIdx.x; c < cols * nbi * 2; c += blockDim.x) {
+            const int j = c / (2 * nbi), rem = c % (2 * nbi), b = rem >> 1, hf = rem & 1;
+            st.x[b][j][hf] = j < ncols ? *reinterpret_cast<const uint4 *>(a.mq.codes + (static_cast<size_t>(first + j) * nbi + b) * 32 + 16 * hf)
+                                       : make_uint4(0, 0, 0, 0);
+        }
+        for (int c = threadIdx.x; c < cols * nbi; c += blockDim.x) {
+            const int j = c / nbi, b = c % nbi;
+            st.hd[b][j] = j < ncols ? a.mq.heads[static_cast<size_t>(first + j) * nbi + b] : 0u;
+        }
+        if (active)
+            for (int c = lane; c < nbi * 4; c += 64)
+                st.d4[wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(scales)[c];
+        __syncthreads();
+        if (!active) return;
+        switch (nsub) {
+        case 1: down_staged<1, Dbg>(a, st, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
+        case 2: down_staged<2, Dbg>(a, st, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
+        case 3: down_staged<3, Dbg>(a, st, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
+        default: down_staged<4, Dbg>(a, st, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
+        }
+    } else {
+        if (!active) return;   // no barrier on this path
+        const uint32_t pairs = static_cast<uint32_t>(a.pairs_bound);
+        TileArgs t;
+        t.wr = buffer_rsrc(a.bank.down_codes + rbase * row_bytes, 32u * row_bytes);
+        t.sr = buffer_rsrc(scales, static_cast<uint32_t>(nbi) * 64u);
+        t.xr = buffer_rsrc(a.mq.codes, pairs * static_cast<uint32_t>(nbi) * 32u);
+        t.hr = buffer_rsrc(a.mq.heads, pairs * static_cast<uint32_t>(nbi) * 4u);
+        t.w_off = static_cast<uint32_t>(prow) * row_bytes;
+        t.s_off0 = 32u * h;
+        t.s_off1 = 32u * h + 16u;
+        t.s_step = 64u;
+#pragma unroll
+        for (int s = 0; s < kSubs; ++s) {
+            const uint32_t p = static_cast<uint32_t>(first + std::min(kSub * s + m, ncols - 1));
+            t.x_off[s] = p * static_cast<uint32_t>(nbi) * 32u + 16u * h;
+            t.h_off[s] = p * static_cast<uint32_t>(nbi) * 4u;
+        }
+        t.cscale = scales + pslot;
+        t.cstride = 32;
+        t.nb = nbi;
+        t.shift = 4 * h;
+        t.dots = Dbg ? a.down_dots : nullptr;
+        t.dot_rows = static_cast<size_t>(H);
+        t.dot_row0 = R0;
+        t.dot_pair0 = first;
+        t.ncols = ncols;
+        t.m = m;
+        t.h = h;
+        tile_dispatch<Dbg, true>(t, nsub, acc);
+    }
 
     // Lane half h holds rows 4q + 2h (v = q) and 4q + 2h + 1 (v = 8 + q),
     // q = 0..7.  After the trade lane half h holds rows 16h .. 16h + 15.
@@ -568,7 +795,8 @@ unsigned mfma_grid(const FfnArgs &a, int slices) {
     const size_t bound = static_cast<size_t>(a.pairs_bound) / kMfmaTile +
                          static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep));
     const size_t units = bound * static_cast<size_t>(slices);
-    return static_cast<unsigned>((units + 7) / 8 * 8);
+    const size_t round = 8 * static_cast<size_t>(kUnitChunk);
+    return static_cast<unsigned>((units + round - 1) / round * round);
 }
 
 }  // namespace
