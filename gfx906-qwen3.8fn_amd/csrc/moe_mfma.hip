@@ -452,6 +452,132 @@ __device__ __forceinline__ void fold_tree_staged(const GuTile &t, const GuStage 
     for (int p = 0; p < 16; ++p) tree_step<Full, Dbg>(t, g, park, lane, p, l1, l2, res);
 }
 
+// ---- H == 2048 (64 blocks): loads in groups of four leaves that use whole
+// cache lines.  Group g covers blocks 4g..4g+3 and 4g+32..4g+35.  Lane half
+// h of row m reads 64 contiguous bytes of its row (blocks 4g+32h+i); a
+// v_permlane32_swap of the low- and high-nibble words then gives, per leaf,
+// the MFMA operand of block 4g+i (low nibbles in lanes < 32, high in lanes
+// >= 32) and of block 4g+32+i.  Lane half h of token n reads bytes
+// 16h..16h+15 of four consecutive 32-byte Q8 blocks, so the two halves of a
+// token use the same lines.
+struct Group {
+    uint4 w[4];           // A row: blocks 4g+i (h = 0) / 4g+32+i (h = 1)
+    uint4 xa[4], xb[4];   // token codes, half h: blocks 4g+i / 4g+32+i
+    uint4 ha, hb;         // token heads of blocks 4g..4g+3 / 4g+32..4g+35
+};
+
+__device__ __forceinline__ void group_load(const GuTile &t, uint32_t w_off, int g, Group &G) {
+    const uint32_t b0 = static_cast<uint32_t>(4 * g);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) G.w[i] = buffer_load16(t.wr, w_off, (b0 + i) * 16u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) G.xa[i] = buffer_load16(t.xr, t.x_off, (b0 + i) * 32u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) G.xb[i] = buffer_load16(t.xr, t.x_off, (b0 + 32 + i) * 32u);
+    G.ha = buffer_load16(t.hr, t.h_off, b0 * 4u);
+    G.hb = buffer_load16(t.hr, t.h_off, (b0 + 32) * 4u);
+}
+
+__device__ __forceinline__ v16i frag_mfma2(uint32_t a0, uint32_t a1, uint32_t x0, uint32_t x1) {
+    const long A = static_cast<long>((static_cast<uint64_t>(a1) << 32) | a0);
+    const long B = static_cast<long>((static_cast<uint64_t>(x1) << 32) | x0);
+    return __builtin_amdgcn_mfma_i32_32x32x16_i8(A, B, v16i{}, 0, 0, 0);
+}
+
+template<bool Dbg>
+__device__ __forceinline__ void leaf_grouped(const GuTile &t, const GuStage &g, const Group &G, int i, int kp, int m,
+                                             int h, float (&v)[16]) {
+    const uint4 wi = G.w[i];
+    const uint32_t wv[4] = {wi.x, wi.y, wi.z, wi.w};
+    uint32_t opa[4], opb[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const auto r = __builtin_amdgcn_permlane32_swap(wv[d] & kNibbles, (wv[d] >> 4) & kNibbles, false, false);
+        opa[d] = r[0];   // block kp: low nibbles (lanes < 32), high nibbles (lanes >= 32)
+        opb[d] = r[1];   // block kp + 32
+    }
+    const uint32_t ha = (&G.ha.x)[i], hb = (&G.hb.x)[i];
+    const uint4 *da4 = reinterpret_cast<const uint4 *>(g.d4 + kp * 16 + 8 * h);
+    const uint4 *db4 = reinterpret_cast<const uint4 *>(g.d4 + (kp + 32) * 16 + 8 * h);
+    const uint4 a0 = da4[0], a1 = da4[1], b0 = db4[0], b1 = db4[1];
+    const uint32_t da[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const uint32_t db[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const float d8a = half_lo(ha), c4a = -4.0f * half_hi(ha);
+    const float d8b = half_lo(hb), c4b = -4.0f * half_hi(hb);
+    const uint4 xa = G.xa[i], xb = G.xb[i];
+    float u0[16];
+    v16i keep_a0, keep_b0;
+    {
+        const v16i Ia = frag_mfma2(opa[0], opa[1], xa.x, xa.y), Ib = frag_mfma2(opb[0], opb[1], xb.x, xb.y);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) u0[j] = frag_value(Ia[j], d8a, c4a, da, j) + frag_value(Ib[j], d8b, c4b, db, j);
+        if constexpr (Dbg) { keep_a0 = Ia; keep_b0 = Ib; }
+    }
+    {
+        const v16i Ia = frag_mfma2(opa[2], opa[3], xa.z, xa.w), Ib = frag_mfma2(opb[2], opb[3], xb.z, xb.w);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = u0[j] + (frag_value(Ia[j], d8a, c4a, da, j) + frag_value(Ib[j], d8b, c4b, db, j));
+        if constexpr (Dbg) {
+            store_dots<Dbg>(t, kp, keep_a0, Ia);
+            store_dots<Dbg>(t, kp + 32, keep_b0, Ib);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Tree merge of the level-1 node p (= w) as in tree_step.
+__device__ __forceinline__ void tree_merge(float (*park)[16][64], int lane, int p, float (&w)[16], float (&l1)[16],
+                                           float (&l2)[16], float (&res)[16]) {
+    if ((p & 1) == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) l1[i] = w[i];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = l1[i] + w[i];
+    if ((p & 2) == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) l2[i] = w[i];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = l2[i] + w[i];
+    int lvl = 0;
+    for (; lvl < 2; ++lvl) {
+        if (((p >> (lvl + 2)) & 1) == 0) break;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = park[lvl][i][lane] + w[i];
+    }
+    if (lvl < 2) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) park[lvl][i][lane] = w[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) res[i] = w[i];
+    }
+}
+
+template<bool Dbg>
+__device__ __forceinline__ void fold_tree_grouped(const GuTile &t, const GuStage &g, uint32_t w_off, float (*park)[16][64],
+                                                  int lane, float (&res)[16]) {
+    const int m = lane & 31, h = lane >> 5;
+    float l1[16], l2[16];
+#pragma unroll 1
+    for (int gi = 0; gi < 8; ++gi) {
+        Group G;
+        group_load(t, w_off, gi, G);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            float w[16], x[16];
+            leaf_grouped<Dbg>(t, g, G, 2 * half, 4 * gi + 2 * half, m, h, w);
+            leaf_grouped<Dbg>(t, g, G, 2 * half + 1, 4 * gi + 2 * half + 1, m, h, x);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
+            tree_merge(park, lane, 2 * gi + half, w, l1, l2, res);
+        }
+    }
+}
+
 // ---- H > 2048 (reference lanes holding several blocks): per-block loads.
 template<bool Dbg>
 __device__ __forceinline__ void fold_leaf_multi(const GuTile &t, int kp, float (&v)[16]) {
@@ -512,7 +638,7 @@ __device__ __forceinline__ void fold_tree_multi(const GuTile &t, float (*park)[1
 // (item, slice, sub) so the 4 tiles of an item that read the same weight rows
 // are adjacent on one XCD.
 template<bool Dbg>
-__global__ __launch_bounds__(128, 3) void k_gate_up_mfma(FfnArgs a) {
+__global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
     // Pending tree levels 3-4 per wave; after the tree the up wave's area
     // carries its result to the gate wave.
     __shared__ float park[2][2][16][64];
@@ -565,7 +691,8 @@ __global__ __launch_bounds__(128, 3) void k_gate_up_mfma(FfnArgs a) {
         }
         __syncthreads();
         const GuStage g{reinterpret_cast<const uint32_t *>(&d4_lds[mat][0][0]), nullptr};
-        if (nb == kGuMaxBlocks) fold_tree_staged<true, Dbg>(t, g, park[mat], lane, res);
+        if (nb == kGuMaxBlocks)
+            fold_tree_grouped<Dbg>(t, g, static_cast<uint32_t>(prow) * row_bytes + 32u * 16u * h, park[mat], lane, res);
         else fold_tree_staged<false, Dbg>(t, g, park[mat], lane, res);
     } else {
         fold_tree_multi<Dbg>(t, park[mat], lane, res);
