@@ -3,8 +3,12 @@
 A "step" is one MoE layer forward (quantize + group + gate/up/SiLU/Q8 + down +
 rank-order fold + shared expert) over one batch of synthetic tokens with all
 inputs resident in HBM.  The headline workload is BASELINE configs[1], B8
-decode (8 tokens, top-10 of 512 experts + 1 shared, H 2048, I 512); the 4K
-Zipf(1.1) prefill layer is reported alongside under "prefill_4k".
+decode (8 tokens, top-10 of 512 experts + 1 shared, H 2048, I 512).  Reported
+alongside: the 4K Zipf(1.1) prefill layer (configs[2], "prefill_4k"), the 16K
+uniform prefill layer (configs[3], "prefill_16k"), the 48-layer stack of 8 + 1024
+tokens with Zipf(1.3) routing (configs[4], "stack_48"), and the practical HBM
+ceiling at the decode gate/up kernel's byte count ("read_ceiling": a plain
+streaming read of the same number of bytes, cold).
 
 Prints ONE JSON line.  --gpus above 1 is refused: this build runs on one GPU.
 """
@@ -86,6 +90,58 @@ def pmc_traffic(kernel, units):
     return rec["traffic_bytes"] / rec["units"] * units
 
 
+def read_ceiling(nbytes, buffers=12, iters=48):
+    """Time the library's plain streaming-read kernel (moe_read_probe) over
+    `nbytes`, rotating `buffers` distinct buffers (together larger than the
+    256 MB Infinity Cache) so every read is cold.  Returns seconds per read."""
+    import torch
+    import moe_ffn
+    nbytes = nbytes // 16 * 16
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device="cuda:0") for _ in range(buffers)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    for b in bufs[:2]:
+        moe_ffn.read_probe(b, sink)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(iters):
+        moe_ffn.read_probe(bufs[i % buffers], sink)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    del bufs
+    return e0.elapsed_time(e1) / 1e3 / iters
+
+
+def time_stack(layers, inputs, steps, warmup):
+    """Seconds per pass of the whole stack: layer l runs on its own resident
+    batch inputs[l] = (x, ids, weights), back to back on one stream."""
+    import torch
+    outs = [torch.empty((x.shape[0], L.H), dtype=torch.float32, device=x.device) for L, (x, _, _) in
+            zip(layers, inputs)]
+    err = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+
+    def one_pass():
+        for L, (x, i, w), y in zip(layers, inputs, outs):
+            L.forward(x, i, w, y=y, error=err)
+
+    for _ in range(warmup):
+        one_pass()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        one_pass()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    if int(err.cpu()[0]) != 0:
+        raise RuntimeError(f"error flags {int(err.cpu()[0])}")
+    return wall, e0.elapsed_time(e1) / 1e3 / steps
+
+
 def cpu_baseline(x, bank, shared, ids, w, target_seconds):
     import oracle as O
     cpus = O.physical_cpus()
@@ -106,6 +162,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-16k", action="store_true", help="skip the 16K uniform prefill layer (configs[3])")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 48-layer stack (configs[4])")
+    ap.add_argument("--stack-steps", type=int, default=5)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy x5 (FETCH_SIZE/WRITE_SIZE scale for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -130,7 +189,7 @@ def main():
     log("[bench] generating Q4_0 bank (512 experts + shared)")
     bank = W.q4_bank(512, seed=1000)
     shared = W.q4_bank(1, seed=1001)
-    max_tokens = 8 if args.no_prefill else 4096
+    max_tokens = 8 if args.no_prefill else 4096 if args.no_16k else 16384
     layer = moe_ffn.MoeLayer(2048, 512, 512, 10, True, max_tokens, experts_q4=bank, shared_q4=shared)
 
     # ---- B8 decode (headline) -------------------------------------------
@@ -182,6 +241,15 @@ def main():
         "stages_us": {"prepare": t_prep * 1e6, "gate_up": t_gate * 1e6, "down": t_down * 1e6, "fold": t_fold * 1e6},
         "down_stage_hbm_frac": down_bytes / float(t_stage[2]) / 1e9 / HBM_PEAK_GBS,
     }
+    # Practical ceiling: a plain streaming read of the same byte count.
+    t_read = read_ceiling(int(gate_bytes / n_stage))
+    result["read_ceiling"] = {
+        "bytes": int(gate_bytes / n_stage) // 16 * 16, "us": t_read * 1e6,
+        "GB/s": gate_bytes / n_stage / t_read / 1e9, "frac_of_peak": gate_bytes / n_stage / t_read / 1e9 / HBM_PEAK_GBS,
+        "gate_up_frac_of_ceiling": t_read / t_gate,
+    }
+    log(f"[bench] read ceiling at {gate_bytes / n_stage / 1e6:.1f} MB: {t_read * 1e6:.1f} us "
+        f"({gate_bytes / n_stage / t_read / 1e9:.0f} GB/s)")
 
     # ---- 4K Zipf prefill (reported beside) --------------------------------
     if not args.no_prefill:
@@ -200,6 +268,49 @@ def main():
         }
         log(f"[bench] 4k prefill {wall_p*1e3:.3f} ms/layer, {NP/wall_p:.0f} tok/s")
 
+    # ---- 16K uniform prefill -----------------------------------
+    if not args.no_prefill and not args.no_16k:
+        NP = 16384
+        xph = W.activations(NP, seed=3002)
+        idp, wp = W.routes_uniform(NP, seed=3003)
+        hp = W.group_histogram(idp)
+        log(f"[bench] 16k prefill: {hp}")
+        wall_p, gpu_p, _ = time_forward(layer, dev(xph), [(dev(idp), dev(wp))], max(3, args.prefill_steps // 2), 2)
+        ops = W.int8_ops(NP)
+        pbytes = W.algorithmic_bytes(NP, hp["touched"])
+        result["prefill_16k"] = {
+            "tokens_per_s": NP / wall_p, "ms_per_layer": wall_p * 1e3, "gpu_event_ms": gpu_p * 1e3,
+            "int8_tops": ops / gpu_p / 1e12, "int8_mfma_frac": ops / gpu_p / 1e12 / INT8_PEAK_TOPS,
+            "hbm_frac": pbytes / gpu_p / 1e9 / HBM_PEAK_GBS, "group_hist": hp, "items": layer.last_stats(),
+        }
+        log(f"[bench] 16k prefill {wall_p*1e3:.3f} ms/layer, {NP/wall_p:.0f} tok/s")
+
+    # ---- 48-layer stack, 8 decode + 1024 prefill tokens per layer --
+    if not args.no_stack:
+        NL, NS = 48, 8 + 1024
+        layer.close()
+        layer = None
+        torch.cuda.empty_cache()
+        layers, inputs, touched_s = [], [], []
+        for l in range(NL):
+            layers.append(moe_ffn.MoeLayer(2048, 512, 512, 10, True, NS, synthetic_seed=5000 + l))
+            ids_l, w_l = W.routes_zipf(NS, 1.3, seed=6000 + l)
+            touched_s.append(W.group_histogram(ids_l)["touched"])
+            inputs.append((dev(W.activations(NS, seed=7000 + l)), dev(ids_l), dev(w_l)))
+        wall_s, gpu_s = time_stack(layers, inputs, args.stack_steps, 1)
+        sbytes = float(sum(W.algorithmic_bytes(NS, t) for t in touched_s))
+        resident = moe_ffn.memory_bytes(2048, 512, 512, 10, True, NS)[0] * NL
+        result["stack_48"] = {
+            "ms_per_stack": wall_s * 1e3, "gpu_event_ms": gpu_s * 1e3, "us_per_layer": wall_s / NL * 1e6,
+            "tokens_per_s": NS / wall_s, "tokens_per_layer": NS,
+            "hbm_frac": sbytes / gpu_s / 1e9 / HBM_PEAK_GBS, "int8_tops": W.int8_ops(NS) * NL / gpu_s / 1e12,
+            "touched_experts_mean": float(np.mean(touched_s)), "resident_weight_gb": resident / 1e9,
+        }
+        log(f"[bench] stack of {NL}: {wall_s*1e3:.2f} ms/pass, {wall_s/NL*1e6:.1f} us/layer, "
+            f"touched {np.mean(touched_s):.1f}, resident {resident/1e9:.2f} GB")
+        for L in layers:
+            L.close()
+
     # ---- CPU baseline (same weights and inputs) ----------------------------
     if not args.no_cpu:
         idh, wh = route_sets[0]
@@ -211,7 +322,8 @@ def main():
         }
         log(f"[bench] cpu {sec*1e3:.3f} ms/layer with {used} workers")
     print(json.dumps(result), flush=True)
-    layer.close()
+    if layer is not None:
+        layer.close()
 
 
 if __name__ == "__main__":

@@ -116,6 +116,7 @@ struct FfnArgs {
     int out_stride_k;  // rows per token in `out` (k+1 for forward, 1 for stages)
     int tokens;
     int pairs_bound;   // upper bound on grouped pairs (for grid sizing)
+    int mfma_min;      // groups of >= mfma_min pairs are MFMA items (0: none; 1: all)
     float *middle_f32; // optional [pairs][I]
     int32_t *gate_dots, *up_dots, *down_dots;  // optional per-block dots [pair][rows][blocks]
     int *error;
@@ -158,6 +159,7 @@ hipError_t launch_fold(const float *contributions, size_t token_stride, const fl
                        hipStream_t s);
 
 hipError_t launch_fill_u32(uint32_t *p, uint32_t value, size_t count, hipStream_t s);
+hipError_t launch_read_probe(const void *p, size_t bytes, uint32_t *sink, hipStream_t s);
 hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s);
 
 }  // namespace moe

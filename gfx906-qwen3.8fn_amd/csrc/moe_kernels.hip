@@ -115,6 +115,29 @@ __global__ __launch_bounds__(256) void k_synthetic(uint32_t *codes, uint16_t *sc
     scales[scale_index(b / nb, static_cast<int>(b % nb), nb, group)] = static_cast<uint16_t>(f2h(fabsf(z) * 0.02f));
 }
 
+// Plain streaming read of n 16-byte words, one contiguous chunk per
+// workgroup, eight loads in flight per thread; the XOR of the words is kept
+// only so that the loads cannot be dropped (written when it equals `never`).
+// It measures how fast this device streams a buffer of a given size from HBM,
+// the practical ceiling the decode kernels are compared with.
+__global__ __launch_bounds__(512) void k_read_probe(const uint4 *__restrict__ p, size_t n, size_t chunk,
+                                                    uint32_t never, uint32_t *sink) {
+    const size_t b = static_cast<size_t>(blockIdx.x) * chunk;
+    const size_t e = b + chunk < n ? b + chunk : n;
+    uint32_t acc = 0;
+    for (size_t i = b + threadIdx.x; i < e; i += static_cast<size_t>(blockDim.x) * 8) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const size_t j = i + static_cast<size_t>(u) * blockDim.x;
+            v[u] = j < e ? p[j] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == never) sink[0] = acc;
+}
+
 __global__ __launch_bounds__(256) void k_expf(const float *x, float *y, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) y[i] = moe_expf(x[i]);
@@ -1129,6 +1152,14 @@ hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, size_t blo
     return hipGetLastError();
 }
 
+hipError_t launch_read_probe(const void *p, size_t bytes, uint32_t *sink, hipStream_t s) {
+    const size_t n = bytes / 16;
+    const unsigned grid = 4096;   // best of 256..8192 for 45-180 MiB on MI355X
+    const size_t chunk = (n + grid - 1) / grid;
+    k_read_probe<<<grid, 512, 0, s>>>(static_cast<const uint4 *>(p), n, chunk, 0x9e3779b9u, sink);
+    return hipGetLastError();
+}
+
 hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s) {
     k_expf<<<blocks_for(static_cast<size_t>(n), 256), 256, 0, s>>>(x, y, n);
     return hipGetLastError();
@@ -1181,17 +1212,21 @@ hipError_t launch_single_expert_items(Shape shape, RouteOut routes, int expert, 
 namespace {
 // Upper bound on streaming items (the size the item array is allocated for):
 // one partial item per nonempty group plus full items.
+// Upper bound on the streaming items the device can produce: a group of n
+// pairs gives ceil(n / 4) items, so at most one partial item per nonempty
+// group plus full items; with mfma_min >= 2 only groups of < mfma_min pairs
+// stream, each giving at most ceil((mfma_min - 1) / 4) items.
 unsigned stream_item_bound(const FfnArgs &a) {
-    return static_cast<unsigned>(static_cast<size_t>(a.pairs_bound) / kStreamTokens +
-                                 static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep)));
+    const size_t P = static_cast<size_t>(a.pairs_bound);
+    const size_t G = std::min(P, static_cast<size_t>(a.shape.Ep));
+    size_t b = P / kStreamTokens + G;
+    if (a.mfma_min >= 2) b = std::min(b, G * ((a.mfma_min - 1 + kStreamTokens - 1) / kStreamTokens));
+    return static_cast<unsigned>(std::max<size_t>(b, 1));
 }
 
 unsigned stream_grid(const FfnArgs &a, int slices) {
-    // Upper bound on streaming items: one partial item per nonempty group plus
-    // full items; the persistent loop covers whatever the device produced.
-    const size_t bound = static_cast<size_t>(a.pairs_bound) / kStreamTokens +
-                         static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep));
-    const size_t units = bound * slices;
+    // The persistent loop covers whatever the device produced.
+    const size_t units = static_cast<size_t>(stream_item_bound(a)) * slices;
     return static_cast<unsigned>(std::min<size_t>(units, 4096));
 }
 }  // namespace

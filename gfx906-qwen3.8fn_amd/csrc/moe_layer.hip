@@ -32,7 +32,14 @@ struct moe_ffn_layer {
     Act xq{}, mq{};
     RouteOut routes{};
     float *contrib = nullptr;
-    int mfma_min = 1;     // smallest group routed to the MFMA path (0 = streaming only)
+    // Smallest group routed to the MFMA path (0 = streaming only).  An MFMA
+    // tile spends the same exact-order epilogue on 32 token columns however
+    // many are filled, and a one-tile group streams its weights from HBM with
+    // little reuse, so groups below 16 pairs stream: measured on MI355X, 16-20
+    // is best for 4K Zipf(1.1) (2.58 vs 2.70 ms at 1), 1032-token Zipf(1.3)
+    // (0.90 vs 1.71 ms) and 256 tokens (0.40 vs 1.21 ms), and neutral at 16K
+    // uniform, whose groups all exceed 256.
+    int mfma_min = 16;
     int decode_mode = -1; // ungrouped decode path: -1 auto, 0 never, 1 whenever shapes allow
     bool last_decode = false;
     int cu_count = 256;   // compute units of the device
@@ -286,6 +293,7 @@ moe::FfnArgs base_args(moe_ffn_layer *L, int tokens, int *error) {
     a.out_stride_k = L->shape.k + 1;
     a.tokens = tokens;
     a.pairs_bound = static_cast<int>(pairs_capacity(L->shape, tokens));
+    a.mfma_min = L->mfma_min;
     a.error = error;
     a.cu_count = L->cu_count;
     return a;
@@ -559,6 +567,7 @@ int moe_ffn_expert_gate_up(moe_ffn_layer *L, int expert, const void *x_q8, int c
     if ((r = moe::launch_single_expert_items(sh, L->routes, expert, columns, mfma, s)) != hipSuccess) return r;
     moe::FfnArgs a = base_args(L, columns, error);
     a.pairs_bound = columns;
+    a.mfma_min = mfma ? 1 : 0;   // the single group is an MFMA item or streaming items
     a.middle_f32 = middle;
     a.gate_dots = gate_dots;
     a.up_dots = up_dots;
@@ -581,6 +590,7 @@ int moe_ffn_expert_down(moe_ffn_layer *L, int expert, const void *middle_q8, int
     if ((r = moe::launch_single_expert_items(sh, L->routes, expert, columns, mfma, s)) != hipSuccess) return r;
     moe::FfnArgs a = base_args(L, columns, error);
     a.pairs_bound = columns;
+    a.mfma_min = mfma ? 1 : 0;   // the single group is an MFMA item or streaming items
     a.out = y;
     a.out_stride_k = 1;
     a.down_dots = down_dots;
@@ -647,6 +657,11 @@ int moe_ffn_last_stats(moe_ffn_layer *L, int32_t *stream_items, int32_t *mfma_it
 int moe_expf_device(const float *x, float *y, int n, void *stream) {
     if (!aligned(x, 4) || !aligned(y, 4) || n < 1) return kInvalid;
     return moe::launch_expf(x, y, n, static_cast<hipStream_t>(stream));
+}
+
+int moe_read_probe(const void *buffer, size_t bytes, void *sink, void *stream) {
+    if (!aligned(buffer, 16) || !aligned(sink, 4) || bytes < 16 || bytes % 16 != 0) return kInvalid;
+    return moe::launch_read_probe(buffer, bytes, static_cast<uint32_t *>(sink), static_cast<hipStream_t>(stream));
 }
 
 int moe_expf_host(const float *x, float *y, size_t n) {

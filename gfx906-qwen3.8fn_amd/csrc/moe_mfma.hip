@@ -918,9 +918,13 @@ __global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
     }
 }
 
+// Upper bound on MFMA items: a group of n >= mfma_min pairs gives
+// ceil(n / 128) items, and at most min(Ep, pairs / mfma_min) groups qualify.
 unsigned mfma_grid(const FfnArgs &a, int slices) {
-    const size_t bound = static_cast<size_t>(a.pairs_bound) / kMfmaTile +
-                         static_cast<size_t>(std::min(a.pairs_bound, a.shape.Ep));
+    const size_t P = static_cast<size_t>(a.pairs_bound);
+    const size_t G = std::min(P, static_cast<size_t>(a.shape.Ep));
+    const size_t big = a.mfma_min >= 1 ? std::min(G, P / static_cast<size_t>(a.mfma_min)) : G;
+    const size_t bound = std::max<size_t>(P / kMfmaTile + big, 1);
     const size_t units = bound * static_cast<size_t>(slices);
     const size_t round = 8 * static_cast<size_t>(kUnitChunk);
     return static_cast<unsigned>((units + round - 1) / round * round);

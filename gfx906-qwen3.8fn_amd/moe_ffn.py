@@ -71,6 +71,7 @@ def library():
         lib.moe_ffn_profile_read.argtypes = [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]
         lib.moe_expf_device.argtypes = [_P, _P, _I, _P]
         lib.moe_expf_host.argtypes = [_P, _P, ctypes.c_size_t]
+        lib.moe_read_probe.argtypes = [_P, ctypes.c_size_t, _P, _P]
         lib.moe_ffn_last_stats.argtypes = [_P, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
                                            ctypes.POINTER(ctypes.c_int32)]
         _lib = lib
@@ -264,6 +265,12 @@ def expf_device(x, stream=None):
     y = torch.empty_like(x)
     _check(library().moe_expf_device(_ptr(x), _ptr(y), x.numel(), _stream(stream)), "moe_expf_device")
     return y
+
+
+def read_probe(buffer, sink, nbytes=None, stream=None):
+    """Enqueue a plain streaming read of `nbytes` (default: all) of a device tensor."""
+    n = buffer.numel() * buffer.element_size() if nbytes is None else nbytes
+    _check(library().moe_read_probe(_ptr(buffer), n, _ptr(sink), _stream(stream)), "moe_read_probe")
 
 
 def quantize_q8_1(x, error=None, stream=None):

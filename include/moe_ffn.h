@@ -200,6 +200,13 @@ int moe_ffn_last_stats(moe_ffn_layer *layer, int32_t *stream_items, int32_t *mfm
 int moe_expf_device(const float *x, float *y, int n, void *stream);
 int moe_expf_host(const float *x, float *y, size_t n);
 
+/* Measurement hook: enqueue a plain streaming read of `bytes` (a multiple of
+ * 16, buffer 16-byte aligned) from device memory; `sink` is a device word the
+ * kernel never writes in practice.  Timing it at a kernel's byte count gives
+ * the practical HBM read ceiling for a launch of that size.  No counterpart
+ * in the reference. */
+int moe_read_probe(const void *buffer, size_t bytes, void *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -286,6 +286,72 @@ def test_prefill_4k_zipf_sampled_tokens(moe512):
     layer_parity(L, x, ids, w, moe512["bank"], moe512["shared"], yh, sample, "4K prefill")
 
 
+def test_prefill_16k_uniform_sampled_tokens(moe512):
+    """16384 tokens, uniform top-10 (every group ~320
+    wide, all on the MFMA path).  Sampled tokens against the oracle, plus
+    determinism of the whole output."""
+    L = moe_ffn.MoeLayer(2048, 512, 512, 10, True, 16384, experts_q4=moe512["bank"], shared_q4=moe512["shared"])
+    x = W.activations(16384, seed=56)
+    ids, w = W.routes_uniform(16384, seed=57)
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    yh = host(y)
+    assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
+    st = L.last_stats()
+    assert st["stream_items"] == 0 and st["mfma_items"] > 0 and st["active_experts"] == 513
+    sample = np.random.default_rng(58).choice(16384, 16, replace=False)
+    layer_parity(L, x, ids, w, moe512["bank"], moe512["shared"], yh, sample, "16K prefill")
+    y2, _ = L.forward(dev(x), dev(ids), dev(w))
+    assert np.array_equal(host(y2), yh)
+    L.close()
+
+
+def _sparse_bank(L, experts):
+    """Canonical bank of layer L with only `experts` exported (others zero)."""
+    eb = moe_ffn.expert_bytes(L.H, L.I)
+    bank = np.zeros(L.E * eb, np.uint8)
+    for e in sorted(set(int(e) for e in experts)):
+        bank[e * eb:(e + 1) * eb] = L.export_expert(e)
+    return bank
+
+
+def test_stack_layers_mixed_batch():
+    """BASELINE configs[4] in miniature: three resident layers with their own
+    seeded weights, each run on a mixed batch of 8 decode + 1024 prefill
+    tokens with Zipf(1.3) routing, back to back on one stream; then every
+    layer's output is checked against the oracle on its 8 decode tokens and 8
+    sampled prefill tokens (weights exported from the device bank)."""
+    NS = 8 + 1024
+    layers = [moe_ffn.MoeLayer(2048, 512, 512, 10, True, NS, synthetic_seed=900 + l) for l in range(3)]
+    runs = []
+    for l, L in enumerate(layers):
+        x = W.activations(NS, seed=910 + l)
+        ids, w = W.routes_zipf(NS, 1.3, seed=920 + l)
+        runs.append((x, ids, w, L.forward(dev(x), dev(ids), dev(w))))
+    rng = np.random.default_rng(930)
+    for l, (L, (x, ids, w, (y, err))) in enumerate(zip(layers, runs)):
+        yh = host(y)
+        assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
+        sample = np.concatenate([np.arange(8), 8 + rng.choice(1024, 8, replace=False)])
+        bank = _sparse_bank(L, ids[sample].reshape(-1))
+        shared = L.export_expert(L.E)
+        # debug_last holds the most recent forward of this handle, which is
+        # this layer's own (each layer has its own workspace).
+        layer_parity(L, x, ids, w, bank, shared, yh, sample, f"stack layer {l}")
+    for L in layers:
+        L.close()
+
+
+def test_read_probe_leaves_sink():
+    """The measurement hook streams a buffer and never writes its sink for
+    non-matching data; bad sizes are rejected before any launch."""
+    buf = torch.ones(1 << 20, dtype=torch.int32, device=DEV)
+    sink = torch.full((1,), 7, dtype=torch.int32, device=DEV)
+    moe_ffn.read_probe(buf, sink)
+    assert int(host(sink)[0]) == 7
+    with pytest.raises(moe_ffn.MoeError):
+        moe_ffn.read_probe(buf, sink, nbytes=20)
+
+
 def test_forward_reuse_smaller_batch_and_determinism(moe512):
     L = moe512["layer"]
     x = W.activations(37, seed=61)
