@@ -54,10 +54,15 @@ struct Unit {
 // popular experts is spread over all XCDs.
 constexpr int kUnitChunk = 4;
 
+// The dealing permutes each round of 8 * kUnitChunk consecutive ids.
+__device__ __forceinline__ int dealt_unit(int id) {
+    const int n = id >> 3, x = id & 7;
+    return ((n / kUnitChunk) * 8 + x) * kUnitChunk + n % kUnitChunk;
+}
+
 __device__ __forceinline__ Unit mfma_unit(int count, int slices) {
     const int units = count * slices;
-    const int n = static_cast<int>(blockIdx.x >> 3), x = static_cast<int>(blockIdx.x & 7);
-    const int u = ((n / kUnitChunk) * 8 + x) * kUnitChunk + n % kUnitChunk;
+    const int u = dealt_unit(static_cast<int>(blockIdx.x));
     Unit r;
     r.ok = u < units;
     r.item = r.ok ? u / slices : 0;
@@ -637,14 +642,17 @@ __device__ __forceinline__ void fold_tree_multi(const GuTile &t, float (*park)[1
 // are elements 16h..16h+15 of one Q8_1 block.  Units are ordered
 // (item, slice, sub) so the 4 tiles of an item that read the same weight rows
 // are adjacent on one XCD.
-template<bool Dbg>
+// Fold: kFoldStaged (H < 2048), kFoldGrouped (H = 2048), kFoldMulti
+// (H > 2048); one instantiation per shape keeps only that path's registers.
+enum { kFoldStaged = 0, kFoldGrouped = 1, kFoldMulti = 2 };
+
+template<int Fold, bool Dbg>
 __global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
     // Pending tree levels 3-4 per wave; after the tree the up wave's area
     // carries its result to the gate wave.
     __shared__ float park[2][2][16][64];
     __shared__ uint4 d4_lds[2][kGuMaxBlocks][4];          // [mat][block][32 halfs]
     float (*xch)[64] = park[1][0];
-    const int lane = threadIdx.x & 63;
     const int mat = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, I = a.shape.I, nb = H / 32, nbi = I / 32;
     const int slices = nbi * kSubs;
@@ -655,6 +663,7 @@ __global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
     const int sub = un.slice % kSubs;
     const int R0 = (un.slice / kSubs) * 32;
     if (kSub * sub >= ncols) return;   // uniform per workgroup: no tokens in this tile
+    const int lane = threadIdx.x & 63;
     const int m = lane & 31, h = lane >> 5;
     const int prow = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
     const int j = kSub * sub + m;
@@ -680,7 +689,7 @@ __global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
     t.dot_ok = Dbg && t.dots && j < ncols;
 
     float res[16];
-    if (nb <= kGuMaxBlocks) {
+    if constexpr (Fold != kFoldMulti) {
         // Stage the tile's scales (both matrices) and its tokens' Q8 heads.
         // Scale group g (rows 8g..8g+7) of block b is one 16-byte chunk of the
         // [rows/8][blocks][8] plane and lands at halfs 8g..8g+7 of [mat][b].
@@ -691,7 +700,7 @@ __global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
         }
         __syncthreads();
         const GuStage g{reinterpret_cast<const uint32_t *>(&d4_lds[mat][0][0]), nullptr};
-        if (nb == kGuMaxBlocks)
+        if constexpr (Fold == kFoldGrouped)
             fold_tree_grouped<Dbg>(t, g, static_cast<uint32_t>(prow) * row_bytes + 32u * 16u * h, park[mat], lane, res);
         else fold_tree_staged<false, Dbg>(t, g, park[mat], lane, res);
     } else {
@@ -935,8 +944,17 @@ unsigned mfma_grid(const FfnArgs &a, int slices) {
 hipError_t launch_gate_up_mfma(const FfnArgs &a, hipStream_t s) {
     const bool dbg = a.middle_f32 || a.gate_dots || a.up_dots;
     const unsigned grid = mfma_grid(a, a.shape.I / 32 * kSubs);
-    if (dbg) k_gate_up_mfma<true><<<grid, 128, 0, s>>>(a);
-    else k_gate_up_mfma<false><<<grid, 128, 0, s>>>(a);
+    const int nb = a.shape.H / 32;
+    if (nb == kGuMaxBlocks) {
+        if (dbg) k_gate_up_mfma<kFoldGrouped, true><<<grid, 128, 0, s>>>(a);
+        else k_gate_up_mfma<kFoldGrouped, false><<<grid, 128, 0, s>>>(a);
+    } else if (nb < kGuMaxBlocks) {
+        if (dbg) k_gate_up_mfma<kFoldStaged, true><<<grid, 128, 0, s>>>(a);
+        else k_gate_up_mfma<kFoldStaged, false><<<grid, 128, 0, s>>>(a);
+    } else {
+        if (dbg) k_gate_up_mfma<kFoldMulti, true><<<grid, 128, 0, s>>>(a);
+        else k_gate_up_mfma<kFoldMulti, false><<<grid, 128, 0, s>>>(a);
+    }
     return hipGetLastError();
 }
 
