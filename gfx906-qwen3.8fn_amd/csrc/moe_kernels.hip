@@ -605,15 +605,19 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
 // one unit per workgroup).  Decode streaming is bound by bytes in flight per
 // CU: each wave keeps its 8 weight rows (8 KB) in flight with a small register
 // footprint, so 4 workgroups (32 waves, 256 KB of loads) fit on a CU.  Grid =
-// (item bound, I/32 slices); same arithmetic and outputs as k_gate_up_stream.
+// item bound x I/32 slices; same arithmetic and outputs as k_gate_up_stream.
 template<bool Dbg>
-__global__ __launch_bounds__(512, 8) void k_gate_up_lean(FfnArgs a) {
+__global__ __launch_bounds__(512, 3) void k_gate_up_lean(FfnArgs a) {
     constexpr int T = kStreamTokens;
     __shared__ float gu[2][32][T];
     // The wave index is uniform: as a scalar it keeps row bases in SGPRs.
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32;
-    const int item = blockIdx.x, s = blockIdx.y;
+    // Workgroup id = item * I/32 + slice: with I/32 a multiple of 8 each
+    // slice stays on one XCD (id % 8), so consecutive items of one expert
+    // find its rows in that XCD's L2.
+    const int S = I / 32;
+    const int item = static_cast<int>(blockIdx.x) / S, s = static_cast<int>(blockIdx.x) % S;
     // Item header, its tokens and the item count are independent loads
     // (the item array is sized for the grid), issued together.
     const int4 hdr = *reinterpret_cast<const int4 *>(a.routes.stream_items + item);
@@ -639,31 +643,42 @@ __global__ __launch_bounds__(512, 8) void k_gate_up_lean(FfnArgs a) {
     const auto sr = buffer_rsrc((mat ? a.bank.up_scales : a.bank.gate_scales) + mrow * nbh, row_bytes);
     const uint32_t lane_off = static_cast<uint32_t>(kb) * 16u;
     const int rho = 4 * ((lane >> 5) & 1) + 2 * (lane & 1) + ((lane >> 1) & 1);   // row rows8_exact leaves in this lane
-    // Weights are loaded per token together with that token's activations:
-    // the first token streams them from HBM, further tokens of the item hit
-    // L2.  Nothing but the token ids stays live across iterations.
-#pragma unroll 1
-    for (int j = 0; j < ncols; ++j) {
-        const int t = j == 0 ? tok.x : j == 1 ? tok.y : j == 2 ? tok.z : tok.w;
-        const size_t xrow = static_cast<size_t>(t) * nbh;
+    // The weights are loaded once per item and held for its tokens (reloading
+    // them per token relied on L2 hits that a busy XCD L2 does not give).
+    uint4 w[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) w[r] = buffer_load16(wr, lane_off, r * row_bytes);
+    const uint4 d4p = buffer_load16(sr, lane_off, 0);
+    // A token's activations are loaded while the previous token computes.
+    const int toks[T] = {tok.x, tok.y, tok.z, tok.w};
+    auto load_x = [&](int j, uint4 &x0, uint4 &x1, uint32_t &hx) {
+        const size_t xrow = static_cast<size_t>(toks[j < ncols ? j : 0]) * nbh;
         const auto xr = buffer_rsrc(a.xq.codes + xrow * 32, static_cast<uint32_t>(nbh) * 32u);
         const auto hr = buffer_rsrc(a.xq.heads + xrow, static_cast<uint32_t>(nbh) * 4u);
-        uint4 w[8];
+        x0 = buffer_load16(xr, 2 * lane_off, 0);
+        x1 = buffer_load16(xr, 2 * lane_off, 16);
+        hx = buffer_load4(hr, lane_off / 4, 0);
+    };
+    uint4 x0, x1;
+    uint32_t hx;
+    load_x(0, x0, x1, hx);
 #pragma unroll
-        for (int r = 0; r < 8; ++r) w[r] = buffer_load16(wr, lane_off, r * row_bytes);
-        const uint4 d4p = buffer_load16(sr, lane_off, 0);
-        const uint4 x0 = buffer_load16(xr, 2 * lane_off, 0);
-        const uint4 x1 = buffer_load16(xr, 2 * lane_off, 16);
-        const uint32_t hx = buffer_load4(hr, lane_off / 4, 0);
-        if constexpr (Dbg) {
-            int32_t *dots = mat ? a.up_dots : a.gate_dots;
-            if (dots && has)
+    for (int j = 0; j < T; ++j) {
+        if (j < ncols) {   // uniform per workgroup
+            uint4 n0 = x0, n1 = x1;
+            uint32_t nh = hx;
+            if (j + 1 < T && j + 1 < ncols) load_x(j + 1, n0, n1, nh);
+            if constexpr (Dbg) {
+                int32_t *dots = mat ? a.up_dots : a.gate_dots;
+                if (dots && has)
 #pragma unroll
-                for (int r = 0; r < 8; ++r)
-                    dots[(static_cast<size_t>(first + j) * I + row0 + r) * nbh + lane] = dot_block(w[r], x0, x1);
+                    for (int r = 0; r < 8; ++r)
+                        dots[(static_cast<size_t>(first + j) * I + row0 + r) * nbh + lane] = dot_block(w[r], x0, x1);
+            }
+            const float v = rows8_exact(w, d4p, x0, x1, hx, has, lane);
+            if ((lane & 28) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
+            x0 = n0; x1 = n1; hx = nh;
         }
-        const float v = rows8_exact(w, d4p, x0, x1, hx, has, lane);
-        if ((lane & 28) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
     }
     __syncthreads();
     if (wave < ncols) {
@@ -753,7 +768,7 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
 
 // High-occupancy streaming down projection for I <= 512 (a row of I/32 <= 16
 // blocks is <= 256 code bytes, 16 lanes; one wave load covers 4 rows).  Work
-// unit = (item, slice of 64 output rows), grid = (item bound, H/64); a 2-wave
+// unit = (item, slice of 64 output rows), grid = item bound x H/64; a 2-wave
 // workgroup gives each wave 32 rows = 8 independent 16-byte loads per lane in
 // flight.  Row sums of the item's pairs are written unweighted to their
 // contribution rows (token * out_stride_k + rank), like the reference's
@@ -761,10 +776,13 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
 // NBI = 16 specialises I = 512 (every lane holds a block); NBI = 0 reads
 // I/32 <= 16 at run time.
 template<int NBI, bool Dbg>
-__global__ __launch_bounds__(128, NBI ? 8 : 7) void k_down_lean(FfnArgs a) {
+__global__ __launch_bounds__(128, 4) void k_down_lean(FfnArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = NBI ? NBI : a.shape.I / 32;
-    const int item = blockIdx.x, slice = blockIdx.y;
+    // Workgroup id = item * H/64 + slice (one XCD per slice, as in
+    // k_gate_up_lean).
+    const int S = H / 64;
+    const int item = static_cast<int>(blockIdx.x) / S, slice = static_cast<int>(blockIdx.x) % S;
     const int4 hdr = *reinterpret_cast<const int4 *>(a.routes.stream_items + item);
     const int4 tok = *reinterpret_cast<const int4 *>(a.routes.stream_items[item].token);
     const int4 rnk = *reinterpret_cast<const int4 *>(a.routes.stream_items[item].rank);
@@ -790,33 +808,44 @@ __global__ __launch_bounds__(128, NBI ? 8 : 7) void k_down_lean(FfnArgs a) {
     // Transposing reduction over the 16 lanes of a row: xor 8/4/2 halve the
     // 8 load-rows, xor 1 finishes; lane ends with load-row lr(lane).
     const int lr = 4 * (lane & 1) + 2 * ((lane >> 1) & 1) + ((lane >> 2) & 1);   // row rows8_down_exact leaves here
-    // Weights are loaded per pair together with its middle activations (the
-    // first pair streams them from HBM, further pairs hit L2).
-#pragma unroll 1
-    for (int j = 0; j < ncols; ++j) {
-        const int pair = first + j;
-        const size_t xrow = static_cast<size_t>(pair) * nbi;
+    // The weights are loaded once per item and held for its pairs.
+    uint4 w[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) w[l] = buffer_load16(wr, lane_off, 4 * l * row_bytes);
+    const uint4 d4p = buffer_load16(sr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
+    // A pair's middle row is loaded while the previous pair computes.
+    auto load_x = [&](int j, uint4 &x0, uint4 &x1, uint32_t &hx) {
+        const size_t xrow = static_cast<size_t>(first + (j < ncols ? j : 0)) * nbi;
         const auto xr = buffer_rsrc(a.mq.codes + xrow * 32, static_cast<uint32_t>(nbi) * 32u);
         const auto hr = buffer_rsrc(a.mq.heads + xrow, static_cast<uint32_t>(nbi) * 4u);
-        uint4 w[8];
+        x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
+        x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
+        hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
+    };
+    const int toks[kStreamTokens] = {tok.x, tok.y, tok.z, tok.w};
+    const int rnks[kStreamTokens] = {rnk.x, rnk.y, rnk.z, rnk.w};
+    uint4 x0, x1;
+    uint32_t hx;
+    load_x(0, x0, x1, hx);
 #pragma unroll
-        for (int l = 0; l < 8; ++l) w[l] = buffer_load16(wr, lane_off, 4 * l * row_bytes);
-        const uint4 d4p = buffer_load16(sr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
-        const uint4 x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
-        const uint4 x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
-        const uint32_t hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
-        if constexpr (Dbg) {
-            if (a.down_dots && has)
+    for (int j = 0; j < kStreamTokens; ++j) {
+        if (j < ncols) {   // uniform per workgroup
+            uint4 n0 = x0, n1 = x1;
+            uint32_t nh = hx;
+            if (j + 1 < kStreamTokens && j + 1 < ncols) load_x(j + 1, n0, n1, nh);
+            if constexpr (Dbg) {
+                if (a.down_dots && has)
 #pragma unroll
-                for (int l = 0; l < 8; ++l)
-                    a.down_dots[(static_cast<size_t>(pair) * H + row0 + 4 * l + sub) * nbi + kl] = dot_block(w[l], x0, x1);
-        }
-        const float v = rows8_down_exact(w, d4p, x0, x1, hx, has, lane);
-        if ((lane & 8) == 0) {
-            const int t = j == 0 ? tok.x : j == 1 ? tok.y : j == 2 ? tok.z : tok.w;
-            const int rk = j == 0 ? rnk.x : j == 1 ? rnk.y : j == 2 ? rnk.z : rnk.w;
-            const size_t orow = static_cast<size_t>(t) * a.out_stride_k + rk;
-            a.out[orow * H + row0 + 4 * lr + sub] = v;
+                    for (int l = 0; l < 8; ++l)
+                        a.down_dots[(static_cast<size_t>(first + j) * H + row0 + 4 * l + sub) * nbi + kl] =
+                            dot_block(w[l], x0, x1);
+            }
+            const float v = rows8_down_exact(w, d4p, x0, x1, hx, has, lane);
+            if ((lane & 8) == 0) {
+                const size_t orow = static_cast<size_t>(toks[j]) * a.out_stride_k + rnks[j];
+                a.out[orow * H + row0 + 4 * lr + sub] = v;
+            }
+            x0 = n0; x1 = n1; hx = nh;
         }
     }
 }
@@ -1243,8 +1272,8 @@ hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s) {
     const unsigned grid = stream_grid(a, a.shape.I / 32);
     const int nbl = (a.shape.H / 32 + 63) / 64;
     if (nbl <= 1) {
-        // One unit per workgroup; grid = (item bound, slices), extra items exit.
-        const dim3 lgrid(stream_item_bound(a), a.shape.I / 32);
+        // One unit per workgroup; grid = item bound x slices, extra items exit.
+        const unsigned lgrid = stream_item_bound(a) * static_cast<unsigned>(a.shape.I / 32);
         if (dbg) k_gate_up_lean<true><<<lgrid, 512, 0, s>>>(a);
         else k_gate_up_lean<false><<<lgrid, 512, 0, s>>>(a);
     } else if (nbl <= 2) gate_up_stream<2>(a, dbg, grid, s);
@@ -1283,7 +1312,7 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
     const unsigned grid = stream_grid(a, a.shape.H / 64);
     const bool dbg = a.down_dots != nullptr;
     if (nbi <= 16) {
-        const dim3 g(stream_item_bound(a), a.shape.H / 64);
+        const unsigned g = stream_item_bound(a) * static_cast<unsigned>(a.shape.H / 64);
         if (dbg) k_down_lean<0, true><<<g, 128, 0, s>>>(a);
         else if (nbi == 16) k_down_lean<16, false><<<g, 128, 0, s>>>(a);
         else k_down_lean<0, false><<<g, 128, 0, s>>>(a);

@@ -35,11 +35,11 @@ struct moe_ffn_layer {
     // Smallest group routed to the MFMA path (0 = streaming only).  An MFMA
     // tile spends the same exact-order epilogue on 32 token columns however
     // many are filled, and a one-tile group streams its weights from HBM with
-    // little reuse, so groups below 16 pairs stream: measured on MI355X, 16-20
-    // is best for 4K Zipf(1.1) (2.58 vs 2.70 ms at 1), 1032-token Zipf(1.3)
-    // (0.90 vs 1.71 ms) and 256 tokens (0.40 vs 1.21 ms), and neutral at 16K
-    // uniform, whose groups all exceed 256.
-    int mfma_min = 16;
+    // little reuse, so groups below 32 pairs stream.  Measured on MI355X
+    // (ms per layer at 16 / 32 / 48): 4K Zipf(1.1) 2.29 / 2.13 / 2.18,
+    // 1032-token Zipf(1.3) 0.76 / 0.75 / 0.75, 256 tokens 0.34 / 0.32 / 0.31;
+    // 16K uniform (all groups above 256) 6.4 either way.
+    int mfma_min = 32;
     int decode_mode = -1; // ungrouped decode path: -1 auto, 0 never, 1 whenever shapes allow
     bool last_decode = false;
     int cu_count = 256;   // compute units of the device
