@@ -1070,59 +1070,87 @@ __global__ __launch_bounds__(256) void k_decode_middle_grouped(Act mq, RouteOut 
 // Nonfinite operands set bit 1, nonfinite results bit 2, and zero the output
 // element (src/hip/session_ops.hip:307-324, 375-391).  Pairs that could not
 // be grouped (pos_of < 0: bad id / duplicate, already flagged) contribute 0.
+// V consecutive elements per thread (V = 4: 16-byte loads when every row is
+// 16-byte aligned); each element is folded on its own, exactly as above.
+template<int V>
 __global__ __launch_bounds__(256) void k_fold(const float *__restrict__ c, size_t token_stride,
                                               const float *__restrict__ w, int k, const int32_t *pos_of,
                                               const float *__restrict__ shared, size_t shared_stride,
                                               const float *__restrict__ shared_gate, int tokens, int H,
                                               float *__restrict__ y, int *error) {
-    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t i = (static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x) * V;
     if (i >= static_cast<size_t>(tokens) * H) return;
-    const size_t t = i / H, h = i % H;
-    int flags = 0;
-    float v = 0.0f;
+    const size_t t = i / H, h = i % H;   // H % V == 0: the V elements share a token
+    auto load = [](const float *p, float (&out)[V]) {
+        if constexpr (V == 4) {
+            const float4 q = *reinterpret_cast<const float4 *>(p);
+            out[0] = q.x; out[1] = q.y; out[2] = q.z; out[3] = q.w;
+        } else {
+            out[0] = *p;
+        }
+    };
+    int flags[V] = {};
+    float v[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = 0.0f;
     // Ranks are taken 8 at a time: all loads of a chunk are issued before the
     // sequential (rank-order) accumulation.  Rows of ungrouped pairs are read
     // but not used.
     for (int r0 = 0; r0 < k; r0 += 8) {
-        float xs[8], ws[8];
+        float xs[8][V], ws[8];
         bool use[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const int r = r0 + q;
             const bool in = r < k;
             use[q] = in && (!pos_of || pos_of[t * k + r] >= 0);
-            xs[q] = in ? c[t * token_stride + static_cast<size_t>(r) * H + h] : 0.0f;
+            if (in) load(c + t * token_stride + static_cast<size_t>(r) * H + h, xs[q]);
             ws[q] = in ? w[t * k + r] : 0.0f;
         }
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             if (!use[q]) continue;
-            float x = xs[q], s = ws[q];
-            if (!isfinite(x)) { flags |= 1; x = 0.0f; }
-            if (!isfinite(s)) { flags |= 1; s = 0.0f; }
-            float p = s * x;
-            if (!isfinite(p)) { flags |= 2; p = 0.0f; }
-            v = v + p;
-            if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                float x = xs[q][e], s = ws[q];
+                if (!isfinite(x)) { flags[e] |= 1; x = 0.0f; }
+                if (!isfinite(s)) { flags[e] |= 1; s = 0.0f; }
+                float p = s * x;
+                if (!isfinite(p)) { flags[e] |= 2; p = 0.0f; }
+                v[e] = v[e] + p;
+                if (!isfinite(v[e])) { flags[e] |= 2; v[e] = 0.0f; }
+            }
         }
     }
     if (shared) {
-        float x = shared[t * shared_stride + h];
-        if (!isfinite(x)) { flags |= 1; x = 0.0f; }
+        float xsh[V];
+        load(shared + t * shared_stride + h, xsh);
         float scale = 1.0f;
+        int gflags = 0;
         if (shared_gate) {
             float g = shared_gate[t];
-            if (!isfinite(g)) { flags |= 1; g = 0.0f; }
+            if (!isfinite(g)) { gflags |= 1; g = 0.0f; }
             scale = 1.0f / (1.0f + moe_expf(-g));
-            if (!isfinite(scale)) { flags |= 2; scale = 0.0f; }
+            if (!isfinite(scale)) { gflags |= 2; scale = 0.0f; }
         }
-        float p = scale * x;
-        if (!isfinite(p)) { flags |= 2; p = 0.0f; }
-        v = v + p;
-        if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            float x = xsh[e];
+            flags[e] |= gflags;
+            if (!isfinite(x)) { flags[e] |= 1; x = 0.0f; }
+            float p = scale * x;
+            if (!isfinite(p)) { flags[e] |= 2; p = 0.0f; }
+            v[e] = v[e] + p;
+            if (!isfinite(v[e])) { flags[e] |= 2; v[e] = 0.0f; }
+        }
     }
-    y[i] = flags ? 0.0f : v;
-    if (flags) atomicOr(error, flags);
+    int any = 0;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        y[i + e] = flags[e] ? 0.0f : v[e];
+        any |= flags[e];
+    }
+    if (any) atomicOr(error, any);
 }
 
 inline unsigned blocks_for(size_t n, unsigned per) { return static_cast<unsigned>((n + per - 1) / per); }
@@ -1333,8 +1361,14 @@ hipError_t launch_fold(const float *contributions, size_t token_stride, const fl
                        const int32_t *pos_of, const float *shared, size_t shared_stride,
                        const float *shared_gate, int tokens, int H, float *y, int *error, hipStream_t s) {
     const size_t n = static_cast<size_t>(tokens) * H;
-    k_fold<<<blocks_for(n, 256), 256, 0, s>>>(contributions, token_stride, weights, k, pos_of, shared,
-                                              shared_stride, shared_gate, tokens, H, y, error);
+    const auto a16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (H % 4 == 0 && token_stride % 4 == 0 && shared_stride % 4 == 0 && a16(contributions) &&
+        (!shared || a16(shared)))
+        k_fold<4><<<blocks_for(n / 4, 256), 256, 0, s>>>(contributions, token_stride, weights, k, pos_of, shared,
+                                                         shared_stride, shared_gate, tokens, H, y, error);
+    else
+        k_fold<1><<<blocks_for(n, 256), 256, 0, s>>>(contributions, token_stride, weights, k, pos_of, shared,
+                                                     shared_stride, shared_gate, tokens, H, y, error);
     return hipGetLastError();
 }
 

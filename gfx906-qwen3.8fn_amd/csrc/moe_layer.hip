@@ -51,6 +51,13 @@ struct moe_ffn_layer {
     int *last_error = nullptr;
     // Stage profiler (moe_ffn_profile): a ring of events, one set per forward.
     static constexpr int kStageMarks = MOE_STAGE_FOLD + 2;
+    // Grouped forwards run the streaming items (small groups, bound by memory
+    // latency) on `side` while the MFMA items (bound by VALU) run on the
+    // caller's stream; fork/join events order them after grouping and before
+    // the fold.
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    bool two_streams = true;
     hipEvent_t *prof_events = nullptr;
     int prof_capacity = 0, prof_used = 0;
 };
@@ -139,6 +146,7 @@ int finish_create(moe_ffn_layer *L) {
     if (hipMemset(L->ws_mem, 0, w.total) != hipSuccess) return hipErrorOutOfMemory;
     if (const char *env = std::getenv("MOE_FFN_MFMA_MIN")) L->mfma_min = std::atoi(env);
     if (const char *env = std::getenv("MOE_FFN_DECODE")) L->decode_mode = std::atoi(env) ? 1 : 0;
+    if (const char *env = std::getenv("MOE_FFN_STREAMS")) L->two_streams = std::atoi(env) != 1;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, L->device) == hipSuccess && cus > 0)
         L->cu_count = cus;
@@ -202,7 +210,11 @@ int create_common(const moe_ffn_config *config, int device, moe_ffn_layer **laye
     L->cfg = *config;
     L->device = device;
     L->shape = shape_of(*config);
-    const int r = alloc_bank(L);
+    int r = alloc_bank(L);
+    if (r == hipSuccess && (hipStreamCreateWithFlags(&L->side, hipStreamNonBlocking) != hipSuccess ||
+                            hipEventCreateWithFlags(&L->fork, hipEventDisableTiming) != hipSuccess ||
+                            hipEventCreateWithFlags(&L->join, hipEventDisableTiming) != hipSuccess))
+        r = hipErrorOutOfMemory;
     if (r != hipSuccess) { moe_ffn_destroy(L); L = nullptr; return r; }
     return hipSuccess;
 }
@@ -379,6 +391,9 @@ int moe_ffn_destroy(moe_ffn_layer *L) {
     (void)hipSetDevice(L->device);
     (void)hipDeviceSynchronize();
     profile_free(L);
+    if (L->join) (void)hipEventDestroy(L->join);
+    if (L->fork) (void)hipEventDestroy(L->fork);
+    if (L->side) (void)hipStreamDestroy(L->side);
     if (L->bank_mem) (void)hipFree(L->bank_mem);
     if (L->ws_mem) (void)hipFree(L->ws_mem);
     delete L;
@@ -462,11 +477,29 @@ int moe_ffn_forward(moe_ffn_layer *L, const float *x, const int32_t *ids, const 
     const bool decode = use_decode(L, tokens);
     hipEvent_t *marks = nullptr;
     if (L->prof_used < L->prof_capacity) marks = L->prof_events + (L->prof_used++) * moe_ffn_layer::kStageMarks;
-    if (marks && hipEventRecord(marks[0], s) != hipSuccess) return kInvalid;
-    for (int stage = MOE_STAGE_PREPARE; stage <= MOE_STAGE_FOLD; ++stage) {
-        const int r = run_stage(L, stage, x, ids, weights, tokens, shared_gate, y, error, s, decode);
+    if (!decode && !marks && L->two_streams && L->mfma_min >= 2) {
+        // Both item kinds can exist: streaming chain on the side stream, MFMA
+        // chain here, joined before the fold (the two chains touch disjoint
+        // middle and contribution rows).
+        int r = run_stage(L, MOE_STAGE_PREPARE, x, ids, weights, tokens, shared_gate, y, error, s, false);
         if (r != hipSuccess) return r;
-        if (marks && hipEventRecord(marks[stage + 1], s) != hipSuccess) return kInvalid;
+        if ((r = hipEventRecord(L->fork, s)) != hipSuccess || (r = hipStreamWaitEvent(L->side, L->fork, 0)) != hipSuccess)
+            return r;
+        const moe::FfnArgs a = base_args(L, tokens, error);
+        if ((r = moe::launch_gate_up(a, false, L->side)) != hipSuccess || (r = moe::launch_down(a, false, L->side)) != hipSuccess ||
+            (r = moe::launch_gate_up(a, true, s)) != hipSuccess || (r = moe::launch_down(a, true, s)) != hipSuccess)
+            return r;
+        if ((r = hipEventRecord(L->join, L->side)) != hipSuccess || (r = hipStreamWaitEvent(s, L->join, 0)) != hipSuccess)
+            return r;
+        if ((r = run_stage(L, MOE_STAGE_FOLD, x, ids, weights, tokens, shared_gate, y, error, s, false)) != hipSuccess)
+            return r;
+    } else {
+        if (marks && hipEventRecord(marks[0], s) != hipSuccess) return kInvalid;
+        for (int stage = MOE_STAGE_PREPARE; stage <= MOE_STAGE_FOLD; ++stage) {
+            const int r = run_stage(L, stage, x, ids, weights, tokens, shared_gate, y, error, s, decode);
+            if (r != hipSuccess) return r;
+            if (marks && hipEventRecord(marks[stage + 1], s) != hipSuccess) return kInvalid;
+        }
     }
     L->last_decode = decode;
     L->last_tokens = tokens;
