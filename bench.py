@@ -268,6 +268,29 @@ def main():
         }
         log(f"[bench] 4k prefill {wall_p*1e3:.3f} ms/layer, {NP/wall_p:.0f} tok/s")
 
+    # ---- device router (softmax + top-10 of 512), the step before the layer --
+    router = {}
+    for NR in (8, 4096):
+        lg = dev(np.random.default_rng(4000 + NR).standard_normal((NR, 512)).astype(np.float32))
+        ids_r = torch.empty((NR, 10), dtype=torch.int32, device="cuda:0")
+        w_r = torch.empty((NR, 10), dtype=torch.float32, device="cuda:0")
+        err_r = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+        lib = moe_ffn.library()
+        call = lambda: lib.moe_router_select(moe_ffn._ptr(lg), NR, 512, 10, None, moe_ffn._ptr(ids_r),
+                                             moe_ffn._ptr(w_r), moe_ffn._ptr(err_r), moe_ffn._stream(None))
+        for _ in range(5):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(50):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        router[f"tokens_{NR}_us"] = e0.elapsed_time(e1) / 50 * 1e3
+    result["router_us"] = router
+    log(f"[bench] router (softmax + top-10 of 512): {router}")
+
     # ---- 16K uniform prefill -----------------------------------
     if not args.no_prefill and not args.no_16k:
         NP = 16384

@@ -159,6 +159,10 @@ hipError_t launch_fold(const float *contributions, size_t token_stride, const fl
                        hipStream_t s);
 
 hipError_t launch_fill_u32(uint32_t *p, uint32_t value, size_t count, hipStream_t s);
+// Router softmax + top-k selection, one token per 64-thread block
+// (experts % 32 == 0, experts <= 1024, top_k <= 32); prob may be null.
+hipError_t launch_router(const float *logits, int tokens, int experts, int top_k, float *prob, int32_t *ids,
+                         float *weights, int *error, hipStream_t s);
 hipError_t launch_read_probe(const void *p, size_t bytes, uint32_t *sink, hipStream_t s);
 hipError_t launch_expf(const float *x, float *y, int n, hipStream_t s);
 

@@ -1153,6 +1153,104 @@ __global__ __launch_bounds__(256) void k_fold(const float *__restrict__ c, size_
     if (any) atomicOr(error, any);
 }
 
+// ---------------------------------------------------------------- router ---
+// One token per wave; lanes l and l + 32 both play reference lane l (the
+// width-32 shuffles keep the halves apart).  Softmax as router_softmax
+// (src/hip/session_ops.hip:401-434): lane l holds logits l + 32k; nonfinite
+// inputs count as 0 with bit 1; row max; per-lane left sums of expf(x - max)
+// from +0; XOR butterfly 1..16 for the total; reciprocal and multiply; any
+// flag zeroes the row.  Selection as select_routes (src/session.hip:666-687):
+// top_k rounds of a wave-wide arg-max (larger value, then lower id), bucket
+// id % 32 accumulated by its lane in rank order, XOR butterfly, denominator
+// max(bucket 0, 1/16384), weight = value * (1 / denominator).  expf is
+// moe_expf (the host C library's bits).
+constexpr int kRouterMaxPer = 32;   // experts <= 1024
+
+__device__ __forceinline__ float router_check(float x, int &flags, int bit) {
+    if (!isfinite(x)) { flags |= bit; return 0.0f; }
+    return x;
+}
+
+__global__ __launch_bounds__(64) void k_router(const float *__restrict__ logits, int E, int top_k,
+                                               float *__restrict__ prob, int32_t *__restrict__ ids,
+                                               float *__restrict__ weights, int *error) {
+    __shared__ int sel_id[32];
+    __shared__ float sel_v[32];
+    const int t = blockIdx.x, l = threadIdx.x & 31, per = E / 32;
+    const float *row = logits + static_cast<size_t>(t) * E;
+    int flags = 0;
+    float x[kRouterMaxPer], w[kRouterMaxPer];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kRouterMaxPer; ++k) {
+        x[k] = k < per ? router_check(row[l + 32 * k], flags, 1) : 0.0f;
+        if (k < per) m = fmaxf(m, x[k]);
+    }
+#pragma unroll
+    for (int d = 1; d < 32; d <<= 1) m = fmaxf(m, __shfl_xor(m, d, 32));
+    float total = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRouterMaxPer; ++k) {
+        w[k] = 0.0f;
+        if (k < per) {
+            const float shifted = router_check(x[k] - m, flags, 2);
+            w[k] = router_check(moe_expf(shifted), flags, 2);
+            total = router_check(total + w[k], flags, 2);
+        }
+    }
+#pragma unroll
+    for (int d = 1; d < 32; d <<= 1) total = total + __shfl_xor(total, d, 32);
+    total = router_check(total, flags, 2);
+    if (!(total > 0.0f)) flags |= 2;
+    const float inverse = total > 0.0f ? router_check(1.0f / total, flags, 2) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRouterMaxPer; ++k)
+        if (k < per) w[k] = router_check(w[k] * inverse, flags, 2);
+#pragma unroll
+    for (int d = 1; d < 32; d <<= 1) flags |= __shfl_xor(flags, d, 32);
+#pragma unroll
+    for (int k = 0; k < kRouterMaxPer; ++k)
+        if (k < per) {
+            if (flags) w[k] = 0.0f;
+            if (prob && threadIdx.x < 32) prob[static_cast<size_t>(t) * E + l + 32 * k] = w[k];
+        }
+    uint32_t taken = 0;
+    float bucket = 0.0f;
+    for (int i = 0; i < top_k; ++i) {
+        float bv = -INFINITY;
+        int bid = 0x7fffffff;
+#pragma unroll
+        for (int k = 0; k < kRouterMaxPer; ++k) {
+            const int id = l + 32 * k;
+            if (k < per && !((taken >> k) & 1u) && (w[k] > bv || (w[k] == bv && id < bid))) { bv = w[k]; bid = id; }
+        }
+#pragma unroll
+        for (int d = 1; d < 32; d <<= 1) {
+            const float ov = __shfl_xor(bv, d, 32);
+            const int oid = __shfl_xor(bid, d, 32);
+            if (ov > bv || (ov == bv && oid < bid)) { bv = ov; bid = oid; }
+        }
+        if ((bid & 31) == l) {
+            taken |= 1u << (bid >> 5);
+            bucket = bucket + bv;
+        }
+        if (threadIdx.x == 0) { sel_id[i] = bid; sel_v[i] = bv; }
+    }
+#pragma unroll
+    for (int d = 1; d < 32; d <<= 1) bucket = bucket + __shfl_xor(bucket, d, 32);
+    const float lowest = 1.0f / 16384.0f;
+    const float denominator = bucket < lowest ? lowest : bucket;
+    const int dflags = (!(denominator > 0.0f) || !isfinite(denominator)) ? 2 : 0;
+    const float dinv = dflags ? 0.0f : 1.0f / denominator;
+    __syncthreads();
+    if (static_cast<int>(threadIdx.x) < top_k) {
+        const size_t o = static_cast<size_t>(t) * top_k + threadIdx.x;
+        ids[o] = sel_id[threadIdx.x];
+        weights[o] = sel_v[threadIdx.x] * dinv;
+    }
+    if (threadIdx.x == 0 && (flags | dflags)) atomicOr(error, flags | dflags);
+}
+
 inline unsigned blocks_for(size_t n, unsigned per) { return static_cast<unsigned>((n + per - 1) / per); }
 
 }  // namespace
@@ -1354,6 +1452,12 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
         if (dbg) k_down_stream<64, true><<<grid, 512, 0, s>>>(a);
         else k_down_stream<64, false><<<grid, 512, 0, s>>>(a);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_router(const float *logits, int tokens, int experts, int top_k, float *prob, int32_t *ids,
+                         float *weights, int *error, hipStream_t s) {
+    k_router<<<tokens, 64, 0, s>>>(logits, experts, top_k, prob, ids, weights, error);
     return hipGetLastError();
 }
 

@@ -692,6 +692,16 @@ int moe_expf_device(const float *x, float *y, int n, void *stream) {
     return moe::launch_expf(x, y, n, static_cast<hipStream_t>(stream));
 }
 
+int moe_router_select(const float *logits, int tokens, int experts, int top_k, float *probabilities,
+                      int32_t *ids, float *weights, int *error, void *stream) {
+    if (!aligned(logits, 4) || !aligned(ids, 4) || !aligned(weights, 4) || !aligned(error, 4) ||
+        (probabilities && !aligned(probabilities, 4)) || tokens < 1 || experts < 32 || experts > 1024 ||
+        experts % 32 != 0 || top_k < 1 || top_k > 32 || top_k > experts)
+        return kInvalid;
+    return moe::launch_router(logits, tokens, experts, top_k, probabilities, ids, weights, error,
+                              static_cast<hipStream_t>(stream));
+}
+
 int moe_read_probe(const void *buffer, size_t bytes, void *sink, void *stream) {
     if (!aligned(buffer, 16) || !aligned(sink, 4) || bytes < 16 || bytes % 16 != 0) return kInvalid;
     return moe::launch_read_probe(buffer, bytes, static_cast<uint32_t *>(sink), static_cast<hipStream_t>(stream));

@@ -72,6 +72,7 @@ def library():
         lib.moe_expf_device.argtypes = [_P, _P, _I, _P]
         lib.moe_expf_host.argtypes = [_P, _P, ctypes.c_size_t]
         lib.moe_read_probe.argtypes = [_P, ctypes.c_size_t, _P, _P]
+        lib.moe_router_select.argtypes = [_P, _I, _I, _I, _P, _P, _P, _P, _P]
         lib.moe_ffn_last_stats.argtypes = [_P, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
                                            ctypes.POINTER(ctypes.c_int32)]
         _lib = lib
@@ -265,6 +266,22 @@ def expf_device(x, stream=None):
     y = torch.empty_like(x)
     _check(library().moe_expf_device(_ptr(x), _ptr(y), x.numel(), _stream(stream)), "moe_expf_device")
     return y
+
+
+def router_select(logits, top_k=10, probabilities=False, error=None, stream=None):
+    """Device router: fp32 logits [tokens][experts] -> (ids int32 [tokens][top_k],
+    weights fp32 [tokens][top_k], probabilities or None, error)."""
+    import torch
+    n, e = logits.shape
+    dev = logits.device
+    ids = torch.empty((n, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((n, top_k), dtype=torch.float32, device=dev)
+    p = torch.empty((n, e), dtype=torch.float32, device=dev) if probabilities else None
+    if error is None:
+        error = torch.zeros(1, dtype=torch.int32, device=dev)
+    _check(library().moe_router_select(_ptr(logits), n, e, top_k, _ptr(p), _ptr(ids), _ptr(w), _ptr(error),
+                                       _stream(stream)), "moe_router_select")
+    return ids, w, p, error
 
 
 def read_probe(buffer, sink, nbytes=None, stream=None):

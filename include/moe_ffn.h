@@ -200,6 +200,21 @@ int moe_ffn_last_stats(moe_ffn_layer *layer, int32_t *stream_items, int32_t *mfm
 int moe_expf_device(const float *x, float *y, int n, void *stream);
 int moe_expf_host(const float *x, float *y, size_t n);
 
+/* Router: replaces launch_router_softmax (src/hip/session_ops.hip:519-527,
+ * kernel :401-434) followed by the host's select_routes
+ * (src/session.hip:666-687) and the probability download / route upload
+ * around them (src/session.hip:1422-1433, 393-410).  For each token row of
+ * `experts` fp32 logits (device): the softmax in router_softmax's order (32
+ * lanes, lane l holding logits l + 32k, XOR-butterfly total, reciprocal
+ * multiply; nonfinite input zeroes the row and sets bit 1), then the top_k
+ * largest probabilities (ties to the lower id) with weights normalised by the
+ * 32-bucket XOR sum floored at 1/16384.  Writes ids / weights [tokens][top_k]
+ * on the device, ready for moe_ffn_forward, and the probabilities
+ * [tokens][experts] when `probabilities` is not NULL.  expf has the host C
+ * library's bits.  experts % 32 == 0, 32 <= experts <= 1024, top_k <= 32. */
+int moe_router_select(const float *logits, int tokens, int experts, int top_k, float *probabilities,
+                      int32_t *ids, float *weights, int *error, void *stream);
+
 /* Measurement hook: enqueue a plain streaming read of `bytes` (a multiple of
  * 16, buffer 16-byte aligned) from device memory; `sink` is a device word the
  * kernel never writes in practice.  Timing it at a kernel's byte count gives

@@ -662,3 +662,98 @@ done:
 void mo_expf_libm(const float *x, float *y, size_t n) {
     for (size_t i = 0; i < n; ++i) y[i] = expf(x[i]);
 }
+
+/* ---- router -------------------------------------------------------------
+ * mo_router_softmax restates router_softmax (src/hip/session_ops.hip:401-434):
+ * 32 lanes, lane l holds logits l + 32k; nonfinite inputs count as 0 and set
+ * bit 1; the row maximum; per lane a left-to-right sum of expf(x - max) from
+ * +0; a width-32 XOR butterfly (1, 2, 4, 8, 16; dpp.cuh:32-36) for the total;
+ * one reciprocal and a multiply per value; any flag zeroes the whole row.
+ * expf is the C library's (the reference's CPU expert uses it; its GPU
+ * router uses the device's, whose bits the reference does not pin:
+ * src/cpu_expert.hpp:73-74).
+ * mo_select_routes restates select_routes (src/session.hip:666-687): the
+ * top_k largest values, ties to the lower id; 32 buckets (id % 32) summed in
+ * rank order, then the XOR butterfly; denominator max(bucket 0, 1/16384);
+ * weight = value * (1 / denominator).  An invalid denominator (the reference
+ * throws) sets bit 2 and gives zero weights.  Both return their flags. */
+static inline float mo_finite_or(float x, int *flags, int bit) {
+    if (!isfinite(x)) { *flags |= bit; return 0.0f; }
+    return x;
+}
+
+int mo_router_softmax(const float *logits, int tokens, int experts, float *prob) {
+    int all = 0;
+    const int per = experts / 32;
+    for (int t = 0; t < tokens; ++t) {
+        const float *row = logits + (size_t)t * experts;
+        float *out = prob + (size_t)t * experts;
+        int flags = 0;
+        float lane_max[32], lane_sum[32];
+        for (int l = 0; l < 32; ++l) {
+            float m = -INFINITY;
+            for (int k = 0; k < per; ++k) m = fmaxf(m, mo_finite_or(row[l + 32 * k], &flags, 1));
+            lane_max[l] = m;
+        }
+        float maximum = -INFINITY;
+        for (int l = 0; l < 32; ++l) maximum = fmaxf(maximum, lane_max[l]);
+        for (int l = 0; l < 32; ++l) {
+            float total = 0.0f;
+            for (int k = 0; k < per; ++k) {
+                const float x = mo_finite_or(row[l + 32 * k], &flags, 0);
+                const float shifted = mo_finite_or(x - maximum, &flags, 2);
+                const float w = mo_finite_or(expf(shifted), &flags, 2);
+                out[l + 32 * k] = w;
+                total = mo_finite_or(total + w, &flags, 2);
+            }
+            lane_sum[l] = total;
+        }
+        for (int d = 1; d < 32; d <<= 1) {
+            float next[32];
+            for (int l = 0; l < 32; ++l) next[l] = lane_sum[l] + lane_sum[l ^ d];
+            memcpy(lane_sum, next, sizeof next);
+        }
+        const float total = mo_finite_or(lane_sum[0], &flags, 2);
+        if (!(total > 0.0f)) flags |= 2;
+        const float inverse = total > 0.0f ? mo_finite_or(1.0f / total, &flags, 2) : 0.0f;
+        for (int e = 0; e < experts; ++e) out[e] = mo_finite_or(out[e] * inverse, &flags, 2);
+        if (flags)
+            for (int e = 0; e < experts; ++e) out[e] = 0.0f;
+        all |= flags;
+    }
+    return all;
+}
+
+int mo_select_routes(const float *prob, int tokens, int experts, int top_k, int32_t *ids, float *weights) {
+    int all = 0;
+    for (int t = 0; t < tokens; ++t) {
+        const float *row = prob + (size_t)t * experts;
+        int32_t *id = ids + (size_t)t * top_k;
+        float *wt = weights + (size_t)t * top_k;
+        for (int i = 0; i < top_k; ++i) {   /* selection: largest value, then lowest id */
+            int best = -1;
+            for (int e = 0; e < experts; ++e) {
+                int taken = 0;
+                for (int q = 0; q < i; ++q) taken |= id[q] == e;
+                if (taken) continue;
+                if (best < 0 || row[e] > row[best]) best = e;   /* ascending e: ties keep the lower id */
+            }
+            id[i] = best;
+        }
+        float buckets[32] = {0};
+        for (int i = 0; i < top_k; ++i) buckets[id[i] % 32] += row[id[i]];
+        for (int d = 1; d < 32; d <<= 1) {
+            float next[32];
+            for (int l = 0; l < 32; ++l) next[l] = buckets[l] + buckets[l ^ d];
+            memcpy(buckets, next, sizeof next);
+        }
+        const float floor_ = 1.0f / 16384.0f;
+        const float denominator = buckets[0] < floor_ ? floor_ : buckets[0];
+        int flags = 0;
+        if (!(denominator > 0) || !isfinite(denominator)) flags = 2;
+        const float inverse = flags ? 0.0f : 1.0f / denominator;
+        for (int i = 0; i < top_k; ++i) wt[i] = row[id[i]] * inverse;
+        all |= flags;
+    }
+    return all;
+}

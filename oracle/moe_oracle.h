@@ -137,6 +137,13 @@ int mo_allowed_physical_cpus(int *cpus, int capacity, int *count);
 /* The C library's expf over an array (checker for the kernels' expf). */
 void mo_expf_libm(const float *x, float *y, size_t n);
 
+/* Router: softmax over each row of `experts` logits (experts % 32 == 0) as
+ * router_softmax (src/hip/session_ops.hip:401-434), and top_k selection with
+ * the XOR-bucket denominator as select_routes (src/session.hip:666-687).
+ * Both return the OR of their flags (1 invalid input, 2 arithmetic). */
+int mo_router_softmax(const float *logits, int tokens, int experts, float *prob);
+int mo_select_routes(const float *prob, int tokens, int experts, int top_k, int32_t *ids, float *weights);
+
 #ifdef __cplusplus
 }
 #endif

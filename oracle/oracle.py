@@ -52,6 +52,8 @@ def _load_oracle():
     lib.mo_quantize_q8.argtypes = [_P, _SZ, _P]
     lib.mo_expf_libm.restype = None
     lib.mo_expf_libm.argtypes = [_P, _P, _SZ]
+    lib.mo_router_softmax.argtypes = [_P, _I, _I, _P]
+    lib.mo_select_routes.argtypes = [_P, _I, _I, _I, _P, _P]
     lib.mo_block_dot.argtypes = [_P, _P]
     lib.mo_scaled_dot_q4_0.restype = ctypes.c_float
     lib.mo_scaled_dot_q4_0.argtypes = [ctypes.c_int32, ctypes.c_uint16, _P]
@@ -130,6 +132,27 @@ def expf_libm(x):
     y = np.empty_like(x)
     lib().mo_expf_libm(_ptr(x), _ptr(y), x.size)
     return y
+
+
+def router_softmax(logits):
+    """Row softmax in the reference's GPU order (C library expf); returns
+    (probabilities float32 [N][E], flags)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    n, e = logits.shape
+    prob = np.empty_like(logits)
+    flags = lib().mo_router_softmax(_ptr(logits), n, e, _ptr(prob))
+    return prob, flags
+
+
+def select_routes(prob, top_k=10):
+    """Top-k ids (ties to the lower id) and XOR-bucket normalised weights;
+    returns (ids int32 [N][k], weights float32 [N][k], flags)."""
+    prob = np.ascontiguousarray(prob, dtype=np.float32)
+    n, e = prob.shape
+    ids = np.empty((n, top_k), np.int32)
+    w = np.empty((n, top_k), np.float32)
+    flags = lib().mo_select_routes(_ptr(prob), n, e, top_k, _ptr(ids), _ptr(w))
+    return ids, w, flags
 
 
 def block_dots(w, K, M, xq):

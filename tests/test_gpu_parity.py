@@ -698,3 +698,58 @@ def test_expf_device_matches_libm():
     nan = np.isnan(ref)
     assert np.array_equal(np.isnan(got), nan)
     assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+# ------------------------------------------------------------------ router ---
+def _router_check(logits, k, what):
+    x = dev(logits)
+    ids, w, p, err = moe_ffn.router_select(x, top_k=k, probabilities=True)
+    p_ref, f_ref = O.router_softmax(logits)
+    i_ref, w_ref, g_ref = O.select_routes(p_ref, k)
+    assert np.array_equal(host(p).view(np.uint32), p_ref.view(np.uint32)), what
+    assert np.array_equal(host(ids), i_ref), what
+    assert np.array_equal(host(w).view(np.uint32), w_ref.view(np.uint32)), what
+    assert int(host(err)[0]) == (f_ref | g_ref), what
+
+
+def test_router_select_bit_exact():
+    """Device router (softmax in router_softmax's order + select_routes) against
+    the oracle restatement: probabilities, ids and weights bit for bit."""
+    rng = np.random.default_rng(700)
+    _router_check((rng.standard_normal((4096, 512)) * 3).astype(np.float32), 10, "random 4096 x 512")
+    _router_check((rng.standard_normal((64, 64)) * 0.1).astype(np.float32), 4, "64 experts, top-4")
+    _router_check(np.zeros((8, 512), np.float32), 10, "uniform: ties to the lower ids")
+    tie = rng.standard_normal((16, 512)).astype(np.float32)
+    tie[:, 100:140] = 5.0                           # forty equal leaders
+    _router_check(tie, 10, "equal leaders")
+    spread = np.zeros((4, 512), np.float32)
+    spread[:, :] = -60.0
+    spread[:, 0] = 60.0                             # one winner, the rest underflow to 0
+    _router_check(spread, 10, "one winner")
+
+
+def test_router_select_flags_bad_rows():
+    x = np.random.default_rng(701).standard_normal((6, 512)).astype(np.float32)
+    x[1, 3] = np.nan
+    x[4, 9] = np.inf
+    ids, w, p, err = moe_ffn.router_select(dev(x), top_k=10, probabilities=True)
+    assert int(host(err)[0]) & 1
+    ph, ih, wh = host(p), host(ids), host(w)
+    for t in (1, 4):   # zero row: ids 0..9, zero weights
+        assert np.all(ph[t] == 0) and list(ih[t]) == list(range(10)) and np.all(wh[t] == 0)
+    _router_check(x, 10, "rows with nonfinite logits")
+
+
+def test_router_then_forward_matches_oracle(moe512):
+    """Logits -> device router -> forward, without a host round trip: B8 output
+    bit-identical to the oracle layer on the oracle's own routes."""
+    rng = np.random.default_rng(702)
+    logits = rng.standard_normal((8, 512)).astype(np.float32)
+    x = W.activations(8, seed=703)
+    ids, w, _, err = moe_ffn.router_select(dev(logits))
+    y, err2 = moe512["layer"].forward(dev(x), ids, w)
+    p_ref, _ = O.router_softmax(logits)
+    i_ref, w_ref, _ = O.select_routes(p_ref, 10)
+    ref = O.moe_layer(x, 2048, 512, 512, moe512["bank"], i_ref, w_ref, shared_q4=moe512["shared"])
+    assert int(host(err)[0]) == 0 and int(host(err2)[0]) == 0
+    assert np.array_equal(host(y).view(np.uint32), ref["y"].view(np.uint32))

@@ -316,3 +316,93 @@ def test_shared_sigmoid_gate_closed_forms():
     scale = np.float32(1.0) / (np.float32(1.0) + np.exp(np.float32(2.0), dtype=np.float32))
     assert np.allclose(neg, folded + scale * sh, rtol=0, atol=1e-6 * float(np.abs(sh).max()))
     assert not np.array_equal(neg, half) and not np.array_equal(neg, one)
+
+
+# ------------------------------------------------------------------ router ---
+def _np_router_softmax(logits):
+    """Independent numpy emulation of router_softmax's order (32 lanes, lane l
+    holds columns l + 32k, per-lane left sums, XOR butterfly, reciprocal
+    multiply), with the C library's expf."""
+    x = np.where(np.isfinite(logits), logits, 0).astype(np.float32)
+    n, e = x.shape
+    lanes = x.reshape(n, e // 32, 32)                       # [t][k][l] = column l + 32k
+    m = lanes.max(axis=(1, 2))
+    w = O.expf_libm((lanes - m[:, None, None]).astype(np.float32))
+    s = np.zeros((n, 32), np.float32)
+    for k in range(e // 32):
+        s = (s + w[:, k, :]).astype(np.float32)
+    idx = np.arange(32)
+    for d in (1, 2, 4, 8, 16):
+        s = (s + s[:, idx ^ d]).astype(np.float32)
+    inv = (np.float32(1) / s[:, 0]).astype(np.float32)
+    return (w * inv[:, None, None]).astype(np.float32).reshape(n, e)
+
+
+def _np_select(prob, k):
+    n, e = prob.shape
+    ids = np.empty((n, k), np.int32)
+    ws = np.empty((n, k), np.float32)
+    for t in range(n):
+        order = np.lexsort((np.arange(e), -prob[t].astype(np.float64)))[:k]   # value desc, id asc
+        b = np.zeros(32, np.float32)
+        for i in order:
+            b[i % 32] = np.float32(b[i % 32] + prob[t, i])
+        for d in (1, 2, 4, 8, 16):
+            b = (b + b[np.arange(32) ^ d]).astype(np.float32)
+        den = max(b[0], np.float32(1.0 / 16384.0))
+        ids[t] = order
+        ws[t] = prob[t, order] * (np.float32(1) / np.float32(den))
+    return ids, ws
+
+
+def test_router_softmax_closed_forms():
+    # Equal logits: every expf is 1, the total 512 exactly, each value 1/512.
+    p, f = O.router_softmax(np.full((3, 512), 0.37, np.float32))
+    assert f == 0 and np.all(p == np.float32(1 / 512))
+    # One logit far above the rest: that value is exactly 1 (the others underflow).
+    x = np.zeros((1, 512), np.float32)
+    x[0, 77] = 200.0
+    p, f = O.router_softmax(x)
+    assert f == 0 and p[0, 77] == 1.0 and np.all(np.delete(p[0], 77) == 0)
+    # A nonfinite logit zeroes the row and sets bit 1; other rows are untouched.
+    x = np.random.default_rng(1).standard_normal((3, 512)).astype(np.float32)
+    x[1, 5] = np.nan
+    p, f = O.router_softmax(x)
+    assert f == 1 and np.all(p[1] == 0) and np.all(p[0] > 0) and np.all(p[2] > 0)
+
+
+def test_router_softmax_matches_independent_emulation():
+    x = (np.random.default_rng(2).standard_normal((64, 512)) * 3).astype(np.float32)
+    p, f = O.router_softmax(x)
+    assert f == 0
+    assert np.array_equal(p.view(np.uint32), _np_router_softmax(x).view(np.uint32))
+    ref = np.exp(x.astype(np.float64) - x.max(1, keepdims=True))
+    ref /= ref.sum(1, keepdims=True)
+    assert np.max(np.abs(p - ref) / ref) < 4e-6   # the mathematics, to float32 rounding
+
+
+def test_select_routes_ties_floor_and_bucket_order():
+    rng = np.random.default_rng(3)
+    p = rng.random((32, 512)).astype(np.float32)
+    p[0, [3, 40, 77]] = 2.0                         # a three-way tie: ids ascending
+    ids, w, f = O.select_routes(p, 10)
+    assert f == 0 and list(ids[0, :3]) == [3, 40, 77]
+    eids, ew = _np_select(p, 10)
+    assert np.array_equal(ids, eids) and np.array_equal(w.view(np.uint32), ew.view(np.uint32))
+    # The bucket tree is not a left-to-right sum: with a rank-order sum as the
+    # denominator some rows' weights come out different.
+    seq_w = np.empty_like(w)
+    for t in range(32):
+        acc = np.float32(0)
+        for v in p[t, ids[t]]:
+            acc = np.float32(acc + v)
+        seq_w[t] = p[t, ids[t]] * (np.float32(1) / acc)
+    assert np.any(seq_w != w)
+    # Tiny probabilities: the 1/16384 floor applies.
+    small = np.full((1, 512), 1e-7, np.float32)
+    ids, w, f = O.select_routes(small, 10)
+    assert f == 0 and list(ids[0]) == list(range(10))
+    assert np.all(w == np.float32(1e-7) * np.float32(16384.0))
+    # Softmax of uniform logits: ten equal weights of exactly fl(0.1).
+    ids, w, f = O.select_routes(np.full((1, 512), np.float32(1 / 512)), 10)
+    assert np.all(w == np.float32(0.1))
