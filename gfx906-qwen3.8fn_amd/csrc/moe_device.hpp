@@ -282,15 +282,39 @@ __device__ __forceinline__ Q8Part<P> quantize_part(float (&v)[32 / P]) {
     return q;
 }
 
-// SiLU(g)*u with the reference's sanitisation (src/hip/linear.hip:106-120).
-__device__ __forceinline__ float silu_mul(float g, float u, int &flags) {
+// moe_expf's 32 64-bit table entries as 64 dwords, one per lane (lane l
+// holds dword l): loaded once at kernel start, read in an epilogue with two
+// lane shuffles instead of a memory access on the epilogue's critical path.
+// Every lane of the wave must take part in the shuffles.
+__device__ __forceinline__ uint32_t expf_table_word(int lane) {
+    return reinterpret_cast<const uint32_t *>(moe_expf_table_device)[lane & 63];
+}
+
+struct LaneExpfTable {
+    uint32_t word;
+    __device__ __forceinline__ uint64_t operator()(int i) const {
+        const uint32_t lo = static_cast<uint32_t>(__shfl(static_cast<int>(word), 2 * i, 64));
+        const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(word), 2 * i + 1, 64));
+        return (static_cast<uint64_t>(hi) << 32) | lo;
+    }
+};
+
+// SiLU(g)*u with the reference's sanitisation (src/hip/linear.hip:106-120),
+// expf's table read through `table` (MoeExpfTable: memory; LaneExpfTable:
+// registers, the whole wave calling).
+template<typename Table>
+__device__ __forceinline__ float silu_mul(float g, float u, int &flags, const Table &table) {
     if (!isfinite(g)) { flags |= 1; g = 0.0f; }
     if (!isfinite(u)) { flags |= 1; u = 0.0f; }
-    float a = g / (1.0f + moe_expf(-g));
+    float a = g / (1.0f + moe_expf_with(-g, table));
     if (!isfinite(a)) { flags |= 2; a = 0.0f; }
     float v = a * u;
     if (!isfinite(v)) { flags |= 2; v = 0.0f; }
     return flags ? 0.0f : v;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u, int &flags) {
+    return silu_mul(g, u, flags, MoeExpfTable{});
 }
 
 // -------------------------------------------------------- buffer loads ---

@@ -30,8 +30,10 @@
 #if defined(__HIPCC__)
 #include <hip/hip_runtime.h>
 #define MOE_EXPF_FN __host__ __device__ __forceinline__
+#define MOE_EXPF_MEMBER __host__ __device__ __forceinline__
 #else
 #define MOE_EXPF_FN static inline
+#define MOE_EXPF_MEMBER inline
 #endif
 
 MOE_EXPF_FN double moe_expf_asdouble(uint64_t u) {
@@ -76,14 +78,16 @@ MOE_EXPF_FN uint64_t moe_expf_table(int i) {
 #endif
 }
 
-MOE_EXPF_FN float moe_expf(float x) {
-    const uint32_t abstop = (moe_expf_asuint(x) >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {                                   /* |x| >= 88 (top bits of 88.0f) */
-        if (moe_expf_asuint(x) == 0xff800000u) return 0.0f;   /* -inf */
-        if (abstop >= 0x7f8u) return x + x;                   /* +inf, nan */
-        if (x > 0x1.62e42ep6f) return __builtin_inff();       /* overflow */
-        if (x < -0x1.9fe368p6f) return 0.0f;                  /* underflow */
-    }
+struct MoeExpfTable {
+    MOE_EXPF_MEMBER uint64_t operator()(int i) const { return moe_expf_table(i); }
+};
+
+/* The function with the table lookup as a parameter (the kernels' epilogues
+ * pass a lookup that reads the table from registers). */
+template<typename Table>
+MOE_EXPF_FN float moe_expf_with(float x, const Table &table) {
+    /* The table is read before any special-case return, by every lane: a
+     * lookup through lane shuffles needs all lanes of the wave present. */
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -92,9 +96,17 @@ MOE_EXPF_FN float moe_expf(float x) {
     const double xd = (double)x;
     double kd = __builtin_fma(inv_ln2_n, xd, shift);
     const uint64_t ki = moe_expf_asuint64(kd);
+    const uint64_t entry = table((int)(ki & 31u));
+    const uint32_t abstop = (moe_expf_asuint(x) >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {                                   /* |x| >= 88 (top bits of 88.0f) */
+        if (moe_expf_asuint(x) == 0xff800000u) return 0.0f;   /* -inf */
+        if (abstop >= 0x7f8u) return x + x;                   /* +inf, nan */
+        if (x > 0x1.62e42ep6f) return __builtin_inff();       /* overflow */
+        if (x < -0x1.9fe368p6f) return 0.0f;                  /* underflow */
+    }
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    const double s = moe_expf_asdouble(moe_expf_table((int)(ki & 31u)) + (ki << 47));
+    const double s = moe_expf_asdouble(entry + (ki << 47));
     const double z = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
@@ -102,5 +114,7 @@ MOE_EXPF_FN float moe_expf(float x) {
     y = y * s;
     return (float)y;
 }
+
+MOE_EXPF_FN float moe_expf(float x) { return moe_expf_with(x, MoeExpfTable{}); }
 
 #endif /* MOE_EXPF_H */

@@ -138,9 +138,14 @@ __global__ __launch_bounds__(512) void k_read_probe(const uint4 *__restrict__ p,
     if (acc == never) sink[0] = acc;
 }
 
+// The kernels' expf as the epilogues use it (table in lane registers, every
+// lane taking part even past n), so special-case inputs mixed into one wave
+// are covered.
 __global__ __launch_bounds__(256) void k_expf(const float *x, float *y, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = moe_expf(x[i]);
+    const LaneExpfTable table{expf_table_word(threadIdx.x & 63)};
+    const float v = moe_expf_with(i < n ? x[i] : 0.0f, table);
+    if (i < n) y[i] = v;
 }
 
 __global__ __launch_bounds__(256) void k_fill_u32(uint32_t *p, uint32_t v, size_t n) {
@@ -499,6 +504,7 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
     constexpr int T = kStreamTokens;
     __shared__ float gu[2][32][T];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t expf_word = expf_table_word(lane);
     const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32, S = I / 32;
     const int units = a.routes.item_counts[0] * S;
     const int mat = wave >> 2;
@@ -585,7 +591,7 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
         if (wave < it.ncols) {
             const int j = wave, i = lane & 31;
             int flags = 0;
-            const float m = silu_mul(gu[0][i][j], gu[1][i][j], flags);
+            const float m = silu_mul(gu[0][i][j], gu[1][i][j], flags, LaneExpfTable{expf_word});
             const Q8Lane q = quantize32(m);
             if (lane < 32) {
                 const size_t pair = static_cast<size_t>(it.first + j);
@@ -612,6 +618,7 @@ __global__ __launch_bounds__(512, 3) void k_gate_up_lean(FfnArgs a) {
     __shared__ float gu[2][32][T];
     // The wave index is uniform: as a scalar it keeps row bases in SGPRs.
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t expf_word = expf_table_word(lane);
     const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32;
     // Workgroup id = item * I/32 + slice: with I/32 a multiple of 8 each
     // slice stays on one XCD (id % 8), so consecutive items of one expert
@@ -684,7 +691,7 @@ __global__ __launch_bounds__(512, 3) void k_gate_up_lean(FfnArgs a) {
     if (wave < ncols) {
         const int j = wave, i = lane & 31;
         int flags = 0;
-        const float m = silu_mul(gu[0][i][j], gu[1][i][j], flags);
+        const float m = silu_mul(gu[0][i][j], gu[1][i][j], flags, LaneExpfTable{expf_word});
         const Q8Lane q = quantize32(m);
         if (lane < 32) {
             const size_t pair = static_cast<size_t>(first + j);
@@ -879,6 +886,7 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
     __shared__ float gu[2][32];
     const FfnArgs &a = d.f;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t expf_word = expf_table_word(lane);
     const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32;
     // XCD-aware order: workgroup id i runs on XCD i % 8.  Ids are laid out so
     // that the tokens of one (rank, slice) are consecutive on one XCD: the
@@ -952,7 +960,7 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
     if (wave == 0) {
         const int i = lane & 31;
         int f = 0;
-        const float m = silu_mul(gu[0][i], gu[1][i], f);
+        const float m = silu_mul(gu[0][i], gu[1][i], f, LaneExpfTable{expf_word});
         const Q8Lane q = quantize32(m);
         if (lane < 32) {
             const size_t mb = (static_cast<size_t>(t) * P1 + r) * nbi + s;
@@ -1171,32 +1179,32 @@ __device__ __forceinline__ float router_check(float x, int &flags, int bit) {
     return x;
 }
 
-__global__ __launch_bounds__(64) void k_router(const float *__restrict__ logits, int E, int top_k,
-                                               float *__restrict__ prob, int32_t *__restrict__ ids,
-                                               float *__restrict__ weights, int *error) {
+// PER = experts / 32 values per lane (compile time, so every array index is
+// static and the lane's values stay in registers).
+template<int PER>
+__global__ __launch_bounds__(64) void k_router(const float *__restrict__ logits, int top_k, float *__restrict__ prob,
+                                               int32_t *__restrict__ ids, float *__restrict__ weights, int *error) {
+    constexpr int E = 32 * PER;
     __shared__ int sel_id[32];
     __shared__ float sel_v[32];
-    const int t = blockIdx.x, l = threadIdx.x & 31, per = E / 32;
+    const int t = blockIdx.x, l = threadIdx.x & 31;
+    const LaneExpfTable table{expf_table_word(threadIdx.x)};
     const float *row = logits + static_cast<size_t>(t) * E;
     int flags = 0;
-    float x[kRouterMaxPer], w[kRouterMaxPer];
+    float x[PER], w[PER];
     float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < kRouterMaxPer; ++k) {
-        x[k] = k < per ? router_check(row[l + 32 * k], flags, 1) : 0.0f;
-        if (k < per) m = fmaxf(m, x[k]);
-    }
+    for (int k = 0; k < PER; ++k) x[k] = router_check(row[l + 32 * k], flags, 1);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) m = fmaxf(m, x[k]);
 #pragma unroll
     for (int d = 1; d < 32; d <<= 1) m = fmaxf(m, __shfl_xor(m, d, 32));
     float total = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kRouterMaxPer; ++k) {
-        w[k] = 0.0f;
-        if (k < per) {
-            const float shifted = router_check(x[k] - m, flags, 2);
-            w[k] = router_check(moe_expf(shifted), flags, 2);
-            total = router_check(total + w[k], flags, 2);
-        }
+    for (int k = 0; k < PER; ++k) {
+        const float shifted = router_check(x[k] - m, flags, 2);
+        w[k] = router_check(moe_expf_with(shifted, table), flags, 2);
+        total = router_check(total + w[k], flags, 2);
     }
 #pragma unroll
     for (int d = 1; d < 32; d <<= 1) total = total + __shfl_xor(total, d, 32);
@@ -1204,25 +1212,22 @@ __global__ __launch_bounds__(64) void k_router(const float *__restrict__ logits,
     if (!(total > 0.0f)) flags |= 2;
     const float inverse = total > 0.0f ? router_check(1.0f / total, flags, 2) : 0.0f;
 #pragma unroll
-    for (int k = 0; k < kRouterMaxPer; ++k)
-        if (k < per) w[k] = router_check(w[k] * inverse, flags, 2);
+    for (int k = 0; k < PER; ++k) w[k] = router_check(w[k] * inverse, flags, 2);
 #pragma unroll
     for (int d = 1; d < 32; d <<= 1) flags |= __shfl_xor(flags, d, 32);
 #pragma unroll
-    for (int k = 0; k < kRouterMaxPer; ++k)
-        if (k < per) {
-            if (flags) w[k] = 0.0f;
-            if (prob && threadIdx.x < 32) prob[static_cast<size_t>(t) * E + l + 32 * k] = w[k];
-        }
+    for (int k = 0; k < PER; ++k) {
+        if (flags) w[k] = 0.0f;
+        if (prob && threadIdx.x < 32) prob[static_cast<size_t>(t) * E + l + 32 * k] = w[k];
+    }
     uint32_t taken = 0;
     float bucket = 0.0f;
     for (int i = 0; i < top_k; ++i) {
         float bv = -INFINITY;
         int bid = 0x7fffffff;
 #pragma unroll
-        for (int k = 0; k < kRouterMaxPer; ++k) {
-            const int id = l + 32 * k;
-            if (k < per && !((taken >> k) & 1u) && (w[k] > bv || (w[k] == bv && id < bid))) { bv = w[k]; bid = id; }
+        for (int k = 0; k < PER; ++k) {   // ascending ids: a tie keeps the lower one
+            if (!((taken >> k) & 1u) && w[k] > bv) { bv = w[k]; bid = l + 32 * k; }
         }
 #pragma unroll
         for (int d = 1; d < 32; d <<= 1) {
@@ -1249,6 +1254,12 @@ __global__ __launch_bounds__(64) void k_router(const float *__restrict__ logits,
         weights[o] = sel_v[threadIdx.x] * dinv;
     }
     if (threadIdx.x == 0 && (flags | dflags)) atomicOr(error, flags | dflags);
+}
+
+template<int PER>
+void router_launch(const float *logits, int tokens, int top_k, float *prob, int32_t *ids, float *weights,
+                   int *error, hipStream_t s) {
+    k_router<PER><<<tokens, 64, 0, s>>>(logits, top_k, prob, ids, weights, error);
 }
 
 inline unsigned blocks_for(size_t n, unsigned per) { return static_cast<unsigned>((n + per - 1) / per); }
@@ -1457,7 +1468,16 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
 
 hipError_t launch_router(const float *logits, int tokens, int experts, int top_k, float *prob, int32_t *ids,
                          float *weights, int *error, hipStream_t s) {
-    k_router<<<tokens, 64, 0, s>>>(logits, experts, top_k, prob, ids, weights, error);
+    using Launch = void (*)(const float *, int, int, float *, int32_t *, float *, int *, hipStream_t);
+    static constexpr Launch table[kRouterMaxPer] = {
+        router_launch<1>, router_launch<2>, router_launch<3>, router_launch<4>, router_launch<5>,
+        router_launch<6>, router_launch<7>, router_launch<8>, router_launch<9>, router_launch<10>,
+        router_launch<11>, router_launch<12>, router_launch<13>, router_launch<14>, router_launch<15>,
+        router_launch<16>, router_launch<17>, router_launch<18>, router_launch<19>, router_launch<20>,
+        router_launch<21>, router_launch<22>, router_launch<23>, router_launch<24>, router_launch<25>,
+        router_launch<26>, router_launch<27>, router_launch<28>, router_launch<29>, router_launch<30>,
+        router_launch<31>, router_launch<32>};
+    table[experts / 32 - 1](logits, tokens, top_k, prob, ids, weights, error, s);
     return hipGetLastError();
 }
 

@@ -692,7 +692,13 @@ def test_expf_device_matches_libm():
     """The kernels' expf on the GPU equals the C library's expf bit for bit
     (the function the reference's CPU SiLU calls, src/cpu_expert.cpp:251)."""
     from test_abi import _expf_sample
-    x = _expf_sample()
+    # Regimes interleaved lane by lane (normal, overflow, underflow, +-inf,
+    # nan, the |x| >= 88 band): the table lookup must not depend on which
+    # lanes of a wave take a special-case exit.
+    special = np.array([0.5, 100.0, -200.0, np.inf, -np.inf, np.nan, 88.5, -95.0, -103.0, 88.7, -104.0, 1e-30],
+                       np.float32)
+    mixed = np.tile(special, 64) * np.repeat(np.float32([1, -1]), special.size * 32)
+    x = np.concatenate([mixed, _expf_sample()])
     got = host(moe_ffn.expf_device(dev(x)))
     ref = O.expf_libm(x)
     nan = np.isnan(ref)
