@@ -209,6 +209,33 @@ void mo_matrix_gpu_order(const uint8_t *w, int K, int M, const mo_q8_1 *x, int c
         }
 }
 
+/* Q4_1 rows (20-byte blocks {half d; half m; u8 qs[16]}, value q*d + m) in
+ * the same lane order (cpu_expert.cpp:167-194): per block dd = half(d4*d8)
+ * and ms = half(m4*s8), both rounded to half (RNE), and per fragment
+ *     acc = acc + fma(float(I_f), dd, ms * 0.5)
+ * (a separate add, not a fused one), then the same fold. */
+void mo_matrix_gpu_order_q41(const uint8_t *w, int K, int M, const mo_q8_1 *x, int cols, float *out) {
+    const int nb = K / 32;
+    for (int c = 0; c < cols; ++c)
+        for (int r = 0; r < M; ++r) {
+            float lane[128];
+            for (int i = 0; i < 128; ++i) lane[i] = 0.0f;
+            for (int k = 0; k < nb; ++k) {
+                const uint8_t *blk = w + ((size_t)r * nb + k) * 20;
+                const mo_q8_1 *a = &x[(size_t)c * nb + k];
+                const float d4 = mo_half_to_float(ld16(blk)), m4 = mo_half_to_float(ld16(blk + 2));
+                const float d8 = mo_half_to_float(a->d), s8 = mo_half_to_float(a->s);
+                const float dd = mo_half_to_float(mo_float_to_half(d4 * d8));
+                const float ms = mo_half_to_float(mo_float_to_half(m4 * s8));
+                for (int f = 0; f < 2; ++f) {
+                    float *acc = &lane[2 * (k % 64) + f];
+                    *acc = *acc + fmaf((float)fragment_dot(blk + 4, a->qs, f), dd, ms * 0.5f);
+                }
+            }
+            fold128(lane, &out[(size_t)c * M + r]);
+        }
+}
+
 int mo_cpu_has_avx2(void) {
 #if MO_X86
     __builtin_cpu_init();
@@ -282,7 +309,7 @@ typedef struct {
 
 /* cpu_expert.cpp:233-267 (whole stage). */
 static int expert_run(const uint8_t *gw, const uint8_t *uw, const uint8_t *dw, int H, int I,
-                      const mo_q8_1 *x, int cols, float *y, expert_scratch *s, int use_avx2) {
+                      const mo_q8_1 *x, int cols, float *y, expert_scratch *s, int use_avx2, int down_q41) {
     if (use_avx2) {
         if (mo_matrix_gpu_order_avx2(gw, H, I, x, cols, s->gate) != MO_OK) return MO_UNSUPPORTED_CPU;
         mo_matrix_gpu_order_avx2(uw, H, I, x, cols, s->up);
@@ -300,16 +327,17 @@ static int expert_run(const uint8_t *gw, const uint8_t *uw, const uint8_t *dw, i
         s->middle[i] = m;
     }
     if (mo_quantize_q8(s->middle, mid, s->mq8) != MO_OK) return MO_NUMERIC_ERROR;
-    if (use_avx2) mo_matrix_gpu_order_avx2(dw, I, H, s->mq8, cols, y);
+    if (down_q41) mo_matrix_gpu_order_q41(dw, I, H, s->mq8, cols, y);
+    else if (use_avx2) mo_matrix_gpu_order_avx2(dw, I, H, s->mq8, cols, y);
     else mo_matrix_gpu_order(dw, I, H, s->mq8, cols, y);
     for (size_t i = 0; i < (size_t)cols * H; ++i)
         if (!isfinite(y[i])) return MO_NUMERIC_ERROR;
     return MO_OK;
 }
 
-int mo_expert_forward(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int H, int I,
-                      const mo_q8_1 *x, int cols, float *y, float *gate_out, float *up_out,
-                      float *middle_out, mo_q8_1 *middle_q8_out, int use_avx2) {
+static int expert_forward_impl(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int H, int I,
+                               const mo_q8_1 *x, int cols, float *y, float *gate_out, float *up_out,
+                               float *middle_out, mo_q8_1 *middle_q8_out, int use_avx2, int down_q41) {
     if (H <= 0 || I <= 0 || H % 32 || I % 32 || cols <= 0) return MO_INVALID_ARGUMENT;
     expert_scratch s;
     const size_t mid = (size_t)cols * I;
@@ -319,7 +347,7 @@ int mo_expert_forward(const uint8_t *gate, const uint8_t *up, const uint8_t *dow
     s.mq8 = malloc(mid / 32 * sizeof(mo_q8_1));
     int rc = MO_INVALID_ARGUMENT;
     if (s.gate && s.up && s.middle && s.mq8) {
-        rc = expert_run(gate, up, down, H, I, x, cols, y, &s, use_avx2);
+        rc = expert_run(gate, up, down, H, I, x, cols, y, &s, use_avx2, down_q41);
         if (gate_out) memcpy(gate_out, s.gate, mid * sizeof(float));
         if (up_out) memcpy(up_out, s.up, mid * sizeof(float));
         if (middle_out) memcpy(middle_out, s.middle, mid * sizeof(float));
@@ -327,6 +355,20 @@ int mo_expert_forward(const uint8_t *gate, const uint8_t *up, const uint8_t *dow
     }
     free(s.gate); free(s.up); free(s.middle); free(s.mq8);
     return rc;
+}
+
+int mo_expert_forward(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int H, int I,
+                      const mo_q8_1 *x, int cols, float *y, float *gate_out, float *up_out,
+                      float *middle_out, mo_q8_1 *middle_q8_out, int use_avx2) {
+    return expert_forward_impl(gate, up, down, H, I, x, cols, y, gate_out, up_out, middle_out, middle_q8_out,
+                               use_avx2, 0);
+}
+
+int mo_expert_forward_q41(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int H, int I,
+                          const mo_q8_1 *x, int cols, float *y, float *gate_out, float *up_out,
+                          float *middle_out, mo_q8_1 *middle_q8_out) {
+    return expert_forward_impl(gate, up, down, H, I, x, cols, y, gate_out, up_out, middle_out, middle_q8_out,
+                               0, 1);
 }
 
 /* ------------------------------------------------------------- routes ----- */
@@ -387,14 +429,18 @@ static void shared_add(const float *s, const float *gate, int t, int H, float *y
     }
 }
 
-static size_t expert_bytes(int H, int I) { return (size_t)3 * H / 32 * I * 18; }
+/* One expert's canonical bytes: gate and up Q4_0, down Q4_0 (18-byte
+ * blocks) or Q4_1 (20-byte blocks). */
+static size_t expert_bytes(int H, int I, int down_q41) {
+    return (size_t)H / 32 * I * (36 + (down_q41 ? 20 : 18));
+}
 
-int mo_moe_layer(const float *x, int tokens, int H, int I, int E, int top_k,
-                 const uint8_t *experts_q4, const uint8_t *shared_q4, const int32_t *ids,
-                 const float *weights, const float *shared_gate, float *y, float *contrib_out,
-                 mo_q8_1 *x_q8_out, const uint8_t *mask, int use_avx2) {
+static int moe_layer_impl(const float *x, int tokens, int H, int I, int E, int top_k,
+                          const uint8_t *experts_q4, const uint8_t *shared_q4, const int32_t *ids,
+                          const float *weights, const float *shared_gate, float *y, float *contrib_out,
+                          mo_q8_1 *x_q8_out, const uint8_t *mask, int use_avx2, int down_q41) {
     if (tokens < 1 || H % 32 || I % 32 || E < 1 || top_k < 1) return MO_INVALID_ARGUMENT;
-    const size_t nbx = (size_t)H / 32, eb = expert_bytes(H, I), mat = (size_t)H / 32 * I * 18;
+    const size_t nbx = (size_t)H / 32, eb = expert_bytes(H, I, down_q41), mat = (size_t)H / 32 * I * 18;
     const size_t assignments = (size_t)tokens * top_k;
     mo_q8_1 *xq = malloc(sizeof(mo_q8_1) * nbx * tokens);
     int32_t *at = malloc(4 * assignments), *ar = malloc(4 * assignments), *ae = malloc(4 * assignments);
@@ -422,7 +468,7 @@ int mo_moe_layer(const float *x, int tokens, int H, int I, int E, int top_k,
         if (mask && !mask[t]) continue;
         const uint8_t *base = experts_q4 + (size_t)e * eb;
         rc = expert_run(base, base + mat, base + 2 * mat, H, I, xq + (size_t)t * nbx, 1,
-                        contrib + ((size_t)t * top_k + r) * H, &s, use_avx2);
+                        contrib + ((size_t)t * top_k + r) * H, &s, use_avx2, down_q41);
         if (rc != MO_OK) goto done;
     }
     for (int t = 0; t < tokens; ++t) {
@@ -431,7 +477,7 @@ int mo_moe_layer(const float *x, int tokens, int H, int I, int E, int top_k,
                        y + (size_t)t * H);
         if (shared_q4) {
             rc = expert_run(shared_q4, shared_q4 + mat, shared_q4 + 2 * mat, H, I, xq + (size_t)t * nbx, 1,
-                            row, &s, use_avx2);
+                            row, &s, use_avx2, down_q41);
             if (rc != MO_OK) goto done;
             shared_add(row, shared_gate, t, H, y);
         }
@@ -443,6 +489,22 @@ done:
     free(xq); free(at); free(ar); free(ae); free(aw); free(counts); free(offsets); free(contrib);
     free(row); free(s.gate); free(s.up); free(s.middle); free(s.mq8);
     return rc;
+}
+
+int mo_moe_layer(const float *x, int tokens, int H, int I, int E, int top_k,
+                 const uint8_t *experts_q4, const uint8_t *shared_q4, const int32_t *ids,
+                 const float *weights, const float *shared_gate, float *y, float *contrib_out,
+                 mo_q8_1 *x_q8_out, const uint8_t *mask, int use_avx2) {
+    return moe_layer_impl(x, tokens, H, I, E, top_k, experts_q4, shared_q4, ids, weights, shared_gate, y,
+                          contrib_out, x_q8_out, mask, use_avx2, 0);
+}
+
+int mo_moe_layer_q41(const float *x, int tokens, int H, int I, int E, int top_k,
+                     const uint8_t *experts_q4, const uint8_t *shared_q4, const int32_t *ids,
+                     const float *weights, const float *shared_gate, float *y, float *contrib_out,
+                     mo_q8_1 *x_q8_out, const uint8_t *mask) {
+    return moe_layer_impl(x, tokens, H, I, E, top_k, experts_q4, shared_q4, ids, weights, shared_gate, y,
+                          contrib_out, x_q8_out, mask, 0, 1);
 }
 
 /* ----------------------------------------------------------- topology ----- */
@@ -508,7 +570,7 @@ typedef struct {
 typedef struct { pool_state *st; int id; } worker_arg;
 
 static void run_phases(pool_state *st, expert_scratch *s, mo_q8_1 *gx, float *out) {
-    const size_t nbx = (size_t)st->H / 32, eb = expert_bytes(st->H, st->I);
+    const size_t nbx = (size_t)st->H / 32, eb = expert_bytes(st->H, st->I, 0);
     const size_t mat = (size_t)st->H / 32 * st->I * 18;
     const int H = st->H, I = st->I, k = st->top_k;
     /* Phase 1: quantize tokens. */
@@ -527,7 +589,7 @@ static void run_phases(pool_state *st, expert_scratch *s, mo_q8_1 *gx, float *ou
         for (int c = 0; c < job->columns; ++c)
             memcpy(gx + c * nbx, st->xq + (size_t)st->at[job->first + c] * nbx, sizeof(mo_q8_1) * nbx);
         const uint8_t *base = st->experts_q4 + (size_t)job->expert * eb;
-        if (expert_run(base, base + mat, base + 2 * mat, H, I, gx, job->columns, out, s, 1) != MO_OK)
+        if (expert_run(base, base + mat, base + 2 * mat, H, I, gx, job->columns, out, s, 1, 0) != MO_OK)
             atomic_store(&st->failure, MO_NUMERIC_ERROR);
         for (int c = 0; c < job->columns; ++c) {
             const int p = job->first + c;
@@ -543,7 +605,7 @@ static void run_phases(pool_state *st, expert_scratch *s, mo_q8_1 *gx, float *ou
             const int n = st->tokens - t0 < 3 ? st->tokens - t0 : 3;
             const uint8_t *base = st->shared_q4;
             if (expert_run(base, base + mat, base + 2 * mat, H, I, st->xq + (size_t)t0 * nbx, n,
-                           st->shared_out + (size_t)t0 * H, s, 1) != MO_OK)
+                           st->shared_out + (size_t)t0 * H, s, 1, 0) != MO_OK)
                 atomic_store(&st->failure, MO_NUMERIC_ERROR);
         }
     }

@@ -137,6 +137,19 @@ int mo_allowed_physical_cpus(int *cpus, int capacity, int *count);
 /* The C library's expf over an array (checker for the kernels' expf). */
 void mo_expf_libm(const float *x, float *y, size_t n);
 
+/* Q4_1 down rows (20-byte blocks {half d; half m; qs[16]}) in the cpu_expert
+ * order with the half-rounded d4*d8 and m4*s8 products (cpu_expert.cpp:167-194),
+ * and the whole expert / layer with Q4_1 down matrices (gate/up stay Q4_0;
+ * an expert's canonical bytes are [gate 18-B blocks | up | down 20-B blocks]). */
+void mo_matrix_gpu_order_q41(const uint8_t *w, int K, int M, const mo_q8_1 *x, int cols, float *out);
+int mo_expert_forward_q41(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int H, int I,
+                          const mo_q8_1 *x, int cols, float *y, float *gate_out, float *up_out,
+                          float *middle_out, mo_q8_1 *middle_q8_out);
+int mo_moe_layer_q41(const float *x, int tokens, int H, int I, int E, int top_k,
+                     const uint8_t *experts_q4, const uint8_t *shared_q4, const int32_t *ids,
+                     const float *weights, const float *shared_gate, float *y, float *contrib_out,
+                     mo_q8_1 *x_q8_out, const uint8_t *mask);
+
 /* Router: softmax over each row of `experts` logits (experts % 32 == 0) as
  * router_softmax (src/hip/session_ops.hip:401-434), and top_k selection with
  * the XOR-bucket denominator as select_routes (src/session.hip:666-687).

@@ -53,6 +53,9 @@ def _load_oracle():
     lib.mo_expf_libm.restype = None
     lib.mo_expf_libm.argtypes = [_P, _P, _SZ]
     lib.mo_router_softmax.argtypes = [_P, _I, _I, _P]
+    lib.mo_matrix_gpu_order_q41.argtypes = [_P, _I, _I, _P, _I, _P]
+    lib.mo_expert_forward_q41.argtypes = [_P, _P, _P, _I, _I, _P, _I, _P, _P, _P, _P, _P]
+    lib.mo_moe_layer_q41.argtypes = [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P]
     lib.mo_select_routes.argtypes = [_P, _I, _I, _I, _P, _P]
     lib.mo_block_dot.argtypes = [_P, _P]
     lib.mo_scaled_dot_q4_0.restype = ctypes.c_float
@@ -103,6 +106,7 @@ def ref():
         r.ref_matmul.argtypes = [_I, _P, _I, _I, _P, _I, _P]
         r.ref_cpu_expert.argtypes = [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P]
         r.ref_route_groups.argtypes = [_P, _P, _I, _P, _P, _P, _P, _P]
+        r.ref_cpu_expert_q41.argtypes = [_P, _P, _P, _P, _I, _P, _P, _P]
         _ref = r
     return _ref
 
@@ -181,8 +185,9 @@ def matrix_gpu_order(w, K, M, xq, avx2=False):
     return out
 
 
-def expert_forward(gate, up, down, H, I, xq, avx2=False):
-    """cpu_expert whole stage.  Returns dict(y, gate, up, middle, middle_q8)."""
+def expert_forward(gate, up, down, H, I, xq, avx2=False, down_q41=False):
+    """cpu_expert whole stage (down Q4_0, or Q4_1 with down_q41).  Returns
+    dict(y, gate, up, middle, middle_q8)."""
     xq = as_q8(xq).reshape(-1, H // 32)
     cols = xq.shape[0]
     y = np.zeros((cols, H), np.float32)
@@ -190,9 +195,12 @@ def expert_forward(gate, up, down, H, I, xq, avx2=False):
     u = np.zeros((cols, I), np.float32)
     m = np.zeros((cols, I), np.float32)
     mq = np.zeros((cols, I // 32), Q8_DTYPE)
-    rc = lib().mo_expert_forward(_ptr(np.ascontiguousarray(gate)), _ptr(np.ascontiguousarray(up)),
-                                 _ptr(np.ascontiguousarray(down)), H, I, _ptr(xq), cols, _ptr(y),
-                                 _ptr(g), _ptr(u), _ptr(m), _ptr(mq), 1 if avx2 else 0)
+    args = (_ptr(np.ascontiguousarray(gate)), _ptr(np.ascontiguousarray(up)), _ptr(np.ascontiguousarray(down)),
+            H, I, _ptr(xq), cols, _ptr(y), _ptr(g), _ptr(u), _ptr(m), _ptr(mq))
+    if down_q41:
+        rc = lib().mo_expert_forward_q41(*args)
+    else:
+        rc = lib().mo_expert_forward(*args, 1 if avx2 else 0)
     _check(rc, "expert_forward")
     return dict(y=y, gate=g, up=u, middle=m, middle_q8=mq)
 
@@ -222,8 +230,9 @@ def routed_fold(contrib, weights):
 
 
 def moe_layer(x, H, I, E, experts_q4, ids, weights, shared_q4=None, shared_gate=None,
-              token_mask=None, avx2=True, want_contrib=False):
-    """Whole MoE layer in the reference order.  Returns dict(y, x_q8[, contrib])."""
+              token_mask=None, avx2=True, want_contrib=False, down_q41=False):
+    """Whole MoE layer in the reference order (down Q4_1 with down_q41).
+    Returns dict(y, x_q8[, contrib])."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     tokens = x.shape[0]
     ids = np.ascontiguousarray(ids, dtype=np.int32)
@@ -234,10 +243,12 @@ def moe_layer(x, H, I, E, experts_q4, ids, weights, shared_q4=None, shared_gate=
     contrib = np.zeros((tokens, k, H), np.float32) if want_contrib else None
     sg = None if shared_gate is None else np.ascontiguousarray(shared_gate, dtype=np.float32)
     mask = None if token_mask is None else np.ascontiguousarray(token_mask, dtype=np.uint8)
-    rc = lib().mo_moe_layer(_ptr(x), tokens, H, I, E, k, _ptr(experts_q4),
-                            _ptr(shared_q4) if shared_q4 is not None else None,
-                            _ptr(ids), _ptr(weights), _ptr(sg), _ptr(y), _ptr(contrib), _ptr(xq),
-                            _ptr(mask), 1 if avx2 else 0)
+    args = (_ptr(x), tokens, H, I, E, k, _ptr(experts_q4), _ptr(shared_q4) if shared_q4 is not None else None,
+            _ptr(ids), _ptr(weights), _ptr(sg), _ptr(y), _ptr(contrib), _ptr(xq), _ptr(mask))
+    if down_q41:
+        rc = lib().mo_moe_layer_q41(*args)
+    else:
+        rc = lib().mo_moe_layer(*args, 1 if avx2 else 0)
     _check(rc, "moe_layer")
     out = dict(y=y, x_q8=xq)
     if want_contrib:
@@ -299,6 +310,17 @@ def ref_cpu_expert(gate, up, down, xq):
     st = ref().ref_cpu_expert(_ptr(gate), _ptr(up), _ptr(down), _ptr(xq), cols, _ptr(y), _ptr(g),
                               _ptr(u), _ptr(m), _ptr(mq))
     return st, dict(y=y, gate=g, up=u, middle=m, middle_q8=mq)
+
+
+def ref_cpu_expert_q41(gate, up, down, xq):
+    """The reference's CPU expert with a Q4_1 down matrix (2560/640)."""
+    xq = as_q8(xq).reshape(-1, 80)
+    cols = xq.shape[0]
+    y = np.zeros((cols, 2560), np.float32)
+    m = np.zeros((cols, 640), np.float32)
+    mq = np.zeros((cols, 20), Q8_DTYPE)
+    st = ref().ref_cpu_expert_q41(_ptr(gate), _ptr(up), _ptr(down), _ptr(xq), cols, _ptr(y), _ptr(m), _ptr(mq))
+    return st, dict(y=y, middle=m, middle_q8=mq)
 
 
 def ref_route_groups(ids, weights):

@@ -84,6 +84,30 @@ int ref_cpu_expert(const void* gate, const void* up, const void* down, const voi
     return rc ? 100 + rc : status;
 }
 
+// The same expert with a Q4_1 down matrix (640 -> 2560, 20-byte blocks), as
+// the checkpoint's layers 0-5 hold it.  Outputs y, middle and middle_q8.
+int ref_cpu_expert_q41(const void* gate, const void* up, const void* down, const void* x, int columns,
+                       float* out, float* middle_out, void* middle_q8_out) {
+    int status = -1;
+    const int rc = guarded([&] {
+        static CpuExpertScratch scratch;
+        const auto down_bytes = static_cast<std::size_t>(640 / 32) * 2560 * sizeof(Q4_1);
+        const QMatrix d{TensorType::Q4_1, 640, 2560, {static_cast<const std::byte*>(down), down_bytes}};
+        const CpuExpert expert(q4(gate, 2560, 640), q4(up, 2560, 640), d);
+        CpuExpertJob job;
+        job.expert = &expert;
+        job.columns = columns;
+        job.output = {out, static_cast<std::size_t>(columns) * 2560};
+        for (int c = 0; c < columns; ++c)
+            job.input[static_cast<std::size_t>(c)] = {static_cast<const Q8_1*>(x) + c * 80, 80};
+        status = static_cast<int>(run_cpu_expert(job, scratch));
+        const auto mid = static_cast<std::size_t>(columns) * 640;
+        if (middle_out) std::memcpy(middle_out, scratch.middle.data(), mid * sizeof(float));
+        if (middle_q8_out) std::memcpy(middle_q8_out, scratch.middle_q8.data(), mid / 32 * sizeof(Q8_1));
+    });
+    return rc ? 100 + rc : status;
+}
+
 // RouteGroups::prepare (512 experts, top-10).  Outputs the grouped
 // assignments as four parallel arrays plus counts[512].
 int ref_route_groups(const std::int32_t* ids, const float* weights, int tokens, std::int32_t* token,

@@ -41,6 +41,23 @@ def q4_matrix(seed, K, M, negative_scales=True):
     return blocks.reshape(-1)
 
 
+def q4_1_matrix(seed, K, M):
+    """M rows x K/32 canonical Q4_1 blocks {half d; half m; 16 code bytes}:
+    d as q4_matrix (signed), m about -8*d so values stay centred, with a
+    seeded spread of +-25% and some exact zeros."""
+    nb = M * K // 32
+    q4 = q4_matrix(seed, K, M).reshape(nb, 18)
+    d = q4[:, :2].copy().view(np.float16).astype(np.float32).reshape(nb)
+    u = uniform(seed + 29, nb)
+    m = (-8.0 * d * (0.75 + 0.5 * u)).astype(np.float32)
+    m = np.where(stream(seed + 31, nb) % np.uint64(17) == 0, np.float32(0), m)
+    blocks = np.empty((nb, 20), np.uint8)
+    blocks[:, :2] = q4[:, :2]
+    blocks[:, 2:4] = m.astype(np.float16).view(np.uint8).reshape(nb, 2)
+    blocks[:, 4:] = q4[:, 2:]
+    return blocks.reshape(-1)
+
+
 def expert_weights(H, I, seed=101):
     return q4_matrix(seed, H, I), q4_matrix(seed + 1, H, I), q4_matrix(seed + 2, I, H)
 

@@ -22,7 +22,7 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, HERE)
 
 import oracle as O  # noqa: E402
-from golden_inputs import expert_weights, quant_blocks, matmul_case, route_cases, expert_input  # noqa: E402
+from golden_inputs import expert_weights, quant_blocks, matmul_case, route_cases, expert_input, q4_1_matrix  # noqa: E402
 
 
 def quant_fixture():
@@ -50,6 +50,21 @@ def expert_fixture():
              up=out["up"], middle=out["middle"], middle_q8=out["middle_q8"].view(np.uint8), y=out["y"],
              weights_sha256=np.array(sha))
     print("cpu_expert_2560x640.npz sha", sha[:16])
+
+
+def expert_q41_fixture():
+    """The same expert shape with a Q4_1 down matrix (gate/up Q4_0)."""
+    gate, up, _ = expert_weights(2560, 640)
+    down = q4_1_matrix(404, 640, 2560)
+    x = expert_input(3, 2560)
+    rc, xq = O.ref_quantize_q8(x)
+    assert rc == 0
+    st, out = O.ref_cpu_expert_q41(gate, up, down, xq)
+    assert st == 0, st
+    sha = hashlib.sha256(gate.tobytes() + up.tobytes() + down.tobytes()).hexdigest()
+    np.savez(os.path.join(HERE, "cpu_expert_2560x640_q41.npz"), middle=out["middle"],
+             middle_q8=out["middle_q8"].view(np.uint8), y=out["y"], weights_sha256=np.array(sha))
+    print("cpu_expert_2560x640_q41.npz sha", sha[:16])
 
 
 def matmul_fixture():
@@ -81,5 +96,6 @@ if __name__ == "__main__":
         sys.exit("oracle/_ref/libref.so missing: run make -C oracle (needs /root/reference)")
     quant_fixture()
     expert_fixture()
+    expert_q41_fixture()
     matmul_fixture()
     routes_fixture()

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from golden_inputs import expert_input, expert_weights, matmul_case, route_cases
+from golden_inputs import expert_input, expert_weights, matmul_case, q4_1_matrix, route_cases
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
@@ -194,6 +194,41 @@ def test_expert_forward_bitwise_vs_reference(expert_fixture, avx2):
     for key in ("gate", "up", "middle", "y"):
         assert np.array_equal(out[key].view(np.uint32), f[key].view(np.uint32)), key
     assert np.array_equal(q8_bytes(out["middle_q8"]), f["middle_q8"].reshape(-1))
+
+
+def test_expert_q41_down_bitwise_vs_reference(expert_fixture):
+    """Q4_1 down (the checkpoint's layers 0-5): the oracle's expert equals the
+    compiled reference's cpu_expert bit for bit; dropping the half rounding of
+    d4*d8 and m4*s8 changes the output (so the rounding is really tested)."""
+    f0, gate, up, _ = expert_fixture
+    f = load("cpu_expert_2560x640_q41.npz")
+    down = q4_1_matrix(404, 640, 2560)
+    assert hashlib.sha256(gate.tobytes() + up.tobytes() + down.tobytes()).hexdigest() == str(f["weights_sha256"])
+    out = O.expert_forward(gate, up, down, 2560, 640, f0["x_q8"], down_q41=True)
+    assert np.array_equal(out["middle"].view(np.uint32), f["middle"].view(np.uint32))
+    assert np.array_equal(q8_bytes(out["middle_q8"]), f["middle_q8"].reshape(-1))
+    assert np.array_equal(out["y"].view(np.uint32), f["y"].view(np.uint32))
+    # Unrounded products, same order otherwise (numpy restatement of one row).
+    mq = O.as_q8(out["middle_q8"]).reshape(3, 20)
+    blk = down.reshape(2560, 20, 20)
+    r = 7
+    lane = np.zeros(128, np.float32)
+    d4 = blk[r, :, :2].copy().view(np.float16).astype(np.float32).reshape(20)
+    m4 = blk[r, :, 2:4].copy().view(np.float16).astype(np.float32).reshape(20)
+    d8 = mq["d"][0].view(np.float16).astype(np.float32)
+    s8 = mq["s"][0].view(np.float16).astype(np.float32)
+    for k in range(20):
+        qs = blk[r, k, 4:]
+        c = mq["qs"][0, k].astype(np.int32)
+        for fr in range(2):
+            j = np.arange(8 * fr, 8 * fr + 8)
+            dot = int(np.sum((qs[j] & 15).astype(np.int32) * c[j] + (qs[j] >> 4).astype(np.int32) * c[j + 16]))
+            dd, ms = np.float32(d4[k] * d8[k]), np.float32(m4[k] * s8[k])
+            lane[2 * k + fr] = np.float32(lane[2 * k + fr] + np.float32(np.float64(dot) * dd + np.float64(ms * np.float32(0.5))))
+    lane[:64] = lane[:64] + lane[64:]
+    for mask in (1, 2, 4, 8, 16, 32):
+        lane[:64] = (lane[:64] + lane[np.arange(64) ^ mask]).astype(np.float32)
+    assert lane[0] != out["y"][0, r]
 
 
 def test_expert_columns_are_independent(expert_fixture):
