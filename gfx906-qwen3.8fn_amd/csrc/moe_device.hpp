@@ -87,9 +87,15 @@ __device__ __forceinline__ float mul_half_hi(uint32_t h2, float t) {
 // (z0 + z1) + 0 for every pair of floats, so each +0 is done once.  Rows are
 // traded during the first three stages: lane l ends with the total of row
 // 4*(l & 1) + 2*(l>>1 & 1) + (l>>2 & 1); lanes l and l ^ 8 agree.
-__device__ __forceinline__ float rows8_down_exact(const uint4 (&w)[8], uint4 d4p, uint4 x0, uint4 x1, uint32_t head,
-                                                  bool has, int lane) {
-    const float d8 = h2f(head), c4 = -4.0f * h2f(head >> 16);
+//
+// Q41: Q4_1 rows (m4p holds the rows' m as d4p holds d).  Per block
+// dd = half(d4*d8), ms = half(m4*s8) (RNE) and per fragment
+// z = +0 + fma(float(I_f), dd, ms*0.5) (src/cpu_expert.cpp:167-194); the
+// fold is the same.
+template<bool Q41>
+__device__ __forceinline__ float rows8_down_exact(const uint4 (&w)[8], uint4 d4p, uint4 m4p, uint4 x0, uint4 x1,
+                                                  uint32_t head, bool has, int lane) {
+    const float d8 = h2f(head), s8 = h2f(head >> 16), c4 = -4.0f * s8;
     const bool c0 = lane & 1, c1 = lane & 2, c2 = lane & 4;
     float v4[4];
 #pragma unroll
@@ -101,9 +107,18 @@ __device__ __forceinline__ float rows8_down_exact(const uint4 (&w)[8], uint4 d4p
             int f0, f1;
             fragment_dots(w[q], x0, x1, f0, f1);
             const uint32_t d4w = (&d4p.x)[q >> 1];
-            const float t0 = fmaf(static_cast<float>(f0), d8, c4), t1 = fmaf(static_cast<float>(f1), d8, c4);
-            const float z0 = (q & 1) ? mul_half_hi(d4w, t0) : mul_half_lo(d4w, t0);
-            const float z1 = (q & 1) ? mul_half_hi(d4w, t1) : mul_half_lo(d4w, t1);
+            float z0, z1;
+            if constexpr (Q41) {
+                const uint32_t m4w = (&m4p.x)[q >> 1];
+                const float d4 = (q & 1) ? h2f(d4w >> 16) : h2f(d4w), m4 = (q & 1) ? h2f(m4w >> 16) : h2f(m4w);
+                const float dd = h2f(f2h(d4 * d8)), hm = h2f(f2h(m4 * s8)) * 0.5f;
+                z0 = fmaf(static_cast<float>(f0), dd, hm);
+                z1 = fmaf(static_cast<float>(f1), dd, hm);
+            } else {
+                const float t0 = fmaf(static_cast<float>(f0), d8, c4), t1 = fmaf(static_cast<float>(f1), d8, c4);
+                z0 = (q & 1) ? mul_half_hi(d4w, t0) : mul_half_lo(d4w, t0);
+                z1 = (q & 1) ? mul_half_hi(d4w, t1) : mul_half_lo(d4w, t1);
+            }
             z[h] = has ? (z0 + z1) + 0.0f : 0.0f;
         }
         const float send = c0 ? z[0] : z[1];

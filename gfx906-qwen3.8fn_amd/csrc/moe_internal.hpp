@@ -40,6 +40,7 @@ __host__ __device__ inline size_t scale_index(size_t row, int kb, int blocks_per
 struct Bank {
     const uint8_t *gate_codes, *up_codes, *down_codes;
     const uint16_t *gate_scales, *up_scales, *down_scales;
+    const uint16_t *down_mins;   // Q4_1 down matrices: fp16 m per block (scale order); nullptr for Q4_0
 };
 
 // A work item: one expert group slice of <= kStreamTokens (stream path) or
@@ -87,12 +88,15 @@ hipError_t launch_planes_to_canonical(Act in, void *q8, int blocks, hipStream_t 
 // Weight planes of one matrix kind (codes / scales = plane bases).  The call
 // covers plane blocks [block0, block0 + blocks); rows hold `blocks_per_row`
 // blocks and scales use scale group `group`.
-hipError_t launch_repack_weights(const uint8_t *canonical, uint8_t *codes, uint16_t *scales, size_t blocks,
-                                 size_t block0, int blocks_per_row, int group, hipStream_t s);
-hipError_t launch_unpack_weights(const uint8_t *codes, const uint16_t *scales, uint8_t *canonical, size_t blocks,
-                                 size_t block0, int blocks_per_row, int group, hipStream_t s);
+// mins == nullptr: 18-byte Q4_0 canonical blocks; else 20-byte Q4_1 blocks
+// whose m goes to / comes from the mins plane.
+hipError_t launch_repack_weights(const uint8_t *canonical, uint8_t *codes, uint16_t *scales, uint16_t *mins,
+                                 size_t blocks, size_t block0, int blocks_per_row, int group, hipStream_t s);
+hipError_t launch_unpack_weights(const uint8_t *codes, const uint16_t *scales, const uint16_t *mins,
+                                 uint8_t *canonical, size_t blocks, size_t block0, int blocks_per_row, int group,
+                                 hipStream_t s);
 // Synthetic blocks: hashed from (seed, hash0 + plane block index).
-hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, size_t blocks, size_t hash0,
+hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, uint16_t *mins, size_t blocks, size_t hash0,
                                     int blocks_per_row, int group, uint64_t seed, hipStream_t s);
 
 // Quantize x into `xq` and group routes (tokens <= kSmallGroupTokens path or

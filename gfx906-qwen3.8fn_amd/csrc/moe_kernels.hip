@@ -58,14 +58,22 @@ __global__ __launch_bounds__(256) void k_planes_to_canonical(const uint8_t *code
 
 // ---------------------------------------------------------- weight planes ---
 // Canonical blocks are 18 bytes with 2-byte alignment: read them as 9 u16.
+// Canonical blocks -> planes.  mins == nullptr: 18-byte Q4_0 blocks {d, qs};
+// else 20-byte Q4_1 blocks {d, m, qs}, m going to its own plane (same order
+// as the scales).
 __global__ __launch_bounds__(256) void k_repack(const uint16_t *canonical, uint32_t *codes,
-                                                uint16_t *scales, size_t blocks, size_t block0, int nb,
-                                                int group) {
+                                                uint16_t *scales, uint16_t *mins, size_t blocks, size_t block0,
+                                                int nb, int group) {
     const size_t b = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= blocks) return;
     const size_t g = block0 + b;
-    const uint16_t *src = canonical + b * 9;
-    scales[scale_index(g / nb, static_cast<int>(g % nb), nb, group)] = src[0];
+    const uint16_t *src = canonical + b * (mins ? 10 : 9);
+    const size_t si = scale_index(g / nb, static_cast<int>(g % nb), nb, group);
+    scales[si] = src[0];
+    if (mins) {
+        mins[si] = src[1];
+        ++src;
+    }
     uint4 c;
     c.x = src[1] | (static_cast<uint32_t>(src[2]) << 16);
     c.y = src[3] | (static_cast<uint32_t>(src[4]) << 16);
@@ -75,14 +83,19 @@ __global__ __launch_bounds__(256) void k_repack(const uint16_t *canonical, uint3
 }
 
 __global__ __launch_bounds__(256) void k_unpack(const uint32_t *codes, const uint16_t *scales,
-                                                uint16_t *canonical, size_t blocks, size_t block0, int nb,
-                                                int group) {
+                                                const uint16_t *mins, uint16_t *canonical, size_t blocks,
+                                                size_t block0, int nb, int group) {
     const size_t b = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= blocks) return;
     const size_t g = block0 + b;
     const uint4 c = reinterpret_cast<const uint4 *>(codes)[g];
-    uint16_t *dst = canonical + b * 9;
-    dst[0] = scales[scale_index(g / nb, static_cast<int>(g % nb), nb, group)];
+    uint16_t *dst = canonical + b * (mins ? 10 : 9);
+    const size_t si = scale_index(g / nb, static_cast<int>(g % nb), nb, group);
+    dst[0] = scales[si];
+    if (mins) {
+        dst[1] = mins[si];
+        ++dst;
+    }
     dst[1] = c.x & 0xffffu; dst[2] = c.x >> 16;
     dst[3] = c.y & 0xffffu; dst[4] = c.y >> 16;
     dst[5] = c.z & 0xffffu; dst[6] = c.z >> 16;
@@ -98,7 +111,9 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
 
 // Synthetic Q4_0 blocks: codes uniform 0..15 (16 random bytes), d =
 // half(|N(0, 0.02)|) by Box-Muller, all from a counter hash of (seed, block).
-__global__ __launch_bounds__(256) void k_synthetic(uint32_t *codes, uint16_t *scales, size_t blocks,
+// With a mins plane (Q4_1): m = half(-8 d (0.75 + 0.5 u)), values centred as
+// in Q4_0.
+__global__ __launch_bounds__(256) void k_synthetic(uint32_t *codes, uint16_t *scales, uint16_t *mins, size_t blocks,
                                                    size_t hash0, int nb, int group, uint64_t seed) {
     const size_t b = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= blocks) return;
@@ -112,7 +127,13 @@ __global__ __launch_bounds__(256) void k_synthetic(uint32_t *codes, uint16_t *sc
     const float u1 = (static_cast<float>(h2 >> 40) + 1.0f) * 0x1p-24f;          // (0, 1]
     const float u2 = static_cast<float>((h2 >> 16) & 0xffffffu) * 0x1p-24f;      // [0, 1)
     const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
-    scales[scale_index(b / nb, static_cast<int>(b % nb), nb, group)] = static_cast<uint16_t>(f2h(fabsf(z) * 0.02f));
+    const float d = h2f(f2h(fabsf(z) * 0.02f));
+    const size_t si = scale_index(b / nb, static_cast<int>(b % nb), nb, group);
+    scales[si] = static_cast<uint16_t>(f2h(d));
+    if (mins) {
+        const float u3 = static_cast<float>(h2 & 0xffffu) * 0x1p-16f;             // [0, 1)
+        mins[si] = static_cast<uint16_t>(f2h(-8.0f * d * (0.75f + 0.5f * u3)));
+    }
 }
 
 // Plain streaming read of n 16-byte words, one contiguous chunk per
@@ -709,8 +730,10 @@ __global__ __launch_bounds__(512, 3) void k_gate_up_lean(FfnArgs a) {
 // rows); 8 waves x 8 rows.  With I/32 = 16 blocks a row is 256 code bytes, so
 // a wave load covers 4 rows (16 lanes per row).  Unweighted results go to the
 // contribution row (token * out_stride_k + rank) like the reference's scatter
-// (src/hip/session_ops.hip:357-373).
-template<int LPR, bool Dbg>
+// (src/hip/session_ops.hip:357-373).  Q41: Q4_1 blocks, per block
+// dot * half(d4 d8) + half(m4 s8) (src/cpu_expert.cpp:167-194 summed over
+// the block's two fragments).
+template<int LPR, bool Q41, bool Dbg>
 __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
     constexpr int T = kStreamTokens, RPL = 64 / LPR, LOADS = 8 / RPL;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -722,7 +745,7 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
         const int row0 = (u % S) * 64 + wave * 8;
         const size_t mrow = static_cast<size_t>(it.expert) * H + row0;
         const uint8_t *codes = a.bank.down_codes + mrow * nbi * 16;
-        const uint16_t *scales = a.bank.down_scales;
+        const uint16_t *scales = a.bank.down_scales, *mins = a.bank.down_mins;
         float acc[LOADS][T];
 #pragma unroll
         for (int l = 0; l < LOADS; ++l)
@@ -730,12 +753,14 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
             for (int j = 0; j < T; ++j) acc[l][j] = 0.0f;
         for (int kb = kb0; kb < nbi; kb += LPR) {
             uint4 w[LOADS];
-            float d4[LOADS];
+            float d4[LOADS], m4[LOADS];
 #pragma unroll
             for (int l = 0; l < LOADS; ++l) {
                 const int r = l * RPL + sub;
                 w[l] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbi + kb) * 16);
-                d4[l] = h2f(scales[scale_index(mrow + r, kb, nbi, kScaleGroupDown)]);
+                const size_t si = scale_index(mrow + r, kb, nbi, kScaleGroupDown);
+                d4[l] = h2f(scales[si]);
+                m4[l] = Q41 ? h2f(mins[si]) : 0.0f;
             }
 #pragma unroll
             for (int j = 0; j < T; ++j) {
@@ -744,7 +769,7 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
                 const uint4 x0 = *reinterpret_cast<const uint4 *>(a.mq.codes + xb * 32);
                 const uint4 x1 = *reinterpret_cast<const uint4 *>(a.mq.codes + xb * 32 + 16);
                 const uint32_t hd = a.mq.heads[xb];
-                const float d8 = h2f(hd), c8 = -8.0f * h2f(hd >> 16);
+                const float d8 = h2f(hd), s8 = h2f(hd >> 16), c8 = -8.0f * s8;
 #pragma unroll
                 for (int l = 0; l < LOADS; ++l) {
                     const int dot = dot_block(w[l], x0, x1);
@@ -752,7 +777,12 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
                         if (a.down_dots)
                             a.down_dots[(static_cast<size_t>(it.first + j) * H + row0 + l * RPL + sub) * nbi + kb] = dot;
                     }
-                    acc[l][j] = fmaf(d4[l], fmaf(static_cast<float>(dot), d8, c8), acc[l][j]);
+                    if constexpr (Q41) {
+                        const float dd = h2f(f2h(d4[l] * d8)), ms = h2f(f2h(m4[l] * s8));
+                        acc[l][j] = acc[l][j] + fmaf(static_cast<float>(dot), dd, ms);
+                    } else {
+                        acc[l][j] = fmaf(d4[l], fmaf(static_cast<float>(dot), d8, c8), acc[l][j]);
+                    }
                 }
             }
         }
@@ -781,8 +811,8 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
 // contribution rows (token * out_stride_k + rank), like the reference's
 // scatter (src/hip/session_ops.hip:357-373).
 // NBI = 16 specialises I = 512 (every lane holds a block); NBI = 0 reads
-// I/32 <= 16 at run time.
-template<int NBI, bool Dbg>
+// I/32 <= 16 at run time.  Q41: Q4_1 blocks (mins plane in the scales' order).
+template<int NBI, bool Q41, bool Dbg>
 __global__ __launch_bounds__(128, 4) void k_down_lean(FfnArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = NBI ? NBI : a.shape.I / 32;
@@ -820,6 +850,11 @@ __global__ __launch_bounds__(128, 4) void k_down_lean(FfnArgs a) {
 #pragma unroll
     for (int l = 0; l < 8; ++l) w[l] = buffer_load16(wr, lane_off, 4 * l * row_bytes);
     const uint4 d4p = buffer_load16(sr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
+    uint4 m4p = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (Q41) {
+        const auto mr = buffer_rsrc(a.bank.down_mins + mrow * nbi, 4 * row_bytes);
+        m4p = buffer_load16(mr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
+    }
     // A pair's middle row is loaded while the previous pair computes.
     auto load_x = [&](int j, uint4 &x0, uint4 &x1, uint32_t &hx) {
         const size_t xrow = static_cast<size_t>(first + (j < ncols ? j : 0)) * nbi;
@@ -847,7 +882,7 @@ __global__ __launch_bounds__(128, 4) void k_down_lean(FfnArgs a) {
                         a.down_dots[(static_cast<size_t>(first + j) * H + row0 + 4 * l + sub) * nbi + kl] =
                             dot_block(w[l], x0, x1);
             }
-            const float v = rows8_down_exact(w, d4p, x0, x1, hx, has, lane);
+            const float v = rows8_down_exact<Q41>(w, d4p, m4p, x0, x1, hx, has, lane);
             if ((lane & 8) == 0) {
                 const size_t orow = static_cast<size_t>(toks[j]) * a.out_stride_k + rnks[j];
                 a.out[orow * H + row0 + 4 * lr + sub] = v;
@@ -977,7 +1012,8 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
 // unweighted row sums of its pair (lane (sub, kb): rows sub + 4l, l < 8, as in
 // k_down_lean), then 32 threads fold the ranks in order and add the shared
 // expert -- the separately rounded fold of k_fold, with no contribution
-// buffer and no second kernel.
+// buffer and no second kernel.  Q41: Q4_1 down blocks.
+template<bool Q41>
 __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
     __shared__ float part[kDecodeMaxPairs][32];
     __shared__ int valid[kDecodeMaxPairs];
@@ -1012,10 +1048,15 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
 #pragma unroll
         for (int l = 0; l < 8; ++l) w[l] = buffer_load16(wr, lane_off, 4 * l * row_bytes);
         const uint4 d4p = buffer_load16(sr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
+        uint4 m4p = make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (Q41) {
+            const auto mr = buffer_rsrc(a.bank.down_mins + mrow * nbi, 4 * row_bytes);
+            m4p = buffer_load16(mr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
+        }
         const uint4 x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
         const uint4 x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
         const uint32_t hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
-        const float v = rows8_down_exact(w, d4p, x0, x1, hx, has, lane);
+        const float v = rows8_down_exact<Q41>(w, d4p, m4p, x0, x1, hx, has, lane);
         const int lr = 4 * (lane & 1) + 2 * ((lane >> 1) & 1) + ((lane >> 2) & 1);
         if ((lane & 8) == 0) part[r][4 * lr + sub] = v;
     }
@@ -1295,25 +1336,27 @@ hipError_t launch_planes_to_canonical(Act in, void *q8, int blocks, hipStream_t 
     return hipGetLastError();
 }
 
-hipError_t launch_repack_weights(const uint8_t *canonical, uint8_t *codes, uint16_t *scales, size_t blocks,
+hipError_t launch_repack_weights(const uint8_t *canonical, uint8_t *codes, uint16_t *scales, uint16_t *mins,
+                                 size_t blocks,
                                  size_t block0, int blocks_per_row, int group, hipStream_t s) {
     k_repack<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<const uint16_t *>(canonical),
-                                                      reinterpret_cast<uint32_t *>(codes), scales, blocks, block0,
-                                                      blocks_per_row, group);
+                                                      reinterpret_cast<uint32_t *>(codes), scales, mins, blocks,
+                                                      block0, blocks_per_row, group);
     return hipGetLastError();
 }
 
-hipError_t launch_unpack_weights(const uint8_t *codes, const uint16_t *scales, uint8_t *canonical, size_t blocks,
+hipError_t launch_unpack_weights(const uint8_t *codes, const uint16_t *scales, const uint16_t *mins,
+                                 uint8_t *canonical, size_t blocks,
                                  size_t block0, int blocks_per_row, int group, hipStream_t s) {
-    k_unpack<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<const uint32_t *>(codes), scales,
+    k_unpack<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<const uint32_t *>(codes), scales, mins,
                                                       reinterpret_cast<uint16_t *>(canonical), blocks, block0,
                                                       blocks_per_row, group);
     return hipGetLastError();
 }
 
-hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, size_t blocks, size_t hash0,
+hipError_t launch_synthetic_weights(uint8_t *codes, uint16_t *scales, uint16_t *mins, size_t blocks, size_t hash0,
                                     int blocks_per_row, int group, uint64_t seed, hipStream_t s) {
-    k_synthetic<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<uint32_t *>(codes), scales, blocks,
+    k_synthetic<<<blocks_for(blocks, 256), 256, 0, s>>>(reinterpret_cast<uint32_t *>(codes), scales, mins, blocks,
                                                          hash0, blocks_per_row, group, seed);
     return hipGetLastError();
 }
@@ -1432,7 +1475,9 @@ hipError_t launch_decode_down_fold(const DecodeArgs &d, hipStream_t s) {
     const Shape &sh = d.f.shape;
     const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0);
     const unsigned groups = static_cast<unsigned>((sh.H / 32 + 7) / 8);
-    k_decode_down_fold<<<8u * groups * d.f.tokens, 64 * P1, 0, s>>>(d);
+    const dim3 grid(8u * groups * d.f.tokens), block(64 * P1);
+    if (d.f.bank.down_mins) k_decode_down_fold<true><<<grid, block, 0, s>>>(d);
+    else k_decode_down_fold<false><<<grid, block, 0, s>>>(d);
     return hipGetLastError();
 }
 
@@ -1447,21 +1492,24 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
     if (mfma) return launch_down_mfma(a, s);
     const int nbi = a.shape.I / 32;
     const unsigned grid = stream_grid(a, a.shape.H / 64);
-    const bool dbg = a.down_dots != nullptr;
+    const bool dbg = a.down_dots != nullptr, q41 = a.bank.down_mins != nullptr;
     if (nbi <= 16) {
         const unsigned g = stream_item_bound(a) * static_cast<unsigned>(a.shape.H / 64);
-        if (dbg) k_down_lean<0, true><<<g, 128, 0, s>>>(a);
-        else if (nbi == 16) k_down_lean<16, false><<<g, 128, 0, s>>>(a);
-        else k_down_lean<0, false><<<g, 128, 0, s>>>(a);
-    } else if (nbi <= 8) {
-        if (dbg) k_down_stream<8, true><<<grid, 512, 0, s>>>(a);
-        else k_down_stream<8, false><<<grid, 512, 0, s>>>(a);
-    } else if (nbi <= 16) {
-        if (dbg) k_down_stream<16, true><<<grid, 512, 0, s>>>(a);
-        else k_down_stream<16, false><<<grid, 512, 0, s>>>(a);
+        if (q41) {
+            if (dbg) k_down_lean<0, true, true><<<g, 128, 0, s>>>(a);
+            else if (nbi == 16) k_down_lean<16, true, false><<<g, 128, 0, s>>>(a);
+            else k_down_lean<0, true, false><<<g, 128, 0, s>>>(a);
+        } else {
+            if (dbg) k_down_lean<0, false, true><<<g, 128, 0, s>>>(a);
+            else if (nbi == 16) k_down_lean<16, false, false><<<g, 128, 0, s>>>(a);
+            else k_down_lean<0, false, false><<<g, 128, 0, s>>>(a);
+        }
+    } else if (q41) {
+        if (dbg) k_down_stream<64, true, true><<<grid, 512, 0, s>>>(a);
+        else k_down_stream<64, true, false><<<grid, 512, 0, s>>>(a);
     } else {
-        if (dbg) k_down_stream<64, true><<<grid, 512, 0, s>>>(a);
-        else k_down_stream<64, false><<<grid, 512, 0, s>>>(a);
+        if (dbg) k_down_stream<64, false, true><<<grid, 512, 0, s>>>(a);
+        else k_down_stream<64, false, false><<<grid, 512, 0, s>>>(a);
     }
     return hipGetLastError();
 }

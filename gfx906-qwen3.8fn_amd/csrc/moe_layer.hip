@@ -27,6 +27,8 @@ struct moe_ffn_layer {
     moe::Bank bank{};
     uint8_t *gate_codes = nullptr, *up_codes = nullptr, *down_codes = nullptr;
     uint16_t *gate_scales = nullptr, *up_scales = nullptr, *down_scales = nullptr;
+    uint16_t *down_mins = nullptr;   // Q4_1 down matrices only
+    bool down_q41 = false;
     void *ws_mem = nullptr;
     size_t ws_bytes = 0;
     Act xq{}, mq{};
@@ -72,7 +74,8 @@ bool config_ok(const moe_ffn_config *c) {
     return c && c->hidden >= 32 && c->hidden <= 16384 && c->hidden % 32 == 0 && c->intermediate >= 32 &&
            c->intermediate <= 16384 && c->intermediate % 32 == 0 && c->experts >= 1 && c->experts <= 4096 &&
            c->top_k >= 1 && c->top_k <= 32 && c->top_k <= c->experts && (c->has_shared == 0 || c->has_shared == 1) &&
-           c->max_tokens >= 1 && c->max_tokens <= 65536 && c->hidden % 64 == 0;
+           c->max_tokens >= 1 && c->max_tokens <= 65536 && c->hidden % 64 == 0 &&
+           (c->down_type == MOE_DOWN_Q4_0 || c->down_type == MOE_DOWN_Q4_1);
 }
 
 Shape shape_of(const moe_ffn_config &c) {
@@ -81,14 +84,26 @@ Shape shape_of(const moe_ffn_config &c) {
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-size_t expert_blocks(const Shape &s) { return static_cast<size_t>(3) * s.H / 32 * s.I; }
+size_t matrix_blocks(const Shape &s) { return static_cast<size_t>(s.H / 32) * s.I; }
 
-// Bank: code planes (16 B/block) then scale planes (2 B/block).
-size_t bank_layout(const Shape &s, size_t off[6]) {
-    const size_t gb = static_cast<size_t>(s.Ep) * s.I * (s.H / 32);   // gate blocks == up blocks == down blocks
+// Canonical bytes of one matrix kind (m: 0 gate, 1 up, 2 down) of one expert,
+// and of one expert: 18-byte Q4_0 blocks, 20-byte Q4_1 blocks for a Q4_1 down.
+size_t matrix_bytes(const Shape &s, bool down_q41, int m) {
+    return matrix_blocks(s) * (m == 2 && down_q41 ? 20 : 18);
+}
+size_t expert_bytes(const Shape &s, bool down_q41) {
+    return matrix_bytes(s, down_q41, 0) + matrix_bytes(s, down_q41, 1) + matrix_bytes(s, down_q41, 2);
+}
+
+// Bank: code planes (16 B/block), scale planes (2 B/block), and for Q4_1
+// down matrices a mins plane (2 B/block).
+size_t bank_layout(const Shape &s, bool down_q41, size_t off[7]) {
+    const size_t gb = static_cast<size_t>(s.Ep) * matrix_blocks(s);   // gate blocks == up blocks == down blocks
     size_t p = 0;
     for (int m = 0; m < 3; ++m) { off[m] = p; p = round_up(p + gb * 16, 256); }
     for (int m = 0; m < 3; ++m) { off[3 + m] = p; p = round_up(p + gb * 2, 256); }
+    off[6] = p;
+    if (down_q41) p = round_up(p + gb * 2, 256);
     return p;
 }
 
@@ -145,6 +160,9 @@ int finish_create(moe_ffn_layer *L) {
     L->contrib = reinterpret_cast<float *>(b + w.contrib);
     if (hipMemset(L->ws_mem, 0, w.total) != hipSuccess) return hipErrorOutOfMemory;
     if (const char *env = std::getenv("MOE_FFN_MFMA_MIN")) L->mfma_min = std::atoi(env);
+    // Q4_1 down matrices have streaming kernels only, and the two item kinds
+    // are shared by gate/up and down: every group streams.
+    if (L->down_q41) L->mfma_min = 0;
     if (const char *env = std::getenv("MOE_FFN_DECODE")) L->decode_mode = std::atoi(env) ? 1 : 0;
     if (const char *env = std::getenv("MOE_FFN_STREAMS")) L->two_streams = std::atoi(env) != 1;
     int cus = 0;
@@ -154,8 +172,8 @@ int finish_create(moe_ffn_layer *L) {
 }
 
 int alloc_bank(moe_ffn_layer *L) {
-    size_t off[6];
-    L->bank_bytes = bank_layout(L->shape, off);
+    size_t off[7];
+    L->bank_bytes = bank_layout(L->shape, L->down_q41, off);
     if (hipMalloc(&L->bank_mem, L->bank_bytes) != hipSuccess) return hipErrorOutOfMemory;
     auto *b = static_cast<uint8_t *>(L->bank_mem);
     L->gate_codes = b + off[0];
@@ -164,37 +182,40 @@ int alloc_bank(moe_ffn_layer *L) {
     L->gate_scales = reinterpret_cast<uint16_t *>(b + off[3]);
     L->up_scales = reinterpret_cast<uint16_t *>(b + off[4]);
     L->down_scales = reinterpret_cast<uint16_t *>(b + off[5]);
-    L->bank = moe::Bank{L->gate_codes, L->up_codes, L->down_codes, L->gate_scales, L->up_scales, L->down_scales};
+    L->down_mins = L->down_q41 ? reinterpret_cast<uint16_t *>(b + off[6]) : nullptr;
+    L->bank = moe::Bank{L->gate_codes, L->up_codes, L->down_codes, L->gate_scales, L->up_scales, L->down_scales,
+                        L->down_mins};
     return hipSuccess;
 }
 
 // One matrix kind's planes: gate (m = 0), up (1), down (2).
 struct Plane {
     uint8_t *codes;
-    uint16_t *scales;
+    uint16_t *scales, *mins;   // mins: Q4_1 down only
     int blocks_per_row, group;
 };
 
 Plane plane(const moe_ffn_layer *L, int m) {
     const int nbh = L->shape.H / 32, nbi = L->shape.I / 32;
-    if (m == 0) return Plane{L->gate_codes, L->gate_scales, nbh, moe::kScaleGroupGateUp};
-    if (m == 1) return Plane{L->up_codes, L->up_scales, nbh, moe::kScaleGroupGateUp};
-    return Plane{L->down_codes, L->down_scales, nbi, moe::kScaleGroupDown};
+    if (m == 0) return Plane{L->gate_codes, L->gate_scales, nullptr, nbh, moe::kScaleGroupGateUp};
+    if (m == 1) return Plane{L->up_codes, L->up_scales, nullptr, nbh, moe::kScaleGroupGateUp};
+    return Plane{L->down_codes, L->down_scales, L->down_mins, nbi, moe::kScaleGroupDown};
 }
 
 // Repack `count` canonical experts starting at expert `first` from a device
 // staging buffer into the planes.
 int repack_experts(moe_ffn_layer *L, const uint8_t *staging, int first, int count) {
     const Shape &s = L->shape;
-    const size_t mblocks = static_cast<size_t>(s.I) * (s.H / 32);   // blocks per matrix
+    const size_t mblocks = matrix_blocks(s);   // blocks per matrix
     for (int i = 0; i < count; ++i) {
         const size_t e = static_cast<size_t>(first + i);
-        const uint8_t *src = staging + static_cast<size_t>(i) * expert_blocks(s) * 18;
+        const uint8_t *src = staging + static_cast<size_t>(i) * expert_bytes(s, L->down_q41);
         for (int m = 0; m < 3; ++m) {
             const Plane pl = plane(L, m);
-            const hipError_t r = moe::launch_repack_weights(src + m * mblocks * 18, pl.codes, pl.scales, mblocks,
-                                                            e * mblocks, pl.blocks_per_row, pl.group, nullptr);
+            const hipError_t r = moe::launch_repack_weights(src, pl.codes, pl.scales, pl.mins, mblocks, e * mblocks,
+                                                            pl.blocks_per_row, pl.group, nullptr);
             if (r != hipSuccess) return r;
+            src += matrix_bytes(s, L->down_q41, m);
         }
     }
     return hipSuccess;
@@ -210,6 +231,7 @@ int create_common(const moe_ffn_config *config, int device, moe_ffn_layer **laye
     L->cfg = *config;
     L->device = device;
     L->shape = shape_of(*config);
+    L->down_q41 = config->down_type == MOE_DOWN_Q4_1;
     int r = alloc_bank(L);
     if (r == hipSuccess && (hipStreamCreateWithFlags(&L->side, hipStreamNonBlocking) != hipSuccess ||
                             hipEventCreateWithFlags(&L->fork, hipEventDisableTiming) != hipSuccess ||
@@ -221,7 +243,7 @@ int create_common(const moe_ffn_config *config, int device, moe_ffn_layer **laye
 
 int upload(moe_ffn_layer *L, const void *experts, const void *shared, bool from_device) {
     const Shape &s = L->shape;
-    const size_t ebytes = expert_blocks(s) * 18;
+    const size_t ebytes = expert_bytes(s, L->down_q41);
     const int chunk = static_cast<int>(std::max<size_t>(1, (size_t{256} << 20) / ebytes));
     uint8_t *staging = nullptr;
     if (!from_device && hipMalloc(&staging, static_cast<size_t>(chunk) * ebytes) != hipSuccess)
@@ -260,14 +282,15 @@ int upload(moe_ffn_layer *L, const void *experts, const void *shared, bool from_
 // one copy and one repack launch.
 int upload_tensors(moe_ffn_layer *L, const void *const routed[3], const void *const shared[3]) {
     const Shape &s = L->shape;
-    const size_t mblocks = static_cast<size_t>(s.I) * (s.H / 32);   // blocks per expert matrix
-    const size_t mbytes = mblocks * 18;
-    const int chunk = static_cast<int>(std::max<size_t>(1, (size_t{256} << 20) / mbytes));
+    const size_t mblocks = matrix_blocks(s);   // blocks per expert matrix
+    const size_t max_bytes = matrix_bytes(s, L->down_q41, 2);
+    const int chunk = static_cast<int>(std::max<size_t>(1, (size_t{256} << 20) / max_bytes));
     uint8_t *staging = nullptr;
-    if (hipMalloc(&staging, static_cast<size_t>(chunk) * mbytes) != hipSuccess) return hipErrorOutOfMemory;
+    if (hipMalloc(&staging, static_cast<size_t>(chunk) * max_bytes) != hipSuccess) return hipErrorOutOfMemory;
     int r = hipSuccess;
     for (int m = 0; m < 3 && r == hipSuccess; ++m) {
         const Plane pl = plane(L, m);
+        const size_t mbytes = matrix_bytes(s, L->down_q41, m);
         for (int first = 0; first < s.Ep && r == hipSuccess; first += chunk) {
             const int n = std::min(chunk, s.Ep - first);
             const int nr = std::max(0, std::min(n, s.E - first));   // routed experts in this chunk
@@ -277,7 +300,7 @@ int upload_tensors(moe_ffn_layer *L, const void *const routed[3], const void *co
             if (r == hipSuccess && nr < n)   // the shared expert follows the routed ones
                 r = hipMemcpy(staging + static_cast<size_t>(nr) * mbytes, shared[m], mbytes, hipMemcpyHostToDevice);
             if (r == hipSuccess)
-                r = moe::launch_repack_weights(staging, pl.codes, pl.scales, static_cast<size_t>(n) * mblocks,
+                r = moe::launch_repack_weights(staging, pl.codes, pl.scales, pl.mins, static_cast<size_t>(n) * mblocks,
                                                static_cast<size_t>(first) * mblocks, pl.blocks_per_row, pl.group,
                                                nullptr);
             if (r == hipSuccess) r = hipDeviceSynchronize();
@@ -317,9 +340,9 @@ extern "C" {
 
 int moe_ffn_memory_bytes(const moe_ffn_config *config, size_t *weight_bytes, size_t *workspace_bytes) {
     if (!config_ok(config) || !weight_bytes || !workspace_bytes) return kInvalid;
-    size_t off[6];
+    size_t off[7];
     const Shape s = shape_of(*config);
-    *weight_bytes = bank_layout(s, off);
+    *weight_bytes = bank_layout(s, config->down_type == MOE_DOWN_Q4_1, off);
     *workspace_bytes = ws_layout(s, config->max_tokens).total;
     return hipSuccess;
 }
@@ -376,7 +399,7 @@ int moe_ffn_create_synthetic(const moe_ffn_config *config, uint64_t seed, int de
     const size_t blocks = static_cast<size_t>(L->shape.Ep) * L->shape.I * (L->shape.H / 32);
     for (int m = 0; m < 3 && r == hipSuccess; ++m) {
         const Plane pl = plane(L, m);
-        r = moe::launch_synthetic_weights(pl.codes, pl.scales, blocks, static_cast<size_t>(m) * blocks,
+        r = moe::launch_synthetic_weights(pl.codes, pl.scales, pl.mins, blocks, static_cast<size_t>(m) * blocks,
                                           pl.blocks_per_row, pl.group, seed, nullptr);
     }
     if (r == hipSuccess) r = hipDeviceSynchronize();
@@ -403,18 +426,21 @@ int moe_ffn_destroy(moe_ffn_layer *L) {
 int moe_ffn_export_expert(moe_ffn_layer *L, int expert, void *host_q4) {
     if (!L || !host_q4 || expert < 0 || expert >= L->shape.Ep) return kInvalid;
     const Shape &s = L->shape;
-    const size_t mblocks = static_cast<size_t>(s.I) * (s.H / 32);
+    const size_t mblocks = matrix_blocks(s);
+    const size_t ebytes = expert_bytes(s, L->down_q41);
     uint8_t *staging = nullptr;
     if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
-    if (hipMalloc(&staging, 3 * mblocks * 18) != hipSuccess) return hipErrorOutOfMemory;
+    if (hipMalloc(&staging, ebytes) != hipSuccess) return hipErrorOutOfMemory;
     const size_t e = static_cast<size_t>(expert);
     int r = hipSuccess;
+    uint8_t *dst = staging;
     for (int m = 0; m < 3 && r == hipSuccess; ++m) {
         const Plane pl = plane(L, m);
-        r = moe::launch_unpack_weights(pl.codes, pl.scales, staging + m * mblocks * 18, mblocks, e * mblocks,
-                                       pl.blocks_per_row, pl.group, nullptr);
+        r = moe::launch_unpack_weights(pl.codes, pl.scales, pl.mins, dst, mblocks, e * mblocks, pl.blocks_per_row,
+                                       pl.group, nullptr);
+        dst += matrix_bytes(s, L->down_q41, m);
     }
-    if (r == hipSuccess) r = hipMemcpy(host_q4, staging, 3 * mblocks * 18, hipMemcpyDeviceToHost);
+    if (r == hipSuccess) r = hipMemcpy(host_q4, staging, ebytes, hipMemcpyDeviceToHost);
     (void)hipFree(staging);
     return r;
 }
@@ -614,7 +640,8 @@ int moe_ffn_expert_down(moe_ffn_layer *L, int expert, const void *middle_q8, int
         !aligned(error, 4) || columns < 1 || columns > L->cfg.max_tokens || (down_dots && !aligned(down_dots, 4)) ||
         path < 0 || path > 2)
         return kInvalid;
-    const bool mfma = path != MOE_PATH_STREAM;
+    if (L->down_q41 && path == MOE_PATH_MFMA) return hipErrorNotSupported;   // Q4_1 down: streaming kernels only
+    const bool mfma = path != MOE_PATH_STREAM && !L->down_q41;
     if (mfma && !aligned(y, 16)) return kInvalid;   // the MFMA down kernel stores float4 rows
     const auto s = static_cast<hipStream_t>(stream);
     const Shape &sh = L->shape;

@@ -23,6 +23,8 @@ HEADER = os.path.join(ROOT, "include", "moe_ffn.h")
 
 Q8_BLOCK = 36
 Q4_BLOCK = 18
+Q4_1_BLOCK = 20
+DOWN_Q4_0, DOWN_Q4_1 = 0, 1     # MOE_DOWN_Q4_0 / MOE_DOWN_Q4_1
 PATH_AUTO, PATH_STREAM, PATH_MFMA = 0, 1, 2
 STAGE_PREPARE, STAGE_GATE_UP, STAGE_DOWN, STAGE_FOLD = 0, 1, 2, 3
 
@@ -35,7 +37,8 @@ class MoeError(RuntimeError):
 
 class Config(ctypes.Structure):
     _fields_ = [("hidden", ctypes.c_int), ("intermediate", ctypes.c_int), ("experts", ctypes.c_int),
-                ("top_k", ctypes.c_int), ("has_shared", ctypes.c_int), ("max_tokens", ctypes.c_int)]
+                ("top_k", ctypes.c_int), ("has_shared", ctypes.c_int), ("max_tokens", ctypes.c_int),
+                ("down_type", ctypes.c_int)]
 
 
 _lib = None
@@ -101,16 +104,19 @@ def _stream(stream):
     return ctypes.c_void_p(s.cuda_stream)
 
 
-def expert_bytes(hidden, intermediate):
-    return 3 * hidden // 32 * intermediate * Q4_BLOCK
+def expert_bytes(hidden, intermediate, down_type=DOWN_Q4_0):
+    """Canonical bytes of one expert: gate and up Q4_0, down Q4_0 or Q4_1."""
+    return hidden // 32 * intermediate * (2 * Q4_BLOCK + (Q4_1_BLOCK if down_type == DOWN_Q4_1 else Q4_BLOCK))
 
 
 class MoeLayer:
     """One MoE layer resident on the GPU (weights + workspace for max_tokens)."""
 
     def __init__(self, hidden, intermediate, experts, top_k, has_shared, max_tokens, experts_q4=None,
-                 shared_q4=None, synthetic_seed=None, device=0, tensors=None, shared_tensors=None):
-        self.cfg = Config(hidden, intermediate, experts, top_k, 1 if has_shared else 0, max_tokens)
+                 shared_q4=None, synthetic_seed=None, device=0, tensors=None, shared_tensors=None,
+                 down_type=DOWN_Q4_0):
+        self.cfg = Config(hidden, intermediate, experts, top_k, 1 if has_shared else 0, max_tokens, down_type)
+        self.down_type = down_type
         self.H, self.I, self.E, self.k = hidden, intermediate, experts, top_k
         self.has_shared = bool(has_shared)
         self.max_tokens = max_tokens
@@ -119,12 +125,13 @@ class MoeLayer:
         lib = library()
         if tensors is not None:   # (gate_exps, up_exps, down_exps) host arrays, reference tensor layout
             ts = [np.ascontiguousarray(t, dtype=np.uint8) for t in tensors]
-            mb = hidden // 32 * intermediate * 18
-            assert all(t.size == experts * mb for t in ts)
+            nb = hidden // 32 * intermediate
+            mb = [nb * Q4_BLOCK, nb * Q4_BLOCK, nb * (Q4_1_BLOCK if down_type == DOWN_Q4_1 else Q4_BLOCK)]
+            assert all(t.size == experts * m for t, m in zip(ts, mb))
             ss = [None, None, None]
             if has_shared:
                 ss = [np.ascontiguousarray(t, dtype=np.uint8) for t in shared_tensors]
-                assert all(t.size == mb for t in ss)
+                assert all(t.size == m for t, m in zip(ss, mb))
             ptr = lambda a: None if a is None else ctypes.c_void_p(a.ctypes.data)
             st = lib.moe_ffn_create_tensors(ctypes.byref(self.cfg), *[ptr(t) for t in ts], *[ptr(t) for t in ss],
                                             device, ctypes.byref(handle))
@@ -133,11 +140,11 @@ class MoeLayer:
                                               ctypes.byref(handle))
         elif isinstance(experts_q4, np.ndarray):
             experts_q4 = np.ascontiguousarray(experts_q4, dtype=np.uint8)
-            assert experts_q4.size == experts * expert_bytes(hidden, intermediate)
+            assert experts_q4.size == experts * expert_bytes(hidden, intermediate, down_type)
             sh = None
             if has_shared:
                 sh = np.ascontiguousarray(shared_q4, dtype=np.uint8)
-                assert sh.size == expert_bytes(hidden, intermediate)
+                assert sh.size == expert_bytes(hidden, intermediate, down_type)
             st = lib.moe_ffn_create(ctypes.byref(self.cfg), ctypes.c_void_p(experts_q4.ctypes.data),
                                     None if sh is None else ctypes.c_void_p(sh.ctypes.data), device,
                                     ctypes.byref(handle))
@@ -160,7 +167,7 @@ class MoeLayer:
 
     # ------------------------------------------------------------ queries --
     def export_expert(self, expert):
-        out = np.zeros(expert_bytes(self.H, self.I), np.uint8)
+        out = np.zeros(expert_bytes(self.H, self.I, self.down_type), np.uint8)
         _check(library().moe_ffn_export_expert(self.handle, expert, ctypes.c_void_p(out.ctypes.data)),
                "moe_ffn_export_expert")
         return out

@@ -2,6 +2,9 @@
 
 Weights: Q4_0 blocks (18 bytes: half d, 16 code bytes), d = half(|N(0, 0.02)|),
 codes uniform 0..15 (low nibble = element j, high nibble = element j+16).
+Q4_1 down blocks (20 bytes: half d, half m, 16 code bytes) take the same d and
+codes with m = half(-8 d (0.75 + 0.5 u)), u uniform [0, 1), so values stay
+centred about zero.
 Activations: fp32 N(0, 1), token-major [N][H].
 Routing: top-k distinct experts per token, weights = softmax of N(0,1) logits.
   uniform  - every expert equally likely
@@ -17,10 +20,12 @@ import numpy as np
 
 H, I, E, TOP_K = 2048, 512, 512, 10
 Q4_BLOCK = 18
+Q4_1_BLOCK = 20
 
 
-def expert_bytes(hidden=H, intermediate=I):
-    return 3 * hidden // 32 * intermediate * Q4_BLOCK
+def expert_bytes(hidden=H, intermediate=I, down_type=0):
+    """Canonical bytes of one expert (down_type 1: Q4_1 down blocks)."""
+    return hidden // 32 * intermediate * (2 * Q4_BLOCK + (Q4_1_BLOCK if down_type == 1 else Q4_BLOCK))
 
 
 def q4_blocks(nblocks, rng):
@@ -32,11 +37,28 @@ def q4_blocks(nblocks, rng):
     return out
 
 
-def q4_bank(n_experts, hidden=H, intermediate=I, seed=0):
-    """n_experts experts, each [gate I x H/32 | up I x H/32 | down H x I/32] blocks."""
+def q4_1_blocks(nblocks, rng):
+    """nblocks canonical Q4_1 blocks as uint8 [nblocks, 20]."""
+    q4 = q4_blocks(nblocks, rng)
+    d = q4[:, :2].copy().view(np.float16).astype(np.float32).reshape(nblocks)
+    m = (-8.0 * d * (0.75 + 0.5 * rng.random(nblocks, dtype=np.float32))).astype(np.float16)
+    out = np.empty((nblocks, Q4_1_BLOCK), np.uint8)
+    out[:, :2] = q4[:, :2]
+    out[:, 2:4] = m.view(np.uint8).reshape(nblocks, 2)
+    out[:, 4:] = q4[:, 2:]
+    return out
+
+
+def q4_bank(n_experts, hidden=H, intermediate=I, seed=0, down_type=0):
+    """n_experts experts, each [gate I x H/32 | up I x H/32 | down H x I/32]
+    blocks; down_type 1 makes the down blocks Q4_1."""
     rng = np.random.default_rng(seed)
-    nb = n_experts * 3 * (hidden // 32) * intermediate
-    return q4_blocks(nb, rng).reshape(-1)
+    mb = (hidden // 32) * intermediate
+    if down_type != 1:
+        return q4_blocks(n_experts * 3 * mb, rng).reshape(-1)
+    gu = q4_blocks(n_experts * 2 * mb, rng).reshape(n_experts, -1)
+    dn = q4_1_blocks(n_experts * mb, rng).reshape(n_experts, -1)
+    return np.ascontiguousarray(np.concatenate([gu, dn], axis=1)).reshape(-1)
 
 
 def activations(tokens, hidden=H, seed=0):
@@ -101,10 +123,10 @@ def routes_for(name, seed=0, tokens=None):
     return routes_zipf(n, kw["s"], seed=seed)
 
 
-def algorithmic_bytes(tokens, touched, shared=True, hidden=H, intermediate=I, k=TOP_K):
+def algorithmic_bytes(tokens, touched, shared=True, hidden=H, intermediate=I, k=TOP_K, down_type=0):
     """Bytes a layer must move at minimum: touched experts' weights (+shared),
     fp32 x in and y out, int32 ids + fp32 weights."""
-    return (touched + (1 if shared else 0)) * expert_bytes(hidden, intermediate) + \
+    return (touched + (1 if shared else 0)) * expert_bytes(hidden, intermediate, down_type) + \
         tokens * hidden * 4 * 2 + tokens * k * 8
 
 

@@ -43,6 +43,13 @@
 extern "C" {
 #endif
 
+/* Down-projection block format (gate and up are always Q4_0).  Q4_1 =
+ * 20-byte block {half d; half m; u8 qs[16]}, value q*d + m, as the
+ * checkpoint's layers 0-5 store ffn_down_exps (src/expert_main.cpp:83-84);
+ * its dot uses half-rounded d4*d8 and m4*s8 products (src/quant.cpp:95-100,
+ * src/cpu_expert.cpp:167-194). */
+enum { MOE_DOWN_Q4_0 = 0, MOE_DOWN_Q4_1 = 1 };
+
 typedef struct moe_ffn_config {
     int hidden;        /* H: multiple of 32, 32..16384 */
     int intermediate;  /* I: multiple of 32, 32..16384 */
@@ -50,13 +57,14 @@ typedef struct moe_ffn_config {
     int top_k;         /* routes per token, 1..32, <= experts */
     int has_shared;    /* 1: one shared expert, always routed (src/session.hip:1384-1410) */
     int max_tokens;    /* capacity of forward(), 1..65536 */
+    int down_type;     /* MOE_DOWN_Q4_0 (0) or MOE_DOWN_Q4_1; Q4_1 layers run streaming kernels only */
 } moe_ffn_config;
 
 typedef struct moe_ffn_layer moe_ffn_layer;
 
 /* Expert weight bank in the reference's canonical layout: for each expert,
- * gate [I rows][H/32 blocks], then up [I][H/32], then down [H][I/32], all
- * 18-byte Q4_0 blocks, rows contiguous (src/session.hip:700-716 expert slots,
+ * gate [I rows][H/32 blocks], then up [I][H/32], then down [H][I/32], 18-byte
+ * Q4_0 blocks (down: 20-byte Q4_1 blocks when down_type is Q4_1), rows contiguous (src/session.hip:700-716 expert slots,
  * src/model.hpp:109-111).  `shared_q4` has the same per-expert layout.
  *
  * moe_ffn_create: uploads from HOST memory, repacking on the device into the
@@ -73,7 +81,8 @@ int moe_ffn_create_from_device(const moe_ffn_config *config, const void *experts
 
 /* Same, from the routed-expert tensors as the reference holds them: three
  * host tensors gate_exps [E][I][H/32], up_exps [E][I][H/32], down_exps
- * [E][H][I/32] of 18-byte Q4_0 blocks (GGUF ffn_{gate,up,down}_exps, rank 3
+ * [E][H][I/32] of 18-byte Q4_0 blocks (down: Q4_1 20-byte blocks when
+ * down_type says so) (GGUF ffn_{gate,up,down}_exps, rank 3
  * [input, output, expert]; Experts::ram, src/session.hip:700-716,
  * src/model.hpp:109-111), plus the shared expert's three matrices (NULL when
  * the layer has none).  Lets Experts' loaded tensors be handed over as is. */
@@ -94,7 +103,7 @@ int moe_ffn_destroy(moe_ffn_layer *layer);
 int moe_ffn_memory_bytes(const moe_ffn_config *config, size_t *weight_bytes, size_t *workspace_bytes);
 
 /* Copy expert `expert` (0..E-1, or E for the shared expert) back to HOST in
- * the canonical 18-byte Q4_0 layout (synchronous; test/diagnostic use). */
+ * the canonical layout above (synchronous; test/diagnostic use). */
 int moe_ffn_export_expert(moe_ffn_layer *layer, int expert, void *host_q4);
 
 /* The routed expert FFN of one MoE layer (replaces src/session.hip:1446-1541

@@ -185,6 +185,15 @@ def matrix_gpu_order(w, K, M, xq, avx2=False):
     return out
 
 
+def matrix_gpu_order_q41(w, K, M, xq):
+    """Q4_1 matrix x Q8_1 columns in the reference cpu_expert order
+    (src/cpu_expert.cpp:167-194)."""
+    xq = as_q8(xq).reshape(-1, K // 32)
+    out = np.zeros((xq.shape[0], M), dtype=np.float32)
+    lib().mo_matrix_gpu_order_q41(_ptr(np.ascontiguousarray(w)), K, M, _ptr(xq), xq.shape[0], _ptr(out))
+    return out
+
+
 def expert_forward(gate, up, down, H, I, xq, avx2=False, down_q41=False):
     """cpu_expert whole stage (down Q4_0, or Q4_1 with down_q41).  Returns
     dict(y, gate, up, middle, middle_q8)."""

@@ -1,0 +1,228 @@
+"""GPU parity of layers whose down matrices are Q4_1 (20-byte blocks {half d,
+half m, 16 code bytes}; gate and up stay Q4_0), as GGUF files may store
+ffn_down_exps.  The reference's CPU expert sums a Q4_1 block per fragment as
+fma(float(I_f), half(d4 d8), half(m4 s8) / 2) (src/cpu_expert.cpp:167-194);
+the oracle restates that order and is pinned bit for bit against the compiled
+reference (tests/golden/cpu_expert_2560x640_q41.npz).
+
+Bars: per-block int32 dots and middle Q8 bytes bit-exact; outputs bit-exact
+where the kernel follows the reference order (H/32 blocks of I <= 512 per
+down row: k_down_lean and the decode down+fold), otherwise within the
+north_star's 1e-3 rms.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import moe_ffn
+import oracle as O
+import workloads as W
+from golden_inputs import expert_weights, q4_1_matrix
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+DEV = "cuda:0"
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+H, I = 2048, 512
+Q41 = moe_ffn.DOWN_Q4_1
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.square(np.asarray(a, np.float64)))))
+
+
+def assert_close(got, ref, tol, what):
+    err = float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))))
+    assert err <= tol * rms(ref), f"{what}: max abs err {err:.3e} > {tol} * rms {rms(ref):.3e}"
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def q8_bytes(q):
+    return np.ascontiguousarray(q).view(np.uint8).reshape(-1)
+
+
+def codes_as_q4_0(q41):
+    """Q4_1 blocks with m dropped: the same nibbles as Q4_0 blocks, so the
+    integer block dots (which use the codes only) come from O.block_dots."""
+    b = np.asarray(q41, np.uint8).reshape(-1, 20)
+    return np.ascontiguousarray(np.concatenate([b[:, :2], b[:, 4:]], axis=1)).reshape(-1)
+
+
+def split(bank, E):
+    """Canonical Q4_1-down bank -> per-expert (gate, up, down) views."""
+    gb = H // 32 * I * 18
+    per = np.asarray(bank).reshape(E, -1)
+    return [(per[e, :gb], per[e, gb:2 * gb], per[e, 2 * gb:]) for e in range(E)]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu_ready():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    yield
+    torch.cuda.synchronize()
+
+
+@pytest.fixture(scope="module")
+def q41_expert():
+    bank = W.q4_bank(1, seed=701, down_type=Q41)
+    g, u, d = split(bank, 1)[0]
+    layer = moe_ffn.MoeLayer(H, I, 1, 1, False, 16, experts_q4=bank, down_type=Q41)
+    yield dict(layer=layer, g=g, u=u, d=d)
+    layer.close()
+
+
+@pytest.mark.parametrize("columns", [1, 5, 16])
+def test_q41_expert_stages_bit_exact(q41_expert, columns):
+    """Single expert: gate/up middle Q8 equal to the oracle's; down per-block
+    dots bit-exact; the down projection (k_down_lean, reference order) bit-
+    identical to the oracle's Q4_1 cpu_expert order; the non-debug kernel
+    gives the same bits; the MFMA down path is refused for Q4_1."""
+    L, g, u, d = q41_expert["layer"], q41_expert["g"], q41_expert["u"], q41_expert["d"]
+    x = W.activations(columns, seed=710 + columns)
+    xq = O.quantize_q8(x)
+    ref = O.expert_forward(g, u, d, H, I, xq, down_q41=True)
+    r = L.expert_gate_up(0, dev(q8_bytes(xq).reshape(columns, -1)), columns, path=moe_ffn.PATH_STREAM)
+    assert np.array_equal(host(r["middle_q8"]).reshape(-1), q8_bytes(ref["middle_q8"]))
+    mq = ref["middle_q8"]
+    rd = L.expert_down(0, dev(q8_bytes(mq).reshape(columns, -1)), columns, path=moe_ffn.PATH_STREAM, dots=True)
+    assert np.array_equal(host(rd["down_dots"]), O.block_dots(codes_as_q4_0(d), I, H, mq))
+    y = host(rd["y"])
+    assert np.array_equal(y.view(np.uint32), O.matrix_gpu_order_q41(d, I, H, mq).view(np.uint32))
+    assert np.array_equal(y.view(np.uint32), ref["y"].view(np.uint32))
+    rd2 = L.expert_down(0, dev(q8_bytes(mq).reshape(columns, -1)), columns, path=moe_ffn.PATH_STREAM)
+    assert np.array_equal(host(rd2["y"]), y)
+    assert int(host(rd["error"])[0]) == 0
+    with pytest.raises(moe_ffn.MoeError):
+        L.expert_down(0, dev(q8_bytes(mq).reshape(columns, -1)), columns, path=moe_ffn.PATH_MFMA)
+
+
+def test_q41_reference_shape_expert_vs_golden():
+    """The compiled reference's Q4_1 cpu_expert at its 2560/640 shape, fed the
+    reference's own middle Q8: per-block dots bit-exact, the wide streaming
+    down (20 blocks per row, its own order across blocks) within 1e-3 rms of
+    the reference output and within 1e-5 rms of the oracle's order."""
+    f = np.load(os.path.join(GOLDEN, "cpu_expert_2560x640_q41.npz"), allow_pickle=False)
+    g, u, _ = expert_weights(2560, 640)
+    d = q4_1_matrix(404, 640, 2560)
+    layer = moe_ffn.MoeLayer(2560, 640, 1, 1, False, 3, experts_q4=np.concatenate([g, u, d]), down_type=Q41)
+    mq = f["middle_q8"].reshape(3, -1)
+    rd = layer.expert_down(0, dev(mq), 3, path=moe_ffn.PATH_STREAM, dots=True)
+    assert np.array_equal(host(rd["down_dots"]), O.block_dots(codes_as_q4_0(d), 640, 2560, mq))
+    y = host(rd["y"])
+    assert_close(y, f["y"], 1e-3, "Q4_1 expert vs reference cpu_expert")
+    assert_close(y, O.matrix_gpu_order_q41(d, 640, 2560, mq), 1e-5, "Q4_1 wide down vs oracle order")
+    layer.close()
+
+
+def _layer_env(env, *args, **kw):
+    """A layer created with the given MOE_FFN_* settings (read at creation)."""
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    try:
+        return moe_ffn.MoeLayer(*args, **kw)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+@pytest.fixture(scope="module")
+def q41_layer():
+    """64 experts + shared with Q4_1 downs: `layer` picks its path itself
+    (grouped here: tokens * k * 4 > E), `decode` is forced onto the ungrouped
+    decode kernels."""
+    E = 64
+    bank = W.q4_bank(E, seed=721, down_type=Q41)
+    shared = W.q4_bank(1, seed=722, down_type=Q41)
+    kw = dict(experts_q4=bank, shared_q4=shared, down_type=Q41)
+    layer = moe_ffn.MoeLayer(H, I, E, 10, True, 512, **kw)
+    decode = _layer_env({"MOE_FFN_DECODE": 1}, H, I, E, 10, True, 8, **kw)
+    yield dict(layer=layer, decode=decode, bank=bank, shared=shared, E=E)
+    layer.close()
+    decode.close()
+
+
+@pytest.mark.parametrize("gate", [False, True])
+def test_q41_decode_layer_bit_exact(q41_layer, gate):
+    """8-token decode batch (uniform top-10 of 64 + shared, optional shared
+    gate): every projection and the rank-order fold follow the reference's
+    fp32 order, so the layer output is bit-identical to the oracle's."""
+    L, E = q41_layer["decode"], q41_layer["E"]
+    x = W.activations(8, seed=731)
+    ids, w = W.routes_uniform(8, experts=E, seed=732)
+    sg = np.random.default_rng(733).standard_normal(8).astype(np.float32) if gate else None
+    y, err = L.forward(dev(x), dev(ids), dev(w), shared_gate=None if sg is None else dev(sg))
+    ref = O.moe_layer(x, H, I, E, q41_layer["bank"], ids, w, shared_q4=q41_layer["shared"], shared_gate=sg,
+                      down_q41=True)
+    assert np.array_equal(host(y).view(np.uint32), ref["y"].view(np.uint32))
+    assert int(host(err)[0]) == 0
+
+
+def test_q41_grouped_layer_bit_exact(q41_layer):
+    """300 Zipf(1.3) tokens on the grouped path (every group on the streaming
+    kernels, which Q4_1 layers use at every size): 32 sampled tokens bit-
+    identical to the oracle; a 5-token prefix batch gives the same bits."""
+    L, E = q41_layer["layer"], q41_layer["E"]
+    x = W.activations(300, seed=741)
+    ids, w = W.routes_zipf(300, 1.3, experts=E, seed=742)
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    yh = host(y)
+    assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
+    st = L.last_stats()
+    assert st["mfma_items"] == 0 and st["stream_items"] > 0
+    sample = np.random.default_rng(743).choice(300, 32, replace=False)
+    mask = np.zeros(300, np.uint8)
+    mask[sample] = 1
+    ref = O.moe_layer(x, H, I, E, q41_layer["bank"], ids, w, shared_q4=q41_layer["shared"], token_mask=mask,
+                      down_q41=True)
+    assert np.array_equal(yh[sample].view(np.uint32), ref["y"][sample].view(np.uint32))
+    y5, _ = L.forward(dev(x[:5].copy()), dev(ids[:5]), dev(w[:5]))
+    assert np.array_equal(host(y5), yh[:5])
+
+
+def test_q41_tensors_and_synthetic_banks():
+    """Q4_1 downs through the reference-tensor upload (three routed tensors,
+    down with 20-byte blocks) and the synthetic generator: exports give the
+    canonical bytes back, m planes are finite and centre the codes, and both
+    layers' forwards match the oracle on their exported banks bit for bit."""
+    E = 6
+    bank = W.q4_bank(E, seed=751, down_type=Q41)
+    shared = W.q4_bank(1, seed=752, down_type=Q41)
+    parts = split(bank, E)
+    ts = [np.concatenate([p[m] for p in parts]) for m in range(3)]
+    ss = list(split(shared, 1)[0])
+    L = moe_ffn.MoeLayer(H, I, E, 2, True, 8, tensors=ts, shared_tensors=ss, down_type=Q41)
+    eb = moe_ffn.expert_bytes(H, I, Q41)
+    assert eb * E == len(bank)
+    for e in range(E):
+        assert np.array_equal(L.export_expert(e), bank[e * eb:(e + 1) * eb]), e
+    assert np.array_equal(L.export_expert(E), shared)
+    S = moe_ffn.MoeLayer(H, I, E, 2, True, 8, synthetic_seed=753, down_type=Q41)
+    sbank = np.concatenate([S.export_expert(e) for e in range(E)])
+    sshared = S.export_expert(E)
+    dn = split(sbank, E)[0][2].reshape(-1, 20)
+    d = dn[:, :2].copy().view(np.float16).astype(np.float32).reshape(-1)
+    m = dn[:, 2:4].copy().view(np.float16).astype(np.float32).reshape(-1)
+    assert np.all(np.isfinite(m)) and np.all(m <= 0) and np.all(m >= -10.0 * d - 1e-3)
+    x = W.activations(8, seed=754)
+    ids = np.array([[(t + 1) % E, t % E] for t in range(8)], np.int32)
+    w = np.full((8, 2), 0.5, np.float32)
+    for layer, b, sh, what in ((L, bank, shared, "tensors"), (S, sbank, sshared, "synthetic")):
+        y, err = layer.forward(dev(x), dev(ids), dev(w))
+        ref = O.moe_layer(x, H, I, E, b, ids, w, shared_q4=sh, down_q41=True)
+        assert np.array_equal(host(y).view(np.uint32), ref["y"].view(np.uint32)), what
+        assert int(host(err)[0]) == 0, what
+    L.close()
+    S.close()
