@@ -142,6 +142,35 @@ def time_stack(layers, inputs, steps, warmup):
     return wall, e0.elapsed_time(e1) / 1e3 / steps
 
 
+def time_linear(K, M, N, iters=64, cold_bytes=320e6):
+    """Seconds per moe_linear_forward_q8 of a Q4_0 [M][K/32] matrix on N
+    columns, rotating enough resident copies (> the 256 MB Infinity Cache)
+    that every launch reads its weights from HBM.  Returns (seconds, bytes)."""
+    import torch
+    import moe_ffn
+    import workloads as W
+    rng = np.random.default_rng(K * 7 + M)
+    wts = W.q4_blocks(M * K // 32, rng).reshape(-1)
+    copies = int(min(128, max(2, -(-cold_bytes // wts.size))))
+    mats = [moe_ffn.MoeLinear(moe_ffn.TYPE_Q4_0, K, M, wts) for _ in range(copies)]
+    xq, _ = moe_ffn.quantize_q8_1(torch.from_numpy(W.activations(N, hidden=K, seed=N)).to("cuda:0"))
+    y = torch.empty((N, M), dtype=torch.float32, device="cuda:0")
+    for L in mats[:2]:
+        L.forward_q8(xq, N, y=y)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(iters):
+        mats[i % copies].forward_q8(xq, N, y=y)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    for L in mats:
+        L.close()
+    nbytes = wts.size + N * K // 32 * 36 + N * M * 4
+    return e0.elapsed_time(e1) / 1e3 / iters, nbytes
+
+
 def cpu_baseline(x, bank, shared, ids, w, target_seconds):
     import oracle as O
     cpus = O.physical_cpus()
@@ -165,6 +194,7 @@ def main():
     ap.add_argument("--no-16k", action="store_true", help="skip the 16K uniform prefill layer (configs[3])")
     ap.add_argument("--no-stack", action="store_true", help="skip the 48-layer stack (configs[4])")
     ap.add_argument("--stack-steps", type=int, default=5)
+    ap.add_argument("--no-linear", action="store_true", help="skip the quantized linear projections")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy x5 (FETCH_SIZE/WRITE_SIZE scale for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -290,6 +320,16 @@ def main():
         router[f"tokens_{NR}_us"] = e0.elapsed_time(e1) / 50 * 1e3
     result["router_us"] = router
     log(f"[bench] router (softmax + top-10 of 512): {router}")
+
+    # ---- non-expert Q4_0 projections (moe_linear_forward_q8), cold weights --
+    if not args.no_linear:
+        lin = {}
+        for K, M, N in ((2048, 2048, 1), (2048, 2048, 8), (2048, 2048, 128), (8192, 8192, 1), (8192, 8192, 8)):
+            sec, nbytes = time_linear(K, M, N)
+            lin[f"{K}x{M}_n{N}"] = {"us": sec * 1e6, "GB/s": nbytes / sec / 1e9,
+                                    "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
+            log(f"[bench] linear Q4_0 {K}->{M} N={N}: {sec*1e6:.2f} us, {nbytes/sec/1e9:.0f} GB/s")
+        result["linear_q4_0"] = lin
 
     # ---- 16K uniform prefill -----------------------------------
     if not args.no_prefill and not args.no_16k:

@@ -1,0 +1,319 @@
+// Quantized linear projections (Q4_0 / Q4_1 weights x Q8_1 activations) for
+// the non-expert matrices around the MoE FFN: the MI355X counterpart of the
+// reference's launch_quantized_linear{,_short,_tiled}
+// (src/hip/linear.hip:444-490, contract src/hip/linear.cuh:24-87) and of
+// Matrix::apply for its Q4 types (src/session.hip:559-591).
+//
+// fp32 order.  The reference's MMVQ kernel (src/hip/linear.hip:214-262) runs
+// 128 threads per row set: thread t takes fragment t % 2 of blocks
+// t / 2, t / 2 + 64, ... in ascending order, accumulating
+//   Q4_0: acc = fma(d4, fma(float(I_f), d8, -4 s8), acc)
+//   Q4_1: acc = acc + fma(float(I_f), half(d4 d8), half(m4 s8) / 2)
+// (accumulate32, src/hip/linear.hip:195-222); wave 1's accumulator is added
+// to wave 0's lane-wise and the 64 lanes are summed by an ascending XOR
+// butterfly.  This is the order src/cpu_expert.cpp:156-213 restates on the
+// CPU (lane 2 (k % 64) + f, fold lane i + 64, XOR 1..32).  Here one wave64
+// covers all 128 reference lanes: lane j holds both fragments of blocks
+// j, j + 64, ...; the fold is "lane j + lane j ^ 32 per fragment", then the
+// two fragments, then XOR 1..16 -- the same additions on the same values, so
+// every output is bit-identical to the reference's.
+//
+// Layout.  At creation the canonical [output][input/32] blocks are split into
+// a code plane [rows][blocks][16 B] and fp16 scale (and Q4_1 min) planes
+// [rows/8][blocks][8], rows padded to a multiple of 8 with zero blocks, so a
+// lane's 8 row codes are eight 16-byte loads and its 8 scales one more.
+//
+// Work: one wave per (8 rows, column tile).  The wave loads its 8 rows'
+// blocks once per 4 columns (2 when a row has more than 64 blocks) and keeps
+// them in registers while it reads the columns' Q8_1 blocks straight from the
+// caller's canonical 36-byte array.
+// Workgroup ids are XCD-aware (id % 8 = XCD): the column tiles of one row
+// slice run on one XCD, so that slice's rows are fetched from HBM once.
+#include "moe_device.hpp"
+#include "moe_ffn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <new>
+
+namespace moe {
+namespace {
+
+constexpr int kLinearCols = 4;          // column-tile granularity (a multiple of every G below)
+constexpr int kLinearWaveTarget = 2048; // waves a launch aims for (8 XCDs x 32 CUs x 8)
+
+struct LinearArgs {
+    const uint8_t *codes;    // [Mp][nb][16 B]
+    const uint16_t *scales;  // [Mp/8][nb][8]
+    const uint16_t *mins;    // Q4_1: same order as scales; Q4_0: nullptr
+    const uint8_t *x;        // canonical Q8_1 [N][nb][36 B]
+    float *y;                // [N][M]
+    int nb, M, N;
+    int slices;              // Mp / 8
+    int tiles, tile_cols;    // column tiles per slice; columns per tile (multiple of kLinearCols)
+};
+
+// Reduce 8 rows' per-fragment lane partials z[row][f] in the reference's
+// order: lane j + lane j ^ 32 per fragment, then the two fragments, then
+// XOR 1, 2, 4, 8, 16.  Rows are traded between lanes during the first three
+// stages so each lane ends with one row: lane l holds row
+// 4 * (l >> 5 & 1) + 2 * (l & 1) + (l >> 1 & 1).
+__device__ __forceinline__ float fold_rows8(const float (&z)[8][2], int lane) {
+    const bool b5 = lane & 32, b0 = lane & 1, b1 = lane & 2;
+    float v4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float u[2];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const float send = b5 ? z[i][f] : z[i + 4][f];
+            const float keep = b5 ? z[i + 4][f] : z[i][f];
+            u[f] = keep + __shfl_xor(send, 32, 64);
+        }
+        v4[i] = u[0] + u[1];
+    }
+    float v2[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float send = b0 ? v4[i] : v4[i + 2];
+        const float keep = b0 ? v4[i + 2] : v4[i];
+        v2[i] = keep + __shfl_xor(send, 1, 64);
+    }
+    float v = (b1 ? v2[1] : v2[0]) + __shfl_xor(b1 ? v2[0] : v2[1], 2, 64);
+    v = xor_sum(v, 4);
+    v = xor_sum(v, 8);
+    return xor_sum(v, 16);
+}
+
+// HOLD = block slots (64 blocks each) whose weights are loaded together;
+// G = columns accumulated per pass over the weights.
+template<bool Q41, int HOLD, int G>
+__global__ __launch_bounds__(64, 2) void k_linear(LinearArgs a) {
+    const int lane = threadIdx.x;
+    const int id = static_cast<int>(blockIdx.x), local = id >> 3;
+    const int slice = (id & 7) + 8 * (local / a.tiles), tile = local % a.tiles;
+    if (slice >= a.slices) return;   // uniform per workgroup (grid padded to 8 slices)
+    const int c0 = tile * a.tile_cols, c1 = min(c0 + a.tile_cols, a.N);
+    if (c0 >= c1) return;
+    const int nb = a.nb, row0 = slice * 8, slots = (nb + 63) / 64;
+    const uint32_t row_bytes = static_cast<uint32_t>(nb) * 16u;
+    const auto wr = buffer_rsrc(a.codes + static_cast<size_t>(row0) * row_bytes, 8 * row_bytes);
+    const auto sr = buffer_rsrc(a.scales + static_cast<size_t>(row0) * nb, row_bytes);
+    const auto mr = buffer_rsrc(Q41 ? a.mins + static_cast<size_t>(row0) * nb : a.scales, row_bytes);
+    const auto xr = buffer_rsrc(a.x, static_cast<uint32_t>(static_cast<size_t>(a.N) * nb * 36));
+    const int rho = 4 * ((lane >> 5) & 1) + 2 * (lane & 1) + ((lane >> 1) & 1);
+    for (int c = c0; c < c1; c += G) {   // uniform
+        float acc[G][8][2];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int r = 0; r < 8; ++r) acc[g][r][0] = acc[g][r][1] = 0.0f;
+        for (int i0 = 0; i0 < slots; i0 += HOLD) {   // uniform
+            uint4 w[HOLD][8];
+            float d4[HOLD][8], m4[HOLD][8];
+            bool has[HOLD];
+            uint32_t kk[HOLD];
+#pragma unroll
+            for (int h = 0; h < HOLD; ++h) {
+                const int k = lane + 64 * (i0 + h);
+                // Lanes past the row end (or past the last slot) load block 0
+                // and keep their accumulators: every load is unconditional.
+                has[h] = i0 + h < slots && k < nb;
+                kk[h] = has[h] ? static_cast<uint32_t>(k) : 0u;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) w[h][r] = buffer_load16(wr, kk[h] * 16u, r * row_bytes);
+                const uint4 dp = buffer_load16(sr, kk[h] * 16u, 0);
+#pragma unroll
+                for (int r = 0; r < 8; ++r) d4[h][r] = h2f((&dp.x)[r >> 1] >> (16 * (r & 1)));
+                if constexpr (Q41) {
+                    const uint4 mp = buffer_load16(mr, kk[h] * 16u, 0);
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) m4[h][r] = h2f((&mp.x)[r >> 1] >> (16 * (r & 1)));
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                if (c + g >= c1) break;   // uniform
+                const uint32_t xs = static_cast<uint32_t>(static_cast<size_t>(c + g) * nb * 36);
+#pragma unroll
+                for (int h = 0; h < HOLD; ++h) {
+                    const uint32_t xo = kk[h] * 36u;
+                    const uint32_t head = buffer_load4(xr, xo, xs);
+                    const uint4 x0 = buffer_load16(xr, xo + 4u, xs);
+                    const uint4 x1 = buffer_load16(xr, xo + 20u, xs);
+                    const float d8 = h2f(head), s8 = h2f(head >> 16), c4 = -4.0f * s8;
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) {
+                        int f[2];
+                        fragment_dots(w[h][r], x0, x1, f[0], f[1]);
+#pragma unroll
+                        for (int q = 0; q < 2; ++q) {
+                            float v;
+                            if constexpr (Q41) {
+                                const float dd = h2f(f2h(d4[h][r] * d8)), hm = h2f(f2h(m4[h][r] * s8)) * 0.5f;
+                                v = acc[g][r][q] + fmaf(static_cast<float>(f[q]), dd, hm);
+                            } else {
+                                v = fmaf(d4[h][r], fmaf(static_cast<float>(f[q]), d8, c4), acc[g][r][q]);
+                            }
+                            acc[g][r][q] = has[h] ? v : acc[g][r][q];
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if (c + g >= c1) break;   // uniform
+            const float v = fold_rows8(acc[g], lane);
+            const int row = row0 + rho;
+            if ((lane & 28) == 0 && row < a.M) a.y[static_cast<size_t>(c + g) * a.M + row] = v;
+        }
+    }
+}
+
+}  // namespace
+}  // namespace moe
+
+// ------------------------------------------------------------------ C ABI ---
+struct moe_linear {
+    int type = 0, input = 0, output = 0, max_columns = 0, device = 0;
+    int nb = 0, Mp = 0;
+    uint8_t *planes = nullptr;   // codes | scales | mins (one allocation)
+    uint8_t *codes = nullptr;
+    uint16_t *scales = nullptr, *mins = nullptr;
+    void *q8 = nullptr;          // moe_linear_apply workspace [max_columns][nb][36 B]
+};
+
+namespace {
+
+constexpr int kInvalid = hipErrorInvalidValue;
+
+bool aligned(const void *p, size_t a) { return p && reinterpret_cast<uintptr_t>(p) % a == 0; }
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+void release(moe_linear *L) {
+    if (!L) return;
+    if (L->planes) (void)hipFree(L->planes);
+    if (L->q8) (void)hipFree(L->q8);
+    delete L;
+}
+
+int block_bytes(int type) { return type == MOE_TYPE_Q4_1 ? 20 : 18; }
+
+}  // namespace
+
+extern "C" {
+
+int moe_linear_create(int type, int input, int output, int max_columns, const void *weights, int weights_on_device,
+                      int device, moe_linear **out) {
+    if (!out) return kInvalid;
+    *out = nullptr;
+    if ((type != MOE_TYPE_Q4_0 && type != MOE_TYPE_Q4_1) || input < 32 || input > 16384 || input % 32 ||
+        output < 1 || output > 16384 || max_columns < 0 || max_columns > 65536 || !aligned(weights, 2))
+        return kInvalid;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return kInvalid;
+    if (hipSetDevice(device) != hipSuccess) return kInvalid;
+    auto *L = new (std::nothrow) moe_linear;
+    if (!L) return hipErrorOutOfMemory;
+    L->type = type;
+    L->input = input;
+    L->output = output;
+    L->max_columns = max_columns;
+    L->device = device;
+    L->nb = input / 32;
+    L->Mp = static_cast<int>(round_up(static_cast<size_t>(output), 8));
+    const size_t pblocks = static_cast<size_t>(L->Mp) * L->nb;
+    const size_t code_bytes = round_up(pblocks * 16, 256), scale_bytes = round_up(pblocks * 2, 256);
+    const size_t total = code_bytes + scale_bytes * (type == MOE_TYPE_Q4_1 ? 2 : 1);
+    hipError_t r = hipMalloc(&L->planes, total);
+    if (r != hipSuccess) { release(L); return r; }
+    L->codes = L->planes;
+    L->scales = reinterpret_cast<uint16_t *>(L->planes + code_bytes);
+    L->mins = type == MOE_TYPE_Q4_1 ? reinterpret_cast<uint16_t *>(L->planes + code_bytes + scale_bytes) : nullptr;
+    if (max_columns > 0 && (r = hipMalloc(&L->q8, static_cast<size_t>(max_columns) * L->nb * 36)) != hipSuccess) {
+        release(L);
+        return r;
+    }
+    // Padding rows stay zero blocks (d = 0): their sums are computed and dropped.
+    if ((r = hipMemset(L->planes, 0, total)) != hipSuccess) { release(L); return r; }
+    const size_t blocks = static_cast<size_t>(output) * L->nb, bytes = blocks * block_bytes(type);
+    const uint8_t *canonical = static_cast<const uint8_t *>(weights);
+    void *staging = nullptr;
+    if (!weights_on_device) {
+        if ((r = hipMalloc(&staging, bytes)) != hipSuccess) { release(L); return r; }
+        if ((r = hipMemcpy(staging, weights, bytes, hipMemcpyHostToDevice)) != hipSuccess) {
+            (void)hipFree(staging);
+            release(L);
+            return r;
+        }
+        canonical = static_cast<const uint8_t *>(staging);
+    }
+    r = moe::launch_repack_weights(canonical, L->codes, L->scales, L->mins, blocks, 0, L->nb, moe::kScaleGroupGateUp,
+                                   nullptr);
+    if (r == hipSuccess) r = hipDeviceSynchronize();
+    if (staging) (void)hipFree(staging);
+    if (r != hipSuccess) { release(L); return r; }
+    *out = L;
+    return 0;
+}
+
+int moe_linear_destroy(moe_linear *L) {
+    if (!L) return kInvalid;
+    (void)hipSetDevice(L->device);
+    release(L);
+    return 0;
+}
+
+int moe_linear_bytes(const moe_linear *L, size_t *weight_bytes) {
+    if (!L || !weight_bytes) return kInvalid;
+    *weight_bytes = static_cast<size_t>(L->output) * L->nb * block_bytes(L->type);
+    return 0;
+}
+
+int moe_linear_forward_q8(moe_linear *L, const void *x_q8, int columns, float *y, void *stream) {
+    if (!L || !aligned(x_q8, 4) || !aligned(y, 4) || columns < 1 || columns > 65536) return kInvalid;
+    moe::LinearArgs a{};
+    a.codes = L->codes;
+    a.scales = L->scales;
+    a.mins = L->mins;
+    a.x = static_cast<const uint8_t *>(x_q8);
+    a.y = y;
+    a.nb = L->nb;
+    a.M = L->output;
+    a.N = columns;
+    a.slices = L->Mp / 8;
+    // Column tiles: enough waves to cover the chip (kLinearWaveTarget), each
+    // tile a whole number of accumulation groups.
+    const int groups = (columns + moe::kLinearCols - 1) / moe::kLinearCols;
+    int tiles = std::max(1, std::min(groups, (moe::kLinearWaveTarget + a.slices - 1) / a.slices));
+    const int per = (groups + tiles - 1) / tiles;
+    a.tile_cols = per * moe::kLinearCols;
+    a.tiles = (columns + a.tile_cols - 1) / a.tile_cols;
+    const size_t grid = round_up(static_cast<size_t>(a.slices), 8) * a.tiles;
+    if (grid > 0x7fffffffu) return kInvalid;
+    const auto s = static_cast<hipStream_t>(stream);
+    const bool q41 = L->type == MOE_TYPE_Q4_1, hold2 = L->nb > 64;
+    const dim3 g(static_cast<unsigned>(grid)), b(64);
+    if (q41) {
+        if (hold2) moe::k_linear<true, 2, 2><<<g, b, 0, s>>>(a);
+        else moe::k_linear<true, 1, 4><<<g, b, 0, s>>>(a);
+    } else {
+        if (hold2) moe::k_linear<false, 2, 2><<<g, b, 0, s>>>(a);
+        else moe::k_linear<false, 1, 4><<<g, b, 0, s>>>(a);
+    }
+    return hipGetLastError();
+}
+
+int moe_linear_apply(moe_linear *L, const float *x, int columns, float *y, int *error, void *stream) {
+    if (!L || !aligned(x, 4) || !aligned(y, 4) || !aligned(error, 4) || columns < 1 || columns > L->max_columns)
+        return kInvalid;
+    const hipError_t r = moe::launch_quantize_canonical(x, L->q8, L->input, columns, error,
+                                                        static_cast<hipStream_t>(stream));
+    if (r != hipSuccess) return r;
+    return moe_linear_forward_q8(L, L->q8, columns, y, stream);
+}
+
+}  // extern "C"

@@ -26,6 +26,7 @@ Q4_BLOCK = 18
 Q4_1_BLOCK = 20
 DOWN_Q4_0, DOWN_Q4_1 = 0, 1     # MOE_DOWN_Q4_0 / MOE_DOWN_Q4_1
 PATH_AUTO, PATH_STREAM, PATH_MFMA = 0, 1, 2
+TYPE_Q4_0, TYPE_Q4_1 = 2, 3     # MOE_TYPE_Q4_0 / MOE_TYPE_Q4_1 (the reference's TensorType ids)
 STAGE_PREPARE, STAGE_GATE_UP, STAGE_DOWN, STAGE_FOLD = 0, 1, 2, 3
 
 
@@ -78,6 +79,11 @@ def library():
         lib.moe_router_select.argtypes = [_P, _I, _I, _I, _P, _P, _P, _P, _P]
         lib.moe_ffn_last_stats.argtypes = [_P, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
                                            ctypes.POINTER(ctypes.c_int32)]
+        lib.moe_linear_create.argtypes = [_I, _I, _I, _I, _P, _I, _I, ctypes.POINTER(_P)]
+        lib.moe_linear_destroy.argtypes = [_P]
+        lib.moe_linear_bytes.argtypes = [_P, ctypes.POINTER(ctypes.c_size_t)]
+        lib.moe_linear_forward_q8.argtypes = [_P, _P, _I, _P, _P]
+        lib.moe_linear_apply.argtypes = [_P, _P, _I, _P, _P, _P]
         _lib = lib
     return _lib
 
@@ -324,3 +330,58 @@ def memory_bytes(hidden, intermediate, experts, top_k, has_shared, max_tokens):
     w, s = ctypes.c_size_t(), ctypes.c_size_t()
     _check(library().moe_ffn_memory_bytes(ctypes.byref(cfg), ctypes.byref(w), ctypes.byref(s)), "memory_bytes")
     return w.value, s.value
+
+
+class MoeLinear:
+    """One resident Q4_0 / Q4_1 matrix [output][input/32] (moe_linear_create):
+    forward_q8 takes canonical Q8_1 columns, apply takes fp32 columns."""
+
+    def __init__(self, type_, input, output, weights, max_columns=0, device=0):
+        import torch
+        self.type, self.K, self.M, self.max_columns = type_, input, output, max_columns
+        handle = ctypes.c_void_p()
+        if isinstance(weights, np.ndarray):
+            w = np.ascontiguousarray(weights, dtype=np.uint8)
+            st = library().moe_linear_create(type_, input, output, max_columns, ctypes.c_void_p(w.ctypes.data), 0,
+                                             device, ctypes.byref(handle))
+        else:
+            assert isinstance(weights, torch.Tensor) and weights.is_cuda
+            st = library().moe_linear_create(type_, input, output, max_columns, _ptr(weights), 1, device,
+                                             ctypes.byref(handle))
+        _check(st, "moe_linear_create")
+        self.handle = handle
+
+    def close(self):
+        if getattr(self, "handle", None):
+            library().moe_linear_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def weight_bytes(self):
+        n = ctypes.c_size_t()
+        _check(library().moe_linear_bytes(self.handle, ctypes.byref(n)), "moe_linear_bytes")
+        return n.value
+
+    def forward_q8(self, x_q8, columns, y=None, stream=None):
+        import torch
+        if y is None:
+            y = torch.empty((columns, self.M), dtype=torch.float32, device=x_q8.device)
+        _check(library().moe_linear_forward_q8(self.handle, _ptr(x_q8), columns, _ptr(y), _stream(stream)),
+               "moe_linear_forward_q8")
+        return y
+
+    def apply(self, x, y=None, error=None, stream=None):
+        import torch
+        n = x.shape[0]
+        if y is None:
+            y = torch.empty((n, self.M), dtype=torch.float32, device=x.device)
+        if error is None:
+            error = torch.zeros(1, dtype=torch.int32, device=x.device)
+        _check(library().moe_linear_apply(self.handle, _ptr(x), n, _ptr(y), _ptr(error), _stream(stream)),
+               "moe_linear_apply")
+        return y, error

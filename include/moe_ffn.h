@@ -231,6 +231,45 @@ int moe_router_select(const float *logits, int tokens, int experts, int top_k, f
  * in the reference. */
 int moe_read_probe(const void *buffer, size_t bytes, void *sink, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Quantized linear projections (the non-expert Q4 matrices around the FFN).
+ * ---------------------------------------------------------------------- */
+
+/* Weight types, numbered as the reference's TensorType (src/model.hpp:17-20). */
+enum { MOE_TYPE_Q4_0 = 2, MOE_TYPE_Q4_1 = 3 };
+
+typedef struct moe_linear moe_linear;
+
+/* One resident matrix, the counterpart of the reference's Matrix
+ * (src/session.hip:559-591) for its Q4_0 / Q4_1 tensors and of the
+ * QuantizedDeviceMatrix it hands to launch_quantized_linear*
+ * (src/hip/linear.cuh:27-32).  `weights` = canonical GGUF blocks
+ * [output][input/32] (18-byte Q4_0 or 20-byte Q4_1, 2-byte aligned), on the
+ * host or (weights_on_device = 1) on `device`; they are copied into the
+ * handle's own planes, so the caller may free them afterwards.  input:
+ * multiple of 32, 32..16384; output 1..16384.  max_columns (0..65536) sizes
+ * the Q8_1 workspace of moe_linear_apply.  Allocates; synchronises the
+ * device once. */
+int moe_linear_create(int type, int input, int output, int max_columns, const void *weights, int weights_on_device,
+                      int device, moe_linear **out);
+int moe_linear_destroy(moe_linear *linear);
+/* Canonical weight bytes the handle was created from. */
+int moe_linear_bytes(const moe_linear *linear, size_t *weight_bytes);
+
+/* y [columns][output] fp32 = W x for canonical Q8_1 columns x_q8
+ * [columns][input/32] (36-byte blocks, 4-byte aligned).  Replaces
+ * launch_quantized_linear / _short / _tiled (src/hip/linear.cuh:70-87,
+ * src/hip/linear.hip:444-490) for Q4_0 / Q4_1, with the same fp32 order
+ * (bit-identical outputs), columns 1..65536 in one launch.  Enqueue only. */
+int moe_linear_forward_q8(moe_linear *linear, const void *x_q8, int columns, float *y, void *stream);
+
+/* Matrix::apply for Q4 types (src/session.hip:561-591): fp32 x
+ * [columns][input] is quantized to Q8_1 into the handle's workspace
+ * (launch_quantize_q8_1 semantics; flags OR-ed into `error`), then
+ * forward_q8.  columns 1..max_columns.  Calls on one handle must not
+ * overlap (they share the workspace). */
+int moe_linear_apply(moe_linear *linear, const float *x, int columns, float *y, int *error, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
