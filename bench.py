@@ -113,6 +113,27 @@ def read_ceiling(nbytes, buffers=12, iters=48):
     return e0.elapsed_time(e1) / 1e3 / iters
 
 
+def time_graph(stack, steps):
+    """Seconds per replay of the stack's captured graph (one pass)."""
+    import torch
+    stack.capture()
+    stack.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        stack.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    if int(stack.error.cpu()[0]) != 0:
+        raise RuntimeError(f"error flags {int(stack.error.cpu()[0])}")
+    stack.graph = None
+    return wall, e0.elapsed_time(e1) / 1e3 / steps
+
+
 def time_stack(layers, inputs, steps, warmup):
     """Seconds per pass of the whole stack: layer l runs on its own resident
     batch inputs[l] = (x, ids, weights), back to back on one stream."""
@@ -152,19 +173,27 @@ def time_linear(K, M, N, iters=64, cold_bytes=320e6):
     rng = np.random.default_rng(K * 7 + M)
     wts = W.q4_blocks(M * K // 32, rng).reshape(-1)
     copies = int(min(128, max(2, -(-cold_bytes // wts.size))))
-    mats = [moe_ffn.MoeLinear(moe_ffn.TYPE_Q4_0, K, M, wts) for _ in range(copies)]
+    mats = [moe_ffn.MoeLinear(moe_ffn.TYPE_Q4_0, K, M, wts, max_columns=N) for _ in range(copies)]
     xq, _ = moe_ffn.quantize_q8_1(torch.from_numpy(W.activations(N, hidden=K, seed=N)).to("cuda:0"))
     y = torch.empty((N, M), dtype=torch.float32, device="cuda:0")
     for L in mats[:2]:
         L.forward_q8(xq, N, y=y)
     torch.cuda.synchronize()
+    # The launches are replayed from a captured graph: a few-microsecond
+    # kernel launched from Python one call at a time would time the host.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(iters):
+            mats[i % copies].forward_q8(xq, N, y=y)
+    graph.replay()
+    torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for i in range(iters):
-        mats[i % copies].forward_q8(xq, N, y=y)
+    graph.replay()
     e1.record(stream)
     torch.cuda.synchronize()
+    del graph
     for L in mats:
         L.close()
     nbytes = wts.size + N * K // 32 * 36 + N * M * 4
@@ -324,7 +353,8 @@ def main():
     # ---- non-expert Q4_0 projections (moe_linear_forward_q8), cold weights --
     if not args.no_linear:
         lin = {}
-        for K, M, N in ((2048, 2048, 1), (2048, 2048, 8), (2048, 2048, 128), (8192, 8192, 1), (8192, 8192, 8)):
+        for K, M, N in ((2048, 2048, 1), (2048, 2048, 8), (2048, 2048, 128), (2048, 2048, 1032), (8192, 8192, 1),
+                        (8192, 8192, 8), (8192, 8192, 128)):
             sec, nbytes = time_linear(K, M, N)
             lin[f"{K}x{M}_n{N}"] = {"us": sec * 1e6, "GB/s": nbytes / sec / 1e9,
                                     "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
@@ -371,6 +401,34 @@ def main():
         }
         log(f"[bench] stack of {NL}: {wall_s*1e3:.2f} ms/pass, {wall_s/NL*1e6:.1f} us/layer, "
             f"touched {np.mean(touched_s):.1f}, resident {resident/1e9:.2f} GB")
+        # The same pass replayed from one captured HIP graph, then the full
+        # per-layer pipeline in a graph: Q4_0 H -> H projection, Q4_0 router
+        # H -> E, device top-10, MoE layer (routes chosen on the device).
+        S = moe_ffn.MoeStack(layers)
+        S.bind([x for x, _, _ in inputs], [i for _, i, _ in inputs], [w for _, _, w in inputs])
+        wall_g, gpu_g = time_graph(S, args.stack_steps)
+        result["stack_48"]["graph_ms_per_stack"] = wall_g * 1e3
+        log(f"[bench] stack of {NL}, one HIP graph: {wall_g*1e3:.2f} ms/pass, {wall_g/NL*1e6:.1f} us/layer")
+        rng = np.random.default_rng(8000)
+        projections = [moe_ffn.MoeLinear(moe_ffn.TYPE_Q4_0, 2048, 2048, W.q4_blocks(2048 * 64, rng).reshape(-1),
+                                         max_columns=NS) for _ in range(NL)]
+        routers = [moe_ffn.MoeLinear(moe_ffn.TYPE_Q4_0, 2048, 512, W.q4_blocks(512 * 64, rng).reshape(-1),
+                                     max_columns=NS) for _ in range(NL)]
+        P = moe_ffn.MoeStack(layers, projections=projections, routers=routers)
+        P.bind([x for x, _, _ in inputs])
+        wall_p, gpu_p = time_graph(P, args.stack_steps)
+        # The MoE layers alone on the routes the device router chose (they
+        # differ from the Zipf routes above), to split the pipeline's time.
+        M = moe_ffn.MoeStack(layers)
+        M.bind([st["h"] for st in P.steps], [st["ids"] for st in P.steps], [st["w"] for st in P.steps])
+        wall_m, _ = time_graph(M, args.stack_steps)
+        result["stack_48"]["pipeline_graph_ms_per_stack"] = wall_p * 1e3
+        result["stack_48"]["pipeline_moe_only_graph_ms_per_stack"] = wall_m * 1e3
+        log(f"[bench] stack of {NL} with projection + router + top-10 per layer, one HIP graph: "
+            f"{wall_p*1e3:.2f} ms/pass, {wall_p/NL*1e6:.1f} us/layer; its MoE layers alone "
+            f"{wall_m/NL*1e6:.1f} us/layer")
+        for m in projections + routers:
+            m.close()
         for L in layers:
             L.close()
 

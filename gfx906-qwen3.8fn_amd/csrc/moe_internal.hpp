@@ -157,6 +157,20 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s);
 hipError_t launch_gate_up_mfma(const FfnArgs &a, hipStream_t s);
 hipError_t launch_down_mfma(const FfnArgs &a, hipStream_t s);
 
+// One Q4_0 matrix (planes, rows padded to a multiple of 32) against N
+// columns in split Q8 planes, in the reference MMVQ fp32 order, on int8 MFMA
+// (moe_mfma.hip); used by moe_linear for wide column counts.
+struct LinearMfmaArgs {
+    const uint8_t *codes;     // [Mp][nb][16 B]
+    const uint16_t *scales;   // [Mp/8][nb][8]
+    Act xq;                   // [N][nb]
+    float *y;                 // [N][M]
+    int nb, M, N;
+    int row_tiles;            // Mp / 32
+    int col_tiles;            // ceil(N / 32)
+};
+hipError_t launch_linear_mfma(const LinearMfmaArgs &a, hipStream_t s);
+
 hipError_t launch_fold(const float *contributions, size_t token_stride, const float *weights, int k,
                        const int32_t *pos_of, const float *shared, size_t shared_stride,
                        const float *shared_gate, int tokens, int H, float *y, int *error,

@@ -20,8 +20,13 @@
 //
 // Layout.  At creation the canonical [output][input/32] blocks are split into
 // a code plane [rows][blocks][16 B] and fp16 scale (and Q4_1 min) planes
-// [rows/8][blocks][8], rows padded to a multiple of 8 with zero blocks, so a
+// [rows/8][blocks][8], rows padded to a multiple of 32 with zero blocks, so a
 // lane's 8 row codes are eight 16-byte loads and its 8 scales one more.
+//
+// Wide batches (Q4_0, within the handle's workspace, at least 32 columns and
+// kMfmaMinOutputs outputs) go to int8 MFMA instead (k_linear_mfma in
+// moe_mfma.hip): the same fp32 order, with the per-fragment integer dots from
+// v_mfma_i32_32x32x16_i8.
 //
 // Work: one wave per (8 rows, column tile).  The wave loads its 8 rows'
 // blocks once per 4 columns (2 when a row has more than 64 blocks) and keeps
@@ -36,6 +41,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <new>
 
 namespace moe {
@@ -179,16 +185,25 @@ __global__ __launch_bounds__(64, 2) void k_linear(LinearArgs a) {
 // ------------------------------------------------------------------ C ABI ---
 struct moe_linear {
     int type = 0, input = 0, output = 0, max_columns = 0, device = 0;
+    int mfma_mode = -1;          // MOE_LINEAR_MFMA at creation: 0 never, 1 whenever eligible, -1 by size
     int nb = 0, Mp = 0;
     uint8_t *planes = nullptr;   // codes | scales | mins (one allocation)
     uint8_t *codes = nullptr;
     uint16_t *scales = nullptr, *mins = nullptr;
-    void *q8 = nullptr;          // moe_linear_apply workspace [max_columns][nb][36 B]
+    // Activation workspace, max_columns x nb x 36 B: canonical Q8_1 blocks
+    // (apply, narrow batches) or split planes (wide batches on MFMA).
+    void *q8 = nullptr;
 };
 
 namespace {
 
 constexpr int kInvalid = hipErrorInvalidValue;
+constexpr int kMfmaMinColumns = 32;        // one MFMA column tile
+// Outputs (rows x columns) from which the MFMA kernel beats the vector one
+// (measured on MI355X: 2048 x 2048 at 64 columns 12.4 vs 12.6 us, at 128
+// columns 22.6 vs 13.5 us; 512 rows at 256 columns 12.2 vs 12.9 us, at 384
+// columns 17.2 vs 13.3 us; 8192 rows at 32 columns 78 vs 56 us).
+constexpr long kMfmaMinOutputs = 160 * 1024;
 
 bool aligned(const void *p, size_t a) { return p && reinterpret_cast<uintptr_t>(p) % a == 0; }
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -224,7 +239,8 @@ int moe_linear_create(int type, int input, int output, int max_columns, const vo
     L->max_columns = max_columns;
     L->device = device;
     L->nb = input / 32;
-    L->Mp = static_cast<int>(round_up(static_cast<size_t>(output), 8));
+    if (const char *env = std::getenv("MOE_LINEAR_MFMA")) L->mfma_mode = std::atoi(env) ? 1 : 0;
+    L->Mp = static_cast<int>(round_up(static_cast<size_t>(output), 32));
     const size_t pblocks = static_cast<size_t>(L->Mp) * L->nb;
     const size_t code_bytes = round_up(pblocks * 16, 256), scale_bytes = round_up(pblocks * 2, 256);
     const size_t total = code_bytes + scale_bytes * (type == MOE_TYPE_Q4_1 ? 2 : 1);
@@ -273,8 +289,44 @@ int moe_linear_bytes(const moe_linear *L, size_t *weight_bytes) {
     return 0;
 }
 
+namespace {
+
+bool use_mfma(const moe_linear *L, int columns) {
+    if (L->type != MOE_TYPE_Q4_0 || columns < kMfmaMinColumns || columns > L->max_columns || L->mfma_mode == 0)
+        return false;
+    return L->mfma_mode == 1 || static_cast<long>(L->output) * columns >= kMfmaMinOutputs;
+}
+
+moe::Act workspace_planes(const moe_linear *L, int columns) {
+    auto *base = static_cast<uint8_t *>(L->q8);
+    return moe::Act{base, reinterpret_cast<uint32_t *>(base + static_cast<size_t>(columns) * L->nb * 32)};
+}
+
+int launch_mfma(const moe_linear *L, moe::Act xq, int columns, float *y, hipStream_t s) {
+    moe::LinearMfmaArgs a{};
+    a.codes = L->codes;
+    a.scales = L->scales;
+    a.xq = xq;
+    a.y = y;
+    a.nb = L->nb;
+    a.M = L->output;
+    a.N = columns;
+    a.row_tiles = L->Mp / 32;
+    a.col_tiles = (columns + 31) / 32;
+    return moe::launch_linear_mfma(a, s);
+}
+
+}  // namespace
+
 int moe_linear_forward_q8(moe_linear *L, const void *x_q8, int columns, float *y, void *stream) {
     if (!L || !aligned(x_q8, 4) || !aligned(y, 4) || columns < 1 || columns > 65536) return kInvalid;
+    if (use_mfma(L, columns)) {
+        const auto s = static_cast<hipStream_t>(stream);
+        const moe::Act xq = workspace_planes(L, columns);
+        const hipError_t r = moe::launch_canonical_to_planes(x_q8, xq, columns * L->nb, s);
+        if (r != hipSuccess) return r;
+        return launch_mfma(L, xq, columns, y, s);
+    }
     moe::LinearArgs a{};
     a.codes = L->codes;
     a.scales = L->scales;
@@ -284,7 +336,7 @@ int moe_linear_forward_q8(moe_linear *L, const void *x_q8, int columns, float *y
     a.nb = L->nb;
     a.M = L->output;
     a.N = columns;
-    a.slices = L->Mp / 8;
+    a.slices = (L->output + 7) / 8;
     // Column tiles: enough waves to cover the chip (kLinearWaveTarget), each
     // tile a whole number of accumulation groups.
     const int groups = (columns + moe::kLinearCols - 1) / moe::kLinearCols;
@@ -310,8 +362,14 @@ int moe_linear_forward_q8(moe_linear *L, const void *x_q8, int columns, float *y
 int moe_linear_apply(moe_linear *L, const float *x, int columns, float *y, int *error, void *stream) {
     if (!L || !aligned(x, 4) || !aligned(y, 4) || !aligned(error, 4) || columns < 1 || columns > L->max_columns)
         return kInvalid;
-    const hipError_t r = moe::launch_quantize_canonical(x, L->q8, L->input, columns, error,
-                                                        static_cast<hipStream_t>(stream));
+    const auto s = static_cast<hipStream_t>(stream);
+    if (use_mfma(L, columns)) {
+        const moe::Act xq = workspace_planes(L, columns);
+        const hipError_t r = moe::launch_quantize_planes(x, xq, L->input, columns, error, s);
+        if (r != hipSuccess) return r;
+        return launch_mfma(L, xq, columns, y, s);
+    }
+    const hipError_t r = moe::launch_quantize_canonical(x, L->q8, L->input, columns, error, s);
     if (r != hipSuccess) return r;
     return moe_linear_forward_q8(L, L->q8, columns, y, stream);
 }

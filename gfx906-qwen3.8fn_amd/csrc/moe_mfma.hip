@@ -939,7 +939,145 @@ unsigned mfma_grid(const FfnArgs &a, int slices) {
     return static_cast<unsigned>((units + round - 1) / round * round);
 }
 
+// ---------------------------------------------------------------- linear ---
+// One Q4_0 matrix against wide column batches (moe_linear), in the gate/up
+// kernel's exact order without the SiLU epilogue.  The reference's pairwise
+// tree over the 16 level-1 nodes (leaves 2p, 2p+1; leaf k' = blocks k' and
+// k' + 32 and, past 64 blocks, their lane's later blocks) splits into four
+// 4-node subtrees whose roots combine as (R0 + R1) + (R2 + R3): workgroup =
+// one 32-row x 32-column tile, wave w builds subtree w, so a tile's
+// sequential work is a quarter of the gate/up kernel's.  The waves share the
+// rows' scales staged in LDS.  Ids are XCD-aware: the column tiles of one row
+// tile run on one XCD, so its rows are fetched from HBM once.
+__device__ __forceinline__ void subtree4_merge(int q, float (&w)[16], float (&l1)[16], float (&l2)[16],
+                                               float (&res)[16]) {
+    if ((q & 1) == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) l1[i] = w[i];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = l1[i] + w[i];
+    if ((q & 2) == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) l2[i] = w[i];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) res[i] = l2[i] + w[i];
+}
+
+template<int Fold>
+__device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint32_t w_off, int wave, int lane,
+                                         float (&res)[16]) {
+    const int m = lane & 31, h = lane >> 5;
+    float l1[16], l2[16];
+    if constexpr (Fold == kFoldGrouped) {
+#pragma unroll 1
+        for (int gi = 2 * wave; gi < 2 * wave + 2; ++gi) {
+            Group G;
+            group_load(t, w_off, gi, G);
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                float w[16], x[16];
+                leaf_grouped<false>(t, g, G, 2 * half, 4 * gi + 2 * half, m, h, w);
+                leaf_grouped<false>(t, g, G, 2 * half + 1, 4 * gi + 2 * half + 1, m, h, x);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
+                subtree4_merge(2 * (gi - 2 * wave) + half, w, l1, l2, res);
+            }
+        }
+    } else {
+#pragma unroll 1
+        for (int q = 0; q < 4; ++q) {
+            const int p = 4 * wave + q;
+            float w[16], x[16];
+            if constexpr (Fold == kFoldStaged) {
+                leaf_staged<false, false>(t, g, 2 * p, m, h, w);
+                leaf_staged<false, false>(t, g, 2 * p + 1, m, h, x);
+            } else {
+                fold_leaf_multi<false>(t, 2 * p, w);
+                fold_leaf_multi<false>(t, 2 * p + 1, x);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
+            subtree4_merge(q, w, l1, l2, res);
+        }
+    }
+}
+
+template<int Fold>
+__global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
+    __shared__ float roots[4][16][64];          // subtree roots [wave][value][lane]
+    __shared__ uint4 d4_lds[kGuMaxBlocks][4];   // [block][32 halfs]
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int id = static_cast<int>(blockIdx.x), local = id >> 3;
+    const int rt = (id & 7) + 8 * (local / a.col_tiles), ct = local % a.col_tiles;
+    if (rt >= a.row_tiles) return;   // uniform per workgroup (grid padded to 8 row tiles)
+    const int nb = a.nb, R0 = rt * 32, c0 = ct * kSub;
+    const int lane = threadIdx.x & 63;
+    const int m = lane & 31, h = lane >> 5;
+    const int prow = 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
+    const uint32_t col = static_cast<uint32_t>(std::min(c0 + m, a.N - 1));
+    const uint32_t row_bytes = static_cast<uint32_t>(nb) * 16u;
+    GuTile t;
+    t.wr = buffer_rsrc(a.codes + static_cast<size_t>(R0) * row_bytes, 32u * row_bytes);
+    t.sr = buffer_rsrc(a.scales + static_cast<size_t>(R0) * nb, 32u * static_cast<uint32_t>(nb) * 2u);
+    t.xr = buffer_rsrc(a.xq.codes, static_cast<uint32_t>(a.N) * static_cast<uint32_t>(nb) * 32u);
+    t.hr = buffer_rsrc(a.xq.heads, static_cast<uint32_t>(a.N) * static_cast<uint32_t>(nb) * 4u);
+    t.w_off = static_cast<uint32_t>(prow) * row_bytes;
+    t.s_off0 = static_cast<uint32_t>(2 * h * nb) * 16u;
+    t.s_off1 = t.s_off0 + static_cast<uint32_t>(nb) * 16u;
+    t.x_off = col * static_cast<uint32_t>(nb) * 32u + 16u * h;
+    t.h_off = col * static_cast<uint32_t>(nb) * 4u;
+    t.nb = nb;
+    t.shift = 4 * h;
+    t.dots = nullptr;
+    t.dot_base = 0;
+    t.dot_ok = false;
+    if constexpr (Fold != kFoldMulti) {
+        // Scale group g (rows 8g..8g+7) of block b lands at halfs 8g..8g+7 of d4_lds[b].
+        for (int c = threadIdx.x; c < 4 * nb; c += blockDim.x) {
+            const int gi = c / nb, b = c % nb;
+            d4_lds[b][gi] = *reinterpret_cast<const uint4 *>(a.scales + static_cast<size_t>(R0 + 8 * gi) * nb + b * 8);
+        }
+        __syncthreads();
+    }
+    const GuStage g{reinterpret_cast<const uint32_t *>(&d4_lds[0][0]), nullptr};
+    float res[16];
+    subtree4<Fold>(t, g, static_cast<uint32_t>(prow) * row_bytes + 32u * 16u * h, wave, lane, res);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) roots[wave][v][lane] = res[v];
+    __syncthreads();
+    // Wave w finishes values 4w..4w+3: rows R0 + 16h + 4w + i of column c0 + m.
+    const int c = c0 + m;
+    const int row = R0 + 16 * h + 4 * wave;
+    if (c >= a.N || row >= a.M) return;
+    float out[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int v = 4 * wave + i;
+        out[i] = (roots[0][v][lane] + roots[1][v][lane]) + (roots[2][v][lane] + roots[3][v][lane]);
+    }
+    float *yr = a.y + static_cast<size_t>(c) * a.M + row;
+    if (row + 4 <= a.M && (a.M & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
+        *reinterpret_cast<float4 *>(yr) = make_float4(out[0], out[1], out[2], out[3]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (row + i < a.M) yr[i] = out[i];
+    }
+}
+
 }  // namespace
+
+hipError_t launch_linear_mfma(const LinearMfmaArgs &a, hipStream_t s) {
+    const unsigned grid = static_cast<unsigned>((a.row_tiles + 7) / 8 * 8) * static_cast<unsigned>(a.col_tiles);
+    if (a.nb == kGuMaxBlocks) k_linear_mfma<kFoldGrouped><<<grid, 256, 0, s>>>(a);
+    else if (a.nb < kGuMaxBlocks) k_linear_mfma<kFoldStaged><<<grid, 256, 0, s>>>(a);
+    else k_linear_mfma<kFoldMulti><<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
 
 hipError_t launch_gate_up_mfma(const FfnArgs &a, hipStream_t s) {
     const bool dbg = a.middle_f32 || a.gate_dots || a.up_dots;

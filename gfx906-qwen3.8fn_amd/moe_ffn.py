@@ -281,14 +281,16 @@ def expf_device(x, stream=None):
     return y
 
 
-def router_select(logits, top_k=10, probabilities=False, error=None, stream=None):
+def router_select(logits, top_k=10, probabilities=False, error=None, stream=None, ids=None, weights=None):
     """Device router: fp32 logits [tokens][experts] -> (ids int32 [tokens][top_k],
-    weights fp32 [tokens][top_k], probabilities or None, error)."""
+    weights fp32 [tokens][top_k], probabilities or None, error).  `ids` /
+    `weights` may be given to write into existing tensors."""
     import torch
     n, e = logits.shape
     dev = logits.device
-    ids = torch.empty((n, top_k), dtype=torch.int32, device=dev)
-    w = torch.empty((n, top_k), dtype=torch.float32, device=dev)
+    if ids is None:
+        ids = torch.empty((n, top_k), dtype=torch.int32, device=dev)
+    w = weights if weights is not None else torch.empty((n, top_k), dtype=torch.float32, device=dev)
     p = torch.empty((n, e), dtype=torch.float32, device=dev) if probabilities else None
     if error is None:
         error = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -385,3 +387,70 @@ class MoeLinear:
         _check(library().moe_linear_apply(self.handle, _ptr(x), n, _ptr(y), _ptr(error), _stream(stream)),
                "moe_linear_apply")
         return y, error
+
+
+class MoeStack:
+    """A stack of resident MoE layers run back to back on one stream, eagerly
+    or replayed from one captured HIP graph (torch.cuda.CUDAGraph over the
+    library's launches).
+
+    Layer l takes its own input batch x[l] (fp32 [N_l][H], device).  With
+    `projections` (MoeLinear H -> H per layer) the layer input is
+    h = projection.apply(x); with `routers` (MoeLinear H -> E per layer) the
+    routes are chosen on the device from router.apply(h) by router_select;
+    otherwise fixed device ids / weights are given to bind().  Every buffer is
+    allocated by bind(), so run() allocates nothing and can be captured."""
+
+    def __init__(self, layers, projections=None, routers=None):
+        self.layers = list(layers)
+        self.projections = projections
+        self.routers = routers
+        self.graph = None
+
+    def bind(self, xs, ids=None, weights=None):
+        import torch
+        dev = xs[0].device
+        self.error = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.steps = []
+        for l, (L, x) in enumerate(zip(self.layers, xs)):
+            n = x.shape[0]
+            st = {"x": x, "y": torch.empty((n, L.H), dtype=torch.float32, device=dev)}
+            st["h"] = torch.empty((n, L.H), dtype=torch.float32, device=dev) if self.projections else x
+            if self.routers:
+                st["logits"] = torch.empty((n, L.E), dtype=torch.float32, device=dev)
+                st["ids"] = torch.empty((n, L.k), dtype=torch.int32, device=dev)
+                st["w"] = torch.empty((n, L.k), dtype=torch.float32, device=dev)
+            else:
+                st["ids"], st["w"] = ids[l], weights[l]
+            self.steps.append(st)
+        self.graph = None
+
+    def run(self, stream=None):
+        for l, (L, st) in enumerate(zip(self.layers, self.steps)):
+            if self.projections:
+                self.projections[l].apply(st["x"], y=st["h"], error=self.error, stream=stream)
+            if self.routers:
+                self.routers[l].apply(st["h"], y=st["logits"], error=self.error, stream=stream)
+                router_select(st["logits"], top_k=L.k, error=self.error, stream=stream, ids=st["ids"],
+                              weights=st["w"])
+            L.forward(st["h"], st["ids"], st["w"], y=st["y"], error=self.error, stream=stream)
+
+    def capture(self):
+        """Record one run() into a HIP graph (after one eager run as warm-up)."""
+        import torch
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.run()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.run()
+        return self.graph
+
+    def replay(self):
+        self.graph.replay()
+
+    def outputs(self):
+        return [st["y"] for st in self.steps]

@@ -107,11 +107,54 @@ CASES = [
 
 @pytest.mark.parametrize("type_,K,M,N", CASES)
 def test_linear_bit_exact_vs_oracle(type_, K, M, N):
+    """Vector kernel (no workspace: every batch stays on k_linear)."""
     w = _weights(type_, K, M, seed=K + M + N)
     x, xq = _columns(K, N, seed=K * 3 + N)
     L = moe_ffn.MoeLinear(type_, K, M, w)
     y = host(L.forward_q8(dev(q8_bytes(xq).reshape(N, -1)), N))
     assert np.array_equal(bits(y), bits(_oracle(type_, w, K, M, xq))), (type_, K, M, N)
+    L.close()
+
+
+MFMA_CASES = [
+    # K, M, N: every fold form of the MFMA kernel
+    (2048, 264, 32),      # 64 blocks (grouped leaves), the narrowest MFMA batch
+    (2048, 512, 128),     # one full column group
+    (1024, 256, 300),     # 32 blocks (staged leaves), partial column tile
+    (32, 1, 40),          # one block, one row (31 padding rows)
+    (2560, 640, 40),      # 80 blocks (lanes holding several blocks)
+    (2080, 1000, 33),     # 65 blocks, rows not a multiple of 32
+]
+
+
+def _linear_env(mode, *args, **kw):
+    """A linear handle created with MOE_LINEAR_MFMA = mode (read at creation)."""
+    old = os.environ.get("MOE_LINEAR_MFMA")
+    os.environ["MOE_LINEAR_MFMA"] = str(mode)
+    try:
+        return moe_ffn.MoeLinear(*args, **kw)
+    finally:
+        if old is None:
+            del os.environ["MOE_LINEAR_MFMA"]
+        else:
+            os.environ["MOE_LINEAR_MFMA"] = old
+
+
+@pytest.mark.parametrize("K,M,N", MFMA_CASES)
+def test_linear_mfma_bit_exact_vs_oracle(K, M, N):
+    """Q4_0 batches of 32 columns or more within the workspace, forced onto
+    int8 MFMA (by default only large ones go there): the same bits as the
+    oracle (and so as the vector kernel), from canonical Q8 input
+    (forward_q8) and from fp32 input (apply, quantized straight into planes)."""
+    w = q4_matrix(K + 2 * M + N, K, M)
+    x, xq = _columns(K, N, seed=K * 5 + N)
+    ref = O.matrix_gpu_order(w, K, M, xq)
+    L = _linear_env(1, Q40, K, M, w, max_columns=N)
+    y = host(L.forward_q8(dev(q8_bytes(xq).reshape(N, -1)), N))
+    assert np.array_equal(bits(y), bits(ref)), ("forward_q8", K, M, N)
+    ya, err = L.apply(dev(x))
+    assert np.array_equal(bits(host(ya)), bits(ref)), ("apply", K, M, N)
+    assert int(host(err)[0]) == 0
     L.close()
 
 
