@@ -137,6 +137,7 @@ struct DecodeArgs {
     const float *weights;      // [tokens][k]
     const float *shared_gate;  // [tokens] or nullptr
     float *y;                  // [tokens][H]
+    const void *x_q8;          // canonical Q8_1 [tokens][H/32] used instead of x, or nullptr
 };
 inline constexpr int kDecodeMaxBlocksH = 64;   // H/32 <= 64: one block per lane
 inline constexpr int kDecodeMaxBlocksI = 16;   // I/32 <= 16: 16 lanes per down row

@@ -915,6 +915,9 @@ __device__ __forceinline__ int decode_route(const DecodeArgs &d, int t, int r, i
 // 8 gate / up rows each as in k_gate_up_lean.  The token's x row is quantized
 // by the whole workgroup into LDS (the same quantize32 as the quantize
 // kernels) while the weight loads are in flight.
+// Q8In: the token rows come as canonical Q8_1 blocks (d.x_q8) and waves 0-3
+// copy them into LDS instead of quantizing x.
+template<bool Q8In>
 __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
     __shared__ uint32_t xs[kDecodeMaxBlocksH * 8];   // Q8 codes of the token, [blocks][32 B]
     __shared__ uint32_t xh[kDecodeMaxBlocksH];       // heads
@@ -945,7 +948,16 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
     const bool quant_wave = wave < 4;
     const int qblk = wave * 16 + (lane & 15), qpart = lane >> 4;
     float xv[8];
-    if (quant_wave) {
+    uint2 qin = make_uint2(0u, 0u);   // Q8In: codes 8 * qpart .. +7 of block qblk
+    uint32_t qhead = 0;
+    if (Q8In && quant_wave && qblk < nbh) {
+        const auto qr = buffer_rsrc(static_cast<const uint8_t *>(d.x_q8) + static_cast<size_t>(t) * nbh * 36,
+                                    static_cast<uint32_t>(nbh) * 36u);
+        const uint32_t off = static_cast<uint32_t>(qblk) * 36u, part = off + 4u + 8u * static_cast<uint32_t>(qpart);
+        qin = make_uint2(buffer_load4(qr, part, 0), buffer_load4(qr, part, 4));
+        qhead = buffer_load4(qr, off, 0);
+    }
+    if (!Q8In && quant_wave) {
         const auto xr = buffer_rsrc(d.x + static_cast<size_t>(t) * H, static_cast<uint32_t>(H) * 4u);
         const uint32_t off = static_cast<uint32_t>(qblk * 32 + qpart * 8) * 4u;   // past H: reads 0
 #pragma unroll
@@ -969,7 +981,16 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) w[q] = buffer_load16(wr, lane_off, q * row_bytes);
     const uint4 d4p = buffer_load16(sr, lane_off, 0);
-    if (quant_wave) {
+    if (Q8In && quant_wave && qblk < nbh) {
+        reinterpret_cast<uint2 *>(xs)[qblk * 4 + qpart] = qin;
+        if (qpart == 0) xh[qblk] = qhead;
+        if (report) {
+            const size_t gb = static_cast<size_t>(t) * nbh + qblk;
+            reinterpret_cast<uint2 *>(a.xq.codes)[gb * 4 + qpart] = qin;
+            if (qpart == 0) a.xq.heads[gb] = qhead;
+        }
+    }
+    if (!Q8In && quant_wave) {
         const Q8Part<4> qp = quantize_part<4>(xv);
         if (qblk < nbh) {
             reinterpret_cast<uint2 *>(xs)[qblk * 4 + qpart] = make_uint2(qp.codes[0], qp.codes[1]);
@@ -1467,7 +1488,9 @@ hipError_t launch_decode_gate_up(const DecodeArgs &d, hipStream_t s) {
     const Shape &sh = d.f.shape;
     const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0);
     const unsigned groups = static_cast<unsigned>((sh.I / 32 + 7) / 8);
-    k_decode_gate_up<<<8u * groups * P1 * d.f.tokens, 512, 0, s>>>(d);
+    const unsigned grid = 8u * groups * P1 * d.f.tokens;
+    if (d.x_q8) k_decode_gate_up<true><<<grid, 512, 0, s>>>(d);
+    else k_decode_gate_up<false><<<grid, 512, 0, s>>>(d);
     return hipGetLastError();
 }
 

@@ -48,6 +48,7 @@ struct moe_ffn_layer {
     int last_tokens = 0;
     // Inputs of the last forward (for moe_ffn_replay_stage).
     const float *last_x = nullptr, *last_weights = nullptr, *last_shared_gate = nullptr;
+    const void *x_q8_in = nullptr;   // canonical Q8_1 input of the current / last forward_q8 (else nullptr)
     const int32_t *last_ids = nullptr;
     float *last_y = nullptr;
     int *last_error = nullptr;
@@ -464,13 +465,19 @@ int run_stage(moe_ffn_layer *L, int stage, const float *x, const int32_t *ids, c
     moe::FfnArgs a = base_args(L, tokens, error);
     hipError_t r = hipSuccess;
     if (decode) {
-        const moe::DecodeArgs d{a, x, ids, weights, shared_gate, y};
+        const moe::DecodeArgs d{a, x, ids, weights, shared_gate, y, L->x_q8_in};
         if (stage == MOE_STAGE_GATE_UP) return moe::launch_decode_gate_up(d, s);
         if (stage == MOE_STAGE_DOWN) return moe::launch_decode_down_fold(d, s);
         return stage >= MOE_STAGE_PREPARE && stage <= MOE_STAGE_FOLD ? hipSuccess : kInvalid;
     }
     switch (stage) {
     case MOE_STAGE_PREPARE:
+        if (L->x_q8_in) {   // grouping only, then the given Q8 rows into the activation planes
+            if ((r = moe::launch_prepare(nullptr, ids, weights, tokens, sh, L->xq, L->routes, L->mfma_min, error, s)) !=
+                hipSuccess)
+                return r;
+            return moe::launch_canonical_to_planes(L->x_q8_in, L->xq, tokens * (sh.H / 32), s);
+        }
         return moe::launch_prepare(x, ids, weights, tokens, sh, L->xq, L->routes, L->mfma_min, error, s);
     // With mfma_min == 1 every nonempty group is an MFMA item and the
     // streaming launch would only start empty workgroups.
@@ -494,11 +501,14 @@ int run_stage(moe_ffn_layer *L, int stage, const float *x, const int32_t *ids, c
 }
 }  // namespace
 
-int moe_ffn_forward(moe_ffn_layer *L, const float *x, const int32_t *ids, const float *weights, int tokens,
-                    const float *shared_gate, float *y, int *error, void *stream) {
-    if (!L || !aligned(x, 4) || !aligned(ids, 4) || !aligned(weights, 4) || !aligned(y, 4) || !aligned(error, 4) ||
-        tokens < 1 || tokens > L->cfg.max_tokens || (shared_gate && !aligned(shared_gate, 4)))
+namespace {
+int forward_impl(moe_ffn_layer *L, const float *x, const void *x_q8, const int32_t *ids, const float *weights,
+                 int tokens, const float *shared_gate, float *y, int *error, void *stream) {
+    if (!L || !(x_q8 ? aligned(x_q8, 4) : aligned(x, 4)) || !aligned(ids, 4) || !aligned(weights, 4) ||
+        !aligned(y, 4) || !aligned(error, 4) || tokens < 1 || tokens > L->cfg.max_tokens ||
+        (shared_gate && !aligned(shared_gate, 4)))
         return kInvalid;
+    L->x_q8_in = x_q8;
     const auto s = static_cast<hipStream_t>(stream);
     const bool decode = use_decode(L, tokens);
     hipEvent_t *marks = nullptr;
@@ -536,6 +546,17 @@ int moe_ffn_forward(moe_ffn_layer *L, const float *x, const int32_t *ids, const 
     L->last_y = y;
     L->last_error = error;
     return hipSuccess;
+}
+}  // namespace
+
+int moe_ffn_forward(moe_ffn_layer *L, const float *x, const int32_t *ids, const float *weights, int tokens,
+                    const float *shared_gate, float *y, int *error, void *stream) {
+    return forward_impl(L, x, nullptr, ids, weights, tokens, shared_gate, y, error, stream);
+}
+
+int moe_ffn_forward_q8(moe_ffn_layer *L, const void *x_q8, const int32_t *ids, const float *weights, int tokens,
+                       const float *shared_gate, float *y, int *error, void *stream) {
+    return forward_impl(L, nullptr, x_q8, ids, weights, tokens, shared_gate, y, error, stream);
 }
 
 int moe_ffn_profile(moe_ffn_layer *L, int forwards) {

@@ -64,6 +64,7 @@ def library():
                                              ctypes.POINTER(ctypes.c_size_t)]
         lib.moe_ffn_export_expert.argtypes = [_P, _I, _P]
         lib.moe_ffn_forward.argtypes = [_P, _P, _P, _P, _I, _P, _P, _P, _P]
+        lib.moe_ffn_forward_q8.argtypes = [_P, _P, _P, _P, _I, _P, _P, _P, _P]
         lib.moe_quantize_q8_1.argtypes = [_P, _P, _I, _I, _P, _P]
         lib.moe_ffn_group_routes.argtypes = [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P]
         lib.moe_ffn_expert_gate_up.argtypes = [_P, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P]
@@ -194,6 +195,18 @@ class MoeLayer:
             error = torch.zeros(1, dtype=torch.int32, device=x.device)
         _check(library().moe_ffn_forward(self.handle, _ptr(x), _ptr(ids), _ptr(weights), n, _ptr(shared_gate),
                                          _ptr(y), _ptr(error), _stream(stream)), "moe_ffn_forward")
+        return y, error
+
+    def forward_q8(self, x_q8, ids, weights, shared_gate=None, y=None, error=None, stream=None):
+        """forward() from canonical Q8_1 rows x_q8 (uint8 [tokens][H/32*36])."""
+        import torch
+        n = ids.shape[0]
+        if y is None:
+            y = torch.empty((n, self.H), dtype=torch.float32, device=ids.device)
+        if error is None:
+            error = torch.zeros(1, dtype=torch.int32, device=ids.device)
+        _check(library().moe_ffn_forward_q8(self.handle, _ptr(x_q8), _ptr(ids), _ptr(weights), n, _ptr(shared_gate),
+                                            _ptr(y), _ptr(error), _stream(stream)), "moe_ffn_forward_q8")
         return y, error
 
     def replay_stage(self, stage, stream=None):

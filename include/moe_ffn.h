@@ -119,6 +119,13 @@ int moe_ffn_export_expert(moe_ffn_layer *layer, int expert, void *host_q4);
 int moe_ffn_forward(moe_ffn_layer *layer, const float *x, const int32_t *ids, const float *weights,
                     int tokens, const float *shared_gate, float *y, int *error, void *stream);
 
+/* forward() from an already quantized input: x_q8 = canonical Q8_1 blocks
+ * [tokens][H/32] (36 bytes each, 4-byte aligned), as the reference's FFN
+ * receives its original Q8 rows f(21) (src/session.hip:1446-1460).  Same
+ * outputs as forward() on the x those blocks quantize. */
+int moe_ffn_forward_q8(moe_ffn_layer *layer, const void *x_q8, const int32_t *ids, const float *weights,
+                       int tokens, const float *shared_gate, float *y, int *error, void *stream);
+
 /* ------------------------------------------------------------------------
  * Stage entry points (parity tests and component timing).
  * ---------------------------------------------------------------------- */

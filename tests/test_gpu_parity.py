@@ -341,6 +341,26 @@ def test_stack_layers_mixed_batch():
         L.close()
 
 
+@pytest.mark.parametrize("tokens", [8, 300, 4096])
+def test_forward_q8_matches_forward(moe512, tokens):
+    """moe_ffn_forward_q8 on the reference quantizer's Q8 rows of x gives
+    forward(x)'s bits on every path (decode at 8 tokens, grouped streaming
+    and MFMA at 300 and 4096), and leaves the same x Q8 for debug_last."""
+    L = moe512["layer"]
+    x = W.activations(tokens, seed=61 + tokens)
+    ids, w = (W.routes_uniform(tokens, seed=62) if tokens == 8 else W.routes_zipf(tokens, 1.1, seed=62 + tokens))
+    g = np.random.default_rng(63).standard_normal(tokens).astype(np.float32)
+    y1, e1 = L.forward(dev(x), dev(ids), dev(w), shared_gate=dev(g))
+    xq1 = host(L.debug_last(tokens)["x_q8"]).copy()
+    y1h = host(y1).copy()
+    xq = q8_bytes(O.quantize_q8(x)).reshape(tokens, -1)
+    assert np.array_equal(xq1.reshape(tokens, -1), xq)
+    y2, e2 = L.forward_q8(dev(xq), dev(ids), dev(w), shared_gate=dev(g))
+    assert np.array_equal(host(y2).view(np.uint32), y1h.view(np.uint32))
+    assert np.array_equal(host(L.debug_last(tokens)["x_q8"]), xq1)
+    assert int(host(e1)[0]) == 0 and int(host(e2)[0]) == 0
+
+
 def test_read_probe_leaves_sink():
     """The measurement hook streams a buffer and never writes its sink for
     non-matching data; bad sizes are rejected before any launch."""
