@@ -146,12 +146,17 @@ __device__ __forceinline__ float rows8_down_exact(const uint4 (&w)[8], uint4 d4p
 // fragments, then the blocks pairwise in index order (XOR 1, 2, 4, 8, 16).
 // Rows are traded between lanes during the first stages so every lane ends
 // with one row's total: lane l holds row 4*(l>>5 & 1) + 2*(l & 1) + (l>>1 & 1).
-// Lanes with `has` false (blocks past H) contribute +0, as the reference's
-// unused lanes do.
+// The first stage is one v_permlane32_swap of rows i and i + 4: lanes < 32
+// then hold (row i own, row i of lane + 32), lanes >= 32 (row i + 4 of lane
+// - 32, own), and one add finishes both (fp32 addition commutes, so each
+// pair gives the reference's bits).  Lanes with `has` false (blocks past H)
+// contribute +0, as the reference's unused lanes do; Full (H/32 == 64) drops
+// that select.
+template<bool Full = false>
 __device__ __forceinline__ float rows8_exact(const uint4 (&w)[8], uint4 d4p, uint4 x0, uint4 x1, uint32_t head,
                                              bool has, int lane) {
     const float d8 = h2f(head), c4 = -4.0f * h2f(head >> 16);
-    const bool b5 = lane & 32, b0 = lane & 1, b1 = lane & 2;
+    const bool b0 = lane & 1, b1 = lane & 2;
     float v4[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -163,15 +168,17 @@ __device__ __forceinline__ float rows8_exact(const uint4 (&w)[8], uint4 d4p, uin
             fragment_dots(w[q], x0, x1, f0, f1);
             const uint32_t d4w = (&d4p.x)[q >> 1];
             const float t0 = fmaf(static_cast<float>(f0), d8, c4), t1 = fmaf(static_cast<float>(f1), d8, c4);
-            z[h][0] = has ? ((q & 1) ? mul_half_hi(d4w, t0) : mul_half_lo(d4w, t0)) : 0.0f;
-            z[h][1] = has ? ((q & 1) ? mul_half_hi(d4w, t1) : mul_half_lo(d4w, t1)) : 0.0f;
+            const float z0 = (q & 1) ? mul_half_hi(d4w, t0) : mul_half_lo(d4w, t0);
+            const float z1 = (q & 1) ? mul_half_hi(d4w, t1) : mul_half_lo(d4w, t1);
+            z[h][0] = Full || has ? z0 : 0.0f;
+            z[h][1] = Full || has ? z1 : 0.0f;
         }
         float u[2];
 #pragma unroll
         for (int f = 0; f < 2; ++f) {
-            const float send = b5 ? z[0][f] : z[1][f];
-            const float keep = b5 ? z[1][f] : z[0][f];
-            u[f] = keep + __shfl_xor(send, 32, 64);
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(z[0][f]), __float_as_uint(z[1][f]),
+                                                            false, false);
+            u[f] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
         }
         v4[i] = u[0] + u[1];
         __builtin_amdgcn_sched_barrier(0);   // one row pair at a time (register pressure)

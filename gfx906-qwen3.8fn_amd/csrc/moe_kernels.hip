@@ -633,7 +633,8 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
 // CU: each wave keeps its 8 weight rows (8 KB) in flight with a small register
 // footprint, so 4 workgroups (32 waves, 256 KB of loads) fit on a CU.  Grid =
 // item bound x I/32 slices; same arithmetic and outputs as k_gate_up_stream.
-template<bool Dbg>
+// Full: H/32 == 64, every lane holds a block.
+template<bool Full, bool Dbg>
 __global__ __launch_bounds__(512, 3) void k_gate_up_lean(FfnArgs a) {
     constexpr int T = kStreamTokens;
     __shared__ float gu[2][32][T];
@@ -703,7 +704,7 @@ __global__ __launch_bounds__(512, 3) void k_gate_up_lean(FfnArgs a) {
                     for (int r = 0; r < 8; ++r)
                         dots[(static_cast<size_t>(first + j) * I + row0 + r) * nbh + lane] = dot_block(w[r], x0, x1);
             }
-            const float v = rows8_exact(w, d4p, x0, x1, hx, has, lane);
+            const float v = rows8_exact<Full>(w, d4p, x0, x1, hx, has, lane);
             if ((lane & 28) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
             x0 = n0; x1 = n1; hx = nh;
         }
@@ -916,8 +917,9 @@ __device__ __forceinline__ int decode_route(const DecodeArgs &d, int t, int r, i
 // by the whole workgroup into LDS (the same quantize32 as the quantize
 // kernels) while the weight loads are in flight.
 // Q8In: the token rows come as canonical Q8_1 blocks (d.x_q8) and waves 0-3
-// copy them into LDS instead of quantizing x.
-template<bool Q8In>
+// copy them into LDS instead of quantizing x.  Full: H/32 == 64, every lane
+// holds a block.
+template<bool Q8In, bool Full>
 __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
     __shared__ uint32_t xs[kDecodeMaxBlocksH * 8];   // Q8 codes of the token, [blocks][32 B]
     __shared__ uint32_t xh[kDecodeMaxBlocksH];       // heads
@@ -1009,7 +1011,7 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
     __syncthreads();
     const uint4 x0 = reinterpret_cast<const uint4 *>(xs)[kb * 2];
     const uint4 x1 = reinterpret_cast<const uint4 *>(xs)[kb * 2 + 1];
-    const float v = rows8_exact(w, d4p, x0, x1, xh[kb], has, lane);
+    const float v = rows8_exact<Full>(w, d4p, x0, x1, xh[kb], has, lane);
     const int rho = 4 * ((lane >> 5) & 1) + 2 * (lane & 1) + ((lane >> 1) & 1);
     if ((lane & 28) == 0) gu[mat][(wave & 3) * 8 + rho] = v;
     __syncthreads();
@@ -1475,8 +1477,9 @@ hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s) {
     if (nbl <= 1) {
         // One unit per workgroup; grid = item bound x slices, extra items exit.
         const unsigned lgrid = stream_item_bound(a) * static_cast<unsigned>(a.shape.I / 32);
-        if (dbg) k_gate_up_lean<true><<<lgrid, 512, 0, s>>>(a);
-        else k_gate_up_lean<false><<<lgrid, 512, 0, s>>>(a);
+        if (dbg) k_gate_up_lean<false, true><<<lgrid, 512, 0, s>>>(a);
+        else if (a.shape.H == 2048) k_gate_up_lean<true, false><<<lgrid, 512, 0, s>>>(a);
+        else k_gate_up_lean<false, false><<<lgrid, 512, 0, s>>>(a);
     } else if (nbl <= 2) gate_up_stream<2>(a, dbg, grid, s);
     else gate_up_stream<0>(a, dbg, grid, s);
     return hipGetLastError();
@@ -1489,8 +1492,14 @@ hipError_t launch_decode_gate_up(const DecodeArgs &d, hipStream_t s) {
     const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0);
     const unsigned groups = static_cast<unsigned>((sh.I / 32 + 7) / 8);
     const unsigned grid = 8u * groups * P1 * d.f.tokens;
-    if (d.x_q8) k_decode_gate_up<true><<<grid, 512, 0, s>>>(d);
-    else k_decode_gate_up<false><<<grid, 512, 0, s>>>(d);
+    const bool full = sh.H == 2048;
+    if (d.x_q8) {
+        if (full) k_decode_gate_up<true, true><<<grid, 512, 0, s>>>(d);
+        else k_decode_gate_up<true, false><<<grid, 512, 0, s>>>(d);
+    } else {
+        if (full) k_decode_gate_up<false, true><<<grid, 512, 0, s>>>(d);
+        else k_decode_gate_up<false, false><<<grid, 512, 0, s>>>(d);
+    }
     return hipGetLastError();
 }
 
