@@ -196,6 +196,39 @@ __device__ __forceinline__ float rows8_exact(const uint4 (&w)[8], uint4 d4p, uin
     return xor_sum(v, 16);
 }
 
+// The same reduction for lane partials already summed over several blocks
+// (lane j holds both fragments' accumulators of blocks j, j + 64, ... for 8
+// rows): z[row][f] -> lane j + lane j ^ 32 per fragment (one
+// v_permlane32_swap per row pair, as in rows8_exact), then the two
+// fragments, then XOR 1, 2, 4, 8, 16.  Lane l ends with row
+// 4*(l>>5 & 1) + 2*(l & 1) + (l>>1 & 1).
+__device__ __forceinline__ float fold_rows8(const float (&z)[8][2], int lane) {
+    const bool b0 = lane & 1, b1 = lane & 2;
+    float v4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float u[2];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(z[i][f]), __float_as_uint(z[i + 4][f]),
+                                                            false, false);
+            u[f] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+        v4[i] = u[0] + u[1];
+    }
+    float v2[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float send = b0 ? v4[i] : v4[i + 2];
+        const float keep = b0 ? v4[i + 2] : v4[i];
+        v2[i] = keep + __shfl_xor(send, 1, 64);
+    }
+    float v = (b1 ? v2[1] : v2[0]) + __shfl_xor(b1 ? v2[0] : v2[1], 2, 64);
+    v = xor_sum(v, 4);
+    v = xor_sum(v, 8);
+    return xor_sum(v, 16);
+}
+
 // One Q8_1 block from 32 lanes (lane32 = element index).  Semantics of the
 // reference GPU quantizer (src/hip/linear.hip:121-149): a nonfinite element
 // poisons its block (bit 1), an unrepresentable scale/sum/code sets bit 2,

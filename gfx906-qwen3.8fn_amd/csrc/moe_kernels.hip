@@ -516,10 +516,13 @@ __global__ void k_single_items(Shape shape, RouteOut r, int expert, int columns,
 // 8 waves: waves 0-3 take gate rows slice*32 + 8w .. +7, waves 4-7 the same
 // up rows.  Lane l takes blocks l, l+64, ... (NBL of them): each row is one
 // coalesced 16-byte-per-lane wave load of the code plane, held in registers
-// while the item's tokens are processed one at a time.  Each token's 8 row
-// sums are reduced across the wave by a transposing butterfly (xor 32/16/8
-// halve the row set, xor 4/2/1 finish the sum), the 64 sums go through LDS,
-// and wave j quantizes token j's 32 SiLU(g)*u values into one Q8_1 block.
+// while the item's tokens are processed one at a time.  For H > 2048 a lane
+// holds several blocks, and each token's rows follow the reference's fp32
+// order (src/cpu_expert.cpp:156-213): the lane keeps one accumulator per row
+// and fragment, acc = fma(d4, fma(float(I_f), d8, -4 s8), acc) over its
+// blocks in ascending order, and fold_rows8 reduces them as the reference's
+// 128-lane fold does.  The 64 row sums go through LDS, and wave j quantizes
+// token j's 32 SiLU(g)*u values into one Q8_1 block.
 template<int NBL, bool Dbg>
 __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
     constexpr int T = kStreamTokens;
@@ -529,8 +532,7 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
     const int H = a.shape.H, I = a.shape.I, nbh = H / 32, nbi = I / 32, S = I / 32;
     const int units = a.routes.item_counts[0] * S;
     const int mat = wave >> 2;
-    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
-    const int rho = (b5 ? 4 : 0) + (b4 ? 2 : 0) + (b3 ? 1 : 0);
+    const int rho = 4 * ((lane >> 5) & 1) + 2 * (lane & 1) + ((lane >> 1) & 1);   // row fold_rows8 leaves here
     for (int u = blockIdx.x; u < units; u += gridDim.x) {
         const Item it = a.routes.stream_items[u / S];
         const int s = u % S;
@@ -560,9 +562,9 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
 #pragma unroll 1
         for (int j = 0; j < it.ncols; ++j) {
             const int tok = a.routes.pair_token[it.first + j];
-            float acc[8];
+            float acc[8][2];
 #pragma unroll
-            for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+            for (int r = 0; r < 8; ++r) acc[r][0] = acc[r][1] = 0.0f;
 #pragma unroll
             for (int nb = 0; nb < (NBL > 0 ? NBL : 1); ++nb)
             for (int kb = lane + 64 * nb; kb < nbh; kb += (NBL > 0 ? nbh : 64)) {
@@ -577,36 +579,21 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
                 const uint4 x0 = *reinterpret_cast<const uint4 *>(a.xq.codes + xb * 32);
                 const uint4 x1 = *reinterpret_cast<const uint4 *>(a.xq.codes + xb * 32 + 16);
                 const uint32_t hd = a.xq.heads[xb];
-                const float d8 = h2f(hd), c8 = -8.0f * h2f(hd >> 16);
+                const float d8 = h2f(hd), c4 = -4.0f * h2f(hd >> 16);
 #pragma unroll
                 for (int r = 0; r < 8; ++r) {
-                    const int dot = dot_block(w[nb][r], x0, x1);
+                    int f0, f1;
+                    fragment_dots(w[nb][r], x0, x1, f0, f1);
                     if constexpr (Dbg) {
                         int32_t *dots = mat ? a.up_dots : a.gate_dots;
-                        if (dots) dots[(static_cast<size_t>(it.first + j) * I + row0 + r) * nbh + kb] = dot;
+                        if (dots) dots[(static_cast<size_t>(it.first + j) * I + row0 + r) * nbh + kb] = f0 + f1;
                     }
-                    acc[r] = fmaf(d4[nb][r], fmaf(static_cast<float>(dot), d8, c8), acc[r]);
+                    acc[r][0] = fmaf(d4[nb][r], fmaf(static_cast<float>(f0), d8, c4), acc[r][0]);
+                    acc[r][1] = fmaf(d4[nb][r], fmaf(static_cast<float>(f1), d8, c4), acc[r][1]);
                 }
             }
-            // Transposing reduction: lane ends with the sum of row rho(lane).
-            float v4[4], v2[2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float send = b5 ? acc[i] : acc[i + 4];
-                const float keep = b5 ? acc[i + 4] : acc[i];
-                v4[i] = keep + __shfl_xor(send, 32, 64);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const float send = b4 ? v4[i] : v4[i + 2];
-                const float keep = b4 ? v4[i + 2] : v4[i];
-                v2[i] = keep + __shfl_xor(send, 16, 64);
-            }
-            float v = (b3 ? v2[1] : v2[0]) + __shfl_xor(b3 ? v2[0] : v2[1], 8, 64);
-            v = xor_sum(v, 4);
-            v = xor_sum(v, 2);
-            v = xor_sum(v, 1);
-            if ((lane & 7) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
+            const float v = fold_rows8(acc, lane);
+            if ((lane & 28) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
         }
         __syncthreads();
         if (wave < it.ncols) {

@@ -61,38 +61,6 @@ struct LinearArgs {
     int tiles, tile_cols;    // column tiles per slice; columns per tile (multiple of kLinearCols)
 };
 
-// Reduce 8 rows' per-fragment lane partials z[row][f] in the reference's
-// order: lane j + lane j ^ 32 per fragment, then the two fragments, then
-// XOR 1, 2, 4, 8, 16.  Rows are traded between lanes during the first three
-// stages so each lane ends with one row: lane l holds row
-// 4 * (l >> 5 & 1) + 2 * (l & 1) + (l >> 1 & 1).
-__device__ __forceinline__ float fold_rows8(const float (&z)[8][2], int lane) {
-    const bool b5 = lane & 32, b0 = lane & 1, b1 = lane & 2;
-    float v4[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float u[2];
-#pragma unroll
-        for (int f = 0; f < 2; ++f) {
-            const float send = b5 ? z[i][f] : z[i + 4][f];
-            const float keep = b5 ? z[i + 4][f] : z[i][f];
-            u[f] = keep + __shfl_xor(send, 32, 64);
-        }
-        v4[i] = u[0] + u[1];
-    }
-    float v2[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const float send = b0 ? v4[i] : v4[i + 2];
-        const float keep = b0 ? v4[i + 2] : v4[i];
-        v2[i] = keep + __shfl_xor(send, 1, 64);
-    }
-    float v = (b1 ? v2[1] : v2[0]) + __shfl_xor(b1 ? v2[0] : v2[1], 2, 64);
-    v = xor_sum(v, 4);
-    v = xor_sum(v, 8);
-    return xor_sum(v, 16);
-}
-
 // HOLD = block slots (64 blocks each) whose weights are loaded together;
 // G = columns accumulated per pass over the weights.
 template<bool Q41, int HOLD, int G>
