@@ -224,6 +224,7 @@ def main():
     ap.add_argument("--no-stack", action="store_true", help="skip the 48-layer stack (configs[4])")
     ap.add_argument("--stack-steps", type=int, default=5)
     ap.add_argument("--no-linear", action="store_true", help="skip the quantized linear projections")
+    ap.add_argument("--no-graph", action="store_true", help="skip the graph-captured stack passes")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy x5 (FETCH_SIZE/WRITE_SIZE scale for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -401,34 +402,35 @@ def main():
         }
         log(f"[bench] stack of {NL}: {wall_s*1e3:.2f} ms/pass, {wall_s/NL*1e6:.1f} us/layer, "
             f"touched {np.mean(touched_s):.1f}, resident {resident/1e9:.2f} GB")
-        # The same pass replayed from one captured HIP graph, then the full
-        # per-layer pipeline in a graph: Q4_0 H -> H projection, Q4_0 router
-        # H -> E, device top-10, MoE layer (routes chosen on the device).
-        S = moe_ffn.MoeStack(layers)
-        S.bind([x for x, _, _ in inputs], [i for _, i, _ in inputs], [w for _, _, w in inputs])
-        wall_g, gpu_g = time_graph(S, args.stack_steps)
-        result["stack_48"]["graph_ms_per_stack"] = wall_g * 1e3
-        log(f"[bench] stack of {NL}, one HIP graph: {wall_g*1e3:.2f} ms/pass, {wall_g/NL*1e6:.1f} us/layer")
-        rng = np.random.default_rng(8000)
-        projections = [moe_ffn.MoeLinear(moe_ffn.TYPE_Q4_0, 2048, 2048, W.q4_blocks(2048 * 64, rng).reshape(-1),
+        if not args.no_graph:
+            # The same pass replayed from one captured HIP graph, then the full
+            # per-layer pipeline in a graph: Q4_0 H -> H projection, Q4_0 router
+            # H -> E, device top-10, MoE layer (routes chosen on the device).
+            S = moe_ffn.MoeStack(layers)
+            S.bind([x for x, _, _ in inputs], [i for _, i, _ in inputs], [w for _, _, w in inputs])
+            wall_g, gpu_g = time_graph(S, args.stack_steps)
+            result["stack_48"]["graph_ms_per_stack"] = wall_g * 1e3
+            log(f"[bench] stack of {NL}, one HIP graph: {wall_g*1e3:.2f} ms/pass, {wall_g/NL*1e6:.1f} us/layer")
+            rng = np.random.default_rng(8000)
+            projections = [moe_ffn.MoeLinear(moe_ffn.TYPE_Q4_0, 2048, 2048, W.q4_blocks(2048 * 64, rng).reshape(-1),
+                                             max_columns=NS) for _ in range(NL)]
+            routers = [moe_ffn.MoeLinear(moe_ffn.TYPE_Q4_0, 2048, 512, W.q4_blocks(512 * 64, rng).reshape(-1),
                                          max_columns=NS) for _ in range(NL)]
-        routers = [moe_ffn.MoeLinear(moe_ffn.TYPE_Q4_0, 2048, 512, W.q4_blocks(512 * 64, rng).reshape(-1),
-                                     max_columns=NS) for _ in range(NL)]
-        P = moe_ffn.MoeStack(layers, projections=projections, routers=routers)
-        P.bind([x for x, _, _ in inputs])
-        wall_p, gpu_p = time_graph(P, args.stack_steps)
-        # The MoE layers alone on the routes the device router chose (they
-        # differ from the Zipf routes above), to split the pipeline's time.
-        M = moe_ffn.MoeStack(layers)
-        M.bind([st["h"] for st in P.steps], [st["ids"] for st in P.steps], [st["w"] for st in P.steps])
-        wall_m, _ = time_graph(M, args.stack_steps)
-        result["stack_48"]["pipeline_graph_ms_per_stack"] = wall_p * 1e3
-        result["stack_48"]["pipeline_moe_only_graph_ms_per_stack"] = wall_m * 1e3
-        log(f"[bench] stack of {NL} with projection + router + top-10 per layer, one HIP graph: "
-            f"{wall_p*1e3:.2f} ms/pass, {wall_p/NL*1e6:.1f} us/layer; its MoE layers alone "
-            f"{wall_m/NL*1e6:.1f} us/layer")
-        for m in projections + routers:
-            m.close()
+            P = moe_ffn.MoeStack(layers, projections=projections, routers=routers)
+            P.bind([x for x, _, _ in inputs])
+            wall_p, gpu_p = time_graph(P, args.stack_steps)
+            # The MoE layers alone on the routes the device router chose (they
+            # differ from the Zipf routes above), to split the pipeline's time.
+            M = moe_ffn.MoeStack(layers)
+            M.bind([st["h"] for st in P.steps], [st["ids"] for st in P.steps], [st["w"] for st in P.steps])
+            wall_m, _ = time_graph(M, args.stack_steps)
+            result["stack_48"]["pipeline_graph_ms_per_stack"] = wall_p * 1e3
+            result["stack_48"]["pipeline_moe_only_graph_ms_per_stack"] = wall_m * 1e3
+            log(f"[bench] stack of {NL} with projection + router + top-10 per layer, one HIP graph: "
+                f"{wall_p*1e3:.2f} ms/pass, {wall_p/NL*1e6:.1f} us/layer; its MoE layers alone "
+                f"{wall_m/NL*1e6:.1f} us/layer")
+            for m in projections + routers:
+                m.close()
         for L in layers:
             L.close()
 
