@@ -35,6 +35,22 @@ def test_invalid_arguments_rejected_before_hip():
     bad = moe_ffn.Config(2048, 500, 512, 10, 1, 8)      # intermediate not a multiple of 32
     w, s = ctypes.c_size_t(), ctypes.c_size_t()
     assert lib.moe_ffn_memory_bytes(ctypes.byref(bad), ctypes.byref(w), ctypes.byref(s)) == 1
+    bad_down = moe_ffn.Config(2048, 512, 512, 10, 1, 8, 2)   # no such down block type
+    assert lib.moe_ffn_memory_bytes(ctypes.byref(bad_down), ctypes.byref(w), ctypes.byref(s)) == 1
+    q41 = moe_ffn.Config(2048, 512, 512, 10, 1, 8, moe_ffn.DOWN_Q4_1)
+    assert lib.moe_ffn_memory_bytes(ctypes.byref(q41), ctypes.byref(w), ctypes.byref(s)) == 0
+    assert w.value >= 513 * moe_ffn.expert_bytes(2048, 512, moe_ffn.DOWN_Q4_1)
+    assert lib.moe_ffn_forward_q8(None, None, None, None, 1, None, None, None, None) == 1
+    assert lib.moe_router_select(None, 8, 512, 10, None, None, None, None, None) == 1
+    # quantized linear: type, shape and pointer checks come first
+    lin = ctypes.c_void_p()
+    for args in ((7, 64, 8, 0), (moe_ffn.TYPE_Q4_0, 48, 8, 0), (moe_ffn.TYPE_Q4_0, 64, 0, 0),
+                 (moe_ffn.TYPE_Q4_1, 64, 16385, 0), (moe_ffn.TYPE_Q4_0, 64, 8, -1)):
+        assert lib.moe_linear_create(*args, buf, 0, 0, ctypes.byref(lin)) == 1, args
+    assert lib.moe_linear_create(moe_ffn.TYPE_Q4_0, 64, 8, 0, None, 0, 0, ctypes.byref(lin)) == 1
+    assert lib.moe_linear_forward_q8(None, buf, 1, buf, None) == 1
+    assert lib.moe_linear_apply(None, buf, 1, buf, buf, None) == 1
+    assert lib.moe_linear_destroy(None) == 1
 
 
 def test_memory_footprint_baseline_shape():
