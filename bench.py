@@ -354,12 +354,12 @@ def main():
     # ---- non-expert Q4_0 projections (moe_linear_forward_q8), cold weights --
     if not args.no_linear:
         lin = {}
-        for K, M, N in ((2048, 2048, 1), (2048, 2048, 8), (2048, 2048, 128), (2048, 2048, 1032), (8192, 8192, 1),
-                        (8192, 8192, 8), (8192, 8192, 128)):
-            sec, nbytes = time_linear(K, M, N)
-            lin[f"{K}x{M}_n{N}"] = {"us": sec * 1e6, "GB/s": nbytes / sec / 1e9,
-                                    "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
-            log(f"[bench] linear Q4_0 {K}->{M} N={N}: {sec*1e6:.2f} us, {nbytes/sec/1e9:.0f} GB/s")
+        for lk, lm, ln in ((2048, 2048, 1), (2048, 2048, 8), (2048, 2048, 128), (2048, 2048, 1032), (8192, 8192, 1),
+                           (8192, 8192, 8), (8192, 8192, 128)):
+            sec, nbytes = time_linear(lk, lm, ln)
+            lin[f"{lk}x{lm}_n{ln}"] = {"us": sec * 1e6, "GB/s": nbytes / sec / 1e9,
+                                       "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
+            log(f"[bench] linear Q4_0 {lk}->{lm} N={ln}: {sec*1e6:.2f} us, {nbytes/sec/1e9:.0f} GB/s")
         result["linear_q4_0"] = lin
 
     # ---- 16K uniform prefill -----------------------------------
