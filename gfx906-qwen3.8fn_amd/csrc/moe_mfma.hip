@@ -458,29 +458,34 @@ __device__ __forceinline__ void fold_tree_staged(const GuTile &t, const GuStage 
 }
 
 // ---- H == 2048 (64 blocks): loads in groups of four leaves that use whole
-// cache lines.  Group g covers blocks 4g..4g+3 and 4g+32..4g+35.  Lane half
-// h of row m reads 64 contiguous bytes of its row (blocks 4g+32h+i); a
-// v_permlane32_swap of the low- and high-nibble words then gives, per leaf,
-// the MFMA operand of block 4g+i (low nibbles in lanes < 32, high in lanes
-// >= 32) and of block 4g+32+i.  Lane half h of token n reads bytes
-// 16h..16h+15 of four consecutive 32-byte Q8 blocks, so the two halves of a
-// token use the same lines.
-struct Group {
-    uint4 w[4];           // A row: blocks 4g+i (h = 0) / 4g+32+i (h = 1)
-    uint4 xa[4], xb[4];   // token codes, half h: blocks 4g+i / 4g+32+i
-    uint4 ha, hb;         // token heads of blocks 4g..4g+3 / 4g+32..4g+35
+// cache lines.  Group g covers blocks 4g..4g+3 and 4g+32..4g+35, loaded half
+// (two leaves) at a time.  Lane half h of row m reads contiguous bytes of its
+// row (blocks 4g+32h+i); a v_permlane32_swap of the low- and high-nibble
+// words then gives, per leaf, the MFMA operand of block 4g+i (low nibbles in
+// lanes < 32, high in lanes >= 32) and of block 4g+32+i.  Lane half h of
+// token n reads bytes 16h..16h+15 of consecutive 32-byte Q8 blocks, so the
+// two halves of a token use the same lines.
+struct HalfGroup {
+    uint4 w[2];           // A row: blocks 4g+2q+i (h = 0) / 4g+32+2q+i (h = 1)
+    uint4 xa[2], xb[2];   // token codes, half h: blocks 4g+2q+i / 4g+32+2q+i
+    uint2 ha, hb;         // token heads of blocks 4g+2q, +1 / 4g+32+2q, +1
 };
 
-__device__ __forceinline__ void group_load(const GuTile &t, uint32_t w_off, int g, Group &G) {
-    const uint32_t b0 = static_cast<uint32_t>(4 * g);
+// The operands of level-1 node p = 2g + q (leaves 4g + 2q and 4g + 2q + 1).
+// Loading half a line group at a time keeps the kernel at 149 VGPRs, three
+// waves per SIMD (a whole group in registers needed 211: two waves).
+__device__ __forceinline__ void half_load(const GuTile &t, uint32_t w_off, int p, HalfGroup &G) {
+    const uint32_t b0 = static_cast<uint32_t>(4 * (p >> 1) + 2 * (p & 1));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) G.w[i] = buffer_load16(t.wr, w_off, (b0 + i) * 16u);
+    for (int i = 0; i < 2; ++i) G.w[i] = buffer_load16(t.wr, w_off, (b0 + i) * 16u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) G.xa[i] = buffer_load16(t.xr, t.x_off, (b0 + i) * 32u);
+    for (int i = 0; i < 2; ++i) G.xa[i] = buffer_load16(t.xr, t.x_off, (b0 + i) * 32u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) G.xb[i] = buffer_load16(t.xr, t.x_off, (b0 + 32 + i) * 32u);
-    G.ha = buffer_load16(t.hr, t.h_off, b0 * 4u);
-    G.hb = buffer_load16(t.hr, t.h_off, (b0 + 32) * 4u);
+    for (int i = 0; i < 2; ++i) G.xb[i] = buffer_load16(t.xr, t.x_off, (b0 + 32 + i) * 32u);
+    const auto a = __builtin_amdgcn_raw_buffer_load_b64(t.hr, t.h_off, b0 * 4u, 0);
+    const auto b = __builtin_amdgcn_raw_buffer_load_b64(t.hr, t.h_off, (b0 + 32) * 4u, 0);
+    G.ha = make_uint2(a[0], a[1]);
+    G.hb = make_uint2(b[0], b[1]);
 }
 
 __device__ __forceinline__ v16i frag_mfma2(uint32_t a0, uint32_t a1, uint32_t x0, uint32_t x1) {
@@ -490,7 +495,7 @@ __device__ __forceinline__ v16i frag_mfma2(uint32_t a0, uint32_t a1, uint32_t x0
 }
 
 template<bool Dbg>
-__device__ __forceinline__ void leaf_grouped(const GuTile &t, const GuStage &g, const Group &G, int i, int kp, int m,
+__device__ __forceinline__ void leaf_grouped(const GuTile &t, const GuStage &g, const HalfGroup &G, int i, int kp, int m,
                                              int h, float (&v)[16]) {
     const uint4 wi = G.w[i];
     const uint32_t wv[4] = {wi.x, wi.y, wi.z, wi.w};
@@ -501,7 +506,7 @@ __device__ __forceinline__ void leaf_grouped(const GuTile &t, const GuStage &g, 
         opa[d] = r[0];   // block kp: low nibbles (lanes < 32), high nibbles (lanes >= 32)
         opb[d] = r[1];   // block kp + 32
     }
-    const uint32_t ha = (&G.ha.x)[i], hb = (&G.hb.x)[i];
+    const uint32_t ha = i ? G.ha.y : G.ha.x, hb = i ? G.hb.y : G.hb.x;
     const uint4 *da4 = reinterpret_cast<const uint4 *>(g.d4 + kp * 16 + 8 * h);
     const uint4 *db4 = reinterpret_cast<const uint4 *>(g.d4 + (kp + 32) * 16 + 8 * h);
     const uint4 a0 = da4[0], a1 = da4[1], b0 = db4[0], b1 = db4[1];
@@ -568,18 +573,15 @@ __device__ __forceinline__ void fold_tree_grouped(const GuTile &t, const GuStage
     const int m = lane & 31, h = lane >> 5;
     float l1[16], l2[16];
 #pragma unroll 1
-    for (int gi = 0; gi < 8; ++gi) {
-        Group G;
-        group_load(t, w_off, gi, G);
+    for (int p = 0; p < 16; ++p) {
+        HalfGroup G;
+        half_load(t, w_off, p, G);
+        float w[16], x[16];
+        leaf_grouped<Dbg>(t, g, G, 0, 2 * p, m, h, w);
+        leaf_grouped<Dbg>(t, g, G, 1, 2 * p + 1, m, h, x);
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            float w[16], x[16];
-            leaf_grouped<Dbg>(t, g, G, 2 * half, 4 * gi + 2 * half, m, h, w);
-            leaf_grouped<Dbg>(t, g, G, 2 * half + 1, 4 * gi + 2 * half + 1, m, h, x);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
-            tree_merge(park, lane, 2 * gi + half, w, l1, l2, res);
-        }
+        for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
+        tree_merge(park, lane, p, w, l1, l2, res);
     }
 }
 
@@ -974,18 +976,16 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
     float l1[16], l2[16];
     if constexpr (Fold == kFoldGrouped) {
 #pragma unroll 1
-        for (int gi = 2 * wave; gi < 2 * wave + 2; ++gi) {
-            Group G;
-            group_load(t, w_off, gi, G);
+        for (int q = 0; q < 4; ++q) {
+            const int p = 4 * wave + q;
+            HalfGroup G;
+            half_load(t, w_off, p, G);
+            float w[16], x[16];
+            leaf_grouped<false>(t, g, G, 0, 2 * p, m, h, w);
+            leaf_grouped<false>(t, g, G, 1, 2 * p + 1, m, h, x);
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                float w[16], x[16];
-                leaf_grouped<false>(t, g, G, 2 * half, 4 * gi + 2 * half, m, h, w);
-                leaf_grouped<false>(t, g, G, 2 * half + 1, 4 * gi + 2 * half + 1, m, h, x);
-#pragma unroll
-                for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
-                subtree4_merge(2 * (gi - 2 * wave) + half, w, l1, l2, res);
-            }
+            for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
+            subtree4_merge(q, w, l1, l2, res);
         }
     } else {
 #pragma unroll 1
