@@ -200,6 +200,71 @@ def time_linear(K, M, N, iters=64, cold_bytes=320e6):
     return e0.elapsed_time(e1) / 1e3 / iters, nbytes
 
 
+def time_calls(fn, iters=32):
+    """Seconds per fn() call, fn's launches replayed from one captured graph
+    (iters calls per replay, the median of 5 replays)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / 1e3 / iters)
+    del graph
+    return float(np.median(times))
+
+
+def reference_components():
+    """The reference's published component timings at its own expert shape
+    (hidden 2560, intermediate 640; gfx906, results.jsonl), measured here with
+    the same operations: a resident expert's whole forward (fp32 x -> quantize
+    -> gate/up -> SiLU*up -> quantize -> down, GpuExpert::run) and the Q4_0 /
+    Q4_1 linear projections.  Weights stay resident and are reused across
+    calls, as in the reference's repeated launches."""
+    import torch
+    import moe_ffn
+    import workloads as W
+    H, I = 2560, 640
+    dev0 = "cuda:0"
+    out = {"expert_forward_us": {}, "linear_us": {}}
+    bank = W.q4_bank(1, hidden=H, intermediate=I, seed=4100, down_type=moe_ffn.DOWN_Q4_1)
+    L = moe_ffn.MoeLayer(H, I, 1, 1, False, 128, experts_q4=bank, down_type=moe_ffn.DOWN_Q4_1)
+    for n in (1, 2, 3, 128):
+        x = torch.from_numpy(W.activations(n, hidden=H, seed=4101)).to(dev0)
+        ids = torch.zeros((n, 1), dtype=torch.int32, device=dev0)
+        w = torch.ones((n, 1), dtype=torch.float32, device=dev0)
+        y = torch.empty((n, H), dtype=torch.float32, device=dev0)
+        err = torch.zeros(1, dtype=torch.int32, device=dev0)
+        out["expert_forward_us"][str(n)] = time_calls(lambda: L.forward(x, ids, w, y=y, error=err)) * 1e6
+        if int(err.cpu()[0]) != 0:
+            raise RuntimeError("reference-shape expert flagged an error")
+    L.close()
+    rng = np.random.default_rng(4102)
+    mats = {("q4_0", H, I): W.q4_blocks(I * H // 32, rng).reshape(-1),
+            ("q4_0", I, H): W.q4_blocks(H * I // 32, rng).reshape(-1),
+            ("q4_1", I, H): W.q4_1_blocks(H * I // 32, rng).reshape(-1)}
+    cases = [("q4_0", H, I, n) for n in (1, 8, 16, 32, 128)] + [("q4_0", I, H, 128)] + \
+            [("q4_1", I, H, n) for n in (1, 8, 32, 128)]
+    for kind, K, M, n in cases:
+        t = moe_ffn.TYPE_Q4_1 if kind == "q4_1" else moe_ffn.TYPE_Q4_0
+        lin = moe_ffn.MoeLinear(t, K, M, mats[(kind, K, M)], max_columns=n)
+        xq, _ = moe_ffn.quantize_q8_1(torch.from_numpy(W.activations(n, hidden=K, seed=4103)).to(dev0))
+        y = torch.empty((n, M), dtype=torch.float32, device=dev0)
+        out["linear_us"][f"{kind}_{K}x{M}_n{n}"] = time_calls(lambda: lin.forward_q8(xq, n, y=y)) * 1e6
+        lin.close()
+    return out
+
+
 def cpu_baseline(x, bank, shared, ids, w, target_seconds):
     import oracle as O
     cpus = O.physical_cpus()
@@ -225,6 +290,7 @@ def main():
     ap.add_argument("--stack-steps", type=int, default=5)
     ap.add_argument("--no-linear", action="store_true", help="skip the quantized linear projections")
     ap.add_argument("--no-graph", action="store_true", help="skip the graph-captured stack passes")
+    ap.add_argument("--no-refshapes", action="store_true", help="skip the reference's component shapes (2560/640)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy x5 (FETCH_SIZE/WRITE_SIZE scale for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -361,6 +427,11 @@ def main():
                                        "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
             log(f"[bench] linear Q4_0 {lk}->{lm} N={ln}: {sec*1e6:.2f} us, {nbytes/sec/1e9:.0f} GB/s")
         result["linear_q4_0"] = lin
+
+    # ---- the reference's own published component shapes (2560/640) ---------
+    if not args.no_refshapes:
+        result["reference_shapes"] = reference_components()
+        log(f"[bench] reference shapes: {json.dumps(result['reference_shapes'])}")
 
     # ---- 16K uniform prefill -----------------------------------
     if not args.no_prefill and not args.no_16k:

@@ -229,6 +229,34 @@ __device__ __forceinline__ float fold_rows8(const float (&z)[8][2], int lane) {
     return xor_sum(v, 16);
 }
 
+// rows8_exact for rows of 65..128 blocks: lane j holds blocks j (w, d4p, x0,
+// x1, head) and j + 64 (w2, ..., present when has2).  The reference's lane
+// 2j + f accumulates its blocks in ascending order,
+// acc = fma(d4, fma(float(I_f), d8, -4 s8), acc) from +0 (src/cpu_expert.cpp:
+// 156-213), and the accumulators are then folded as by rows8_exact.
+__device__ __forceinline__ float rows8_exact2(const uint4 (&w)[8], uint4 d4p, uint4 x0, uint4 x1, uint32_t head,
+                                              const uint4 (&w2)[8], uint4 d4p2, uint4 y0, uint4 y1, uint32_t head2,
+                                              bool has2, int lane) {
+    const float d8 = h2f(head), c4 = -4.0f * h2f(head >> 16);
+    const float e8 = h2f(head2), e4 = -4.0f * h2f(head2 >> 16);
+    float acc[8][2];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        int f0, f1, g0, g1;
+        fragment_dots(w[q], x0, x1, f0, f1);
+        fragment_dots(w2[q], y0, y1, g0, g1);
+        const uint32_t da = (&d4p.x)[q >> 1] >> (16 * (q & 1)), db = (&d4p2.x)[q >> 1] >> (16 * (q & 1));
+        const float a4 = h2f(da), b4 = h2f(db);
+        const float a0 = fmaf(a4, fmaf(static_cast<float>(f0), d8, c4), 0.0f);
+        const float a1 = fmaf(a4, fmaf(static_cast<float>(f1), d8, c4), 0.0f);
+        const float s0 = fmaf(b4, fmaf(static_cast<float>(g0), e8, e4), a0);
+        const float s1 = fmaf(b4, fmaf(static_cast<float>(g1), e8, e4), a1);
+        acc[q][0] = has2 ? s0 : a0;
+        acc[q][1] = has2 ? s1 : a1;
+    }
+    return fold_rows8(acc, lane);
+}
+
 // One Q8_1 block from 32 lanes (lane32 = element index).  Semantics of the
 // reference GPU quantizer (src/hip/linear.hip:121-149): a nonfinite element
 // poisons its block (bit 1), an unrepresentable scale/sum/code sets bit 2,

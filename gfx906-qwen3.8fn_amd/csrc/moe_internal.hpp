@@ -139,8 +139,8 @@ struct DecodeArgs {
     float *y;                  // [tokens][H]
     const void *x_q8;          // canonical Q8_1 [tokens][H/32] used instead of x, or nullptr
 };
-inline constexpr int kDecodeMaxBlocksH = 64;   // H/32 <= 64: one block per lane
-inline constexpr int kDecodeMaxBlocksI = 16;   // I/32 <= 16: 16 lanes per down row
+inline constexpr int kDecodeMaxBlocksH = 128;  // H/32 <= 128: one or two blocks per lane
+inline constexpr int kDecodeMaxBlocksI = 32;   // I/32 <= 32: 16 lanes per down row, one or two blocks each
 inline constexpr int kDecodeMaxPairs = 16;     // k + has_shared <= 16: one wave per rank in the fold
 // gate/up + SiLU + Q8 (quantizes each token's x on the fly; rank 0 / slice 0
 // also writes the token's x Q8 planes for debugging).

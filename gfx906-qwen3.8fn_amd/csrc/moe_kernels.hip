@@ -905,9 +905,11 @@ __device__ __forceinline__ int decode_route(const DecodeArgs &d, int t, int r, i
 // kernels) while the weight loads are in flight.
 // Q8In: the token rows come as canonical Q8_1 blocks (d.x_q8) and waves 0-3
 // copy them into LDS instead of quantizing x.  Full: H/32 == 64, every lane
-// holds a block.
-template<bool Q8In, bool Full>
-__global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
+// holds a block.  Two: H/32 in 65..128 (the reference model's 2560: 80
+// blocks), lane j holds blocks j and j + 64, and all 8 waves take part in
+// quantizing the row.
+template<bool Q8In, bool Full, bool Two>
+__global__ __launch_bounds__(512, Two ? 4 : 8) void k_decode_gate_up(DecodeArgs d) {
     __shared__ uint32_t xs[kDecodeMaxBlocksH * 8];   // Q8 codes of the token, [blocks][32 B]
     __shared__ uint32_t xh[kDecodeMaxBlocksH];       // heads
     __shared__ float gu[2][32];
@@ -934,7 +936,7 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
     // block 16w + l % 16, elements 8 * (l / 16) .. +7).  They issue their x
     // loads before their weight loads, so waiting for x never waits behind
     // the weights.
-    const bool quant_wave = wave < 4;
+    const bool quant_wave = Two || wave < 4;
     const int qblk = wave * 16 + (lane & 15), qpart = lane >> 4;
     float xv[8];
     uint2 qin = make_uint2(0u, 0u);   // Q8In: codes 8 * qpart .. +7 of block qblk
@@ -970,6 +972,16 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) w[q] = buffer_load16(wr, lane_off, q * row_bytes);
     const uint4 d4p = buffer_load16(sr, lane_off, 0);
+    // Two: the lane's second block, lane + 64 (block 0 when past the row end).
+    const bool has2 = Two && lane + 64 < nbh;
+    const uint32_t lane_off2 = has2 ? static_cast<uint32_t>(lane + 64) * 16u : 0u;
+    uint4 w2[8];
+    uint4 d4p2 = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (Two) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) w2[q] = buffer_load16(wr, lane_off2, q * row_bytes);
+        d4p2 = buffer_load16(sr, lane_off2, 0);
+    }
     if (Q8In && quant_wave && qblk < nbh) {
         reinterpret_cast<uint2 *>(xs)[qblk * 4 + qpart] = qin;
         if (qpart == 0) xh[qblk] = qhead;
@@ -998,7 +1010,15 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
     __syncthreads();
     const uint4 x0 = reinterpret_cast<const uint4 *>(xs)[kb * 2];
     const uint4 x1 = reinterpret_cast<const uint4 *>(xs)[kb * 2 + 1];
-    const float v = rows8_exact<Full>(w, d4p, x0, x1, xh[kb], has, lane);
+    float v;
+    if constexpr (Two) {
+        const int kb2 = has2 ? lane + 64 : 0;
+        const uint4 y0 = reinterpret_cast<const uint4 *>(xs)[kb2 * 2];
+        const uint4 y1 = reinterpret_cast<const uint4 *>(xs)[kb2 * 2 + 1];
+        v = rows8_exact2(w, d4p, x0, x1, xh[kb], w2, d4p2, y0, y1, xh[kb2], has2, lane);
+    } else {
+        v = rows8_exact<Full>(w, d4p, x0, x1, xh[kb], has, lane);
+    }
     const int rho = 4 * ((lane >> 5) & 1) + 2 * (lane & 1) + ((lane >> 1) & 1);
     if ((lane & 28) == 0) gu[mat][(wave & 3) * 8 + rho] = v;
     __syncthreads();
@@ -1023,7 +1043,11 @@ __global__ __launch_bounds__(512, 8) void k_decode_gate_up(DecodeArgs d) {
 // k_down_lean), then 32 threads fold the ranks in order and add the shared
 // expert -- the separately rounded fold of k_fold, with no contribution
 // buffer and no second kernel.  Q41: Q4_1 down blocks.
-template<bool Q41>
+// Two: I/32 in 17..32 (the reference model's 640: 20 blocks); lane kl also
+// takes block kl + 16.  The reference's fold pairs blocks k and k ^ 16 last,
+// so the row is (tree over blocks 0..15) + (tree over blocks 16..31), each
+// tree as rows8_down_exact sums it.
+template<bool Q41, bool Two>
 __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
     __shared__ float part[kDecodeMaxPairs][32];
     __shared__ int valid[kDecodeMaxPairs];
@@ -1066,7 +1090,25 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
         const uint4 x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
         const uint4 x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
         const uint32_t hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
-        const float v = rows8_down_exact<Q41>(w, d4p, m4p, x0, x1, hx, has, lane);
+        float v = rows8_down_exact<Q41>(w, d4p, m4p, x0, x1, hx, has, lane);
+        if constexpr (Two) {
+            const bool has2 = kl + 16 < nbi;
+            const int kb2 = has2 ? kl + 16 : 0;
+            const uint32_t lane_off2 = static_cast<uint32_t>(sub * nbi + kb2) * 16u;
+            uint4 w2[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) w2[l] = buffer_load16(wr, lane_off2, 4 * l * row_bytes);
+            const uint4 d4p2 = buffer_load16(sr, static_cast<uint32_t>(kb2 * 32 + sub * 8) * 2u, 0);
+            uint4 m4p2 = make_uint4(0u, 0u, 0u, 0u);
+            if constexpr (Q41) {
+                const auto mr = buffer_rsrc(a.bank.down_mins + mrow * nbi, 4 * row_bytes);
+                m4p2 = buffer_load16(mr, static_cast<uint32_t>(kb2 * 32 + sub * 8) * 2u, 0);
+            }
+            const uint4 y0 = buffer_load16(xr, static_cast<uint32_t>(kb2) * 32u, 0);
+            const uint4 y1 = buffer_load16(xr, static_cast<uint32_t>(kb2) * 32u, 16);
+            const uint32_t hy = buffer_load4(hr, static_cast<uint32_t>(kb2) * 4u, 0);
+            v = v + rows8_down_exact<Q41>(w2, d4p2, m4p2, y0, y1, hy, has2, lane);
+        }
         const int lr = 4 * (lane & 1) + 2 * ((lane >> 1) & 1) + ((lane >> 2) & 1);
         if ((lane & 8) == 0) part[r][4 * lr + sub] = v;
     }
@@ -1479,13 +1521,15 @@ hipError_t launch_decode_gate_up(const DecodeArgs &d, hipStream_t s) {
     const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0);
     const unsigned groups = static_cast<unsigned>((sh.I / 32 + 7) / 8);
     const unsigned grid = 8u * groups * P1 * d.f.tokens;
-    const bool full = sh.H == 2048;
+    const bool full = sh.H == 2048, two = sh.H > 2048;
     if (d.x_q8) {
-        if (full) k_decode_gate_up<true, true><<<grid, 512, 0, s>>>(d);
-        else k_decode_gate_up<true, false><<<grid, 512, 0, s>>>(d);
+        if (two) k_decode_gate_up<true, false, true><<<grid, 512, 0, s>>>(d);
+        else if (full) k_decode_gate_up<true, true, false><<<grid, 512, 0, s>>>(d);
+        else k_decode_gate_up<true, false, false><<<grid, 512, 0, s>>>(d);
     } else {
-        if (full) k_decode_gate_up<false, true><<<grid, 512, 0, s>>>(d);
-        else k_decode_gate_up<false, false><<<grid, 512, 0, s>>>(d);
+        if (two) k_decode_gate_up<false, false, true><<<grid, 512, 0, s>>>(d);
+        else if (full) k_decode_gate_up<false, true, false><<<grid, 512, 0, s>>>(d);
+        else k_decode_gate_up<false, false, false><<<grid, 512, 0, s>>>(d);
     }
     return hipGetLastError();
 }
@@ -1495,8 +1539,14 @@ hipError_t launch_decode_down_fold(const DecodeArgs &d, hipStream_t s) {
     const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0);
     const unsigned groups = static_cast<unsigned>((sh.H / 32 + 7) / 8);
     const dim3 grid(8u * groups * d.f.tokens), block(64 * P1);
-    if (d.f.bank.down_mins) k_decode_down_fold<true><<<grid, block, 0, s>>>(d);
-    else k_decode_down_fold<false><<<grid, block, 0, s>>>(d);
+    const bool two = sh.I > 512;
+    if (d.f.bank.down_mins) {
+        if (two) k_decode_down_fold<true, true><<<grid, block, 0, s>>>(d);
+        else k_decode_down_fold<true, false><<<grid, block, 0, s>>>(d);
+    } else {
+        if (two) k_decode_down_fold<false, true><<<grid, block, 0, s>>>(d);
+        else k_decode_down_fold<false, false><<<grid, block, 0, s>>>(d);
+    }
     return hipGetLastError();
 }
 

@@ -170,6 +170,25 @@ def test_q41_decode_layer_bit_exact(q41_layer, gate):
     assert int(host(err)[0]) == 0
 
 
+def test_q41_decode_reference_shape_bit_exact():
+    """The reference model's own expert shape, hidden 2560 / intermediate 640
+    with Q4_1 down matrices (its layers 0-5), on the decode kernels (two
+    blocks per lane in gate/up and in down): 8 tokens, top-4 of 16 + shared,
+    bit-identical to the oracle."""
+    H2, I2, E, K = 2560, 640, 16, 4
+    bank = W.q4_bank(E, hidden=H2, intermediate=I2, seed=761, down_type=Q41)
+    shared = W.q4_bank(1, hidden=H2, intermediate=I2, seed=762, down_type=Q41)
+    x = W.activations(8, hidden=H2, seed=763)
+    ids, w = W.routes_uniform(8, experts=E, k=K, seed=764)
+    g = np.random.default_rng(765).standard_normal(8).astype(np.float32)
+    L = _layer_env({"MOE_FFN_DECODE": 1}, H2, I2, E, K, True, 8, experts_q4=bank, shared_q4=shared, down_type=Q41)
+    y, err = L.forward(dev(x), dev(ids), dev(w), shared_gate=dev(g))
+    ref = O.moe_layer(x, H2, I2, E, bank, ids, w, shared_q4=shared, shared_gate=g, down_q41=True)
+    assert np.array_equal(host(y).view(np.uint32), ref["y"].view(np.uint32))
+    assert int(host(err)[0]) == 0
+    L.close()
+
+
 def test_q41_grouped_layer_bit_exact(q41_layer):
     """300 Zipf(1.3) tokens on the grouped path (every group on the streaming
     kernels, which Q4_1 layers use at every size): 32 sampled tokens bit-
