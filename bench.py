@@ -249,6 +249,23 @@ def reference_components():
         if int(err.cpu()[0]) != 0:
             raise RuntimeError("reference-shape expert flagged an error")
     L.close()
+    # B8 decode at this shape, Q4_1 downs (the checkpoint's layers 0-5):
+    # 512 experts + shared, top-10, 64 rotated route sets.
+    L = moe_ffn.MoeLayer(H, I, 512, 10, True, 8, synthetic_seed=4104, down_type=moe_ffn.DOWN_Q4_1)
+    sets = [tuple(torch.from_numpy(a).to(dev0) for a in W.routes_uniform(8, seed=4105 + r)) for r in range(64)]
+    x = torch.from_numpy(W.activations(8, hidden=H, seed=4106)).to(dev0)
+    y = torch.empty((8, H), dtype=torch.float32, device=dev0)
+    err = torch.zeros(1, dtype=torch.int32, device=dev0)
+    step = [0]
+
+    def b8():
+        ids, w = sets[step[0] % 64]
+        step[0] += 1
+        L.forward(x, ids, w, y=y, error=err)
+    out["b8_decode_q4_1_us"] = time_calls(b8, iters=64) * 1e6
+    if int(err.cpu()[0]) != 0:
+        raise RuntimeError("reference-shape B8 layer flagged an error")
+    L.close()
     rng = np.random.default_rng(4102)
     mats = {("q4_0", H, I): W.q4_blocks(I * H // 32, rng).reshape(-1),
             ("q4_0", I, H): W.q4_blocks(H * I // 32, rng).reshape(-1),

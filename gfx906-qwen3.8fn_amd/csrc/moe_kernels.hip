@@ -981,6 +981,9 @@ __global__ __launch_bounds__(512, Two ? 4 : 8) void k_decode_gate_up(DecodeArgs 
 #pragma unroll
         for (int q = 0; q < 8; ++q) w2[q] = buffer_load16(wr, lane_off2, q * row_bytes);
         d4p2 = buffer_load16(sr, lane_off2, 0);
+        // Every load is issued before the quantisation waits on x (the
+        // scheduler would otherwise sink half of them behind that wait).
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (Q8In && quant_wave && qblk < nbh) {
         reinterpret_cast<uint2 *>(xs)[qblk * 4 + qpart] = qin;

@@ -449,14 +449,16 @@ int moe_ffn_export_expert(moe_ffn_layer *L, int expert, void *host_q4) {
 namespace {
 // The ungrouped decode path: shapes its kernels cover, and (in auto mode)
 // few enough routes per expert that re-reading an expert shared by two tokens
-// costs less than grouping (tokens * k <= E / 4).
+// costs less than grouping (tokens * k <= E / 4), or few routes in all
+// (tokens * k <= 16: a single expert's first 16 tokens, whose re-reads hit L2).
 bool use_decode(const moe_ffn_layer *L, int tokens) {
     const Shape &sh = L->shape;
     const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0);
     const bool fits = sh.H / 32 <= moe::kDecodeMaxBlocksH && sh.I / 32 <= moe::kDecodeMaxBlocksI &&
                       P1 <= moe::kDecodeMaxPairs;
     if (!fits || L->decode_mode == 0) return false;
-    return L->decode_mode == 1 || static_cast<long>(tokens) * sh.k * 4 <= sh.E;
+    const long routes = static_cast<long>(tokens) * sh.k;
+    return L->decode_mode == 1 || routes * 4 <= sh.E || routes <= 16;
 }
 
 int run_stage(moe_ffn_layer *L, int stage, const float *x, const int32_t *ids, const float *weights, int tokens,
