@@ -620,9 +620,10 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
 // CU: each wave keeps its 8 weight rows (8 KB) in flight with a small register
 // footprint, so 4 workgroups (32 waves, 256 KB of loads) fit on a CU.  Grid =
 // item bound x I/32 slices; same arithmetic and outputs as k_gate_up_stream.
-// Full: H/32 == 64, every lane holds a block.
-template<bool Full, bool Dbg>
-__global__ __launch_bounds__(512, 3) void k_gate_up_lean(FfnArgs a) {
+// Full: H/32 == 64, every lane holds a block.  Two: H/32 in 65..128, lane
+// j also holds block j + 64 (rows8_exact2, the reference lane's FMA chain).
+template<bool Full, bool Two, bool Dbg>
+__global__ __launch_bounds__(512, Two ? 2 : 3) void k_gate_up_lean(FfnArgs a) {
     constexpr int T = kStreamTokens;
     __shared__ float gu[2][32][T];
     // The wave index is uniform: as a scalar it keeps row bases in SGPRs.
@@ -665,35 +666,61 @@ __global__ __launch_bounds__(512, 3) void k_gate_up_lean(FfnArgs a) {
 #pragma unroll
     for (int r = 0; r < 8; ++r) w[r] = buffer_load16(wr, lane_off, r * row_bytes);
     const uint4 d4p = buffer_load16(sr, lane_off, 0);
-    // A token's activations are loaded while the previous token computes.
+    const bool has2 = Two && lane + 64 < nbh;
+    const uint32_t lane_off2 = has2 ? static_cast<uint32_t>(lane + 64) * 16u : 0u;
+    uint4 w2[8];
+    uint4 d4p2 = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (Two) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) w2[r] = buffer_load16(wr, lane_off2, r * row_bytes);
+        d4p2 = buffer_load16(sr, lane_off2, 0);
+    }
+    // A token's activations (the lane's one or two blocks) are loaded while
+    // the previous token computes.
     const int toks[T] = {tok.x, tok.y, tok.z, tok.w};
-    auto load_x = [&](int j, uint4 &x0, uint4 &x1, uint32_t &hx) {
+    struct Xb {
+        uint4 x0, x1, y0, y1;
+        uint32_t hx, hy;
+    };
+    auto load_x = [&](int j, Xb &b) {
         const size_t xrow = static_cast<size_t>(toks[j < ncols ? j : 0]) * nbh;
         const auto xr = buffer_rsrc(a.xq.codes + xrow * 32, static_cast<uint32_t>(nbh) * 32u);
         const auto hr = buffer_rsrc(a.xq.heads + xrow, static_cast<uint32_t>(nbh) * 4u);
-        x0 = buffer_load16(xr, 2 * lane_off, 0);
-        x1 = buffer_load16(xr, 2 * lane_off, 16);
-        hx = buffer_load4(hr, lane_off / 4, 0);
+        b.x0 = buffer_load16(xr, 2 * lane_off, 0);
+        b.x1 = buffer_load16(xr, 2 * lane_off, 16);
+        b.hx = buffer_load4(hr, lane_off / 4, 0);
+        if constexpr (Two) {
+            b.y0 = buffer_load16(xr, 2 * lane_off2, 0);
+            b.y1 = buffer_load16(xr, 2 * lane_off2, 16);
+            b.hy = buffer_load4(hr, lane_off2 / 4, 0);
+        }
     };
-    uint4 x0, x1;
-    uint32_t hx;
-    load_x(0, x0, x1, hx);
+    Xb cur;
+    load_x(0, cur);
 #pragma unroll
     for (int j = 0; j < T; ++j) {
         if (j < ncols) {   // uniform per workgroup
-            uint4 n0 = x0, n1 = x1;
-            uint32_t nh = hx;
-            if (j + 1 < T && j + 1 < ncols) load_x(j + 1, n0, n1, nh);
+            Xb nxt = cur;
+            if (j + 1 < T && j + 1 < ncols) load_x(j + 1, nxt);
             if constexpr (Dbg) {
                 int32_t *dots = mat ? a.up_dots : a.gate_dots;
                 if (dots && has)
 #pragma unroll
                     for (int r = 0; r < 8; ++r)
-                        dots[(static_cast<size_t>(first + j) * I + row0 + r) * nbh + lane] = dot_block(w[r], x0, x1);
+                        dots[(static_cast<size_t>(first + j) * I + row0 + r) * nbh + lane] = dot_block(w[r], cur.x0, cur.x1);
+                if (Two && dots && has2)
+#pragma unroll
+                    for (int r = 0; r < 8; ++r)
+                        dots[(static_cast<size_t>(first + j) * I + row0 + r) * nbh + lane + 64] =
+                            dot_block(w2[r], cur.y0, cur.y1);
             }
-            const float v = rows8_exact<Full>(w, d4p, x0, x1, hx, has, lane);
+            float v;
+            if constexpr (Two)
+                v = rows8_exact2(w, d4p, cur.x0, cur.x1, cur.hx, w2, d4p2, cur.y0, cur.y1, cur.hy, has2, lane);
+            else
+                v = rows8_exact<Full>(w, d4p, cur.x0, cur.x1, cur.hx, has, lane);
             if ((lane & 28) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
-            x0 = n0; x1 = n1; hx = nh;
+            cur = nxt;
         }
     }
     __syncthreads();
@@ -800,8 +827,11 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
 // scatter (src/hip/session_ops.hip:357-373).
 // NBI = 16 specialises I = 512 (every lane holds a block); NBI = 0 reads
 // I/32 <= 16 at run time.  Q41: Q4_1 blocks (mins plane in the scales' order).
-template<int NBI, bool Q41, bool Dbg>
-__global__ __launch_bounds__(128, 4) void k_down_lean(FfnArgs a) {
+// Two: I/32 in 17..32, lane kl also holds block kl + 16; the row is (tree over
+// blocks 0..15) + (tree over blocks 16..31), the last stage of the reference's
+// fold.
+template<int NBI, bool Q41, bool Two, bool Dbg>
+__global__ __launch_bounds__(128, Two ? 2 : 4) void k_down_lean(FfnArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = NBI ? NBI : a.shape.I / 32;
     // Workgroup id = item * H/64 + slice (one XCD per slice, as in
@@ -839,43 +869,66 @@ __global__ __launch_bounds__(128, 4) void k_down_lean(FfnArgs a) {
     for (int l = 0; l < 8; ++l) w[l] = buffer_load16(wr, lane_off, 4 * l * row_bytes);
     const uint4 d4p = buffer_load16(sr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
     uint4 m4p = make_uint4(0u, 0u, 0u, 0u);
-    if constexpr (Q41) {
-        const auto mr = buffer_rsrc(a.bank.down_mins + mrow * nbi, 4 * row_bytes);
-        m4p = buffer_load16(mr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
+    const auto mr = buffer_rsrc(Q41 ? a.bank.down_mins + mrow * nbi : a.bank.down_scales, 4 * row_bytes);
+    if constexpr (Q41) m4p = buffer_load16(mr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
+    const bool has2 = Two && kl + 16 < nbi;
+    const int kb2 = has2 ? kl + 16 : 0;
+    uint4 w2[8];
+    uint4 d4p2 = make_uint4(0u, 0u, 0u, 0u), m4p2 = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (Two) {
+        const uint32_t lane_off2 = static_cast<uint32_t>(sub * nbi + kb2) * 16u;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) w2[l] = buffer_load16(wr, lane_off2, 4 * l * row_bytes);
+        d4p2 = buffer_load16(sr, static_cast<uint32_t>(kb2 * 32 + sub * 8) * 2u, 0);
+        if constexpr (Q41) m4p2 = buffer_load16(mr, static_cast<uint32_t>(kb2 * 32 + sub * 8) * 2u, 0);
     }
-    // A pair's middle row is loaded while the previous pair computes.
-    auto load_x = [&](int j, uint4 &x0, uint4 &x1, uint32_t &hx) {
+    // A pair's middle row (the lane's one or two blocks) is loaded while the
+    // previous pair computes.
+    struct Xb {
+        uint4 x0, x1, y0, y1;
+        uint32_t hx, hy;
+    };
+    auto load_x = [&](int j, Xb &b) {
         const size_t xrow = static_cast<size_t>(first + (j < ncols ? j : 0)) * nbi;
         const auto xr = buffer_rsrc(a.mq.codes + xrow * 32, static_cast<uint32_t>(nbi) * 32u);
         const auto hr = buffer_rsrc(a.mq.heads + xrow, static_cast<uint32_t>(nbi) * 4u);
-        x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
-        x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
-        hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
+        b.x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
+        b.x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
+        b.hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
+        if constexpr (Two) {
+            b.y0 = buffer_load16(xr, static_cast<uint32_t>(kb2) * 32u, 0);
+            b.y1 = buffer_load16(xr, static_cast<uint32_t>(kb2) * 32u, 16);
+            b.hy = buffer_load4(hr, static_cast<uint32_t>(kb2) * 4u, 0);
+        }
     };
     const int toks[kStreamTokens] = {tok.x, tok.y, tok.z, tok.w};
     const int rnks[kStreamTokens] = {rnk.x, rnk.y, rnk.z, rnk.w};
-    uint4 x0, x1;
-    uint32_t hx;
-    load_x(0, x0, x1, hx);
+    Xb cur;
+    load_x(0, cur);
 #pragma unroll
     for (int j = 0; j < kStreamTokens; ++j) {
         if (j < ncols) {   // uniform per workgroup
-            uint4 n0 = x0, n1 = x1;
-            uint32_t nh = hx;
-            if (j + 1 < kStreamTokens && j + 1 < ncols) load_x(j + 1, n0, n1, nh);
+            Xb nxt = cur;
+            if (j + 1 < kStreamTokens && j + 1 < ncols) load_x(j + 1, nxt);
             if constexpr (Dbg) {
                 if (a.down_dots && has)
 #pragma unroll
                     for (int l = 0; l < 8; ++l)
                         a.down_dots[(static_cast<size_t>(first + j) * H + row0 + 4 * l + sub) * nbi + kl] =
-                            dot_block(w[l], x0, x1);
+                            dot_block(w[l], cur.x0, cur.x1);
+                if (Two && a.down_dots && has2)
+#pragma unroll
+                    for (int l = 0; l < 8; ++l)
+                        a.down_dots[(static_cast<size_t>(first + j) * H + row0 + 4 * l + sub) * nbi + kl + 16] =
+                            dot_block(w2[l], cur.y0, cur.y1);
             }
-            const float v = rows8_down_exact<Q41>(w, d4p, m4p, x0, x1, hx, has, lane);
+            float v = rows8_down_exact<Q41>(w, d4p, m4p, cur.x0, cur.x1, cur.hx, has, lane);
+            if constexpr (Two) v = v + rows8_down_exact<Q41>(w2, d4p2, m4p2, cur.y0, cur.y1, cur.hy, has2, lane);
             if ((lane & 8) == 0) {
                 const size_t orow = static_cast<size_t>(toks[j]) * a.out_stride_k + rnks[j];
                 a.out[orow * H + row0 + 4 * lr + sub] = v;
             }
-            x0 = n0; x1 = n1; hx = nh;
+            cur = nxt;
         }
     }
 }
@@ -1506,14 +1559,16 @@ hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s) {
     const bool dbg = a.middle_f32 || a.gate_dots || a.up_dots;
     const unsigned grid = stream_grid(a, a.shape.I / 32);
     const int nbl = (a.shape.H / 32 + 63) / 64;
-    if (nbl <= 1) {
+    if (nbl <= 2) {
         // One unit per workgroup; grid = item bound x slices, extra items exit.
         const unsigned lgrid = stream_item_bound(a) * static_cast<unsigned>(a.shape.I / 32);
-        if (dbg) k_gate_up_lean<false, true><<<lgrid, 512, 0, s>>>(a);
-        else if (a.shape.H == 2048) k_gate_up_lean<true, false><<<lgrid, 512, 0, s>>>(a);
-        else k_gate_up_lean<false, false><<<lgrid, 512, 0, s>>>(a);
-    } else if (nbl <= 2) gate_up_stream<2>(a, dbg, grid, s);
-    else gate_up_stream<0>(a, dbg, grid, s);
+        if (nbl == 2) {
+            if (dbg) k_gate_up_lean<false, true, true><<<lgrid, 512, 0, s>>>(a);
+            else k_gate_up_lean<false, true, false><<<lgrid, 512, 0, s>>>(a);
+        } else if (dbg) k_gate_up_lean<false, false, true><<<lgrid, 512, 0, s>>>(a);
+        else if (a.shape.H == 2048) k_gate_up_lean<true, false, false><<<lgrid, 512, 0, s>>>(a);
+        else k_gate_up_lean<false, false, false><<<lgrid, 512, 0, s>>>(a);
+    } else gate_up_stream<0>(a, dbg, grid, s);
     return hipGetLastError();
 }
 
@@ -1568,13 +1623,22 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
     if (nbi <= 16) {
         const unsigned g = stream_item_bound(a) * static_cast<unsigned>(a.shape.H / 64);
         if (q41) {
-            if (dbg) k_down_lean<0, true, true><<<g, 128, 0, s>>>(a);
-            else if (nbi == 16) k_down_lean<16, true, false><<<g, 128, 0, s>>>(a);
-            else k_down_lean<0, true, false><<<g, 128, 0, s>>>(a);
+            if (dbg) k_down_lean<0, true, false, true><<<g, 128, 0, s>>>(a);
+            else if (nbi == 16) k_down_lean<16, true, false, false><<<g, 128, 0, s>>>(a);
+            else k_down_lean<0, true, false, false><<<g, 128, 0, s>>>(a);
         } else {
-            if (dbg) k_down_lean<0, false, true><<<g, 128, 0, s>>>(a);
-            else if (nbi == 16) k_down_lean<16, false, false><<<g, 128, 0, s>>>(a);
-            else k_down_lean<0, false, false><<<g, 128, 0, s>>>(a);
+            if (dbg) k_down_lean<0, false, false, true><<<g, 128, 0, s>>>(a);
+            else if (nbi == 16) k_down_lean<16, false, false, false><<<g, 128, 0, s>>>(a);
+            else k_down_lean<0, false, false, false><<<g, 128, 0, s>>>(a);
+        }
+    } else if (nbi <= 32) {
+        const unsigned g = stream_item_bound(a) * static_cast<unsigned>(a.shape.H / 64);
+        if (q41) {
+            if (dbg) k_down_lean<0, true, true, true><<<g, 128, 0, s>>>(a);
+            else k_down_lean<0, true, true, false><<<g, 128, 0, s>>>(a);
+        } else {
+            if (dbg) k_down_lean<0, false, true, true><<<g, 128, 0, s>>>(a);
+            else k_down_lean<0, false, true, false><<<g, 128, 0, s>>>(a);
         }
     } else if (q41) {
         if (dbg) k_down_stream<64, true, true><<<grid, 512, 0, s>>>(a);

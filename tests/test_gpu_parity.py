@@ -177,8 +177,10 @@ def test_reference_shape_expert_vs_golden():
     assert np.array_equal(host(r["gate_dots"]), O.block_dots(g, 2560, 640, xq))
     assert np.array_equal(host(r["middle"]).view(np.uint32), f["middle"].view(np.uint32))
     assert np.array_equal(host(r["middle_q8"]).reshape(-1), f["middle_q8"].reshape(-1))
+    # I = 640: the lean down kernel with two blocks per lane, also in the
+    # reference's order: the output is the reference's, bit for bit.
     y = layer.expert_down(0, r["middle_q8"], 3, path=moe_ffn.PATH_STREAM)["y"]
-    assert_close(host(y), f["y"], what="expert vs reference cpu_expert")
+    assert np.array_equal(host(y).view(np.uint32), f["y"].view(np.uint32))
     layer.close()
 
 
