@@ -42,6 +42,13 @@ struct moe_ffn_layer {
     // 1032-token Zipf(1.3) 0.76 / 0.75 / 0.75, 256 tokens 0.34 / 0.32 / 0.31;
     // 16K uniform (all groups above 256) 6.4 either way.
     int mfma_min = 32;
+    // Batches of fewer routes (tokens x k) stream every group: below this the
+    // MFMA items are too few to fill the chip and the streaming kernels win
+    // (single-expert and 8-expert layers at 2048/512 and 2560/640: MFMA ahead
+    // from about 1024 routes, streaming up to 3x ahead below 256).  An explicit
+    // MOE_FFN_MFMA_MIN turns this off; MOE_FFN_MFMA_ROUTES sets it.
+    int mfma_routes = 1024;
+    int active_mfma_min = 32;   // mfma_min of the current / last forward
     int decode_mode = -1; // ungrouped decode path: -1 auto, 0 never, 1 whenever shapes allow
     bool last_decode = false;
     int cu_count = 256;   // compute units of the device
@@ -160,10 +167,15 @@ int finish_create(moe_ffn_layer *L) {
     L->routes.wprefix = reinterpret_cast<uint32_t *>(b + w.wprefix);
     L->contrib = reinterpret_cast<float *>(b + w.contrib);
     if (hipMemset(L->ws_mem, 0, w.total) != hipSuccess) return hipErrorOutOfMemory;
-    if (const char *env = std::getenv("MOE_FFN_MFMA_MIN")) L->mfma_min = std::atoi(env);
-    // Q4_1 down matrices have streaming kernels only, and the two item kinds
-    // are shared by gate/up and down: every group streams.
-    if (L->down_q41) L->mfma_min = 0;
+    if (const char *env = std::getenv("MOE_FFN_MFMA_MIN")) {
+        L->mfma_min = std::atoi(env);
+        L->mfma_routes = 0;
+    }
+    if (const char *env = std::getenv("MOE_FFN_MFMA_ROUTES")) L->mfma_routes = std::atoi(env);
+    // Q4_1 down matrices: MFMA items run gate/up on MFMA and their down on
+    // the lean kernel (k_down_lean_items, rows of up to 32 blocks); wider
+    // rows stream every group.
+    if (L->down_q41 && L->shape.I / 32 > 32) L->mfma_min = 0;
     if (const char *env = std::getenv("MOE_FFN_DECODE")) L->decode_mode = std::atoi(env) ? 1 : 0;
     if (const char *env = std::getenv("MOE_FFN_STREAMS")) L->two_streams = std::atoi(env) != 1;
     int cus = 0;
@@ -329,7 +341,7 @@ moe::FfnArgs base_args(moe_ffn_layer *L, int tokens, int *error) {
     a.out_stride_k = L->shape.k + 1;
     a.tokens = tokens;
     a.pairs_bound = static_cast<int>(pairs_capacity(L->shape, tokens));
-    a.mfma_min = L->mfma_min;
+    a.mfma_min = L->active_mfma_min;
     a.error = error;
     a.cu_count = L->cu_count;
     return a;
@@ -475,21 +487,21 @@ int run_stage(moe_ffn_layer *L, int stage, const float *x, const int32_t *ids, c
     switch (stage) {
     case MOE_STAGE_PREPARE:
         if (L->x_q8_in) {   // grouping only, then the given Q8 rows into the activation planes
-            if ((r = moe::launch_prepare(nullptr, ids, weights, tokens, sh, L->xq, L->routes, L->mfma_min, error, s)) !=
+            if ((r = moe::launch_prepare(nullptr, ids, weights, tokens, sh, L->xq, L->routes, L->active_mfma_min, error, s)) !=
                 hipSuccess)
                 return r;
             return moe::launch_canonical_to_planes(L->x_q8_in, L->xq, tokens * (sh.H / 32), s);
         }
-        return moe::launch_prepare(x, ids, weights, tokens, sh, L->xq, L->routes, L->mfma_min, error, s);
+        return moe::launch_prepare(x, ids, weights, tokens, sh, L->xq, L->routes, L->active_mfma_min, error, s);
     // With mfma_min == 1 every nonempty group is an MFMA item and the
     // streaming launch would only start empty workgroups.
     case MOE_STAGE_GATE_UP:
-        if (L->mfma_min != 1 && (r = moe::launch_gate_up(a, false, s)) != hipSuccess) return r;
-        if (L->mfma_min > 0) r = moe::launch_gate_up(a, true, s);
+        if (a.mfma_min != 1 && (r = moe::launch_gate_up(a, false, s)) != hipSuccess) return r;
+        if (a.mfma_min > 0) r = moe::launch_gate_up(a, true, s);
         return r;
     case MOE_STAGE_DOWN:
-        if (L->mfma_min != 1 && (r = moe::launch_down(a, false, s)) != hipSuccess) return r;
-        if (L->mfma_min > 0) r = moe::launch_down(a, true, s);
+        if (a.mfma_min != 1 && (r = moe::launch_down(a, false, s)) != hipSuccess) return r;
+        if (a.mfma_min > 0) r = moe::launch_down(a, true, s);
         return r;
     case MOE_STAGE_FOLD: {
         const size_t stride = static_cast<size_t>(sh.k + 1) * sh.H;
@@ -513,9 +525,10 @@ int forward_impl(moe_ffn_layer *L, const float *x, const void *x_q8, const int32
     L->x_q8_in = x_q8;
     const auto s = static_cast<hipStream_t>(stream);
     const bool decode = use_decode(L, tokens);
+    L->active_mfma_min = static_cast<long>(tokens) * L->shape.k < L->mfma_routes ? 0 : L->mfma_min;
     hipEvent_t *marks = nullptr;
     if (L->prof_used < L->prof_capacity) marks = L->prof_events + (L->prof_used++) * moe_ffn_layer::kStageMarks;
-    if (!decode && !marks && L->two_streams && L->mfma_min >= 2) {
+    if (!decode && !marks && L->two_streams && L->active_mfma_min >= 2) {
         // Both item kinds can exist: streaming chain on the side stream, MFMA
         // chain here, joined before the fold (the two chains touch disjoint
         // middle and contribution rows).
@@ -703,7 +716,7 @@ int moe_ffn_debug_last(moe_ffn_layer *L, void *x_q8, void *middle_q8, int32_t *r
     if (L->last_decode) {
         // The decode path does not group: group the same routes now (the last
         // inputs must still be valid) and reorder its middle rows to match.
-        if ((r = moe::launch_prepare(nullptr, L->last_ids, L->last_weights, N, sh, L->xq, L->routes, L->mfma_min,
+        if ((r = moe::launch_prepare(nullptr, L->last_ids, L->last_weights, N, sh, L->xq, L->routes, L->active_mfma_min,
                                      L->last_error, s)) != hipSuccess)
             return r;
         if (middle_q8 && (r = moe::launch_decode_middle_grouped(L->mq, L->routes, sh, N, middle_q8, s)) != hipSuccess)
@@ -726,7 +739,7 @@ int moe_ffn_last_stats(moe_ffn_layer *L, int32_t *stream_items, int32_t *mfma_it
     if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
     if (L->last_decode && L->last_tokens > 0) {   // group the last batch's routes (not done by the decode path)
         const hipError_t g = moe::launch_prepare(nullptr, L->last_ids, L->last_weights, L->last_tokens, L->shape,
-                                                 L->xq, L->routes, L->mfma_min, L->last_error, nullptr);
+                                                 L->xq, L->routes, L->active_mfma_min, L->last_error, nullptr);
         if (g != hipSuccess) return g;
     }
     const hipError_t r = hipMemcpy(c, L->routes.item_counts, sizeof(c), hipMemcpyDeviceToHost);

@@ -190,9 +190,11 @@ def test_q41_decode_reference_shape_bit_exact():
 
 
 def test_q41_grouped_layer_bit_exact(q41_layer):
-    """300 Zipf(1.3) tokens on the grouped path (every group on the streaming
-    kernels, which Q4_1 layers use at every size): 32 sampled tokens bit-
-    identical to the oracle; a 5-token prefix batch gives the same bits."""
+    """300 Zipf(1.3) tokens on the grouped path: groups of >= 32 pairs run
+    gate/up on int8 MFMA and their Q4_1 down on the lean kernel over MFMA
+    items, smaller groups stream; every kernel keeps the reference's order,
+    so 32 sampled tokens are bit-identical to the oracle, and a 5-token
+    prefix batch gives the same bits."""
     L, E = q41_layer["layer"], q41_layer["E"]
     x = W.activations(300, seed=741)
     ids, w = W.routes_zipf(300, 1.3, experts=E, seed=742)
@@ -200,7 +202,7 @@ def test_q41_grouped_layer_bit_exact(q41_layer):
     yh = host(y)
     assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
     st = L.last_stats()
-    assert st["mfma_items"] == 0 and st["stream_items"] > 0
+    assert st["mfma_items"] > 0 and st["stream_items"] > 0
     sample = np.random.default_rng(743).choice(300, 32, replace=False)
     mask = np.zeros(300, np.uint8)
     mask[sample] = 1
@@ -245,3 +247,32 @@ def test_q41_tensors_and_synthetic_banks():
         assert int(host(err)[0]) == 0, what
     L.close()
     S.close()
+
+
+def test_q41_small_batch_route_gate():
+    """Batches of fewer than 1024 routes stream every group (few MFMA items
+    cannot fill the chip); MOE_FFN_MFMA_ROUTES=0 lifts the gate.  A single
+    2560/640 expert with 128 tokens (one 128-pair group) gives the same bits
+    either way: the MFMA gate/up and the lean down over MFMA items keep the
+    streaming kernels' order.  Sampled tokens match the oracle bit for bit."""
+    H2, I2, N = 2560, 640, 128
+    bank = W.q4_bank(1, hidden=H2, intermediate=I2, seed=761, down_type=Q41)
+    x = W.activations(N, hidden=H2, seed=762)
+    ids = np.zeros((N, 1), np.int32)
+    w = np.ones((N, 1), np.float32)
+    out = {}
+    for env in ({}, {"MOE_FFN_MFMA_ROUTES": 0}):
+        L = _layer_env(dict(env, MOE_FFN_DECODE=0), H2, I2, 1, 1, False, N, experts_q4=bank, down_type=Q41)
+        y, err = L.forward(dev(x), dev(ids), dev(w))
+        st = L.last_stats()
+        out[bool(env)] = (host(y).copy(), st)
+        assert int(host(err)[0]) == 0
+        L.close()
+    assert out[False][1]["mfma_items"] == 0 and out[False][1]["stream_items"] > 0
+    assert out[True][1]["mfma_items"] == 1 and out[True][1]["stream_items"] == 0
+    assert np.array_equal(out[False][0].view(np.uint32), out[True][0].view(np.uint32))
+    sample = np.array([0, 1, 63, 64, 127])
+    mask = np.zeros(N, np.uint8)
+    mask[sample] = 1
+    ref = O.moe_layer(x, H2, I2, 1, bank, ids, w, token_mask=mask, down_q41=True)
+    assert np.array_equal(out[False][0][sample].view(np.uint32), ref["y"][sample].view(np.uint32))
