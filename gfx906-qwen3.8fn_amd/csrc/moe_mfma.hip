@@ -852,17 +852,36 @@ __global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
         uint4 wa[kDnMaxBlocks];
 #pragma unroll
         for (int b = 0; b < kDnMaxBlocks; ++b) wa[b] = buffer_load16(wr, w_off, static_cast<uint32_t>(b < nbi ? b : 0) * 16u);
-        // Middle codes and heads of the item's pairs (zero past ncols).
+        // Middle codes and heads of the item's pairs, every load issued
+        // before the first LDS write.  Thread t keeps one (block, half) of the
+        // code rows, block (t % 32) / 2 and half t % 2, for pairs t / 32 + 8 i,
+        // and one block of the heads, t % 16, for pairs t / 16 + 16 i.  The
+        // descriptors end at the item's last pair: pairs past ncols read zero.
+        static_assert(kMfmaTile == 128 && kDnMaxBlocks == 16, "staging map: 256 threads, 128 pairs, 16 blocks");
         const int cols = nsub * kSub;
-        for (int c = threadIdx.x; c < cols * nbi * 2; c += blockDim.x) {
-            const int j = c / (2 * nbi), rem = c % (2 * nbi), b = rem >> 1, hf = rem & 1;
-            st.x[b][j][hf] = j < ncols ? *reinterpret_cast<const uint4 *>(a.mq.codes + (static_cast<size_t>(first + j) * nbi + b) * 32 + 16 * hf)
-                                       : make_uint4(0, 0, 0, 0);
-        }
-        for (int c = threadIdx.x; c < cols * nbi; c += blockDim.x) {
-            const int j = c / nbi, b = c % nbi;
-            st.hd[b][j] = j < ncols ? a.mq.heads[static_cast<size_t>(first + j) * nbi + b] : 0u;
-        }
+        const uint32_t pair_bytes = static_cast<uint32_t>(nbi) * 32u;
+        const auto xr = buffer_rsrc(a.mq.codes + static_cast<size_t>(first) * pair_bytes,
+                                    static_cast<uint32_t>(ncols) * pair_bytes);
+        const auto hr = buffer_rsrc(a.mq.heads + static_cast<size_t>(first) * nbi,
+                                    static_cast<uint32_t>(ncols * nbi) * 4u);
+        const int tid = static_cast<int>(threadIdx.x);
+        const int xb = (tid & 31) >> 1, xh = tid & 1, xj = tid >> 5, hb = tid & 15, hj = tid >> 4;
+        const uint32_t x_off = static_cast<uint32_t>(xj) * pair_bytes + static_cast<uint32_t>(32 * xb + 16 * xh);
+        const uint32_t h_off = static_cast<uint32_t>(hj * nbi + hb) * 4u;
+        uint4 xv[kMfmaTile / 8];
+        uint32_t hv[kMfmaTile / 16];
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 8; ++i)
+            if (8 * i < cols && xb < nbi) xv[i] = buffer_load16(xr, x_off, 8u * i * pair_bytes);
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 16; ++i)
+            if (16 * i < cols && hb < nbi) hv[i] = buffer_load4(hr, h_off, 64u * i * static_cast<uint32_t>(nbi));
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 8; ++i)
+            if (8 * i < cols && xb < nbi) st.x[xb][xj + 8 * i][xh] = xv[i];
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 16; ++i)
+            if (16 * i < cols && hb < nbi) st.hd[hb][hj + 16 * i] = hv[i];
         if (active)
             for (int c = lane; c < nbi * 4; c += 64)
                 st.d4[wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(scales)[c];
