@@ -1013,17 +1013,21 @@ __global__ __launch_bounds__(128, Two ? 2 : 4) void k_down_lean_items(FfnArgs a)
 // Route (t, r) of a decode batch, validated as RouteGroups::prepare does
 // (src/routes.cpp:145-157): returns the expert (E = shared for r == k) or -1
 // for a bad id or a duplicate of an earlier rank.  `flags` gets bit 1 for a
-// bad id, a duplicate, or a negative / nonfinite weight.
+// bad id, a duplicate, or a negative / nonfinite weight.  Every lane of the
+// wave calls it with the same (t, r): lane j < k reads id j of the row, so
+// the row arrives in one round trip and the duplicate test is a ballot, not
+// a chain of dependent loads in front of the weight address.
 __device__ __forceinline__ int decode_route(const DecodeArgs &d, int t, int r, int &flags) {
     const int k = d.f.shape.k, E = d.f.shape.E;
     if (r == k) return E;
-    const int32_t *row = d.ids + static_cast<size_t>(t) * k;
-    const int e = row[r];
-    const float w = d.weights[static_cast<size_t>(t) * k + r];
+    const int lane = threadIdx.x & 63;
+    const size_t base = static_cast<size_t>(t) * k;
+    const int mine = lane < k ? d.ids[base + lane] : -1;
+    const float w = d.weights[base + r];
+    const int e = __builtin_amdgcn_readlane(mine, r);
     if (!isfinite(w) || w < 0.0f) flags |= 1;
-    bool ok = e >= 0 && e < E;
-    for (int q = 0; q < r; ++q) ok = ok && row[q] != e;
-    if (!ok) { flags |= 1; return -1; }
+    const bool dup = __builtin_amdgcn_ballot_w64(lane < r && mine == e) != 0;
+    if (e < 0 || e >= E || dup) { flags |= 1; return -1; }
     return e;
 }
 
@@ -1183,6 +1187,7 @@ template<bool Q41, bool Two>
 __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
     __shared__ float part[kDecodeMaxPairs][32];
     __shared__ int valid[kDecodeMaxPairs];
+    __shared__ float wt[kDecodeMaxPairs];   // the token's routing weights, then its shared gate
     const FfnArgs &a = d.f;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = a.shape.I / 32, k = a.shape.k;
@@ -1195,6 +1200,10 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
     const int t = j % N, slice = (id & 7) + 8 * (j / N);
     if (slice >= S) return;
     const int row0 = slice * 32, r = wave;
+    // The fold's operands into LDS now: after the barrier it reads no
+    // global memory (the weights were one dependent round trip per rank).
+    if (threadIdx.x < static_cast<unsigned>(k)) wt[threadIdx.x] = d.weights[static_cast<size_t>(t) * k + threadIdx.x];
+    if (threadIdx.x == static_cast<unsigned>(k) && P1 > k && d.shared_gate) wt[k] = d.shared_gate[t];
     int dummy = 0;
     const int expert = decode_route(d, t, r, dummy);
     if (lane == 0) valid[r] = expert >= 0;
@@ -1247,7 +1256,6 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
     __syncthreads();
     if (threadIdx.x < 32) {
         const int row = threadIdx.x;
-        const float *wt = d.weights + static_cast<size_t>(t) * k;
         int flags = 0;
         float v = 0.0f;
         for (int q = 0; q < k; ++q) {
@@ -1266,7 +1274,7 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
             if (!isfinite(x)) { flags |= 1; x = 0.0f; }
             float scale = 1.0f;
             if (d.shared_gate) {
-                float g = d.shared_gate[t];
+                float g = wt[k];
                 if (!isfinite(g)) { flags |= 1; g = 0.0f; }
                 scale = 1.0f / (1.0f + moe_expf(-g));
                 if (!isfinite(scale)) { flags |= 2; scale = 0.0f; }
