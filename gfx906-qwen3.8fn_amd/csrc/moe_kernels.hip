@@ -357,24 +357,62 @@ __global__ __launch_bounds__(1024) void k_prepare_small(GroupParams p, const flo
 // Validates entry (t, r) (src/routes.cpp:145-157) and returns its expert, or
 // -1 when it cannot be grouped (bad id, duplicate of an earlier rank); bad
 // ids, duplicates and negative or nonfinite weights set flag bit 1.
-__device__ __forceinline__ int staged_entry(const int32_t *sid, const float *weights, int t, int tl, int r,
-                                            int k, int E, int &flags) {
+__device__ __forceinline__ int staged_entry(const int32_t *sid, int tl, int r, int k, int E, int &flags) {
     const int e = sid[tl * k + r];
-    const float w = weights[static_cast<size_t>(t) * k + r];
-    if (!isfinite(w) || w < 0.0f) flags |= 1;
     if (e < 0 || e >= E) { flags |= 1; return -1; }
     for (int q = 0; q < r; ++q)
         if (sid[tl * k + q] == e) { flags |= 1; return -1; }
     return e;
 }
 
+// The ids of tokens t0 .. t0 + 255 into LDS: up to 16 rounds with every
+// load issued before the first LDS write (a strided loop would wait for each
+// load in turn), a plain loop for the rest (k > 16).
 __device__ void stage_ids(const GroupParams &p, int t0, int32_t *sid) {
     const int k = p.shape.k;
     const int n = min(256, p.tokens - t0) * k;
     const int32_t *src = p.ids + static_cast<size_t>(t0) * k;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) sid[i] = src[i];
+    constexpr int kRounds = 16;
+    const int step = static_cast<int>(blockDim.x);
+    int v[kRounds];
+#pragma unroll
+    for (int u = 0; u < kRounds; ++u) {
+        const int i = static_cast<int>(threadIdx.x) + u * step;
+        if (i < n) v[u] = src[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kRounds; ++u) {
+        const int i = static_cast<int>(threadIdx.x) + u * step;
+        if (i < n) sid[i] = v[u];
+    }
+    for (int i = static_cast<int>(threadIdx.x) + kRounds * step; i < n; i += step) sid[i] = src[i];
     __syncthreads();
 }
+
+// Bit 1 for a negative or nonfinite routing weight of tokens t0 .. t0 + 255,
+// each weight read once, coalesced, with the loads issued together.
+__device__ int weight_flags(const GroupParams &p, int t0) {
+    const int k = p.shape.k;
+    const int n = min(256, p.tokens - t0) * k;
+    const float *src = p.weights + static_cast<size_t>(t0) * k;
+    constexpr int kRounds = 16;
+    const int step = static_cast<int>(blockDim.x);
+    int flags = 0;
+    for (int i0 = 0; i0 < n; i0 += kRounds * step) {
+        float v[kRounds];
+#pragma unroll
+        for (int u = 0; u < kRounds; ++u) {
+            const int i = i0 + static_cast<int>(threadIdx.x) + u * step;
+            v[u] = i < n ? src[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kRounds; ++u)
+            if (!isfinite(v[u]) || v[u] < 0.0f) flags |= 1;
+    }
+    return flags;
+}
+
+constexpr int kQuantPer = 8;   // quantized elements per thread in k_mark_quantize
 
 // Step 1: blocks [0, mark_blocks) set bitmap bits (one thread per token),
 // the rest quantize x.  The bitmap is [W][Ep] (word-major) so the
@@ -387,25 +425,38 @@ __global__ __launch_bounds__(256) void k_mark_quantize(GroupParams p, int mark_b
         int32_t *sid = reinterpret_cast<int32_t *>(lds);
         const int t0 = blockIdx.x * 256;
         stage_ids(p, t0, sid);
+        int flags = weight_flags(p, t0);
         const int t = t0 + threadIdx.x;
-        if (t >= p.tokens) return;
-        int flags = 0;
-        for (int r = 0; r < p.shape.k; ++r) {
-            const int e = staged_entry(sid, p.weights, t, threadIdx.x, r, p.shape.k, p.shape.E, flags);
-            if (e >= 0) atomicOr(&p.r.bitmap[static_cast<size_t>(t >> 5) * p.shape.Ep + e], 1u << (t & 31));
-        }
+        if (t < p.tokens)
+            for (int r = 0; r < p.shape.k; ++r) {
+                const int e = staged_entry(sid, threadIdx.x, r, p.shape.k, p.shape.E, flags);
+                if (e >= 0) atomicOr(&p.r.bitmap[static_cast<size_t>(t >> 5) * p.shape.Ep + e], 1u << (t & 31));
+            }
         if (flags) atomicOr(p.error, flags);
         return;
     }
-    const size_t i = static_cast<size_t>(blockIdx.x - mark_blocks) * blockDim.x + threadIdx.x;
-    if (i >= q_elements) return;
-    const Q8Lane q = quantize32(x[i]);
-    const size_t block = i >> 5;
-    const int lane = static_cast<int>(i & 31);
-    xq.codes[block * 32 + lane] = static_cast<uint8_t>(q.code);
-    if (lane == 0) {
-        xq.heads[block] = q.head;
-        if (q.flags) atomicOr(p.error, q.flags);
+    // kQuantPer elements per thread, 256 apart (a workgroup quantizes 2048
+    // consecutive floats); loads first.  q_elements is a multiple of 32, so
+    // the bound check keeps or drops whole 32-lane blocks.
+    const size_t i0 = static_cast<size_t>(blockIdx.x - mark_blocks) * (256 * kQuantPer) + threadIdx.x;
+    float v[kQuantPer];
+#pragma unroll
+    for (int u = 0; u < kQuantPer; ++u) {
+        const size_t i = i0 + 256 * u;
+        v[u] = i < q_elements ? x[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kQuantPer; ++u) {
+        const size_t i = i0 + 256 * u;
+        if (i >= q_elements) break;   // uniform per 32-lane block
+        const Q8Lane q = quantize32(v[u]);
+        const size_t block = i >> 5;
+        const int lane = static_cast<int>(i & 31);
+        xq.codes[block * 32 + lane] = static_cast<uint8_t>(q.code);
+        if (lane == 0) {
+            xq.heads[block] = q.head;
+            if (q.flags) atomicOr(p.error, q.flags);
+        }
     }
 }
 
@@ -460,7 +511,7 @@ __global__ __launch_bounds__(256) void k_scatter_pairs(GroupParams p) {
     const int k = p.shape.k, E = p.shape.E, Ep = p.shape.Ep;
     for (int r = 0; r < k; ++r) {
         int dummy = 0;
-        const int e = staged_entry(sid, p.weights, t, threadIdx.x, r, k, E, dummy);
+        const int e = staged_entry(sid, threadIdx.x, r, k, E, dummy);
         int pos = -1;
         if (e >= 0) {
             const size_t wi = static_cast<size_t>(t >> 5) * Ep + e;
@@ -1589,7 +1640,8 @@ hipError_t launch_prepare(const float *x, const int32_t *ids, const float *weigh
     if (e != hipSuccess) return e;
     const int mark_blocks = static_cast<int>(blocks_for(static_cast<size_t>(tokens), 256));
     const size_t id_lds = static_cast<size_t>(256) * shape.k * 4;
-    k_mark_quantize<<<mark_blocks + blocks_for(q_elements, 256), 256, id_lds, s>>>(p, mark_blocks, x, xq, q_elements);
+    k_mark_quantize<<<mark_blocks + blocks_for(q_elements, 256 * kQuantPer), 256, id_lds, s>>>(p, mark_blocks, x, xq,
+                                                                                           q_elements);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     k_word_prefix<<<blocks_for(static_cast<size_t>(shape.E), 4), 256, 0, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
