@@ -11,6 +11,7 @@
 #include "moe_device.hpp"
 
 #include <algorithm>
+#include <climits>
 
 #pragma clang fp contract(off)
 
@@ -673,10 +674,12 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
 // item bound x I/32 slices; same arithmetic and outputs as k_gate_up_stream.
 // Full: H/32 == 64, every lane holds a block.  Two: H/32 in 65..128, lane
 // j also holds block j + 64 (rows8_exact2, the reference lane's FMA chain).
+// One unit (item, slice) of k_gate_up_lean; false once the item is past the
+// stream item count (which it stores in `count`).
 template<bool Full, bool Two, bool Dbg>
-__global__ __launch_bounds__(512, Two ? 2 : 3) void k_gate_up_lean(FfnArgs a) {
+__device__ __forceinline__ bool gate_up_lean_unit(const FfnArgs &a, int uid, int &count,
+                                                  float (&gu)[2][32][kStreamTokens]) {
     constexpr int T = kStreamTokens;
-    __shared__ float gu[2][32][T];
     // The wave index is uniform: as a scalar it keeps row bases in SGPRs.
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t expf_word = expf_table_word(lane);
@@ -685,15 +688,16 @@ __global__ __launch_bounds__(512, Two ? 2 : 3) void k_gate_up_lean(FfnArgs a) {
     // slice stays on one XCD (id % 8), so consecutive items of one expert
     // find its rows in that XCD's L2.
     const int S = I / 32;
-    const int item = static_cast<int>(blockIdx.x) / S, s = static_cast<int>(blockIdx.x) % S;
+    const int item = uid / S, s = uid % S;
     // Item header, its tokens and the item count are independent loads
-    // (the item array is sized for the grid), issued together.
+    // (the item is below the grid's item bound, or below the count the
+    // workgroup's previous unit read), issued together.
     const int4 hdr = *reinterpret_cast<const int4 *>(a.routes.stream_items + item);
     const int4 tok = *reinterpret_cast<const int4 *>(a.routes.stream_items[item].token);
-    const int count = a.routes.item_counts[0];
+    count = a.routes.item_counts[0];
     // Keeps the compiler from deferring the item loads behind the count check.
     asm volatile("" ::"s"(hdr.x), "s"(hdr.y), "s"(hdr.z), "s"(tok.x), "s"(tok.y), "s"(tok.z), "s"(tok.w), "s"(count));
-    if (item >= count) return;   // uniform per workgroup
+    if (item >= count) return false;   // uniform per workgroup
     const int expert = hdr.x, first = hdr.y, ncols = hdr.z;
     const int mat = wave >> 2;
     const int row0 = s * 32 + (wave & 3) * 8;
@@ -790,6 +794,20 @@ __global__ __launch_bounds__(512, Two ? 2 : 3) void k_gate_up_lean(FfnArgs a) {
             if (f) atomicOr(a.error, f);
         }
     }
+    __syncthreads();   // gu is free for the workgroup's next unit
+    return true;
+}
+
+// Units id, id + grid, ...: the grid is capped (kLeanGridCap), a multiple of
+// 8 and of I/32, so a workgroup keeps its XCD and slice and a batch with no
+// streaming items starts few workgroups.
+template<bool Full, bool Two, bool Dbg>
+__global__ __launch_bounds__(512, Two ? 2 : 3) void k_gate_up_lean(FfnArgs a) {
+    __shared__ float gu[2][32][kStreamTokens];
+    const int S = a.shape.I / 32;
+    int count = INT_MAX;
+    for (int u = static_cast<int>(blockIdx.x); u / S < count; u += static_cast<int>(gridDim.x))
+        if (!gate_up_lean_unit<Full, Two, Dbg>(a, u, count, gu)) break;
 }
 
 // Down projection, streaming path.  Work unit = (item, slice of 64 output
@@ -881,21 +899,22 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
 // Two: I/32 in 17..32, lane kl also holds block kl + 16; the row is (tree over
 // blocks 0..15) + (tree over blocks 16..31), the last stage of the reference's
 // fold.
+// One unit (item, slice of 64 rows) of k_down_lean; false once the item is
+// past the stream item count (stored in `count`).
 template<int NBI, bool Q41, bool Two, bool Dbg>
-__global__ __launch_bounds__(128, Two ? 2 : 4) void k_down_lean(FfnArgs a) {
+__device__ __forceinline__ bool down_lean_unit(const FfnArgs &a, int uid, int &count) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = NBI ? NBI : a.shape.I / 32;
-    // Workgroup id = item * H/64 + slice (one XCD per slice, as in
-    // k_gate_up_lean).
+    // Unit id = item * H/64 + slice (one XCD per slice, as in k_gate_up_lean).
     const int S = H / 64;
-    const int item = static_cast<int>(blockIdx.x) / S, slice = static_cast<int>(blockIdx.x) % S;
+    const int item = uid / S, slice = uid % S;
     const int4 hdr = *reinterpret_cast<const int4 *>(a.routes.stream_items + item);
     const int4 tok = *reinterpret_cast<const int4 *>(a.routes.stream_items[item].token);
     const int4 rnk = *reinterpret_cast<const int4 *>(a.routes.stream_items[item].rank);
-    const int count = a.routes.item_counts[0];
+    count = a.routes.item_counts[0];
     asm volatile("" ::"s"(hdr.x), "s"(hdr.y), "s"(hdr.z), "s"(tok.x), "s"(tok.y), "s"(tok.z), "s"(tok.w),
                  "s"(rnk.x), "s"(rnk.y), "s"(rnk.z), "s"(rnk.w), "s"(count));
-    if (item >= count) return;   // uniform per workgroup
+    if (item >= count) return false;   // uniform per workgroup
     const int expert = hdr.x, first = hdr.y, ncols = hdr.z;
     const int row0 = slice * 64 + wave * 32;
     const int sub = lane >> 4, kl = lane & 15;
@@ -982,6 +1001,17 @@ __global__ __launch_bounds__(128, Two ? 2 : 4) void k_down_lean(FfnArgs a) {
             cur = nxt;
         }
     }
+    return true;
+}
+
+// Units id, id + grid, ... over a capped grid (a multiple of 8 and of H/64,
+// as in k_gate_up_lean).
+template<int NBI, bool Q41, bool Two, bool Dbg>
+__global__ __launch_bounds__(128, Two ? 2 : 4) void k_down_lean(FfnArgs a) {
+    const int S = a.shape.H / 64;
+    int count = INT_MAX;
+    for (int u = static_cast<int>(blockIdx.x); u / S < count; u += static_cast<int>(gridDim.x))
+        if (!down_lean_unit<NBI, Q41, Two, Dbg>(a, u, count)) break;
 }
 
 // Down projection of the MFMA items (groups of >= mfma_min pairs, <= 128
@@ -1677,6 +1707,23 @@ unsigned stream_item_bound(const FfnArgs &a) {
     return static_cast<unsigned>(std::max<size_t>(b, 1));
 }
 
+// Grid of a lean streaming launch (k_gate_up_lean, k_down_lean): one
+// workgroup per unit of the item bound, capped at kLeanGridCap rounded down to
+// a multiple of 8 x slices (the kernels loop over units id, id + grid, ...).
+// The bound holds for any grouping, so a batch whose groups all go to MFMA
+// would otherwise start up to ~10^5 workgroups that find no item.  Measured
+// per layer (2048/512, 512 experts), cap 8192 / 16384 / 32768 / none, us:
+// 1032 uniform tokens 1160 / 1125 / 1090 / 1105, 1032 Zipf(1.3) 680 / 684 /
+// 705 / 755, 4K Zipf(1.1) 1867 / 1856 / 1867 / 1926, 16K uniform 5338 /
+// 5334 / 5338 / 5436.
+constexpr unsigned kLeanGridCap = 16384;
+unsigned lean_grid(unsigned item_bound, unsigned slices) {
+    const size_t units = static_cast<size_t>(item_bound) * slices;
+    const unsigned step = 8u * slices;
+    const unsigned cap = std::max(step, kLeanGridCap / step * step);
+    return units < cap ? static_cast<unsigned>(units) : cap;
+}
+
 unsigned stream_grid(const FfnArgs &a, int slices) {
     // The persistent loop covers whatever the device produced.
     const size_t units = static_cast<size_t>(stream_item_bound(a)) * slices;
@@ -1697,7 +1744,7 @@ hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s) {
     const int nbl = (a.shape.H / 32 + 63) / 64;
     if (nbl <= 2) {
         // One unit per workgroup; grid = item bound x slices, extra items exit.
-        const unsigned lgrid = stream_item_bound(a) * static_cast<unsigned>(a.shape.I / 32);
+        const unsigned lgrid = lean_grid(stream_item_bound(a), static_cast<unsigned>(a.shape.I / 32));
         if (nbl == 2) {
             if (dbg) k_gate_up_lean<false, true, true><<<lgrid, 512, 0, s>>>(a);
             else k_gate_up_lean<false, true, false><<<lgrid, 512, 0, s>>>(a);
@@ -1768,7 +1815,7 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
     const unsigned grid = stream_grid(a, a.shape.H / 64);
     const bool dbg = a.down_dots != nullptr, q41 = a.bank.down_mins != nullptr;
     if (nbi <= 16) {
-        const unsigned g = stream_item_bound(a) * static_cast<unsigned>(a.shape.H / 64);
+        const unsigned g = lean_grid(stream_item_bound(a), static_cast<unsigned>(a.shape.H / 64));
         if (q41) {
             if (dbg) k_down_lean<0, true, false, true><<<g, 128, 0, s>>>(a);
             else if (nbi == 16) k_down_lean<16, true, false, false><<<g, 128, 0, s>>>(a);
@@ -1779,7 +1826,7 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
             else k_down_lean<0, false, false, false><<<g, 128, 0, s>>>(a);
         }
     } else if (nbi <= 32) {
-        const unsigned g = stream_item_bound(a) * static_cast<unsigned>(a.shape.H / 64);
+        const unsigned g = lean_grid(stream_item_bound(a), static_cast<unsigned>(a.shape.H / 64));
         if (q41) {
             if (dbg) k_down_lean<0, true, true, true><<<g, 128, 0, s>>>(a);
             else k_down_lean<0, true, true, false><<<g, 128, 0, s>>>(a);
