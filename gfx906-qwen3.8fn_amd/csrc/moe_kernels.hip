@@ -510,18 +510,35 @@ __global__ __launch_bounds__(256) void k_scatter_pairs(GroupParams p) {
     const int t = t0 + threadIdx.x;
     if (t >= p.tokens) return;
     const int k = p.shape.k, E = p.shape.E, Ep = p.shape.Ep;
-    for (int r = 0; r < k; ++r) {
-        int dummy = 0;
-        const int e = staged_entry(sid, threadIdx.x, r, k, E, dummy);
-        int pos = -1;
-        if (e >= 0) {
-            const size_t wi = static_cast<size_t>(t >> 5) * Ep + e;
-            pos = p.r.offsets[e] + static_cast<int>(p.r.wprefix[wi]) +
-                  __popc(p.r.bitmap[wi] & ((1u << (t & 31)) - 1u));
-            p.r.pair_token[pos] = t;
-            p.r.pair_rank[pos] = r;
+    // Ranks in chunks of kChunk: the chunk's offset, prefix and bitmap loads
+    // are issued before any is used (one round trip per chunk, not per rank).
+    constexpr int kChunk = 8;
+    for (int r0 = 0; r0 < k; r0 += kChunk) {
+        int ev[kChunk], off[kChunk];
+        uint32_t pre[kChunk], bits[kChunk];
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            int dummy = 0;
+            ev[u] = r0 + u < k ? staged_entry(sid, threadIdx.x, r0 + u, k, E, dummy) : -1;
+            if (ev[u] >= 0) {
+                const size_t wi = static_cast<size_t>(t >> 5) * Ep + ev[u];
+                off[u] = p.r.offsets[ev[u]];
+                pre[u] = p.r.wprefix[wi];
+                bits[u] = p.r.bitmap[wi];
+            }
         }
-        p.r.pos_of[static_cast<size_t>(t) * k + r] = pos;
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            const int r = r0 + u;
+            if (r >= k) break;
+            int pos = -1;
+            if (ev[u] >= 0) {
+                pos = off[u] + static_cast<int>(pre[u]) + __popc(bits[u] & ((1u << (t & 31)) - 1u));
+                p.r.pair_token[pos] = t;
+                p.r.pair_rank[pos] = r;
+            }
+            p.r.pos_of[static_cast<size_t>(t) * k + r] = pos;
+        }
     }
     if (Ep > E) {
         const int s = p.r.offsets[E] + t;
