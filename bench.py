@@ -3,8 +3,12 @@
 A "step" is one MoE layer forward (quantize + group + gate/up/SiLU/Q8 + down +
 rank-order fold + shared expert) over one batch of synthetic tokens with all
 inputs resident in HBM.  The headline workload is BASELINE configs[1], B8
-decode (8 tokens, top-10 of 512 experts + 1 shared, H 2048, I 512).  Reported
-alongside: the 4K Zipf(1.1) prefill layer (configs[2], "prefill_4k"), the 16K
+decode (8 tokens, top-10 of 512 experts + 1 shared, H 2048, I 512), measured
+cold: step i runs layer i % 48 of 48 resident layers with their own weights
+(43.5 GB, far past the 256 MB Infinity Cache) on route set i % 64, so no step
+finds its weights in any cache.  The same rotation over ONE layer's bank is
+reported as "b8_decode_warm" (consecutive route sets share experts, so part
+of a step can hit the Infinity Cache).  Reported alongside: the 4K Zipf(1.1) prefill layer (configs[2], "prefill_4k"), the 16K
 uniform prefill layer (configs[3], "prefill_16k"), the 48-layer stack of 8 + 1024
 tokens with Zipf(1.3) routing (configs[4], "stack_48"), and the practical HBM
 ceiling at the decode gate/up kernel's byte count ("read_ceiling": a plain
@@ -35,21 +39,23 @@ def log(*a):
 
 
 def time_forward(layer, x, sets, steps, warmup):
-    """Wall and GPU-event time per forward; step i uses route set i % len(sets),
-    so consecutive steps touch different experts (weights are not left hot in
-    the 256 MB Infinity Cache by a repeated identical step)."""
+    """Wall and GPU-event time per forward; step i uses route set i % len(sets)
+    and, when `layer` is a list of layers, layer i % len(layer) (each with its
+    own resident weights, so a rotation over many layers reads every step's
+    weights from HBM)."""
     import torch
-    y = torch.empty((x.shape[0], layer.H), dtype=torch.float32, device=x.device)
+    layers = layer if isinstance(layer, (list, tuple)) else [layer]
+    y = torch.empty((x.shape[0], layers[0].H), dtype=torch.float32, device=x.device)
     err = torch.zeros(1, dtype=torch.int32, device=x.device)
     for i in range(warmup):
-        layer.forward(x, *sets[i % len(sets)], y=y, error=err)
+        layers[i % len(layers)].forward(x, *sets[i % len(sets)], y=y, error=err)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
     for i in range(steps):
-        layer.forward(x, *sets[i % len(sets)], y=y, error=err)
+        layers[i % len(layers)].forward(x, *sets[i % len(sets)], y=y, error=err)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
@@ -65,22 +71,31 @@ def time_stages(layer, x, sets, steps):
     stream before the first and after every stage; read once at the end.
     Returns the summed seconds per stage."""
     import torch
-    y = torch.empty((x.shape[0], layer.H), dtype=torch.float32, device=x.device)
+    layers = layer if isinstance(layer, (list, tuple)) else [layer]
+    y = torch.empty((x.shape[0], layers[0].H), dtype=torch.float32, device=x.device)
     err = torch.zeros(1, dtype=torch.int32, device=x.device)
-    layer.profile(steps)
+    per = -(-steps // len(layers))
+    for L in layers:
+        L.profile(per)
     for i in range(steps):
-        layer.forward(x, *sets[i % len(sets)], y=y, error=err)
-    total, n = layer.profile_read()
-    layer.profile(0)
-    assert n == steps
-    return np.array(total)
+        layers[i % len(layers)].forward(x, *sets[i % len(sets)], y=y, error=err)
+    total, count = np.zeros(4), 0
+    for L in layers:
+        t, n = L.profile_read()
+        L.profile(0)
+        total += np.array(t)
+        count += n
+    assert count == steps
+    if int(err.cpu()[0]) != 0:
+        raise RuntimeError(f"error flags {int(err.cpu()[0])}")
+    return total
 
 
-def pmc_traffic(kernel, units):
+def pmc_traffic(kernel, units, record="pmc_b8_decode.json"):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc record
     (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a 1 GiB copy calibration),
     at `units` expert units per launch; None when no record exists."""
-    path = os.path.join(ROOT, "profiles", "pmc_b8_decode.json")
+    path = os.path.join(ROOT, "profiles", record)
     try:
         rec = json.load(open(path))["kernels"][kernel]
     except (OSError, KeyError, ValueError):
@@ -282,15 +297,25 @@ def reference_components():
     return out
 
 
-def cpu_baseline(x, bank, shared, ids, w, target_seconds):
+def cpu_baseline(x, bank, shared, ids, w, target_seconds, workers):
+    """Seconds per B8 layer of the oracle's pinned pool with `workers` workers
+    (one per allowed physical core), repeated for about target_seconds."""
     import oracle as O
-    cpus = O.physical_cpus()
-    workers = max(1, min(16, len(cpus)))
     sec, used, _ = O.baseline_layer(x, 2048, 512, 512, bank, ids, w, shared_q4=shared, workers=workers, repeats=2)
     repeats = max(3, int(target_seconds / max(sec, 1e-6)))
     sec, used, _ = O.baseline_layer(x, 2048, 512, 512, bank, ids, w, shared_q4=shared, workers=workers,
                                     repeats=repeats)
     return sec, used, repeats
+
+
+def sparse_bank(layer, experts):
+    """Canonical host bank of `layer` with only `experts` exported from the
+    device (the others left zero: a layer forward reads only routed experts)."""
+    eb = layer.export_expert(0).size
+    bank = np.zeros(layer.E * eb, np.uint8)
+    for e in sorted(set(int(e) for e in np.asarray(experts).reshape(-1))):
+        bank[e * eb:(e + 1) * eb] = layer.export_expert(e)
+    return bank
 
 
 def main():
@@ -308,6 +333,8 @@ def main():
     ap.add_argument("--no-linear", action="store_true", help="skip the quantized linear projections")
     ap.add_argument("--no-graph", action="store_true", help="skip the graph-captured stack passes")
     ap.add_argument("--no-refshapes", action="store_true", help="skip the reference's component shapes (2560/640)")
+    ap.add_argument("--only", choices=["b8", "4k", "16k", "stack"],
+                    help="run one section alone (for profiler runs); the JSON line then holds that section only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy x5 (FETCH_SIZE/WRITE_SIZE scale for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -329,73 +356,101 @@ def main():
     import workloads as W
 
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
-    log("[bench] generating Q4_0 bank (512 experts + shared)")
-    bank = W.q4_bank(512, seed=1000)
-    shared = W.q4_bank(1, seed=1001)
-    max_tokens = 8 if args.no_prefill else 4096 if args.no_16k else 16384
-    layer = moe_ffn.MoeLayer(2048, 512, 512, 10, True, max_tokens, experts_q4=bank, shared_q4=shared)
+    only = args.only
+    want = lambda section: only is None or only == section
+    if only is not None:
+        args.no_cpu = args.no_linear = args.no_refshapes = True
+        args.no_prefill = only not in ("4k", "16k")
+        args.no_16k = only != "16k"
+        args.no_stack = only != "stack"
+    NL, NS = 48, 8 + 1024
+    result = {}
+    layers = []
+    if want("b8") or want("stack"):
+        # ---- resident layers: 48 with their own synthetic weights (configs[4]'s
+        # stack, also the cold rotation of the B8 headline) ------------------
+        log(f"[bench] creating {NL} resident layers (synthetic Q4_0, 512 experts + shared each)")
+        layers = [moe_ffn.MoeLayer(2048, 512, 512, 10, True, NS, synthetic_seed=5000 + l) for l in range(NL)]
 
-    # ---- B8 decode (headline) -------------------------------------------
-    N, R = 8, 64
-    xh = W.activations(N, seed=1002)
-    route_sets = [W.routes_uniform(N, seed=1003 + r) for r in range(R)]
-    x = dev(xh)
-    sets = [(dev(i), dev(w)) for i, w in route_sets]
-    touched = np.array([W.group_histogram(i)["touched"] for i, _ in route_sets])
-    log(f"[bench] b8 decode: {R} route sets, touched experts mean {touched.mean():.1f} "
-        f"(min {touched.min()}, max {touched.max()})")
-    wall, gpu, _ = time_forward(layer, x, sets, args.steps, args.warmup)
-    stats = layer.last_stats()
-    # Stage durations over the same rotation; step i touched[i % R] + 1 units.
-    n_stage = max(R, args.steps)
-    t_stage = time_stages(layer, x, sets, n_stage)
-    units = touched[np.arange(n_stage) % R] + 1
-    gate_bytes = float(np.sum(units)) * GATE_UP_BYTES_PER_EXPERT
-    down_bytes = float(np.sum(units)) * DOWN_BYTES_PER_EXPERT
-    t_prep, t_gate, t_down, t_fold = (t_stage / n_stage).tolist()
-    achieved = gate_bytes / float(t_stage[1]) / 1e9
-    layer_bytes = float(np.mean([W.algorithmic_bytes(N, int(t)) for t in touched]))
-    log(f"[bench] b8 wall {wall*1e6:.1f} us gpu {gpu*1e6:.1f} us; stages prep {t_prep*1e6:.1f} gate/up "
-        f"{t_gate*1e6:.1f} down {t_down*1e6:.1f} fold {t_fold*1e6:.1f} us; items {stats}")
+    # ---- B8 decode (headline, cold) ---------------------------------------
+    route_sets = []
+    if want("b8"):
+        N, R = 8, 64
+        xh = W.activations(N, seed=1002)
+        route_sets = [W.routes_uniform(N, seed=1003 + r) for r in range(R)]
+        x = dev(xh)
+        sets = [(dev(i), dev(w)) for i, w in route_sets]
+        touched = np.array([W.group_histogram(i)["touched"] for i, _ in route_sets])
+        log(f"[bench] b8 decode: {R} route sets over {NL} layers, touched experts mean {touched.mean():.1f} "
+            f"(min {touched.min()}, max {touched.max()})")
+        wall, gpu, _ = time_forward(layers, x, sets, args.steps, args.warmup)
+        stats = layers[0].last_stats()
+        # Stage durations over the same rotation; step i touched[i % R] + 1 units.
+        n_stage = max(R, args.steps)
+        t_stage = time_stages(layers, x, sets, n_stage)
+        units = touched[np.arange(n_stage) % R] + 1
+        gate_bytes = float(np.sum(units)) * GATE_UP_BYTES_PER_EXPERT
+        down_bytes = float(np.sum(units)) * DOWN_BYTES_PER_EXPERT
+        t_prep, t_gate, t_down, t_fold = (t_stage / n_stage).tolist()
+        achieved = gate_bytes / float(t_stage[1]) / 1e9
+        layer_bytes = float(np.mean([W.algorithmic_bytes(N, int(t)) for t in touched]))
+        log(f"[bench] b8 cold wall {wall*1e6:.1f} us gpu {gpu*1e6:.1f} us; stages prep {t_prep*1e6:.1f} gate/up "
+            f"{t_gate*1e6:.1f} down {t_down*1e6:.1f} fold {t_fold*1e6:.1f} us; items {stats}")
 
-    result = {
-        "metric": "MoE Q4_0 expert FFN tokens/s (B8 decode, 4K prefill); % HBM/MFMA-i8 roofline",
-        "value": N / wall,
-        "unit": "tokens/s per MoE layer",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": wall * 1e3,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8xint4->int32, fp32 accumulate",
-        "data": "synthetic (seeded Q4_0 weights d=|N(0,.02)|, x~N(0,1), uniform top-10 routing, "
-                f"{R} route sets rotated per step)",
-        "config": {"workload": "b8_decode", "tokens": N, "hidden": 2048, "intermediate": 512, "experts": 512,
-                   "top_k": 10, "shared_experts": 1, "route_sets": R,
-                   "touched_experts_mean": float(touched.mean()),
-                   "gpu_event_us_per_layer": gpu * 1e6,
-                   "layer_hbm_frac": layer_bytes / gpu / 1e9 / HBM_PEAK_GBS},
-        "roofline": {"kernel": "k_decode_gate_up (x Q8 + gate/up + SiLU + middle Q8)", "bound": "hbm",
-                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": pmc_traffic("k_decode_gate_up", float(touched.mean()) + 1),
-                     "bytes_per_launch": gate_bytes / n_stage, "us_per_launch": t_gate * 1e6},
-        "stages_us": {"prepare": t_prep * 1e6, "gate_up": t_gate * 1e6, "down": t_down * 1e6, "fold": t_fold * 1e6},
-        "down_stage_hbm_frac": down_bytes / float(t_stage[2]) / 1e9 / HBM_PEAK_GBS,
-    }
-    # Practical ceiling: a plain streaming read of the same byte count.
-    t_read = read_ceiling(int(gate_bytes / n_stage))
-    result["read_ceiling"] = {
-        "bytes": int(gate_bytes / n_stage) // 16 * 16, "us": t_read * 1e6,
-        "GB/s": gate_bytes / n_stage / t_read / 1e9, "frac_of_peak": gate_bytes / n_stage / t_read / 1e9 / HBM_PEAK_GBS,
-        "gate_up_frac_of_ceiling": t_read / t_gate,
-    }
-    log(f"[bench] read ceiling at {gate_bytes / n_stage / 1e6:.1f} MB: {t_read * 1e6:.1f} us "
-        f"({gate_bytes / n_stage / t_read / 1e9:.0f} GB/s)")
+        result.update({
+            "metric": "MoE Q4_0 expert FFN tokens/s (B8 decode, 4K prefill); % HBM/MFMA-i8 roofline",
+            "value": N / wall,
+            "unit": "tokens/s per MoE layer",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": wall * 1e3,
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "int8xint4->int32, fp32 accumulate",
+            "data": "synthetic (seeded Q4_0 weights d=|N(0,.02)|, x~N(0,1), uniform top-10 routing, "
+                    f"{R} route sets x {NL} resident layers rotated per step: cold weights)",
+            "config": {"workload": "b8_decode", "tokens": N, "hidden": 2048, "intermediate": 512, "experts": 512,
+                       "top_k": 10, "shared_experts": 1, "route_sets": R, "layers_rotated": NL,
+                       "rotated_weight_gb": moe_ffn.memory_bytes(2048, 512, 512, 10, True, NS)[0] * NL / 1e9,
+                       "touched_experts_mean": float(touched.mean()),
+                       "gpu_event_us_per_layer": gpu * 1e6,
+                       "layer_hbm_frac": layer_bytes / gpu / 1e9 / HBM_PEAK_GBS},
+            "roofline": {"kernel": "k_decode_gate_up (x Q8 + gate/up + SiLU + middle Q8)", "bound": "hbm",
+                         "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                         "traffic": pmc_traffic("k_decode_gate_up", float(touched.mean()) + 1),
+                         "bytes_per_launch": gate_bytes / n_stage, "us_per_launch": t_gate * 1e6},
+            "stages_us": {"prepare": t_prep * 1e6, "gate_up": t_gate * 1e6, "down": t_down * 1e6, "fold": t_fold * 1e6},
+            "down_stage_hbm_frac": down_bytes / float(t_stage[2]) / 1e9 / HBM_PEAK_GBS,
+        })
+    if only is None:
+        # Warm extra: the same rotation of route sets over ONE layer's bank.
+        wall_w, gpu_w, _ = time_forward(layers[0], x, sets, args.steps, args.warmup)
+        tw = time_stages(layers[0], x, sets, n_stage) / n_stage
+        result["b8_decode_warm"] = {
+            "tokens_per_s": N / wall_w, "us_per_layer": wall_w * 1e6, "gpu_event_us": gpu_w * 1e6,
+            "gate_up_us": tw[1] * 1e6, "down_us": tw[2] * 1e6,
+            "gate_up_hbm_frac": gate_bytes / n_stage / tw[1] / 1e9 / HBM_PEAK_GBS,
+            "note": "one layer's bank, 64 rotated route sets: consecutive steps share experts, so part of a step "
+                    "can be served from the 256 MB Infinity Cache",
+        }
+        log(f"[bench] b8 warm (one bank) wall {wall_w*1e6:.1f} us; gate/up {tw[1]*1e6:.1f} down {tw[2]*1e6:.1f} us")
+        # Practical ceiling: a plain streaming read of the same byte count.
+        t_read = read_ceiling(int(gate_bytes / n_stage))
+        result["read_ceiling"] = {
+            "bytes": int(gate_bytes / n_stage) // 16 * 16, "us": t_read * 1e6,
+            "GB/s": gate_bytes / n_stage / t_read / 1e9, "frac_of_peak": gate_bytes / n_stage / t_read / 1e9 / HBM_PEAK_GBS,
+            "gate_up_frac_of_ceiling": t_read / t_gate,
+        }
+        log(f"[bench] read ceiling at {gate_bytes / n_stage / 1e6:.1f} MB: {t_read * 1e6:.1f} us "
+            f"({gate_bytes / n_stage / t_read / 1e9:.0f} GB/s)")
 
-    # ---- 4K Zipf prefill (reported beside) --------------------------------
+    # ---- 4K Zipf prefill and 16K uniform prefill ----
+    layer = None
     if not args.no_prefill:
+        layer = moe_ffn.MoeLayer(2048, 512, 512, 10, True, 4096 if args.no_16k else 16384, synthetic_seed=1000)
+    if layer is not None and want("4k"):
         NP = 4096
         xph = W.activations(NP, seed=2002)
         idp, wp = W.routes_zipf(NP, 1.1, seed=2003)
@@ -410,10 +465,29 @@ def main():
             "hbm_frac": pbytes / gpu_p / 1e9 / HBM_PEAK_GBS, "group_hist": hp, "items": layer.last_stats(),
         }
         log(f"[bench] 4k prefill {wall_p*1e3:.3f} ms/layer, {NP/wall_p:.0f} tok/s")
+    if layer is not None and not args.no_16k:
+        NP = 16384
+        xph = W.activations(NP, seed=3002)
+        idp, wp = W.routes_uniform(NP, seed=3003)
+        hp = W.group_histogram(idp)
+        log(f"[bench] 16k prefill: {hp}")
+        wall_p, gpu_p, _ = time_forward(layer, dev(xph), [(dev(idp), dev(wp))], max(3, args.prefill_steps // 2), 2)
+        ops = W.int8_ops(NP)
+        pbytes = W.algorithmic_bytes(NP, hp["touched"])
+        result["prefill_16k"] = {
+            "tokens_per_s": NP / wall_p, "ms_per_layer": wall_p * 1e3, "gpu_event_ms": gpu_p * 1e3,
+            "int8_tops": ops / gpu_p / 1e12, "int8_mfma_frac": ops / gpu_p / 1e12 / INT8_PEAK_TOPS,
+            "hbm_frac": pbytes / gpu_p / 1e9 / HBM_PEAK_GBS, "group_hist": hp, "items": layer.last_stats(),
+        }
+        log(f"[bench] 16k prefill {wall_p*1e3:.3f} ms/layer, {NP/wall_p:.0f} tok/s")
+    if layer is not None:
+        layer.close()
+        layer = None
+        torch.cuda.empty_cache()
 
     # ---- device router (softmax + top-10 of 512), the step before the layer --
     router = {}
-    for NR in (8, 4096):
+    for NR in ((8, 4096) if only is None else ()):
         lg = dev(np.random.default_rng(4000 + NR).standard_normal((NR, 512)).astype(np.float32))
         ids_r = torch.empty((NR, 10), dtype=torch.int32, device="cuda:0")
         w_r = torch.empty((NR, 10), dtype=torch.float32, device="cuda:0")
@@ -431,8 +505,9 @@ def main():
         e1.record()
         torch.cuda.synchronize()
         router[f"tokens_{NR}_us"] = e0.elapsed_time(e1) / 50 * 1e3
-    result["router_us"] = router
-    log(f"[bench] router (softmax + top-10 of 512): {router}")
+    if router:
+        result["router_us"] = router
+        log(f"[bench] router (softmax + top-10 of 512): {router}")
 
     # ---- non-expert Q4_0 projections (moe_linear_forward_q8), cold weights --
     if not args.no_linear:
@@ -450,32 +525,10 @@ def main():
         result["reference_shapes"] = reference_components()
         log(f"[bench] reference shapes: {json.dumps(result['reference_shapes'])}")
 
-    # ---- 16K uniform prefill -----------------------------------
-    if not args.no_prefill and not args.no_16k:
-        NP = 16384
-        xph = W.activations(NP, seed=3002)
-        idp, wp = W.routes_uniform(NP, seed=3003)
-        hp = W.group_histogram(idp)
-        log(f"[bench] 16k prefill: {hp}")
-        wall_p, gpu_p, _ = time_forward(layer, dev(xph), [(dev(idp), dev(wp))], max(3, args.prefill_steps // 2), 2)
-        ops = W.int8_ops(NP)
-        pbytes = W.algorithmic_bytes(NP, hp["touched"])
-        result["prefill_16k"] = {
-            "tokens_per_s": NP / wall_p, "ms_per_layer": wall_p * 1e3, "gpu_event_ms": gpu_p * 1e3,
-            "int8_tops": ops / gpu_p / 1e12, "int8_mfma_frac": ops / gpu_p / 1e12 / INT8_PEAK_TOPS,
-            "hbm_frac": pbytes / gpu_p / 1e9 / HBM_PEAK_GBS, "group_hist": hp, "items": layer.last_stats(),
-        }
-        log(f"[bench] 16k prefill {wall_p*1e3:.3f} ms/layer, {NP/wall_p:.0f} tok/s")
-
     # ---- 48-layer stack, 8 decode + 1024 prefill tokens per layer --
     if not args.no_stack:
-        NL, NS = 48, 8 + 1024
-        layer.close()
-        layer = None
-        torch.cuda.empty_cache()
-        layers, inputs, touched_s = [], [], []
+        inputs, touched_s = [], []
         for l in range(NL):
-            layers.append(moe_ffn.MoeLayer(2048, 512, 512, 10, True, NS, synthetic_seed=5000 + l))
             ids_l, w_l = W.routes_zipf(NS, 1.3, seed=6000 + l)
             touched_s.append(W.group_histogram(ids_l)["touched"])
             inputs.append((dev(W.activations(NS, seed=7000 + l)), dev(ids_l), dev(w_l)))
@@ -519,22 +572,30 @@ def main():
                 f"{wall_m/NL*1e6:.1f} us/layer")
             for m in projections + routers:
                 m.close()
-        for L in layers:
-            L.close()
 
-    # ---- CPU baseline (same weights and inputs) ----------------------------
+    # ---- CPU baseline (same weights and inputs as the first B8 step) --------
     if not args.no_cpu:
+        import oracle as O
         idh, wh = route_sets[0]
-        sec, used, repeats = cpu_baseline(xh, bank, shared, idh, wh, args.cpu_seconds)
+        bank = sparse_bank(layers[0], idh)
+        shared = layers[0].export_expert(512)
+        cpus = O.physical_cpus()
+        workers = max(1, min(16, len(cpus)))
+        sec, used, repeats = cpu_baseline(xh, bank, shared, idh, wh, args.cpu_seconds, workers)
+        sec1, used1, repeats1 = cpu_baseline(xh, bank, shared, idh, wh, args.cpu_seconds, 1)
         result["cpu_baseline"] = {
             "value": N / sec, "unit": "tokens/s per MoE layer", "cores": used, "kind": "port",
-            "sample": f"b8_decode layer x{repeats} repeats (quantize + group + experts + fold + shared), "
-                      f"oracle/moe_oracle.c AVX2 cpu_expert order, {used} pinned workers",
+            "allowed_physical_cores": len(cpus), "workers": used,
+            "value_1_worker": N / sec1, "ms_per_layer": sec * 1e3, "ms_per_layer_1_worker": sec1 * 1e3,
+            "sample": f"b8_decode layer (route set 0 of layer 0) x{repeats} repeats with {used} pinned workers "
+                      f"(one per allowed physical core, at most 16) and x{repeats1} with 1 worker: quantize + "
+                      f"group + experts + rank-order fold + shared, oracle/moe_oracle.c AVX2 cpu_expert order",
         }
-        log(f"[bench] cpu {sec*1e3:.3f} ms/layer with {used} workers")
+        log(f"[bench] cpu {sec*1e3:.3f} ms/layer with {used} workers ({len(cpus)} allowed physical cores), "
+            f"{sec1*1e3:.3f} ms/layer with 1 worker")
     print(json.dumps(result), flush=True)
-    if layer is not None:
-        layer.close()
+    for L in layers:
+        L.close()
 
 
 if __name__ == "__main__":

@@ -8,7 +8,12 @@
  * middle value across a Q8 rounding boundary, and one changed middle code of
  * the shared expert moves its token's output by ~1e-2 rms.  So the device
  * evaluates expf exactly as the host library on the target image does
- * (glibc 2.35, x86-64 FMA build), restated from the published method:
+ * (glibc 2.35, x86-64 FMA build), restated from the published method.
+ * Source of the method: Szabolcs Nagy's expf in ARM's optimized-routines
+ * (math/expf.c, MIT OR Apache-2.0 WITH LLVM-exception), which glibc adopted
+ * as sysdeps/ieee754/flt-32/e_expf.c (LGPL-2.1-or-later); no code of either
+ * is copied here, only the algorithm and its published polynomial and shift
+ * constants, which fix the result bits:
  *
  *   k = round(x * 32/ln2), r = x * 32/ln2 - k          (double, via 1.5*2^52 shift)
  *   2^(k/32) = table[k % 32] with k/32 added to the exponent field

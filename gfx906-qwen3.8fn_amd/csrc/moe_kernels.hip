@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) void k_fill_u32(uint32_t *p, uint32_t v, size_
 }
 
 // ------------------------------------------------------------- grouping ----
-// Grouping replaces RouteGroups::prepare (src/routes.cpp:126-182): groups
+// Grouping replaces RouteGroups::prepare (src/routes.cpp:59-115): groups
 // ascend by expert, within a group by token then rank.  Each expert keeps a
 // token bitmap; a pair's position is offset[e] + (popcount of the expert's
 // bits for earlier tokens), which is the stable counting-sort position,
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(1024) void k_prepare_small(GroupParams p, const flo
     for (int i = threadIdx.x; i < E * W; i += blockDim.x) bits[i] = 0;
     for (int i = threadIdx.x; i < N * k; i += blockDim.x) eid[i] = p.ids[i];
     __syncthreads();
-    // Validate (src/routes.cpp:145-157) from LDS.  Thread tid owns entries
+    // Validate (src/routes.cpp:76-90) from LDS.  Thread tid owns entries
     // tid + m*blockDim (m < 32, N*k <= 32*blockDim); bit m of `valid` records
     // entry m's validity for the scatter below.
     int flags = 0;
@@ -354,8 +354,8 @@ __global__ __launch_bounds__(1024) void k_prepare_small(GroupParams p, const flo
 
 // Large path.  Mark and scatter blocks take 256 tokens each and stage their
 // ids in LDS ([256][k] ints, dynamic), so the duplicate checks of
-// src/routes.cpp:145-157 read LDS rather than chains of global loads.
-// Validates entry (t, r) (src/routes.cpp:145-157) and returns its expert, or
+// src/routes.cpp:76-90 read LDS rather than chains of global loads.
+// Validates entry (t, r) (src/routes.cpp:76-90) and returns its expert, or
 // -1 when it cannot be grouped (bad id, duplicate of an earlier rank); bad
 // ids, duplicates and negative or nonfinite weights set flag bit 1.
 __device__ __forceinline__ int staged_entry(const int32_t *sid, int tl, int r, int k, int E, int &flags) {
@@ -1109,7 +1109,7 @@ __global__ __launch_bounds__(128, Two ? 2 : 4) void k_down_lean_items(FfnArgs a)
 
 // ----------------------------------------------------- ungrouped decode ---
 // Route (t, r) of a decode batch, validated as RouteGroups::prepare does
-// (src/routes.cpp:145-157): returns the expert (E = shared for r == k) or -1
+// (src/routes.cpp:76-90): returns the expert (E = shared for r == k) or -1
 // for a bad id or a duplicate of an earlier rank.  `flags` gets bit 1 for a
 // bad id, a duplicate, or a negative / nonfinite weight.  Every lane of the
 // wave calls it with the same (t, r): lane j < k reads id j of the row, so
@@ -1367,23 +1367,27 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
             v = v + p;
             if (!isfinite(v)) { flags |= 2; v = 0.0f; }
         }
+        // The routed fold writes 0 on a flag, and the shared add starts from
+        // that value with flags of its own (two kernels in the reference).
+        if (flags) v = 0.0f;
+        int sflags = 0;
         if (P1 > k) {
             float x = part[k][row];
-            if (!isfinite(x)) { flags |= 1; x = 0.0f; }
+            if (!isfinite(x)) { sflags |= 1; x = 0.0f; }
             float scale = 1.0f;
             if (d.shared_gate) {
                 float g = wt[k];
-                if (!isfinite(g)) { flags |= 1; g = 0.0f; }
+                if (!isfinite(g)) { sflags |= 1; g = 0.0f; }
                 scale = 1.0f / (1.0f + moe_expf(-g));
-                if (!isfinite(scale)) { flags |= 2; scale = 0.0f; }
+                if (!isfinite(scale)) { sflags |= 2; scale = 0.0f; }
             }
             float p = scale * x;
-            if (!isfinite(p)) { flags |= 2; p = 0.0f; }
+            if (!isfinite(p)) { sflags |= 2; p = 0.0f; }
             v = v + p;
-            if (!isfinite(v)) { flags |= 2; v = 0.0f; }
+            if (!isfinite(v)) { sflags |= 2; v = 0.0f; }
         }
-        d.y[static_cast<size_t>(t) * H + row0 + row] = flags ? 0.0f : v;
-        if (flags) atomicOr(a.error, flags);
+        d.y[static_cast<size_t>(t) * H + row0 + row] = sflags ? 0.0f : v;
+        if (flags | sflags) atomicOr(a.error, flags | sflags);
     }
 }
 
@@ -1406,8 +1410,9 @@ __global__ __launch_bounds__(256) void k_decode_middle_grouped(Act mq, RouteOut 
 // ------------------------------------------------------------------ fold ---
 // y = +0; y = y + (w_r * c_r) for r = 0..k-1 (separately rounded, rank
 // order); then y = y + scale * shared with scale = 1/(1+expf(-g)) or 1 (moe_expf).
-// Nonfinite operands set bit 1, nonfinite results bit 2, and zero the output
-// element (src/hip/session_ops.hip:307-324, 375-391).  Pairs that could not
+// Nonfinite operands set bit 1, nonfinite results bit 2; the routed fold's
+// flags zero its value (src/hip/session_ops.hip:307-324) before the shared
+// add, whose own flags zero the output (:375-391).  Pairs that could not
 // be grouped (pos_of < 0: bad id / duplicate, already flagged) contribute 0.
 // V consecutive elements per thread (V = 4: 16-byte loads when every row is
 // 16-byte aligned); each element is folded on its own, exactly as above.
@@ -1461,6 +1466,13 @@ __global__ __launch_bounds__(256) void k_fold(const float *__restrict__ c, size_
             }
         }
     }
+    // The routed fold's value is 0 where it raised a flag; the shared add
+    // starts from it with flags of its own and zeroes only on those (the
+    // reference runs these as two kernels).
+    int sflags[V] = {};
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+        if (flags[e]) v[e] = 0.0f;
     if (shared) {
         float xsh[V];
         load(shared + t * shared_stride + h, xsh);
@@ -1475,19 +1487,19 @@ __global__ __launch_bounds__(256) void k_fold(const float *__restrict__ c, size_
 #pragma unroll
         for (int e = 0; e < V; ++e) {
             float x = xsh[e];
-            flags[e] |= gflags;
-            if (!isfinite(x)) { flags[e] |= 1; x = 0.0f; }
+            sflags[e] |= gflags;
+            if (!isfinite(x)) { sflags[e] |= 1; x = 0.0f; }
             float p = scale * x;
-            if (!isfinite(p)) { flags[e] |= 2; p = 0.0f; }
+            if (!isfinite(p)) { sflags[e] |= 2; p = 0.0f; }
             v[e] = v[e] + p;
-            if (!isfinite(v[e])) { flags[e] |= 2; v[e] = 0.0f; }
+            if (!isfinite(v[e])) { sflags[e] |= 2; v[e] = 0.0f; }
         }
     }
     int any = 0;
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-        y[i + e] = flags[e] ? 0.0f : v[e];
-        any |= flags[e];
+        y[i + e] = sflags[e] ? 0.0f : v[e];
+        any |= flags[e] | sflags[e];
     }
     if (any) atomicOr(error, any);
 }

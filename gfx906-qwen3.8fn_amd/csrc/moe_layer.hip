@@ -34,6 +34,9 @@ struct moe_ffn_layer {
     Act xq{}, mq{};
     RouteOut routes{};
     float *contrib = nullptr;
+    // Error word of the diagnostics (debug_last / last_stats re-group a
+    // decode-path batch): never the caller's flag of a finished forward.
+    int *diag_error = nullptr;
     // Smallest group routed to the MFMA path (0 = streaming only).  An MFMA
     // tile spends the same exact-order epilogue on 32 token columns however
     // many are filled, and a one-tile group streams its weights from HBM with
@@ -117,7 +120,7 @@ size_t bank_layout(const Shape &s, bool down_q41, size_t off[7]) {
 
 struct WsLayout {
     size_t xq_codes, xq_heads, mq_codes, mq_heads, pair_token, pair_rank, pos_of, counts, offsets,
-        stream_items, mfma_items, item_counts, bitmap, wprefix, contrib, total;
+        stream_items, mfma_items, item_counts, bitmap, wprefix, contrib, diag_error, total;
 };
 
 size_t pairs_capacity(const Shape &s, int N) { return static_cast<size_t>(N) * s.k + (s.Ep > s.E ? N : 0); }
@@ -143,6 +146,7 @@ WsLayout ws_layout(const Shape &s, int N) {
     w.bitmap = take(W * s.Ep * 4);
     w.wprefix = take(W * s.Ep * 4);
     w.contrib = take(static_cast<size_t>(N) * (s.k + 1) * s.H * 4);
+    w.diag_error = take(4);
     w.total = p;
     return w;
 }
@@ -166,6 +170,7 @@ int finish_create(moe_ffn_layer *L) {
     L->routes.bitmap = reinterpret_cast<uint32_t *>(b + w.bitmap);
     L->routes.wprefix = reinterpret_cast<uint32_t *>(b + w.wprefix);
     L->contrib = reinterpret_cast<float *>(b + w.contrib);
+    L->diag_error = reinterpret_cast<int *>(b + w.diag_error);
     if (hipMemset(L->ws_mem, 0, w.total) != hipSuccess) return hipErrorOutOfMemory;
     if (const char *env = std::getenv("MOE_FFN_MFMA_MIN")) {
         L->mfma_min = std::atoi(env);
@@ -717,7 +722,7 @@ int moe_ffn_debug_last(moe_ffn_layer *L, void *x_q8, void *middle_q8, int32_t *r
         // The decode path does not group: group the same routes now (the last
         // inputs must still be valid) and reorder its middle rows to match.
         if ((r = moe::launch_prepare(nullptr, L->last_ids, L->last_weights, N, sh, L->xq, L->routes, L->active_mfma_min,
-                                     L->last_error, s)) != hipSuccess)
+                                     L->diag_error, s)) != hipSuccess)
             return r;
         if (middle_q8 && (r = moe::launch_decode_middle_grouped(L->mq, L->routes, sh, N, middle_q8, s)) != hipSuccess)
             return r;
@@ -737,9 +742,12 @@ int moe_ffn_last_stats(moe_ffn_layer *L, int32_t *stream_items, int32_t *mfma_it
     if (!L) return kInvalid;
     int32_t c[4] = {0, 0, 0, 0};
     if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
+    // Synchronous diagnostic: wait for the device first, so the counts are
+    // those of the last forward whatever stream it ran on.
+    if (hipDeviceSynchronize() != hipSuccess) return kInvalid;
     if (L->last_decode && L->last_tokens > 0) {   // group the last batch's routes (not done by the decode path)
         const hipError_t g = moe::launch_prepare(nullptr, L->last_ids, L->last_weights, L->last_tokens, L->shape,
-                                                 L->xq, L->routes, L->active_mfma_min, L->last_error, nullptr);
+                                                 L->xq, L->routes, L->active_mfma_min, L->diag_error, nullptr);
         if (g != hipSuccess) return g;
     }
     const hipError_t r = hipMemcpy(c, L->routes.item_counts, sizeof(c), hipMemcpyDeviceToHost);

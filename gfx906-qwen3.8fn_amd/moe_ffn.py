@@ -105,6 +105,34 @@ def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def _need(t, name, dtype, shape, device=None):
+    """Check a tensor handed to the C ABI: dtype, exact shape, contiguity and
+    device.  The ABI takes raw pointers and sizes, so a tensor with fewer rows,
+    another element type or a strided view would be read past its end on the
+    GPU; the reference's RouteGroups::prepare likewise rejects a size
+    mismatch before touching anything (src/routes.cpp:63-68)."""
+    import torch
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.device.type != "cuda" or (device is not None and t.device != device):
+        raise ValueError(f"{name} must be on {device if device is not None else 'a GPU'}, got {t.device}")
+    return t
+
+
+def _routes_check(ids, weights, n, k, device):
+    import torch
+    _need(ids, "ids", torch.int32, (n, k), device)
+    _need(weights, "weights", torch.float32, (n, k), device)
+
+
 def _stream(stream):
     import torch
     s = stream if stream is not None else torch.cuda.current_stream()
@@ -186,13 +214,26 @@ class MoeLayer:
         return dict(stream_items=a.value, mfma_items=b.value, active_experts=c.value)
 
     # ------------------------------------------------------------ forward --
+    def _io_check(self, n, dev, ids, weights, shared_gate, y, error):
+        import torch
+        if not 1 <= n <= self.max_tokens:
+            raise ValueError(f"tokens {n} outside 1..{self.max_tokens}")
+        _routes_check(ids, weights, n, self.k, dev)
+        if shared_gate is not None:
+            _need(shared_gate, "shared_gate", torch.float32, (n,), dev)
+        if y is None:
+            y = torch.empty((n, self.H), dtype=torch.float32, device=dev)
+        _need(y, "y", torch.float32, (n, self.H), dev)
+        if error is None:
+            error = torch.zeros(1, dtype=torch.int32, device=dev)
+        _need(error, "error", torch.int32, (1,), dev)
+        return y, error
+
     def forward(self, x, ids, weights, shared_gate=None, y=None, error=None, stream=None):
         import torch
         n = x.shape[0]
-        if y is None:
-            y = torch.empty((n, self.H), dtype=torch.float32, device=x.device)
-        if error is None:
-            error = torch.zeros(1, dtype=torch.int32, device=x.device)
+        _need(x, "x", torch.float32, (n, self.H), x.device)
+        y, error = self._io_check(n, x.device, ids, weights, shared_gate, y, error)
         _check(library().moe_ffn_forward(self.handle, _ptr(x), _ptr(ids), _ptr(weights), n, _ptr(shared_gate),
                                          _ptr(y), _ptr(error), _stream(stream)), "moe_ffn_forward")
         return y, error
@@ -201,10 +242,8 @@ class MoeLayer:
         """forward() from canonical Q8_1 rows x_q8 (uint8 [tokens][H/32*36])."""
         import torch
         n = ids.shape[0]
-        if y is None:
-            y = torch.empty((n, self.H), dtype=torch.float32, device=ids.device)
-        if error is None:
-            error = torch.zeros(1, dtype=torch.int32, device=ids.device)
+        _need(x_q8, "x_q8", torch.uint8, (n, self.H // 32 * Q8_BLOCK), ids.device)
+        y, error = self._io_check(n, ids.device, ids, weights, shared_gate, y, error)
         _check(library().moe_ffn_forward_q8(self.handle, _ptr(x_q8), _ptr(ids), _ptr(weights), n, _ptr(shared_gate),
                                             _ptr(y), _ptr(error), _stream(stream)), "moe_ffn_forward_q8")
         return y, error
@@ -239,6 +278,9 @@ class MoeLayer:
         import torch
         n = ids.shape[0]
         dev = ids.device
+        if not 1 <= n <= self.max_tokens:
+            raise ValueError(f"tokens {n} outside 1..{self.max_tokens}")
+        _routes_check(ids, weights, n, self.k, dev)
         counts = torch.empty(self.E, dtype=torch.int32, device=dev)
         offsets = torch.empty(self.E + 1, dtype=torch.int32, device=dev)
         rt = torch.empty(n * self.k, dtype=torch.int32, device=dev)
@@ -301,12 +343,15 @@ def router_select(logits, top_k=10, probabilities=False, error=None, stream=None
     import torch
     n, e = logits.shape
     dev = logits.device
+    _need(logits, "logits", torch.float32, (n, e), dev)
     if ids is None:
         ids = torch.empty((n, top_k), dtype=torch.int32, device=dev)
     w = weights if weights is not None else torch.empty((n, top_k), dtype=torch.float32, device=dev)
+    _routes_check(ids, w, n, top_k, dev)
     p = torch.empty((n, e), dtype=torch.float32, device=dev) if probabilities else None
     if error is None:
         error = torch.zeros(1, dtype=torch.int32, device=dev)
+    _need(error, "error", torch.int32, (1,), dev)
     _check(library().moe_router_select(_ptr(logits), n, e, top_k, _ptr(p), _ptr(ids), _ptr(w), _ptr(error),
                                        _stream(stream)), "moe_router_select")
     return ids, w, p, error
@@ -322,9 +367,11 @@ def quantize_q8_1(x, error=None, stream=None):
     """fp32 [cols, width] (device) -> uint8 [cols, width/32*36] canonical Q8_1."""
     import torch
     cols, width = x.shape
+    _need(x, "x", torch.float32, (cols, width), x.device)
     out = torch.empty((cols, width // 32 * Q8_BLOCK), dtype=torch.uint8, device=x.device)
     if error is None:
         error = torch.zeros(1, dtype=torch.int32, device=x.device)
+    _need(error, "error", torch.int32, (1,), x.device)
     _check(library().moe_quantize_q8_1(_ptr(x), _ptr(out), width, cols, _ptr(error), _stream(stream)),
            "moe_quantize_q8_1")
     return out, error
@@ -333,6 +380,13 @@ def quantize_q8_1(x, error=None, stream=None):
 def combine(contributions, weights, shared=None, shared_gate=None, stream=None):
     import torch
     n, k, h = contributions.shape
+    dev = contributions.device
+    _need(contributions, "contributions", torch.float32, (n, k, h), dev)
+    _need(weights, "weights", torch.float32, (n, k), dev)
+    if shared is not None:
+        _need(shared, "shared", torch.float32, (n, h), dev)
+    if shared_gate is not None:
+        _need(shared_gate, "shared_gate", torch.float32, (n,), dev)
     y = torch.empty((n, h), dtype=torch.float32, device=contributions.device)
     error = torch.zeros(1, dtype=torch.int32, device=contributions.device)
     _check(library().moe_combine(_ptr(contributions), _ptr(weights), _ptr(shared), _ptr(shared_gate), n, k, h,
@@ -384,8 +438,11 @@ class MoeLinear:
 
     def forward_q8(self, x_q8, columns, y=None, stream=None):
         import torch
+        if x_q8.dtype != torch.uint8 or not x_q8.is_contiguous() or x_q8.numel() < columns * (self.K // 32) * Q8_BLOCK:
+            raise ValueError("x_q8 must be contiguous uint8 holding columns x input/32 Q8_1 blocks")
         if y is None:
             y = torch.empty((columns, self.M), dtype=torch.float32, device=x_q8.device)
+        _need(y, "y", torch.float32, (columns, self.M), x_q8.device)
         _check(library().moe_linear_forward_q8(self.handle, _ptr(x_q8), columns, _ptr(y), _stream(stream)),
                "moe_linear_forward_q8")
         return y
@@ -393,10 +450,13 @@ class MoeLinear:
     def apply(self, x, y=None, error=None, stream=None):
         import torch
         n = x.shape[0]
+        _need(x, "x", torch.float32, (n, self.K), x.device)
         if y is None:
             y = torch.empty((n, self.M), dtype=torch.float32, device=x.device)
+        _need(y, "y", torch.float32, (n, self.M), x.device)
         if error is None:
             error = torch.zeros(1, dtype=torch.int32, device=x.device)
+        _need(error, "error", torch.int32, (1,), x.device)
         _check(library().moe_linear_apply(self.handle, _ptr(x), n, _ptr(y), _ptr(error), _stream(stream)),
                "moe_linear_apply")
         return y, error

@@ -5,7 +5,7 @@
  * replaces everything between "token activations + host/device route ids and
  * weights" and "routed (+shared) FFN aggregate [N][H] fp32" in the reference's
  * Layer::ffn (src/session.hip:1446-1541, 1384-1410), i.e. the work of
- *   RouteGroups::prepare / upload_routes     src/routes.cpp:126-182, src/session.hip:393-410
+ *   RouteGroups::prepare / upload_routes     src/routes.cpp:59-115, src/session.hip:393-410
  *   launch_quantize_q8_1                     src/hip/linear.cuh:107-108
  *   launch_moe_gather_q8 / launch_moe_scatter src/hip/session_ops.cuh:175-199
  *   launch_quantized_linear{,_short,_tiled}  src/hip/linear.cuh:70-87
@@ -137,7 +137,7 @@ int moe_ffn_forward_q8(moe_ffn_layer *layer, const void *x_q8, const int32_t *id
 int moe_quantize_q8_1(const float *x, void *q8, int width, int columns, int *error, void *stream);
 
 /* Route grouping on the device (replaces RouteGroups::prepare,
- * src/routes.cpp:126-182, and upload_routes src/session.hip:393-410).
+ * src/routes.cpp:59-115, and upload_routes src/session.hip:393-410).
  * Outputs (device): counts [E], offsets [E+1], route_token / route_rank
  * [tokens*top_k] grouped by ascending expert, then token, then rank. */
 int moe_ffn_group_routes(moe_ffn_layer *layer, const int32_t *ids, const float *weights, int tokens,
@@ -179,7 +179,11 @@ int moe_combine(const float *contributions, const float *weights, const float *s
 /* Debug view of the last forward() on this layer (device copies, any may be
  * NULL): x_q8 [tokens][H/32] canonical Q8_1 of the input, middle_q8
  * [tokens*top_k (+tokens)][I/32] canonical Q8_1 in grouped pair order,
- * route_token/route_rank [tokens*top_k] grouped order.  Enqueue only. */
+ * route_token/route_rank [tokens*top_k] grouped order.  Enqueue only, on
+ * `stream`.  When the last forward took the ungrouped decode path, this call
+ * groups its routes again, so that forward's ids and weights must still be
+ * valid; any flag that raises goes to a word inside the layer, never to the
+ * forward's `error`. */
 int moe_ffn_debug_last(moe_ffn_layer *layer, void *x_q8, void *middle_q8, int32_t *route_token,
                        int32_t *route_rank, void *stream);
 
@@ -201,8 +205,11 @@ int moe_ffn_replay_stage(moe_ffn_layer *layer, int stage, void *stream);
 int moe_ffn_profile(moe_ffn_layer *layer, int forwards);
 int moe_ffn_profile_read(moe_ffn_layer *layer, double *stage_ms, int *forwards);
 
-/* Last-forward statistics (host, synchronous): work items per path and the
- * number of experts (incl. shared) that received tokens. */
+/* Last-forward statistics (host, synchronous: waits for the device first):
+ * work items per path and the number of experts (incl. shared) that received
+ * tokens.  After a decode-path forward it groups that forward's routes again
+ * (its ids and weights must still be valid), flagging into a word inside the
+ * layer, never into the forward's `error`. */
 int moe_ffn_last_stats(moe_ffn_layer *layer, int32_t *stream_items, int32_t *mfma_items,
                        int32_t *active_experts);
 

@@ -372,7 +372,7 @@ int mo_expert_forward_q41(const uint8_t *gate, const uint8_t *up, const uint8_t 
 }
 
 /* ------------------------------------------------------------- routes ----- */
-/* routes.cpp:126-182: validate the whole input first (ids in range, unique
+/* routes.cpp:59-115: validate the whole input first (ids in range, unique
  * per token, weights finite and >= 0), then histogram, exclusive scan and a
  * stable scatter in (token, rank) order; raw weight bits are preserved. */
 int mo_route_groups(const int32_t *ids, const float *weights, int tokens, int top_k, int experts,
@@ -427,6 +427,56 @@ static void shared_add(const float *s, const float *gate, int t, int H, float *y
         const float p = scale * s[i];
         y[(size_t)t * H + i] = y[(size_t)t * H + i] + p;
     }
+}
+
+/* The reference's fold with its error semantics: routed_fold
+ * (session_ops.hip:307-324) then shared_sigmoid_add (:375-391), as two passes.
+ * operand(): a nonfinite input sets bit 1 and reads as 0 (:161-164);
+ * arithmetic(): a nonfinite result sets bit 2 and becomes 0 (:166-169).  The
+ * routed pass writes 0 where it raised any flag; the shared pass reads that
+ * value as its accumulator and writes 0 where it raised a flag of its own.
+ * shared may be NULL (no shared add); shared_gate NULL means scale 1.0.
+ * Returns the OR of all flags; y [tokens][H]. */
+static float mo_operand(float x, int *flags) {
+    if (!isfinite(x)) { *flags |= 1; return 0.0f; }
+    return x;
+}
+static float mo_arith(float x, int *flags) {
+    if (!isfinite(x)) { *flags |= 2; return 0.0f; }
+    return x;
+}
+int mo_combine_flags(const float *contrib, const float *weights, const float *shared, const float *shared_gate,
+                     int tokens, int top_k, int H, float *y) {
+    int all = 0;
+    for (int t = 0; t < tokens; ++t)
+        for (int i = 0; i < H; ++i) {
+            int f = 0;
+            float v = 0.0f;
+            for (int r = 0; r < top_k; ++r) {
+                const float x = mo_operand(contrib[((size_t)t * top_k + r) * H + i], &f);
+                const float w = mo_operand(weights[(size_t)t * top_k + r], &f);
+                const float c = mo_arith(w * x, &f);
+                v = mo_arith(v + c, &f);
+            }
+            v = f ? 0.0f : v;
+            all |= f;
+            if (shared) {
+                int g = 0;
+                const float x = mo_operand(shared[(size_t)t * H + i], &g);
+                const float acc = mo_operand(v, &g);
+                float scale = 1.0f;
+                if (shared_gate) {
+                    const float gate = mo_operand(shared_gate[t], &g);
+                    scale = mo_arith(1.0f / (1.0f + expf(-gate)), &g);
+                }
+                const float c = mo_arith(scale * x, &g);
+                const float sum = mo_arith(acc + c, &g);
+                v = g ? 0.0f : sum;
+                all |= g;
+            }
+            y[(size_t)t * H + i] = v;
+        }
+    return all;
 }
 
 /* One expert's canonical bytes: gate and up Q4_0, down Q4_0 (18-byte

@@ -18,7 +18,7 @@
  *   - cpu_expert two-fragment / FMA / 128-lane XOR order
  *                                                    src/cpu_expert.cpp:156-213
  *   - cpu_expert whole-expert execute                src/cpu_expert.cpp:216-272
- *   - RouteGroups::prepare counting sort             src/routes.cpp:126-182
+ *   - RouteGroups::prepare counting sort             src/routes.cpp:59-115
  *   - routed_fold rank-order left fold               src/hip/session_ops.hip:307-324
  *   - shared_sigmoid_add                             src/hip/session_ops.hip:375-391
  *   - allowed physical CPU discovery                 src/cpu_expert.cpp:334-362
@@ -92,7 +92,7 @@ int mo_expert_forward(const uint8_t *gate, const uint8_t *up, const uint8_t *dow
                       float *gate_out, float *up_out, float *middle_out,
                       mo_q8_1 *middle_q8_out, int use_avx2);
 
-/* routes.cpp:126-182.  ids/weights [tokens][top_k].  Outputs:
+/* routes.cpp:59-115.  ids/weights [tokens][top_k].  Outputs:
  * assign_token/rank/expert/weight [tokens*top_k] grouped by ascending expert,
  * within a group by token then rank; counts [experts]; offsets [experts+1]. */
 int mo_route_groups(const int32_t *ids, const float *weights, int tokens, int top_k, int experts,
@@ -103,6 +103,15 @@ int mo_route_groups(const int32_t *ids, const float *weights, int tokens, int to
  * weights [tokens][top_k].  y = +0; for r: y = y + (w*c), separately rounded. */
 void mo_routed_fold(const float *contributions, const float *weights, int tokens, int top_k,
                     int H, float *y);
+
+/* session_ops.hip:307-324 then :375-391 with their flag semantics: a
+ * nonfinite operand sets bit 1 and reads as 0, a nonfinite result sets bit 2
+ * and becomes 0; the routed fold writes 0 where it raised a flag, the shared
+ * sigmoid add (skipped when shared is NULL; scale 1 when shared_gate is NULL)
+ * starts from that value and writes 0 where it raised one.  Returns the OR of
+ * the flags. */
+int mo_combine_flags(const float *contributions, const float *weights, const float *shared,
+                     const float *shared_gate, int tokens, int top_k, int H, float *y);
 
 /* Whole MoE layer, reference order:
  *   Q8 of x -> groups -> per (token,rank) expert forward (cpu_expert order)

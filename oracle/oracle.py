@@ -67,6 +67,7 @@ def _load_oracle():
     lib.mo_expert_forward.argtypes = [_P, _P, _P, _I, _I, _P, _I, _P, _P, _P, _P, _P, _I]
     lib.mo_route_groups.argtypes = [_P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P]
     lib.mo_routed_fold.argtypes = [_P, _P, _I, _I, _I, _P]
+    lib.mo_combine_flags.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P]
     lib.mo_moe_layer.argtypes = [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I]
     lib.mo_baseline_layer.argtypes = [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I,
                                       ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]
@@ -236,6 +237,19 @@ def routed_fold(contrib, weights):
     y = np.zeros((tokens, H), np.float32)
     lib().mo_routed_fold(_ptr(contrib), _ptr(weights), tokens, k, H, _ptr(y))
     return y
+
+
+def combine_flags(contrib, weights, shared=None, shared_gate=None):
+    """routed_fold then shared_sigmoid_add with the reference's flag semantics
+    (session_ops.hip:307-324, 375-391).  Returns (y, flags)."""
+    contrib = np.ascontiguousarray(contrib, dtype=np.float32)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    tokens, k, H = contrib.shape
+    sh = None if shared is None else np.ascontiguousarray(shared, dtype=np.float32)
+    g = None if shared_gate is None else np.ascontiguousarray(shared_gate, dtype=np.float32)
+    y = np.zeros((tokens, H), np.float32)
+    flags = lib().mo_combine_flags(_ptr(contrib), _ptr(weights), _ptr(sh), _ptr(g), tokens, k, H, _ptr(y))
+    return y, int(flags)
 
 
 def moe_layer(x, H, I, E, experts_q4, ids, weights, shared_q4=None, shared_gate=None,

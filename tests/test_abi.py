@@ -82,3 +82,23 @@ def test_expf_host_build_matches_libm():
     nan = np.isnan(ref)
     assert np.array_equal(np.isnan(got), nan)
     assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_binding_rejects_mismatched_tensors():
+    """The Python binding checks dtype, exact shape, contiguity and device of
+    every tensor before it hands raw pointers to the C ABI (a short or int64
+    ids tensor would otherwise be read past its end on the GPU)."""
+    import pytest
+    torch = pytest.importorskip("torch")
+    ids = torch.zeros((4, 10), dtype=torch.int32)
+    w = torch.zeros((4, 10), dtype=torch.float32)
+    with pytest.raises(TypeError):
+        moe_ffn._routes_check(ids.to(torch.int64), w, 4, 10, None)
+    with pytest.raises(ValueError):
+        moe_ffn._routes_check(ids[:3], w, 4, 10, None)
+    with pytest.raises(ValueError):
+        moe_ffn._routes_check(torch.zeros((10, 4), dtype=torch.int32).t(), w, 4, 10, None)
+    with pytest.raises(ValueError):   # CPU tensors never reach the library
+        moe_ffn._routes_check(ids, w, 4, 10, None)
+    with pytest.raises(TypeError):
+        moe_ffn._need(w.to(torch.float64), "w", torch.float32, (4, 10))

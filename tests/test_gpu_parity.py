@@ -238,6 +238,36 @@ def test_combine_bit_exact():
     assert int(host(err)[0]) == 0
 
 
+@pytest.mark.parametrize("gated", [False, True])
+def test_combine_flags_match_two_kernel_sequence(gated):
+    """Nonfinite operands and overflowing products in the fold: the routed
+    value is zeroed where the routed fold flags, the shared add starts from
+    it with flags of its own (the reference's routed_fold, then
+    shared_sigmoid_add).  Output bits and the error word equal the oracle's."""
+    rng = np.random.default_rng(44)
+    T, K, H = 6, 10, 256
+    c = rng.standard_normal((T, K, H), dtype=np.float32)
+    w = rng.random((T, K), dtype=np.float32)
+    s = rng.standard_normal((T, H), dtype=np.float32)
+    c[1, 3, 7] = np.nan
+    c[2, 0, 9] = np.inf
+    c[3, 5, 11] = np.float32(3e38)
+    w[3, 5] = 8.0
+    s[4, 13] = np.nan
+    s[1, 7] = -np.inf
+    g = rng.standard_normal(T).astype(np.float32) if gated else None
+    if gated:
+        g[5] = np.nan
+    y, err = moe_ffn.combine(dev(c), dev(w), shared=dev(s), shared_gate=None if g is None else dev(g))
+    ref, flags = O.combine_flags(c, w, shared=s, shared_gate=g)
+    assert np.array_equal(host(y).view(np.uint32), ref.view(np.uint32))
+    assert int(host(err)[0]) == flags == 3
+    y2, err2 = moe_ffn.combine(dev(c), dev(w))
+    ref2, flags2 = O.combine_flags(c, w)
+    assert np.array_equal(host(y2).view(np.uint32), ref2.view(np.uint32))
+    assert int(host(err2)[0]) == flags2
+
+
 # -------------------------------------------------------- whole layer ------
 @pytest.fixture(scope="module")
 def moe512():

@@ -441,3 +441,78 @@ def test_select_routes_ties_floor_and_bucket_order():
     # Softmax of uniform logits: ten equal weights of exactly fl(0.1).
     ids, w, f = O.select_routes(np.full((1, 512), np.float32(1 / 512)), 10)
     assert np.all(w == np.float32(0.1))
+
+
+def test_router_softmax_lane_order_pinned_by_absorption():
+    """Hand-derived cases that fix router_softmax's summation order
+    (src/hip/session_ops.hip:401-434): lane l holds logits l + 32j, each lane
+    sums its values left to right from +0, and the 32 lane sums meet in an XOR
+    butterfly.  delta = expf(x_d) ~ 0.7 * 2^-24 is below half an ulp of 1, so
+    1 + delta rounds back to 1 while delta + delta = 1.4 * 2^-24 does not."""
+    x_d = np.float32(np.log(0.7) - 24 * np.log(2.0))
+    far = np.float32(-200.0)                         # expf underflows to exactly 0
+    # (a) Logits 0, 32, ..., 480 share lane 0; the 1 comes first, so each delta
+    # is absorbed and the total is exactly 1: p = expf(x) * (1/1).
+    x = np.full((1, 512), far, np.float32)
+    x[0, 0] = 0.0
+    x[0, 32::32] = x_d
+    p, f = O.router_softmax(x)
+    e = O.expf_libm(np.array([x_d], np.float32))[0]
+    assert f == 0 and p[0, 0] == 1.0 and np.all(p[0, 32::32] == e)
+    # (b) Same lane, the 1 last (logit 480): fifteen deltas are summed first
+    # and survive the add of 1, so the total exceeds 1 and p[480] < 1.
+    x = np.full((1, 512), far, np.float32)
+    x[0, 480] = 0.0
+    x[0, 0:480:32] = x_d
+    p, f = O.router_softmax(x)
+    assert f == 0 and p[0, 480] < 1.0
+    # (c) One value per lane (logits 0..31): lane 0 holds the 1, lanes 1..31 a
+    # delta.  The butterfly pairs equal partial sums (2, 4, 8, 16 deltas,
+    # exact doublings) before they reach lane 0:
+    #   1 + 2d -> 1 + 1 ulp, + 4d -> 1 + 2 ulp, + 8d -> 1 + 5 ulp,
+    #   + 16d -> 1 + 11 ulp  (ulp = 2^-23; none of these near a tie),
+    # whereas a left-to-right sum over lanes would absorb every delta (total 1).
+    x = np.full((1, 512), far, np.float32)
+    x[0, 0] = 0.0
+    x[0, 1:32] = x_d
+    p, f = O.router_softmax(x)
+    total = np.float32(1.0 + 11 * 2.0 ** -23)
+    assert f == 0 and p[0, 0] == np.float32(1.0) / total
+
+
+def test_combine_flags_closed_forms():
+    """The fold's error semantics (routed_fold, then shared_sigmoid_add:
+    src/hip/session_ops.hip:307-324, 375-391; operand/arithmetic :161-169)."""
+    c = np.array([[[1.0, 2.0], [3.0, 4.0], [5.0, 6.0]]], np.float32)
+    w = np.array([[0.5, 0.25, 0.125]], np.float32)
+    s = np.array([[10.0, 20.0]], np.float32)
+    # Finite: the plain fold plus the shared row (gate absent: scale 1).
+    y, f = O.combine_flags(c, w, shared=s)
+    assert f == 0 and np.array_equal(y, O.routed_fold(c, w) + s)
+    # A NaN contribution: bit 1, the routed value of that element becomes 0,
+    # the shared add still happens from 0 (the other element is untouched).
+    cb = c.copy()
+    cb[0, 1, 0] = np.nan
+    y, f = O.combine_flags(cb, w, shared=s)
+    assert f == 1 and y[0, 0] == 10.0 and y[0, 1] == np.float32(0.5 * 2 + 0.25 * 4 + 0.125 * 6 + 20)
+    # With a gate of 0 the shared scale is exactly 1/2: y = 0 + 0.5 * 10.
+    y, f = O.combine_flags(cb, w, shared=s, shared_gate=np.zeros(1, np.float32))
+    assert f == 1 and y[0, 0] == 5.0
+    # An overflowing product is an arithmetic flag (bit 2) and reads as 0.
+    cb = c.copy()
+    cb[0, 0, 1] = np.float32(3e38)
+    wb = w.copy()
+    wb[0, 0] = 4.0
+    y, f = O.combine_flags(cb, wb, shared=s)
+    assert f == 2 and y[0, 1] == 20.0 and y[0, 0] == np.float32(4 * 1 + 0.25 * 3 + 0.125 * 5 + 10)
+    # A nonfinite shared value zeroes the output element (bit 1).
+    sb = s.copy()
+    sb[0, 1] = np.inf
+    y, f = O.combine_flags(c, w, shared=sb)
+    assert f == 1 and y[0, 1] == 0.0 and y[0, 0] == np.float32(0.5 + 0.75 + 0.625 + 10)
+    # A nonfinite gate zeroes the whole token row (bit 1), routed part included.
+    y, f = O.combine_flags(c, w, shared=s, shared_gate=np.array([np.nan], np.float32))
+    assert f == 1 and np.all(y == 0)
+    # No shared expert: only the routed fold, with its flags.
+    y, f = O.combine_flags(cb, wb)
+    assert f == 2 and y[0, 1] == 0.0
