@@ -42,6 +42,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
+#include <mutex>
 #include <new>
 
 namespace moe {
@@ -150,6 +151,40 @@ __global__ __launch_bounds__(64, 2) void k_linear(LinearArgs a) {
 }  // namespace
 }  // namespace moe
 
+// Activation staging of moe_linear_apply_noalloc: a file-scope device array,
+// one copy per GPU the library runs on, held until the process ends.  Its
+// name is a host-side stand-in, never a device address: host code uses only
+// the per-device address that hipGetSymbolAddress returns (noalloc_scratch).
+constexpr size_t kNoallocScratchBytes = size_t{4} << 20;
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+uint8_t *scratch_ptr[kMaxDevices] = {};
+
+// Looks up (once per device, with that device current) the device address of
+// `scratch`.  Called by moe_linear_create, the library's set-up call, so that
+// the no-allocation entry point itself only reads the table.
+hipError_t init_noalloc_scratch(int device) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidValue;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (scratch_ptr[device]) return hipSuccess;
+    void *p = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (r != hipSuccess) return r;
+    if (!p) return hipErrorInvalidSymbol;
+    scratch_ptr[device] = static_cast<uint8_t *>(p);
+    return hipSuccess;
+}
+
+uint8_t *noalloc_scratch(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    return scratch_ptr[device];
+}
+}  // namespace
+
 // ------------------------------------------------------------------ C ABI ---
 struct moe_linear {
     int type = 0, input = 0, output = 0, max_columns = 0, device = 0;
@@ -238,6 +273,7 @@ int moe_linear_create(int type, int input, int output, int max_columns, const vo
     r = moe::launch_repack_weights(canonical, L->codes, L->scales, L->mins, blocks, 0, L->nb, moe::kScaleGroupGateUp,
                                    nullptr);
     if (r == hipSuccess) r = hipDeviceSynchronize();
+    if (r == hipSuccess) r = init_noalloc_scratch(device);
     if (staging) (void)hipFree(staging);
     if (r != hipSuccess) { release(L); return r; }
     *out = L;
@@ -259,16 +295,20 @@ int moe_linear_bytes(const moe_linear *L, size_t *weight_bytes) {
 
 namespace {
 
-bool use_mfma(const moe_linear *L, int columns) {
-    if (L->type != MOE_TYPE_Q4_0 || columns < kMfmaMinColumns || columns > L->max_columns || L->mfma_mode == 0)
+// MFMA for wide Q4_0 batches that fit the staging area (`capacity` columns).
+bool use_mfma_within(const moe_linear *L, int columns, int capacity) {
+    if (L->type != MOE_TYPE_Q4_0 || columns < kMfmaMinColumns || columns > capacity || L->mfma_mode == 0)
         return false;
     return L->mfma_mode == 1 || static_cast<long>(L->output) * columns >= kMfmaMinOutputs;
 }
+bool use_mfma(const moe_linear *L, int columns) { return use_mfma_within(L, columns, L->max_columns); }
 
-moe::Act workspace_planes(const moe_linear *L, int columns) {
-    auto *base = static_cast<uint8_t *>(L->q8);
+// Split Q8 planes for `columns` columns at `base` (codes, then heads).
+moe::Act staging_planes(const moe_linear *L, void *base_ptr, int columns) {
+    auto *base = static_cast<uint8_t *>(base_ptr);
     return moe::Act{base, reinterpret_cast<uint32_t *>(base + static_cast<size_t>(columns) * L->nb * 32)};
 }
+moe::Act workspace_planes(const moe_linear *L, int columns) { return staging_planes(L, L->q8, columns); }
 
 int launch_mfma(const moe_linear *L, moe::Act xq, int columns, float *y, hipStream_t s) {
     moe::LinearMfmaArgs a{};
@@ -284,17 +324,8 @@ int launch_mfma(const moe_linear *L, moe::Act xq, int columns, float *y, hipStre
     return moe::launch_linear_mfma(a, s);
 }
 
-}  // namespace
-
-int moe_linear_forward_q8(moe_linear *L, const void *x_q8, int columns, float *y, void *stream) {
-    if (!L || !aligned(x_q8, 4) || !aligned(y, 4) || columns < 1 || columns > 65536) return kInvalid;
-    if (use_mfma(L, columns)) {
-        const auto s = static_cast<hipStream_t>(stream);
-        const moe::Act xq = workspace_planes(L, columns);
-        const hipError_t r = moe::launch_canonical_to_planes(x_q8, xq, columns * L->nb, s);
-        if (r != hipSuccess) return r;
-        return launch_mfma(L, xq, columns, y, s);
-    }
+// The vector kernel on canonical Q8_1 columns x_q8.
+int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, hipStream_t s) {
     moe::LinearArgs a{};
     a.codes = L->codes;
     a.scales = L->scales;
@@ -314,7 +345,6 @@ int moe_linear_forward_q8(moe_linear *L, const void *x_q8, int columns, float *y
     a.tiles = (columns + a.tile_cols - 1) / a.tile_cols;
     const size_t grid = round_up(static_cast<size_t>(a.slices), 8) * a.tiles;
     if (grid > 0x7fffffffu) return kInvalid;
-    const auto s = static_cast<hipStream_t>(stream);
     const bool q41 = L->type == MOE_TYPE_Q4_1, hold2 = L->nb > 64;
     const dim3 g(static_cast<unsigned>(grid)), b(64);
     if (q41) {
@@ -325,6 +355,20 @@ int moe_linear_forward_q8(moe_linear *L, const void *x_q8, int columns, float *y
         else moe::k_linear<false, 1, 4><<<g, b, 0, s>>>(a);
     }
     return hipGetLastError();
+}
+
+}  // namespace
+
+int moe_linear_forward_q8(moe_linear *L, const void *x_q8, int columns, float *y, void *stream) {
+    if (!L || !aligned(x_q8, 4) || !aligned(y, 4) || columns < 1 || columns > 65536) return kInvalid;
+    const auto s = static_cast<hipStream_t>(stream);
+    if (use_mfma(L, columns)) {
+        const moe::Act xq = workspace_planes(L, columns);
+        const hipError_t r = moe::launch_canonical_to_planes(x_q8, xq, columns * L->nb, s);
+        if (r != hipSuccess) return r;
+        return launch_mfma(L, xq, columns, y, s);
+    }
+    return launch_vector(L, x_q8, columns, y, s);
 }
 
 int moe_linear_apply(moe_linear *L, const float *x, int columns, float *y, int *error, void *stream) {
@@ -340,6 +384,28 @@ int moe_linear_apply(moe_linear *L, const float *x, int columns, float *y, int *
     const hipError_t r = moe::launch_quantize_canonical(x, L->q8, L->input, columns, error, s);
     if (r != hipSuccess) return r;
     return moe_linear_forward_q8(L, L->q8, columns, y, stream);
+}
+
+int moe_linear_apply_noalloc(moe_linear *L, const float *x, int columns, float *y, int *error, void *stream) {
+    if (!L || !aligned(x, 4) || !aligned(y, 4) || !aligned(error, 4) || columns < 1) return kInvalid;
+    // The staging (canonical Q8_1 blocks, or the MFMA kernel's split planes:
+    // 36 bytes per block either way) must fit the static array.
+    if (static_cast<size_t>(columns) * L->nb * 36 > kNoallocScratchBytes) return kInvalid;
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device != L->device) return kInvalid;
+    uint8_t *ws = noalloc_scratch(device);
+    if (!ws) return hipErrorNotInitialized;
+    const auto s = static_cast<hipStream_t>(stream);
+    const int capacity = static_cast<int>(kNoallocScratchBytes / (static_cast<size_t>(L->nb) * 36));
+    if (use_mfma_within(L, columns, capacity)) {
+        const moe::Act xq = staging_planes(L, ws, columns);
+        const hipError_t r = moe::launch_quantize_planes(x, xq, L->input, columns, error, s);
+        if (r != hipSuccess) return r;
+        return launch_mfma(L, xq, columns, y, s);
+    }
+    const hipError_t r = moe::launch_quantize_canonical(x, ws, L->input, columns, error, s);
+    if (r != hipSuccess) return r;
+    return launch_vector(L, ws, columns, y, s);
 }
 
 }  // extern "C"

@@ -85,6 +85,7 @@ def library():
         lib.moe_linear_bytes.argtypes = [_P, ctypes.POINTER(ctypes.c_size_t)]
         lib.moe_linear_forward_q8.argtypes = [_P, _P, _I, _P, _P]
         lib.moe_linear_apply.argtypes = [_P, _P, _I, _P, _P, _P]
+        lib.moe_linear_apply_noalloc.argtypes = [_P, _P, _I, _P, _P, _P]
         _lib = lib
     return _lib
 
@@ -459,6 +460,19 @@ class MoeLinear:
         _need(error, "error", torch.int32, (1,), x.device)
         _check(library().moe_linear_apply(self.handle, _ptr(x), n, _ptr(y), _ptr(error), _stream(stream)),
                "moe_linear_apply")
+        return y, error
+
+    def apply_noalloc(self, x, y, error, stream=None):
+        """apply() through moe_linear_apply_noalloc: the activation staging is
+        the library's static per-device array (4 MiB), not the handle's
+        workspace; y and error must be given (nothing is allocated)."""
+        import torch
+        n = x.shape[0]
+        _need(x, "x", torch.float32, (n, self.K), x.device)
+        _need(y, "y", torch.float32, (n, self.M), x.device)
+        _need(error, "error", torch.int32, (1,), x.device)
+        _check(library().moe_linear_apply_noalloc(self.handle, _ptr(x), n, _ptr(y), _ptr(error), _stream(stream)),
+               "moe_linear_apply_noalloc")
         return y, error
 
 

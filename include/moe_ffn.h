@@ -284,6 +284,20 @@ int moe_linear_forward_q8(moe_linear *linear, const void *x_q8, int columns, flo
  * overlap (they share the workspace). */
 int moe_linear_apply(moe_linear *linear, const float *x, int columns, float *y, int *error, void *stream);
 
+/* moe_linear_apply without the handle's workspace: the Q8_1 staging of x
+ * lives in a static device array of the library, 4 MiB per GPU (held until
+ * the process ends), so this call allocates nothing and works on handles
+ * created with max_columns = 0.  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Limit: columns * (input/32) * 36
+ * <= 4 MiB (e.g. 1820 columns at input 2048), else 1 (invalid value) before
+ * any HIP call; the handle's device must be current (moe_linear_create set
+ * the array up for it), else 1.  Same outputs and flags as moe_linear_apply.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (on any handle or stream) race. */
+int moe_linear_apply_noalloc(moe_linear *linear, const float *x, int columns, float *y, int *error,
+                             void *stream);
+
 #ifdef __cplusplus
 }
 #endif
