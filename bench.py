@@ -281,6 +281,15 @@ def reference_components():
     if int(err.cpu()[0]) != 0:
         raise RuntimeError("reference-shape B8 layer flagged an error")
     L.close()
+    # 4K Zipf(1.1) prefill layer at this shape, Q4_1 and Q4_0 downs.
+    NP = 4096
+    xp = torch.from_numpy(W.activations(NP, hidden=H, seed=4107)).to(dev0)
+    idp, wp = (torch.from_numpy(a).to(dev0) for a in W.routes_zipf(NP, 1.1, seed=4108))
+    for name, dt in (("prefill_4k_q4_1_ms", moe_ffn.DOWN_Q4_1), ("prefill_4k_q4_0_ms", moe_ffn.DOWN_Q4_0)):
+        L = moe_ffn.MoeLayer(H, I, 512, 10, True, NP, synthetic_seed=4109, down_type=dt)
+        wall, _, _ = time_forward(L, xp, [(idp, wp)], 10, 2)
+        out[name] = wall * 1e3
+        L.close()
     rng = np.random.default_rng(4102)
     mats = {("q4_0", H, I): W.q4_blocks(I * H // 32, rng).reshape(-1),
             ("q4_0", I, H): W.q4_blocks(H * I // 32, rng).reshape(-1),

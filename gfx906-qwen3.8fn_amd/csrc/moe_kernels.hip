@@ -1031,82 +1031,6 @@ __global__ __launch_bounds__(128, Two ? 2 : 4) void k_down_lean(FfnArgs a) {
         if (!down_lean_unit<NBI, Q41, Two, Dbg>(a, u, count)) break;
 }
 
-// Down projection of the MFMA items (groups of >= mfma_min pairs, <= 128
-// pairs an item) for layers whose down matrices the MFMA kernel does not
-// take (Q4_1): k_down_lean's row and lane layout and exact order, with the
-// weight rows held in registers across a chunk of kItemChunk of the item's
-// pairs (workgroup = (item, chunk, slice), so one large group still spreads
-// over many workgroups).  Tokens and ranks come from the grouped pair arrays.
-constexpr int kItemChunk = 32;
-template<bool Q41, bool Two>
-__global__ __launch_bounds__(128, Two ? 2 : 4) void k_down_lean_items(FfnArgs a) {
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int H = a.shape.H, nbi = a.shape.I / 32, S = H / 64;
-    constexpr int C = kMfmaTile / kItemChunk;
-    const int unit = static_cast<int>(blockIdx.x) / S, slice = static_cast<int>(blockIdx.x) % S;
-    const int item = unit / C, chunk = unit % C;
-    const int4 hdr = *reinterpret_cast<const int4 *>(a.routes.mfma_items + item);
-    const int count = a.routes.item_counts[1];
-    asm volatile("" ::"s"(hdr.x), "s"(hdr.y), "s"(hdr.z), "s"(count));
-    if (item >= count || chunk * kItemChunk >= hdr.z) return;   // uniform per workgroup
-    const int expert = hdr.x, first = hdr.y + chunk * kItemChunk, ncols = min(kItemChunk, hdr.z - chunk * kItemChunk);
-    const int row0 = slice * 64 + wave * 32;
-    const int sub = lane >> 4, kl = lane & 15;
-    const bool has = kl < nbi, has2 = Two && kl + 16 < nbi;
-    const int kb = has ? kl : 0, kb2 = has2 ? kl + 16 : 0;
-    const size_t mrow = static_cast<size_t>(expert) * H + row0;
-    const uint32_t row_bytes = static_cast<uint32_t>(nbi) * 16u;
-    const auto wr = buffer_rsrc(a.bank.down_codes + mrow * row_bytes, 32 * row_bytes);
-    const auto sr = buffer_rsrc(a.bank.down_scales + mrow * nbi, 4 * row_bytes);
-    const auto mr = buffer_rsrc(Q41 ? a.bank.down_mins + mrow * nbi : a.bank.down_scales, 4 * row_bytes);
-    const int lr = 4 * (lane & 1) + 2 * ((lane >> 1) & 1) + ((lane >> 2) & 1);
-    uint4 w[8], w2[8];
-    const uint32_t lane_off = static_cast<uint32_t>(sub * nbi + kb) * 16u;
-#pragma unroll
-    for (int l = 0; l < 8; ++l) w[l] = buffer_load16(wr, lane_off, 4 * l * row_bytes);
-    const uint4 d4p = buffer_load16(sr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
-    uint4 m4p = make_uint4(0u, 0u, 0u, 0u), d4p2 = make_uint4(0u, 0u, 0u, 0u), m4p2 = make_uint4(0u, 0u, 0u, 0u);
-    if constexpr (Q41) m4p = buffer_load16(mr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
-    if constexpr (Two) {
-        const uint32_t lane_off2 = static_cast<uint32_t>(sub * nbi + kb2) * 16u;
-#pragma unroll
-        for (int l = 0; l < 8; ++l) w2[l] = buffer_load16(wr, lane_off2, 4 * l * row_bytes);
-        d4p2 = buffer_load16(sr, static_cast<uint32_t>(kb2 * 32 + sub * 8) * 2u, 0);
-        if constexpr (Q41) m4p2 = buffer_load16(mr, static_cast<uint32_t>(kb2 * 32 + sub * 8) * 2u, 0);
-    }
-    struct Xb {
-        uint4 x0, x1, y0, y1;
-        uint32_t hx, hy;
-    };
-    auto load_x = [&](int j, Xb &b) {
-        const size_t xrow = static_cast<size_t>(first + j) * nbi;
-        const auto xr = buffer_rsrc(a.mq.codes + xrow * 32, static_cast<uint32_t>(nbi) * 32u);
-        const auto hr = buffer_rsrc(a.mq.heads + xrow, static_cast<uint32_t>(nbi) * 4u);
-        b.x0 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 0);
-        b.x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
-        b.hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
-        if constexpr (Two) {
-            b.y0 = buffer_load16(xr, static_cast<uint32_t>(kb2) * 32u, 0);
-            b.y1 = buffer_load16(xr, static_cast<uint32_t>(kb2) * 32u, 16);
-            b.hy = buffer_load4(hr, static_cast<uint32_t>(kb2) * 4u, 0);
-        }
-    };
-    Xb cur;
-    load_x(0, cur);
-    for (int j = 0; j < ncols; ++j) {   // uniform per workgroup
-        Xb nxt = cur;
-        if (j + 1 < ncols) load_x(j + 1, nxt);
-        const int tok = a.routes.pair_token[first + j], rnk = a.routes.pair_rank[first + j];
-        float v = rows8_down_exact<Q41>(w, d4p, m4p, cur.x0, cur.x1, cur.hx, has, lane);
-        if constexpr (Two) v = v + rows8_down_exact<Q41>(w2, d4p2, m4p2, cur.y0, cur.y1, cur.hy, has2, lane);
-        if ((lane & 8) == 0) {
-            const size_t orow = static_cast<size_t>(tok) * a.out_stride_k + rnk;
-            a.out[orow * H + row0 + 4 * lr + sub] = v;
-        }
-        cur = nxt;
-    }
-}
-
 // ----------------------------------------------------- ungrouped decode ---
 // Route (t, r) of a decode batch, validated as RouteGroups::prepare does
 // (src/routes.cpp:76-90): returns the expert (E = shared for r == k) or -1
@@ -1828,18 +1752,7 @@ hipError_t launch_decode_middle_grouped(Act mq, RouteOut routes, Shape shape, in
 }
 
 hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
-    if (mfma && a.bank.down_mins) {
-        // Q4_1 down rows (I/32 <= 32): the MFMA items' down on the lean kernel.
-        const size_t P = static_cast<size_t>(a.pairs_bound);
-        const size_t G = std::min(P, static_cast<size_t>(a.shape.Ep));
-        const size_t big = a.mfma_min >= 1 ? std::min(G, P / static_cast<size_t>(a.mfma_min)) : G;
-        const unsigned g = static_cast<unsigned>(std::max<size_t>(P / kMfmaTile + big, 1) * (kMfmaTile / kItemChunk) *
-                                                 (a.shape.H / 64));
-        if (a.shape.I / 32 > 16) k_down_lean_items<true, true><<<g, 128, 0, s>>>(a);
-        else k_down_lean_items<true, false><<<g, 128, 0, s>>>(a);
-        return hipGetLastError();
-    }
-    if (mfma) return launch_down_mfma(a, s);
+    if (mfma) return launch_down_mfma(a, s);   // Q4_0 and Q4_1 down rows
     const int nbi = a.shape.I / 32;
     const unsigned grid = stream_grid(a, a.shape.H / 64);
     const bool dbg = a.down_dots != nullptr, q41 = a.bank.down_mins != nullptr;

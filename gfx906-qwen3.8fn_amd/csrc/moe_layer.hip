@@ -177,10 +177,6 @@ int finish_create(moe_ffn_layer *L) {
         L->mfma_routes = 0;
     }
     if (const char *env = std::getenv("MOE_FFN_MFMA_ROUTES")) L->mfma_routes = std::atoi(env);
-    // Q4_1 down matrices: MFMA items run gate/up on MFMA and their down on
-    // the lean kernel (k_down_lean_items, rows of up to 32 blocks); wider
-    // rows stream every group.
-    if (L->down_q41 && L->shape.I / 32 > 32) L->mfma_min = 0;
     if (const char *env = std::getenv("MOE_FFN_DECODE")) L->decode_mode = std::atoi(env) ? 1 : 0;
     if (const char *env = std::getenv("MOE_FFN_STREAMS")) L->two_streams = std::atoi(env) != 1;
     int cus = 0;
@@ -681,8 +677,7 @@ int moe_ffn_expert_down(moe_ffn_layer *L, int expert, const void *middle_q8, int
         !aligned(error, 4) || columns < 1 || columns > L->cfg.max_tokens || (down_dots && !aligned(down_dots, 4)) ||
         path < 0 || path > 2)
         return kInvalid;
-    if (L->down_q41 && path == MOE_PATH_MFMA) return hipErrorNotSupported;   // Q4_1 down: streaming kernels only
-    const bool mfma = path != MOE_PATH_STREAM && !L->down_q41;
+    const bool mfma = path != MOE_PATH_STREAM;
     if (mfma && !aligned(y, 16)) return kInvalid;   // the MFMA down kernel stores float4 rows
     const auto s = static_cast<hipStream_t>(stream);
     const Shape &sh = L->shape;

@@ -26,6 +26,7 @@
 #include "moe_device.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 #pragma clang fp contract(off)
 
@@ -105,10 +106,31 @@ __device__ __forceinline__ void scale_block(float (&acc)[16], v16i r, uint32_t h
     }
 }
 
+// Q4_1 blocks {d4, m4, codes}: the reference's per-fragment value is
+// fma(float(I_f), half(d4*d8), half(m4*s8) / 2) (src/cpu_expert.cpp:167-194),
+// i.e. per block half(d4*d8) * I + half(m4*s8) with both products rounded to
+// fp16 (d4*d8 and m4*s8 are exact in fp32: fp16 times fp16).  Here, per
+// block: acc = fma(I, dd, acc) + ms with the same two fp16 roundings; only
+// the fp32 summation order is this kernel's own.
+__device__ __forceinline__ void scale_block_q41(float (&acc)[16], v16i r, uint32_t head, const uint32_t (&d4)[8],
+                                                const uint32_t (&m4)[8]) {
+    const v16f f = __builtin_bit_cast(v16f, r);
+    const float d8 = half_lo(head), s8 = half_hi(head);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const float I = f[v] - kMagicF;   // exact: F = 12582912 + I
+        const float d = (v & 1) ? half_hi(d4[v >> 1]) : half_lo(d4[v >> 1]);
+        const float mn = (v & 1) ? half_hi(m4[v >> 1]) : half_lo(m4[v >> 1]);
+        const float dd = h2f(f2h(d * d8)), ms = h2f(f2h(mn * s8));
+        acc[v] = fmaf(I, dd, acc[v]) + ms;
+    }
+}
+
 // What one wave needs to project its 32 weight rows against up to kSubs
 // token tiles.  Offsets are per lane; per-block steps are uniform.
 struct TileArgs {
     __amdgpu_buffer_rsrc_t wr, sr, xr, hr;   // weight codes, weight scales, activation codes, activation heads
+    __amdgpu_buffer_rsrc_t mr;               // Q4_1: weight mins (the scales' layout); unused for Q4_0
     uint32_t w_off;                          // lane's A row (block b at + 16 b)
     uint32_t s_off0, s_off1, s_step;         // lane's two 16-byte scale groups (block b at + b s_step)
     uint32_t x_off[kSubs], h_off[kSubs];     // lane's token rows (block b at + 32 b / + 4 b)
@@ -128,18 +150,22 @@ __device__ __forceinline__ int acc_row(int v, int h) {
 }
 
 struct Loads {
-    uint4 w, d0, d1;
+    uint4 w, d0, d1, m0, m1;
     uint4 x[kSubs];
     uint32_t hd[kSubs];
 };
 
-template<int NS>
+template<int NS, bool Q41 = false>
 __device__ __forceinline__ Loads tile_loads(const TileArgs &t, int b) {
     Loads l;
     const uint32_t ub = static_cast<uint32_t>(b);
     l.w = buffer_load16(t.wr, t.w_off, ub * 16u);
     l.d0 = buffer_load16(t.sr, t.s_off0, ub * t.s_step);
     l.d1 = buffer_load16(t.sr, t.s_off1, ub * t.s_step);
+    if constexpr (Q41) {
+        l.m0 = buffer_load16(t.mr, t.s_off0, ub * t.s_step);
+        l.m1 = buffer_load16(t.mr, t.s_off1, ub * t.s_step);
+    }
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         l.x[s] = buffer_load16(t.xr, t.x_off[s], ub * 32u);
@@ -148,14 +174,15 @@ __device__ __forceinline__ Loads tile_loads(const TileArgs &t, int b) {
     return l;
 }
 
-// acc[s] = -8 * sum_b d4 s8 + sum_b d4 round(I d8) for the NS token tiles.
+// acc[s] = -8 * sum_b d4 s8 + sum_b d4 round(I d8) for the NS token tiles
+// (Q41: sum_b of scale_block_q41's terms from +0).
 // The loads of block b + 1 are issued before block b is computed.
-template<int NS, bool Dbg, bool Down>
+template<int NS, bool Dbg, bool Down, bool Q41 = false>
 __device__ __forceinline__ void tile_project(const TileArgs &t, float (&acc)[kSubs][16]) {
     v16f corr[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) corr[s] = v16f{};
-    for (int c = 0; c < t.nb; c += 16) {
+    for (int c = 0; c < (Q41 ? 0 : t.nb); c += 16) {
         const int kb0 = c + 8 * t.h;
         uint32_t dw[4];
 #pragma unroll
@@ -176,16 +203,17 @@ __device__ __forceinline__ void tile_project(const TileArgs &t, float (&acc)[kSu
 #pragma unroll
     for (int s = 0; s < NS; ++s)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[s][v] = -8.0f * corr[s][v];
+        for (int v = 0; v < 16; ++v) acc[s][v] = Q41 ? 0.0f : -8.0f * corr[s][v];
 
     v16i magic;
 #pragma unroll
     for (int v = 0; v < 16; ++v) magic[v] = kMagic;
-    Loads cur = tile_loads<NS>(t, 0);
+    Loads cur = tile_loads<NS, Q41>(t, 0);
 #pragma unroll 1
     for (int b = 0; b < t.nb; ++b) {
-        const Loads nxt = tile_loads<NS>(t, std::min(b + 1, t.nb - 1));
+        const Loads nxt = tile_loads<NS, Q41>(t, std::min(b + 1, t.nb - 1));
         const uint32_t d4[8] = {cur.d0.x, cur.d0.y, cur.d0.z, cur.d0.w, cur.d1.x, cur.d1.y, cur.d1.z, cur.d1.w};
+        const uint32_t m4[8] = {cur.m0.x, cur.m0.y, cur.m0.z, cur.m0.w, cur.m1.x, cur.m1.y, cur.m1.z, cur.m1.w};
         const v4i A = {static_cast<int>((cur.w.x >> t.shift) & kNibbles), static_cast<int>((cur.w.y >> t.shift) & kNibbles),
                        static_cast<int>((cur.w.z >> t.shift) & kNibbles), static_cast<int>((cur.w.w >> t.shift) & kNibbles)};
         v16i r[NS];
@@ -197,7 +225,8 @@ __device__ __forceinline__ void tile_project(const TileArgs &t, float (&acc)[kSu
         }
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            scale_block(acc[s], r[s], cur.hd[s], d4);
+            if constexpr (Q41) scale_block_q41(acc[s], r[s], cur.hd[s], d4, m4);
+            else scale_block(acc[s], r[s], cur.hd[s], d4);
             if constexpr (Dbg) {
                 const int j = kSub * s + t.m;
                 if (t.dots && j < t.ncols)
@@ -211,13 +240,13 @@ __device__ __forceinline__ void tile_project(const TileArgs &t, float (&acc)[kSu
     }
 }
 
-template<bool Dbg, bool Down>
+template<bool Dbg, bool Down, bool Q41 = false>
 __device__ __forceinline__ void tile_dispatch(const TileArgs &t, int nsub, float (&acc)[kSubs][16]) {
     switch (nsub) {
-    case 1: tile_project<1, Dbg, Down>(t, acc); break;
-    case 2: tile_project<2, Dbg, Down>(t, acc); break;
-    case 3: tile_project<3, Dbg, Down>(t, acc); break;
-    default: tile_project<4, Dbg, Down>(t, acc); break;
+    case 1: tile_project<1, Dbg, Down, Q41>(t, acc); break;
+    case 2: tile_project<2, Dbg, Down, Q41>(t, acc); break;
+    case 3: tile_project<3, Dbg, Down, Q41>(t, acc); break;
+    default: tile_project<4, Dbg, Down, Q41>(t, acc); break;
     }
 }
 
@@ -758,12 +787,25 @@ struct DownStage {
     uint32_t hd[kDnMaxBlocks][kMfmaTile];    // middle heads [block][pair]
     uint4 d4[4][kDnMaxBlocks][4];            // per wave: scales [block][32 slots]
 };
+// Q4_1 down rows also stage their mins (80 KiB: two workgroups per CU).
+struct DownStageQ41 : DownStage {
+    uint4 m4[4][kDnMaxBlocks][4];            // per wave: mins [block][32 slots]
+};
 
-template<int NS, bool Dbg>
-__device__ __forceinline__ void down_staged(const FfnArgs &a, const DownStage &st, int wave, const uint4 (&wa)[kDnMaxBlocks],
-                                            int nbi, int first, int ncols, int R0, int prow, int pslot, float (&acc)[kSubs][16]) {
+// m4s: the wave's staged Q4_1 mins ([block][4] chunks as st.d4[wave]), or
+// nullptr for Q4_0 rows.
+template<int NS, bool Dbg, bool Q41>
+__device__ __forceinline__ void down_staged(const FfnArgs &a, const DownStage &st, const uint4 (*m4s)[4], int wave,
+                                            const uint4 (&wa)[kDnMaxBlocks], int nbi, int first, int ncols, int R0, int prow,
+                                            int pslot, float (&acc)[kSubs][16]) {
     const int lane = threadIdx.x & 63, m = lane & 31, h = lane >> 5, shift = 4 * h;
     const uint16_t *d4h = reinterpret_cast<const uint16_t *>(&st.d4[wave][0][0]);
+    if constexpr (Q41) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[s][v] = 0.0f;
+    } else {
     // Seed: -8 * sum_b d4 s8, 16 blocks in one f16 MFMA.
     uint32_t dw[4];
 #pragma unroll
@@ -788,6 +830,7 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const DownStage &s
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[s][v] = -8.0f * corr[v];
     }
+    }
     v16i magic;
 #pragma unroll
     for (int v = 0; v < 16; ++v) magic[v] = kMagic;
@@ -797,6 +840,12 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const DownStage &s
         const uint4 w = wa[b];
         const uint4 d0 = st.d4[wave][b][2 * h], d1 = st.d4[wave][b][2 * h + 1];
         const uint32_t d4[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+        uint32_t m4[8] = {};
+        if constexpr (Q41) {
+            const uint4 n0 = m4s[b][2 * h], n1 = m4s[b][2 * h + 1];
+            m4[0] = n0.x; m4[1] = n0.y; m4[2] = n0.z; m4[3] = n0.w;
+            m4[4] = n1.x; m4[5] = n1.y; m4[6] = n1.z; m4[7] = n1.w;
+        }
         const v4i A = {static_cast<int>((w.x >> shift) & kNibbles), static_cast<int>((w.y >> shift) & kNibbles),
                        static_cast<int>((w.z >> shift) & kNibbles), static_cast<int>((w.w >> shift) & kNibbles)};
         v16i r[NS];
@@ -808,7 +857,8 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const DownStage &s
         }
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            scale_block(acc[s], r[s], st.hd[b][kSub * s + m], d4);
+            if constexpr (Q41) scale_block_q41(acc[s], r[s], st.hd[b][kSub * s + m], d4, m4);
+            else scale_block(acc[s], r[s], st.hd[b][kSub * s + m], d4);
             if constexpr (Dbg) {
                 const int j = kSub * s + m;
                 if (a.down_dots && j < ncols)
@@ -822,9 +872,9 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const DownStage &s
     }
 }
 
-template<bool Dbg>
+template<bool Dbg, bool Q41>
 __global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
-    __shared__ DownStage st;
+    __shared__ std::conditional_t<Q41, DownStageQ41, DownStage> st;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = a.shape.I / 32;
@@ -885,13 +935,21 @@ __global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
         if (active)
             for (int c = lane; c < nbi * 4; c += 64)
                 st.d4[wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(scales)[c];
+        const uint4 (*m4s)[4] = nullptr;
+        if constexpr (Q41) {
+            const uint16_t *mins = a.bank.down_mins + rbase * nbi;   // same layout as the scales
+            if (active)
+                for (int c = lane; c < nbi * 4; c += 64)
+                    st.m4[wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(mins)[c];
+            m4s = st.m4[wave];
+        }
         __syncthreads();
         if (!active) return;
         switch (nsub) {
-        case 1: down_staged<1, Dbg>(a, st, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
-        case 2: down_staged<2, Dbg>(a, st, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
-        case 3: down_staged<3, Dbg>(a, st, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
-        default: down_staged<4, Dbg>(a, st, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
+        case 1: down_staged<1, Dbg, Q41>(a, st, m4s, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
+        case 2: down_staged<2, Dbg, Q41>(a, st, m4s, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
+        case 3: down_staged<3, Dbg, Q41>(a, st, m4s, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
+        default: down_staged<4, Dbg, Q41>(a, st, m4s, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
         }
     } else {
         if (!active) return;   // no barrier on this path
@@ -899,6 +957,7 @@ __global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
         TileArgs t;
         t.wr = buffer_rsrc(a.bank.down_codes + rbase * row_bytes, 32u * row_bytes);
         t.sr = buffer_rsrc(scales, static_cast<uint32_t>(nbi) * 64u);
+        t.mr = buffer_rsrc(Q41 ? a.bank.down_mins + rbase * nbi : scales, static_cast<uint32_t>(nbi) * 64u);
         t.xr = buffer_rsrc(a.mq.codes, pairs * static_cast<uint32_t>(nbi) * 32u);
         t.hr = buffer_rsrc(a.mq.heads, pairs * static_cast<uint32_t>(nbi) * 4u);
         t.w_off = static_cast<uint32_t>(prow) * row_bytes;
@@ -922,7 +981,7 @@ __global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
         t.ncols = ncols;
         t.m = m;
         t.h = h;
-        tile_dispatch<Dbg, true>(t, nsub, acc);
+        tile_dispatch<Dbg, true, Q41>(t, nsub, acc);
     }
 
     // Lane half h holds rows 4q + 2h (v = q) and 4q + 2h + 1 (v = 8 + q),
@@ -1117,8 +1176,12 @@ hipError_t launch_gate_up_mfma(const FfnArgs &a, hipStream_t s) {
 
 hipError_t launch_down_mfma(const FfnArgs &a, hipStream_t s) {
     const unsigned grid = mfma_grid(a, (a.shape.H + 127) / 128);
-    if (a.down_dots) k_down_mfma<true><<<grid, 256, 0, s>>>(a);
-    else k_down_mfma<false><<<grid, 256, 0, s>>>(a);
+    const bool q41 = a.bank.down_mins != nullptr;
+    if (a.down_dots) {
+        if (q41) k_down_mfma<true, true><<<grid, 256, 0, s>>>(a);
+        else k_down_mfma<true, false><<<grid, 256, 0, s>>>(a);
+    } else if (q41) k_down_mfma<false, true><<<grid, 256, 0, s>>>(a);
+    else k_down_mfma<false, false><<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -57,7 +57,7 @@ typedef struct moe_ffn_config {
     int top_k;         /* routes per token, 1..32, <= experts */
     int has_shared;    /* 1: one shared expert, always routed (src/session.hip:1384-1410) */
     int max_tokens;    /* capacity of forward(), 1..65536 */
-    int down_type;     /* MOE_DOWN_Q4_0 (0) or MOE_DOWN_Q4_1 (Q4_1 down rows run on the streaming kernels) */
+    int down_type;     /* MOE_DOWN_Q4_0 (0) or MOE_DOWN_Q4_1 (1): format of the down matrices */
 } moe_ffn_config;
 
 typedef struct moe_ffn_layer moe_ffn_layer;

@@ -6,9 +6,10 @@ the oracle restates that order and is pinned bit for bit against the compiled
 reference (tests/golden/cpu_expert_2560x640_q41.npz).
 
 Bars: per-block int32 dots and middle Q8 bytes bit-exact; outputs bit-exact
-where the kernel follows the reference order (H/32 blocks of I <= 512 per
-down row: k_down_lean and the decode down+fold), otherwise within the
-north_star's 1e-3 rms.
+where the kernel follows the reference order (the streaming down kernels and
+the decode down+fold); the int8-MFMA down kernel keeps the reference's fp16
+roundings of d4*d8 and m4*s8 per block but sums blocks in its own order, so
+its outputs are held to 1e-5 rms (the north_star bar is 1e-3 rms).
 """
 import os
 
@@ -86,7 +87,8 @@ def test_q41_expert_stages_bit_exact(q41_expert, columns):
     """Single expert: gate/up middle Q8 equal to the oracle's; down per-block
     dots bit-exact; the down projection (k_down_lean, reference order) bit-
     identical to the oracle's Q4_1 cpu_expert order; the non-debug kernel
-    gives the same bits; the MFMA down path is refused for Q4_1."""
+    gives the same bits; the int8-MFMA down kernel's dots are bit-exact and
+    its outputs within 1e-5 rms."""
     L, g, u, d = q41_expert["layer"], q41_expert["g"], q41_expert["u"], q41_expert["d"]
     x = W.activations(columns, seed=710 + columns)
     xq = O.quantize_q8(x)
@@ -102,15 +104,20 @@ def test_q41_expert_stages_bit_exact(q41_expert, columns):
     rd2 = L.expert_down(0, dev(q8_bytes(mq).reshape(columns, -1)), columns, path=moe_ffn.PATH_STREAM)
     assert np.array_equal(host(rd2["y"]), y)
     assert int(host(rd["error"])[0]) == 0
-    with pytest.raises(moe_ffn.MoeError):
-        L.expert_down(0, dev(q8_bytes(mq).reshape(columns, -1)), columns, path=moe_ffn.PATH_MFMA)
+    rm = L.expert_down(0, dev(q8_bytes(mq).reshape(columns, -1)), columns, path=moe_ffn.PATH_MFMA, dots=True)
+    assert np.array_equal(host(rm["down_dots"]), host(rd["down_dots"]))
+    assert_close(host(rm["y"]), ref["y"], 1e-5, "Q4_1 MFMA down")
+    rm2 = L.expert_down(0, dev(q8_bytes(mq).reshape(columns, -1)), columns, path=moe_ffn.PATH_MFMA)
+    assert np.array_equal(host(rm2["y"]), host(rm["y"]))
+    assert int(host(rm["error"])[0]) == 0
 
 
 def test_q41_reference_shape_expert_vs_golden():
     """The compiled reference's Q4_1 cpu_expert at its 2560/640 shape, fed the
     reference's own middle Q8: per-block dots bit-exact and the down output
     (the lean kernel with two blocks per lane, the reference's order)
-    bit-identical to the reference's."""
+    bit-identical to the reference's; the int8-MFMA down kernel (20 blocks a
+    row: its unstaged path) gives the same dots and outputs within 1e-5 rms."""
     f = np.load(os.path.join(GOLDEN, "cpu_expert_2560x640_q41.npz"), allow_pickle=False)
     g, u, _ = expert_weights(2560, 640)
     d = q4_1_matrix(404, 640, 2560)
@@ -121,6 +128,9 @@ def test_q41_reference_shape_expert_vs_golden():
     y = host(rd["y"])
     assert np.array_equal(y.view(np.uint32), f["y"].view(np.uint32))
     assert np.array_equal(y.view(np.uint32), O.matrix_gpu_order_q41(d, 640, 2560, mq).view(np.uint32))
+    rm = layer.expert_down(0, dev(mq), 3, path=moe_ffn.PATH_MFMA, dots=True)
+    assert np.array_equal(host(rm["down_dots"]), host(rd["down_dots"]))
+    assert_close(host(rm["y"]), f["y"], 1e-5, "Q4_1 MFMA down at 2560/640")
     layer.close()
 
 
@@ -189,12 +199,13 @@ def test_q41_decode_reference_shape_bit_exact():
     L.close()
 
 
-def test_q41_grouped_layer_bit_exact(q41_layer):
+def test_q41_grouped_layer(q41_layer):
     """300 Zipf(1.3) tokens on the grouped path: groups of >= 32 pairs run
-    gate/up on int8 MFMA and their Q4_1 down on the lean kernel over MFMA
-    items, smaller groups stream; every kernel keeps the reference's order,
-    so 32 sampled tokens are bit-identical to the oracle, and a 5-token
-    prefix batch gives the same bits."""
+    gate/up and the Q4_1 down on int8 MFMA, smaller groups stream.  Every
+    middle Q8 row of 32 sampled tokens is byte-equal to the oracle's and their
+    outputs are within 1e-5 rms; a 5-token prefix batch (fewer than 1024
+    routes: every group streams, in the reference's order throughout) is
+    bit-identical to the oracle."""
     L, E = q41_layer["layer"], q41_layer["E"]
     x = W.activations(300, seed=741)
     ids, w = W.routes_zipf(300, 1.3, experts=E, seed=742)
@@ -208,9 +219,31 @@ def test_q41_grouped_layer_bit_exact(q41_layer):
     mask[sample] = 1
     ref = O.moe_layer(x, H, I, E, q41_layer["bank"], ids, w, shared_q4=q41_layer["shared"], token_mask=mask,
                       down_q41=True)
-    assert np.array_equal(yh[sample].view(np.uint32), ref["y"][sample].view(np.uint32))
+    assert_close(yh[sample], ref["y"][sample], 1e-5, "Q4_1 grouped layer")
+    # Middle rows: debug_last holds this forward's grouped middle Q8 rows.
+    nbi = I // 32
+    mid = host(L.debug_last(300)["middle_q8"]).reshape(-1, nbi, 36)
+    groups = O.route_groups(ids, w, E)
+    xq = O.quantize_q8(x)
+    eb = moe_ffn.expert_bytes(H, I, Q41)
+    experts = split(q41_layer["bank"], E)
+    pos = set(int(t) for t in sample)
+    P = int(groups["offsets"][-1])
+    for p in range(P):
+        t = int(groups["token"][p])
+        if t in pos:
+            g, u, dn = experts[int(groups["expert"][p])]
+            ro = O.expert_forward(g, u, dn, H, I, xq[t:t + 1], down_q41=True)
+            assert np.array_equal(mid[p], q8_bytes(ro["middle_q8"]).reshape(nbi, 36)), p
+    sg, su, sd = split(q41_layer["shared"], 1)[0]
+    for t in sample:
+        ro = O.expert_forward(sg, su, sd, H, I, xq[t:t + 1], down_q41=True)
+        assert np.array_equal(mid[P + int(t)], q8_bytes(ro["middle_q8"]).reshape(nbi, 36)), ("shared", t)
+    assert eb * E == len(q41_layer["bank"])
     y5, _ = L.forward(dev(x[:5].copy()), dev(ids[:5]), dev(w[:5]))
-    assert np.array_equal(host(y5), yh[:5])
+    ref5 = O.moe_layer(x[:5].copy(), H, I, E, q41_layer["bank"], ids[:5], w[:5], shared_q4=q41_layer["shared"],
+                       down_q41=True)
+    assert np.array_equal(host(y5).view(np.uint32), ref5["y"].view(np.uint32))
 
 
 def test_q41_tensors_and_synthetic_banks():
@@ -252,9 +285,9 @@ def test_q41_tensors_and_synthetic_banks():
 def test_q41_small_batch_route_gate():
     """Batches of fewer than 1024 routes stream every group (few MFMA items
     cannot fill the chip); MOE_FFN_MFMA_ROUTES=0 lifts the gate.  A single
-    2560/640 expert with 128 tokens (one 128-pair group) gives the same bits
-    either way: the MFMA gate/up and the lean down over MFMA items keep the
-    streaming kernels' order.  Sampled tokens match the oracle bit for bit."""
+    2560/640 expert with 128 tokens (one 128-pair group): streamed, sampled
+    tokens match the oracle bit for bit; on MFMA (gate/up in the reference's
+    order, the Q4_1 down in its own block order) within 1e-5 rms."""
     H2, I2, N = 2560, 640, 128
     bank = W.q4_bank(1, hidden=H2, intermediate=I2, seed=761, down_type=Q41)
     x = W.activations(N, hidden=H2, seed=762)
@@ -270,9 +303,9 @@ def test_q41_small_batch_route_gate():
         L.close()
     assert out[False][1]["mfma_items"] == 0 and out[False][1]["stream_items"] > 0
     assert out[True][1]["mfma_items"] == 1 and out[True][1]["stream_items"] == 0
-    assert np.array_equal(out[False][0].view(np.uint32), out[True][0].view(np.uint32))
     sample = np.array([0, 1, 63, 64, 127])
     mask = np.zeros(N, np.uint8)
     mask[sample] = 1
     ref = O.moe_layer(x, H2, I2, 1, bank, ids, w, token_mask=mask, down_q41=True)
     assert np.array_equal(out[False][0][sample].view(np.uint32), ref["y"][sample].view(np.uint32))
+    assert_close(out[True][0][sample], ref["y"][sample], 1e-5, "Q4_1 128-pair group on MFMA")
