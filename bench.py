@@ -251,7 +251,7 @@ def reference_components():
     import workloads as W
     H, I = 2560, 640
     dev0 = "cuda:0"
-    out = {"expert_forward_us": {}, "linear_us": {}}
+    out = {"expert_forward_us": {}, "expert_run": {}, "linear_us": {}}
     bank = W.q4_bank(1, hidden=H, intermediate=I, seed=4100, down_type=moe_ffn.DOWN_Q4_1)
     L = moe_ffn.MoeLayer(H, I, 1, 1, False, 128, experts_q4=bank, down_type=moe_ffn.DOWN_Q4_1)
     for n in (1, 2, 3, 128):
@@ -263,6 +263,15 @@ def reference_components():
         out["expert_forward_us"][str(n)] = time_calls(lambda: L.forward(x, ids, w, y=y, error=err)) * 1e6
         if int(err.cpu()[0]) != 0:
             raise RuntimeError("reference-shape expert flagged an error")
+        # GpuExpert::run's protocol (src/expert_main.cpp:88-90, 135-138): the
+        # harness input, 50 repeats (5 at 128 columns), ExpertTiming fields.
+        i = np.arange(H * n, dtype=np.float32)
+        xh = (np.float32(0.7) * np.sin(i * np.float32(0.137)) +
+              np.float32(0.2) * np.cos(i * np.float32(0.071))).astype(np.float32).reshape(n, H)
+        _, t, flags = L.expert_run(0, xh, repeats=5 if n == 128 else 50)
+        if flags:
+            raise RuntimeError("expert_run flagged an error")
+        out["expert_run"][str(n)] = t
     L.close()
     # B8 decode at this shape, Q4_1 downs (the checkpoint's layers 0-5):
     # 512 experts + shared, top-10, 64 rotated route sets.
@@ -342,7 +351,7 @@ def main():
     ap.add_argument("--no-linear", action="store_true", help="skip the quantized linear projections")
     ap.add_argument("--no-graph", action="store_true", help="skip the graph-captured stack passes")
     ap.add_argument("--no-refshapes", action="store_true", help="skip the reference's component shapes (2560/640)")
-    ap.add_argument("--only", choices=["b8", "4k", "16k", "stack"],
+    ap.add_argument("--only", choices=["b8", "4k", "16k", "stack", "refshapes"],
                     help="run one section alone (for profiler runs); the JSON line then holds that section only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy x5 (FETCH_SIZE/WRITE_SIZE scale for rocprofv3 --pmc)")
@@ -368,7 +377,8 @@ def main():
     only = args.only
     want = lambda section: only is None or only == section
     if only is not None:
-        args.no_cpu = args.no_linear = args.no_refshapes = True
+        args.no_cpu = args.no_linear = True
+        args.no_refshapes = only != "refshapes"
         args.no_prefill = only not in ("4k", "16k")
         args.no_16k = only != "16k"
         args.no_stack = only != "stack"

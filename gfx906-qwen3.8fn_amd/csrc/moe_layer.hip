@@ -3,12 +3,14 @@
 // Boundary conventions follow the reference launchers (src/hip/linear.cuh:35-45,
 // src/hip/session_ops.cuh:22-45): every argument is checked before the first
 // HIP call, launchers only enqueue on the caller's stream, and only create /
-// destroy / export allocate or synchronise.
+// destroy / export, the diagnostics and the expert timing harness allocate or
+// synchronise.
 #include "moe_expf.h"
 #include "moe_ffn.h"
 #include "moe_internal.hpp"
 
 #include <algorithm>
+#include <chrono>
 #include <cstdlib>
 #include <cstring>
 #include <new>
@@ -22,6 +24,10 @@ struct moe_ffn_layer {
     moe_ffn_config cfg{};
     int device = 0;
     Shape shape{};
+    // Weight upload time (ExpertTiming::upload_ms): from the start of the
+    // bank allocation until the repacked planes are complete.
+    std::chrono::steady_clock::time_point create_start{};
+    double upload_ms = 0.0;
     void *bank_mem = nullptr;
     size_t bank_bytes = 0;
     moe::Bank bank{};
@@ -246,6 +252,7 @@ int create_common(const moe_ffn_config *config, int device, moe_ffn_layer **laye
     L->device = device;
     L->shape = shape_of(*config);
     L->down_q41 = config->down_type == MOE_DOWN_Q4_1;
+    L->create_start = std::chrono::steady_clock::now();
     int r = alloc_bank(L);
     if (r == hipSuccess && (hipStreamCreateWithFlags(&L->side, hipStreamNonBlocking) != hipSuccess ||
                             hipEventCreateWithFlags(&L->fork, hipEventDisableTiming) != hipSuccess ||
@@ -331,6 +338,10 @@ void profile_free(moe_ffn_layer *L) {
     L->prof_capacity = L->prof_used = 0;
 }
 
+void mark_uploaded(moe_ffn_layer *L) {
+    L->upload_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - L->create_start).count();
+}
+
 moe::FfnArgs base_args(moe_ffn_layer *L, int tokens, int *error) {
     moe::FfnArgs a{};
     a.shape = L->shape;
@@ -368,6 +379,7 @@ int moe_ffn_create(const moe_ffn_config *config, const void *experts_q4, const v
     int r = create_common(config, device, layer, L);
     if (r != hipSuccess) return r;
     r = upload(L, experts_q4, shared_q4, false);
+    mark_uploaded(L);
     if (r == hipSuccess) r = finish_create(L);
     if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
     *layer = L;
@@ -383,6 +395,7 @@ int moe_ffn_create_from_device(const moe_ffn_config *config, const void *experts
     int r = create_common(config, device, layer, L);
     if (r != hipSuccess) return r;
     r = upload(L, experts_q4_device, shared_q4_device, true);
+    mark_uploaded(L);
     if (r == hipSuccess) r = finish_create(L);
     if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
     *layer = L;
@@ -400,6 +413,7 @@ int moe_ffn_create_tensors(const moe_ffn_config *config, const void *gate_exps, 
     const void *const routed[3] = {gate_exps, up_exps, down_exps};
     const void *const shared[3] = {shared_gate, shared_up, shared_down};
     r = upload_tensors(L, routed, shared);
+    mark_uploaded(L);
     if (r == hipSuccess) r = finish_create(L);
     if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
     *layer = L;
@@ -417,6 +431,7 @@ int moe_ffn_create_synthetic(const moe_ffn_config *config, uint64_t seed, int de
                                           pl.blocks_per_row, pl.group, seed, nullptr);
     }
     if (r == hipSuccess) r = hipDeviceSynchronize();
+    mark_uploaded(L);
     if (r == hipSuccess) r = finish_create(L);
     if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
     *layer = L;
@@ -691,6 +706,74 @@ int moe_ffn_expert_down(moe_ffn_layer *L, int expert, const void *middle_q8, int
     a.out_stride_k = 1;
     a.down_dots = down_dots;
     return moe::launch_down(a, mfma, s);
+}
+
+int moe_ffn_expert_run(moe_ffn_layer *L, int expert, const float *x, int columns, float *y, int repeats, int path,
+                       int *flags, moe_expert_timing *timing, void *stream) {
+    if (!L || expert < 0 || expert >= L->shape.Ep || !x || !y || !flags || !timing || columns < 1 ||
+        columns > L->cfg.max_tokens || repeats < 1 || repeats > 10000 || path < 0 || path > 2)
+        return kInvalid;
+    using Clock = std::chrono::steady_clock;
+    const Shape &sh = L->shape;
+    bool mfma = path == MOE_PATH_MFMA;
+    if (path == MOE_PATH_AUTO) {   // forward()'s rule for one group of `columns` pairs
+        const int active = columns < L->mfma_routes ? 0 : L->mfma_min;
+        mfma = active > 0 && columns >= active;
+    }
+    // x and y live in the contribution buffer (>= 2 * max_tokens rows of H
+    // floats); y starts a whole number of 128-byte rows in, as the MFMA down
+    // kernel's float4 stores need.
+    const size_t elems = static_cast<size_t>(columns) * sh.H;
+    float *xd = L->contrib, *yd = L->contrib + elems;
+    int *err = L->diag_error;
+    const auto s = static_cast<hipStream_t>(stream);
+    if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
+    // One forward: quantize x, gate/up + SiLU*up + Q8, down (the work list
+    // of the single group is built once, before the warm-up).
+    auto pass = [&]() -> hipError_t {
+        hipError_t r = moe::launch_quantize_planes(xd, L->xq, sh.H, columns, err, s);
+        moe::FfnArgs a = base_args(L, columns, err);
+        a.pairs_bound = columns;
+        a.mfma_min = mfma ? 1 : 0;
+        a.out = yd;
+        a.out_stride_k = 1;
+        if (r == hipSuccess) r = moe::launch_gate_up(a, mfma, s);
+        if (r == hipSuccess) r = moe::launch_down(a, mfma, s);
+        return r;
+    };
+    auto read_flags = [&](int *value) -> hipError_t {
+        hipError_t r = hipMemcpyAsync(value, err, sizeof(int), hipMemcpyDeviceToHost, s);
+        return r == hipSuccess ? hipStreamSynchronize(s) : r;
+    };
+    hipError_t r = moe::launch_fill_u32(reinterpret_cast<uint32_t *>(err), 0u, 1, s);
+    if (r == hipSuccess) r = moe::launch_single_expert_items(sh, L->routes, expert, columns, mfma, s);
+    if (r == hipSuccess) r = hipMemcpyAsync(xd, x, elems * sizeof(float), hipMemcpyHostToDevice, s);
+    if (r == hipSuccess) r = pass();   // warm-up outside the timing
+    int value = 0;
+    if (r == hipSuccess) r = read_flags(&value);
+    if (r != hipSuccess) return r;
+    *flags = value;
+    if (value) return hipSuccess;
+    hipEvent_t begin = nullptr, end = nullptr;
+    if (hipEventCreate(&begin) != hipSuccess) return hipErrorOutOfMemory;
+    if (hipEventCreate(&end) != hipSuccess) { (void)hipEventDestroy(begin); return hipErrorOutOfMemory; }
+    const auto start = Clock::now();
+    r = hipEventRecord(begin, s);
+    for (int i = 0; i < repeats && r == hipSuccess; ++i) r = pass();
+    if (r == hipSuccess) r = hipEventRecord(end, s);
+    float ms = 0.0f;
+    if (r == hipSuccess) r = hipEventSynchronize(end);
+    if (r == hipSuccess) r = hipEventElapsedTime(&ms, begin, end);
+    if (r == hipSuccess) r = hipMemcpyAsync(&value, err, sizeof(int), hipMemcpyDeviceToHost, s);
+    if (r == hipSuccess) r = hipMemcpyAsync(y, yd, elems * sizeof(float), hipMemcpyDeviceToHost, s);
+    if (r == hipSuccess) r = hipStreamSynchronize(s);
+    const double wall = std::chrono::duration<double, std::milli>(Clock::now() - start).count();
+    (void)hipEventDestroy(begin);
+    (void)hipEventDestroy(end);
+    if (r != hipSuccess) return r;
+    *flags = value;
+    *timing = moe_expert_timing{L->upload_ms, static_cast<double>(ms) / repeats, wall / repeats};
+    return hipSuccess;
 }
 
 int moe_combine(const float *contributions, const float *weights, const float *shared, const float *shared_gate,

@@ -42,6 +42,12 @@ class Config(ctypes.Structure):
                 ("down_type", ctypes.c_int)]
 
 
+class ExpertTiming(ctypes.Structure):
+    """moe_expert_timing (ExpertTiming, src/gpu_expert.hpp:6)."""
+    _fields_ = [("upload_ms", ctypes.c_double), ("resident_ms", ctypes.c_double),
+                ("completed_wall_ms", ctypes.c_double)]
+
+
 _lib = None
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -69,6 +75,8 @@ def library():
         lib.moe_ffn_group_routes.argtypes = [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P]
         lib.moe_ffn_expert_gate_up.argtypes = [_P, _I, _P, _I, _P, _P, _P, _P, _I, _P, _P]
         lib.moe_ffn_expert_down.argtypes = [_P, _I, _P, _I, _P, _P, _I, _P, _P]
+        lib.moe_ffn_expert_run.argtypes = [_P, _I, _P, _I, _P, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(ExpertTiming),
+                                           _P]
         lib.moe_combine.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P]
         lib.moe_ffn_debug_last.argtypes = [_P, _P, _P, _P, _P, _P]
         lib.moe_ffn_replay_stage.argtypes = [_P, _I, _P]
@@ -318,6 +326,26 @@ class MoeLayer:
         _check(library().moe_ffn_expert_down(self.handle, expert, _ptr(middle_q8), columns, _ptr(y), _ptr(dd), path,
                                              _ptr(error), _stream(stream)), "moe_ffn_expert_down")
         return dict(y=y, down_dots=dd, error=error)
+
+    def expert_run(self, expert, x, repeats, path=PATH_AUTO, stream=None):
+        """GpuExpert::run (src/hip/expert.hip:228-241): host float32 x
+        [columns][H] through one resident expert's whole forward, `repeats`
+        timed forwards.  Returns (y, timing dict, error word); y and timing are
+        None when the warm-up forward raised the error word."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim != 2 or x.shape[1] != self.H:
+            raise ValueError(f"x: expected [columns][{self.H}] float32, got {x.shape}")
+        columns = x.shape[0]
+        y = np.empty_like(x)
+        flags = _I(0)
+        t = ExpertTiming()
+        _check(library().moe_ffn_expert_run(self.handle, expert, ctypes.c_void_p(x.ctypes.data), columns,
+                                            ctypes.c_void_p(y.ctypes.data), repeats, path, ctypes.byref(flags),
+                                            ctypes.byref(t), _stream(stream)), "moe_ffn_expert_run")
+        if flags.value:
+            return None, None, flags.value
+        return y, dict(upload_ms=t.upload_ms, resident_ms=t.resident_ms,
+                       completed_wall_ms=t.completed_wall_ms), 0
 
 
 def expf_host(x):

@@ -167,6 +167,32 @@ int moe_ffn_expert_gate_up(moe_ffn_layer *layer, int expert, const void *x_q8, i
 int moe_ffn_expert_down(moe_ffn_layer *layer, int expert, const void *middle_q8, int columns,
                         float *y, int32_t *down_dots, int path, int *error, void *stream);
 
+/* Timing of one resident expert (ExpertTiming, src/gpu_expert.hpp:6).
+ *   upload_ms          create: weight allocation, copy and repack until complete
+ *   resident_ms        device time per forward (events around the repeats)
+ *   completed_wall_ms  host wall time per forward, from before the first timed
+ *                      forward until the output is back in host memory */
+typedef struct moe_expert_timing {
+    double upload_ms;
+    double resident_ms;
+    double completed_wall_ms;
+} moe_expert_timing;
+
+/* GpuExpert::run (src/gpu_expert.hpp:16, src/hip/expert.hip:228-241): one
+ * expert's whole forward, fp32 x -> Q8_1 -> gate/up -> SiLU*up -> Q8_1 ->
+ * down, on HOST buffers x [columns][H] and y [columns][H].  Uploads x once,
+ * runs one untimed forward and checks its error word, then times `repeats`
+ * forwards between events on `stream` and reads y back; synchronous.
+ * columns 1..max_tokens, repeats 1..10000.  path: MOE_PATH_STREAM or
+ * MOE_PATH_MFMA, or MOE_PATH_AUTO for the kernels forward() would give a
+ * group of `columns` pairs.  *flags receives the error word (bit 1:
+ * nonfinite x, bit 2: x not representable in Q8_1; the reference's
+ * check_error throws on either); when the warm-up raises it, the call
+ * returns 0 without timing (timing and y untouched).
+ * Uses the layer's workspace: calls on one layer must not overlap. */
+int moe_ffn_expert_run(moe_ffn_layer *layer, int expert, const float *x, int columns, float *y, int repeats,
+                       int path, int *flags, moe_expert_timing *timing, void *stream);
+
 /* Rank-order weighted combine (replaces launch_routed_fold +
  * launch_shared_sigmoid_add_rows, src/hip/session_ops.hip:307-324, 375-391):
  *   contributions [tokens][top_k][H] unweighted expert outputs
