@@ -501,12 +501,18 @@ struct HalfGroup {
 };
 
 // The operands of level-1 node p = 2g + q (leaves 4g + 2q and 4g + 2q + 1).
-// Loading half a line group at a time keeps the kernel at 149 VGPRs, three
-// waves per SIMD (a whole group in registers needed 211: two waves).
-__device__ __forceinline__ void half_load(const GuTile &t, uint32_t w_off, int p, HalfGroup &G) {
+// Loading half a line group at a time keeps the kernel at three waves per
+// SIMD (a whole group in registers needed 211 VGPRs: two waves).  The weight
+// half (8 VGPRs) of node p + 1 is loaded while node p computes (157 VGPRs;
+// 16K layer 5.42 -> 5.35 ms); the activation half as well would need 177
+// VGPRs, two waves per SIMD.
+__device__ __forceinline__ void half_load_w(const GuTile &t, uint32_t w_off, int p, uint4 (&w)[2]) {
     const uint32_t b0 = static_cast<uint32_t>(4 * (p >> 1) + 2 * (p & 1));
 #pragma unroll
-    for (int i = 0; i < 2; ++i) G.w[i] = buffer_load16(t.wr, w_off, (b0 + i) * 16u);
+    for (int i = 0; i < 2; ++i) w[i] = buffer_load16(t.wr, w_off, (b0 + i) * 16u);
+}
+__device__ __forceinline__ void half_load_x(const GuTile &t, int p, HalfGroup &G) {
+    const uint32_t b0 = static_cast<uint32_t>(4 * (p >> 1) + 2 * (p & 1));
 #pragma unroll
     for (int i = 0; i < 2; ++i) G.xa[i] = buffer_load16(t.xr, t.x_off, (b0 + i) * 32u);
 #pragma unroll
@@ -601,10 +607,15 @@ __device__ __forceinline__ void fold_tree_grouped(const GuTile &t, const GuStage
                                                   int lane, float (&res)[16]) {
     const int m = lane & 31, h = lane >> 5;
     float l1[16], l2[16];
+    uint4 wn[2];
+    half_load_w(t, w_off, 0, wn);
 #pragma unroll 1
     for (int p = 0; p < 16; ++p) {
         HalfGroup G;
-        half_load(t, w_off, p, G);
+        G.w[0] = wn[0];
+        G.w[1] = wn[1];
+        half_load_x(t, p, G);
+        half_load_w(t, w_off, p < 15 ? p + 1 : p, wn);   // node p + 1's weights in flight during node p
         float w[16], x[16];
         leaf_grouped<Dbg>(t, g, G, 0, 2 * p, m, h, w);
         leaf_grouped<Dbg>(t, g, G, 1, 2 * p + 1, m, h, x);
@@ -1057,7 +1068,8 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
         for (int q = 0; q < 4; ++q) {
             const int p = 4 * wave + q;
             HalfGroup G;
-            half_load(t, w_off, p, G);
+            half_load_w(t, w_off, p, G.w);
+            half_load_x(t, p, G);
             float w[16], x[16];
             leaf_grouped<false>(t, g, G, 0, 2 * p, m, h, w);
             leaf_grouped<false>(t, g, G, 1, 2 * p + 1, m, h, x);
