@@ -45,19 +45,21 @@ struct moe_ffn_layer {
     int *diag_error = nullptr;
     // Smallest group routed to the MFMA path (0 = streaming only).  An MFMA
     // tile spends the same exact-order epilogue on 32 token columns however
-    // many are filled, and a one-tile group streams its weights from HBM with
-    // little reuse, so groups below 32 pairs stream.  Measured on MI355X
-    // (ms per layer at 16 / 32 / 48): 4K Zipf(1.1) 2.29 / 2.13 / 2.18,
-    // 1032-token Zipf(1.3) 0.76 / 0.75 / 0.75, 256 tokens 0.34 / 0.32 / 0.31;
-    // 16K uniform (all groups above 256) 6.4 either way.
-    int mfma_min = 32;
+    // many are filled; the streaming kernels do their integer dots on VALU at
+    // about 3x the work per column, so from about 12 pairs a part-filled
+    // tile is cheaper.  Measured on MI355X (us per layer at mfma_min 32 / 16
+    // / 12 / 8): 4K Zipf(1.1) 1801 / 1552 / 1534 / 1537, 1032-token
+    // Zipf(1.3) 662 / 608 / 580 / 579, 1032 uniform 1270 / 644 / 631 / 627,
+    // 300 Zipf(1.3) 319 / 299 / 300 / 297, 256 uniform 358 / 355 / 348 / 354;
+    // 16K uniform (all groups above 256) unaffected.
+    int mfma_min = 12;
     // Batches of fewer routes (tokens x k) stream every group: below this the
     // MFMA items are too few to fill the chip and the streaming kernels win
     // (single-expert and 8-expert layers at 2048/512 and 2560/640: MFMA ahead
     // from about 1024 routes, streaming up to 3x ahead below 256).  An explicit
     // MOE_FFN_MFMA_MIN turns this off; MOE_FFN_MFMA_ROUTES sets it.
     int mfma_routes = 1024;
-    int active_mfma_min = 32;   // mfma_min of the current / last forward
+    int active_mfma_min = 12;   // mfma_min of the current / last forward
     int decode_mode = -1; // ungrouped decode path: -1 auto, 0 never, 1 whenever shapes allow
     bool last_decode = false;
     int cu_count = 256;   // compute units of the device
