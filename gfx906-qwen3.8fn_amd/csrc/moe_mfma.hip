@@ -99,6 +99,40 @@ __device__ __forceinline__ v8h head_sums(uint4 h0, uint4 h1, int kb0, int nb) {
     return pack8(w);
 }
 
+// fp16 -> fp32 conversions the compiler cannot fold into v_fma_mix_f32.  On
+// gfx950 v_fma_mix_f32 issues at about the rate of a conversion (measured:
+// 0.5 wave-instructions per SIMD per ns against 0.9 for v_fma_f32, v_mul_f32
+// and v_add_f32), so a scale used by several products is converted once and
+// the products are plain fp32 fmas.  (Same values: fp16 -> fp32 is exact.)
+__device__ __forceinline__ float cvt_half_lo(uint32_t w) {
+    float r;
+    asm("v_cvt_f32_f16 %0, %1" : "=v"(r) : "v"(w));
+    return r;
+}
+__device__ __forceinline__ float cvt_half_hi(uint32_t w) {
+    float r;
+    asm("v_cvt_f32_f16_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1" : "=v"(r) : "v"(w));
+    return r;
+}
+
+// As scale_block below, with the 16 row scales already in fp32.
+__device__ __forceinline__ void scale_block_f32(float (&acc)[16], v16i r, uint32_t head, const float (&d4)[16]) {
+    const v16f f = __builtin_bit_cast(v16f, r);
+    const float d8 = cvt_half_lo(head);
+    const float nk = -kMagicF * d8;
+    // Eight independent products, then their eight accumulations: at two
+    // waves per SIMD back-to-back dependent fmas issue at about 60 % of the
+    // rate of independent ones (measured).
+#pragma unroll
+    for (int g = 0; g < 16; g += 8) {
+        float t[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) t[v] = fmaf(f[g + v], d8, nk);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) acc[g + v] = fmaf(d4[g + v], t[v], acc[g + v]);
+    }
+}
+
 // acc[v] += d4[v] * round(I[v] * d8) for one MFMA result (see the file comment).
 __device__ __forceinline__ void scale_block(float (&acc)[16], v16i r, uint32_t head, const uint32_t (&d4)[8]) {
     const v16f f = __builtin_bit_cast(v16f, r);
@@ -795,28 +829,55 @@ __global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
 // lane holds 16 consecutive rows (4 float4 stores per tile).
 //
 // I <= 512 (16 blocks): the four waves read the same middle rows, so the
-// item's middle codes and heads are staged once in LDS; each wave issues all
-// 16 weight-block loads up front and stages its 32-row scale tile in LDS.
+// item's middle codes and heads are staged once in LDS, and each wave stages
+// its 32-row scale tile there.  Weight blocks stream through a window of
+// kDnWin registers: block b's register is reloaded with block b + kDnWin as
+// soon as block b's A operand is formed.  With Q4_0 rows and 8 or 16 blocks
+// a workgroup runs kDnSlicesPerGroup slices of 128 rows against the
+// one staging: the window runs on into the next slice's blocks, and the next
+// slice's scale tile goes to the other half of a double buffer.
 constexpr int kDnMaxBlocks = 16;
+constexpr int kDnWin = 8;
+constexpr int kDnSlicesPerGroup = 4;
 
-struct DownStage {
+template<int NB>
+struct DownStageT {
     uint4 x[kDnMaxBlocks][kMfmaTile][2];     // middle codes [block][pair][32 bytes]
     uint32_t hd[kDnMaxBlocks][kMfmaTile];    // middle heads [block][pair]
-    uint4 d4[4][kDnMaxBlocks][4];            // per wave: scales [block][32 slots]
+    uint4 d4[NB][4][kDnMaxBlocks][4];        // [buffer][wave]: scales [block][32 slots]
 };
-// Q4_1 down rows also stage their mins (80 KiB: two workgroups per CU).
-struct DownStageQ41 : DownStage {
+using DownStage = DownStageT<2>;             // Q4_0 rows: 80 KiB, two workgroups per CU
+// Q4_1 rows also stage their mins (80 KiB: two workgroups per CU) and take
+// one slice per workgroup (a second scale buffer would not fit twice).
+struct DownStageQ41 : DownStageT<1> {
     uint4 m4[4][kDnMaxBlocks][4];            // per wave: mins [block][32 slots]
 };
 
-// m4s: the wave's staged Q4_1 mins ([block][4] chunks as st.d4[wave]), or
-// nullptr for Q4_0 rows.
-template<int NS, bool Dbg, bool Q41>
-__device__ __forceinline__ void down_staged(const FfnArgs &a, const DownStage &st, const uint4 (*m4s)[4], int wave,
-                                            const uint4 (&wa)[kDnMaxBlocks], int nbi, int first, int ncols, int R0, int prow,
-                                            int pslot, float (&acc)[kSubs][16]) {
-    const int lane = threadIdx.x & 63, m = lane & 31, h = lane >> 5, shift = 4 * h;
-    const uint16_t *d4h = reinterpret_cast<const uint16_t *>(&st.d4[wave][0][0]);
+// Slices of 128 rows per work unit of the down kernel.  Running on into the
+// next slice keeps block j of every slice in window register j % kDnWin only
+// when the block count is a multiple of kDnWin.
+__host__ __device__ constexpr int down_span(int nbi, bool q41) {
+    return nbi % kDnWin == 0 && nbi <= kDnMaxBlocks && !q41 ? kDnSlicesPerGroup : 1;
+}
+// Work units per item.
+__host__ __device__ constexpr int down_groups(int H, int nbi, bool q41) {
+    const int slices = (H + 127) / 128, span = down_span(nbi, q41);
+    return (slices + span - 1) / span;
+}
+
+// d4s: the wave's staged scale tile ([block][4] chunks); m4s: its staged
+// Q4_1 mins (same layout), or nullptr for Q4_0 rows.  wa: the weight window
+// (block b in register b % kDnWin); block b + kDnWin is read through wr
+// (this slice's 32 rows, and the next slice's 32 rows at next_off when there
+// is a next slice: past its end the descriptor reads zeros), at lane offset
+// w_off.
+template<int NS, bool Dbg, bool Q41, class Stage>
+__device__ __forceinline__ void down_staged(const FfnArgs &a, const Stage &st, const uint4 (*d4s)[4], const uint4 (*m4s)[4],
+                                            uint4 (&wa)[kDnWin], __amdgpu_buffer_rsrc_t wr, uint32_t next_off,
+                                            uint32_t w_off, int nbi, int first, int ncols, int R0, int pslot, int lane,
+                                            float (&acc)[kSubs][16]) {
+    const int m = lane & 31, h = lane >> 5, shift = 4 * h;
+    const uint16_t *d4h = reinterpret_cast<const uint16_t *>(&d4s[0][0]);
     if constexpr (Q41) {
 #pragma unroll
         for (int s = 0; s < NS; ++s)
@@ -851,56 +912,163 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const DownStage &s
     v16i magic;
 #pragma unroll
     for (int v = 0; v < 16; ++v) magic[v] = kMagic;
+    // Each step's B operand and head are read from LDS one step ahead (block
+    // b + 1's first at block b's last step; past nbi they are never used).
+    uint4 xb = st.x[0][m][h];
+    uint32_t hx = st.hd[0][m];
 #pragma unroll
     for (int b = 0; b < kDnMaxBlocks; ++b) {
         if (b < nbi) {   // uniform; a guard rather than a break keeps the loop unrolled
-        const uint4 w = wa[b];
-        const uint4 d0 = st.d4[wave][b][2 * h], d1 = st.d4[wave][b][2 * h + 1];
+        const uint4 w = wa[b % kDnWin];
+        const uint4 d0 = d4s[b][2 * h], d1 = d4s[b][2 * h + 1];
         const uint32_t d4[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
         uint32_t m4[8] = {};
+        float d4f[16];
         if constexpr (Q41) {
             const uint4 n0 = m4s[b][2 * h], n1 = m4s[b][2 * h + 1];
             m4[0] = n0.x; m4[1] = n0.y; m4[2] = n0.z; m4[3] = n0.w;
             m4[4] = n1.x; m4[5] = n1.y; m4[6] = n1.z; m4[7] = n1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                d4f[2 * e] = cvt_half_lo(d4[e]);
+                d4f[2 * e + 1] = cvt_half_hi(d4[e]);
+            }
         }
         const v4i A = {static_cast<int>((w.x >> shift) & kNibbles), static_cast<int>((w.y >> shift) & kNibbles),
                        static_cast<int>((w.z >> shift) & kNibbles), static_cast<int>((w.w >> shift) & kNibbles)};
-        v16i r[NS];
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const uint4 xb = st.x[b][kSub * s + m][h];
-            const v4i B = {static_cast<int>(xb.x), static_cast<int>(xb.y), static_cast<int>(xb.z), static_cast<int>(xb.w)};
-            r[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, magic, 0, 0, 0);
+        {
+            // The offset goes into the per-lane operand, which the range check covers.
+            const int nb = b + kDnWin;
+            const uint32_t o = nb < nbi ? static_cast<uint32_t>(nb) * 16u : next_off + static_cast<uint32_t>(nb - nbi) * 16u;
+            wa[b % kDnWin] = buffer_load16(wr, w_off + o, 0);
         }
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            if constexpr (Q41) scale_block_q41(acc[s], r[s], st.hd[b][kSub * s + m], d4, m4);
-            else scale_block(acc[s], r[s], st.hd[b][kSub * s + m], d4);
+        // Each tile's MFMA is issued before the previous tile is scaled, so
+        // the matrix unit works under the scaling and two results are live.
+        v16i rp;
+        uint32_t hp = 0;
+        auto scale_prev = [&](int sp) {
+            if constexpr (Q41) scale_block_q41(acc[sp], rp, hp, d4, m4);
+            else scale_block_f32(acc[sp], rp, hp, d4f);
             if constexpr (Dbg) {
-                const int j = kSub * s + m;
+                const int j = kSub * sp + m;
                 if (a.down_dots && j < ncols)
 #pragma unroll
                     for (int v = 0; v < 16; ++v)
                         a.down_dots[(static_cast<size_t>(first + j) * a.shape.H + R0 + 4 * (v & 7) + 2 * h + (v >> 3)) * nbi + b] =
-                            r[s][v] - kMagic;
+                            rp[v] - kMagic;
             }
+        };
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const v4i B = {static_cast<int>(xb.x), static_cast<int>(xb.y), static_cast<int>(xb.z), static_cast<int>(xb.w)};
+            const v16i r = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, magic, 0, 0, 0);
+            const uint32_t hs = hx;
+            if (s + 1 < NS) {
+                xb = st.x[b][kSub * (s + 1) + m][h];
+                hx = st.hd[b][kSub * (s + 1) + m];
+            } else if (b + 1 < kDnMaxBlocks) {
+                xb = st.x[b + 1][m][h];
+                hx = st.hd[b + 1][m];
+            }
+            if (s > 0) scale_prev(s - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            rp = r;
+            hp = hs;
         }
+        scale_prev(NS - 1);
         }
     }
 }
 
+// Writes a wave's 32-row x (32 x nsub)-pair result tile to the pairs'
+// contribution rows.  Lane half h holds rows 4q + 2h (v = q) and
+// 4q + 2h + 1 (v = 8 + q), q = 0..7; after the trade lane half h holds rows
+// 16h .. 16h + 15 (4 float4 stores per tile).
+__device__ __forceinline__ void store_down_tile(const FfnArgs &a, const float (&acc)[kSubs][16], int nsub, int first,
+                                                int ncols, int R0) {
+    const int lane = threadIdx.x & 63, m = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int s = 0; s < kSubs; ++s) {
+        if (s >= nsub) break;
+        const int j = kSub * s + m;
+        const bool valid = j < ncols;
+        const int p = first + std::min(j, ncols - 1);
+        const size_t orow = static_cast<size_t>(a.routes.pair_token[p]) * a.out_stride_k + a.routes.pair_rank[p];
+        float *dst = a.out + orow * a.shape.H + R0 + 16 * h;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float send0 = h ? acc[s][q] : acc[s][4 + q];
+            const float send1 = h ? acc[s][8 + q] : acc[s][12 + q];
+            const float recv0 = __shfl_xor(send0, 32, 64);
+            const float recv1 = __shfl_xor(send1, 32, 64);
+            const float4 o = h ? make_float4(recv0, recv1, acc[s][4 + q], acc[s][12 + q])
+                               : make_float4(acc[s][q], acc[s][8 + q], recv0, recv1);
+            if (valid) *reinterpret_cast<float4 *>(dst + 4 * q) = o;
+        }
+    }
+}
+
+// The staged path's slices s0 .. s1-1 for one wave, after the staging
+// barrier.  wa holds slice s0's first kDnWin weight blocks; buffer 0 of
+// st.d4 its scales.
+template<int NS, bool Dbg, bool Q41, class Stage>
+__device__ __forceinline__ void down_slices(const FfnArgs &a, Stage &st, int wave, uint4 (&wa)[kDnWin], int nbi,
+                                            int expert, int first, int ncols, int s0, int s1, uint32_t w_off, int pslot) {
+    const int lane = threadIdx.x & 63, H = a.shape.H;
+    const uint32_t row_bytes = static_cast<uint32_t>(nbi) * 16u;
+    for (int sl = s0; sl < s1; ++sl) {
+        const int R0 = sl * 128 + wave * 32;
+        if (R0 >= H) break;                     // wave-uniform; later slices lie further down
+        // Opaque zeros added to the lane index, the weight offset and the
+        // block count keep the per-lane LDS and weight addresses (about 80
+        // VGPRs) and the window's block offsets (16 SGPRs) from being
+        // hoisted out of the loop into registers.
+        int zero, szero;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+        asm volatile("s_mov_b32 %0, 0" : "=s"(szero));
+        const int buf = Q41 ? 0 : (sl - s0) & 1;
+        const int Rn = R0 + 128;
+        const bool pf = sl + 1 < s1 && Rn < H;
+        // Loads are unconditional: past the last slice the descriptors are
+        // empty and read zeros.
+        const size_t rc = static_cast<size_t>(expert) * H + R0, rn = static_cast<size_t>(expert) * H + (pf ? Rn : R0);
+        // Rows R0 .. R0 + 31, and R0 + 128 .. R0 + 159 when there is a next slice.
+        const auto wr = buffer_rsrc(a.bank.down_codes + rc * row_bytes, (pf ? 160u : 32u) * row_bytes);
+        // The next slice's scale tile: nbi * 4 chunks of 16 bytes, one per lane.
+        uint4 dn = make_uint4(0, 0, 0, 0);
+        if constexpr (!Q41)
+            dn = buffer_load16(buffer_rsrc(a.bank.down_scales + rn * nbi, pf ? static_cast<uint32_t>(nbi) * 64u : 0u),
+                               16u * static_cast<uint32_t>(lane), 0);
+        float acc[kSubs][16];
+        const uint4 (*m4s)[4] = nullptr;
+        if constexpr (Q41) m4s = st.m4[wave];
+        down_staged<NS, Dbg, Q41>(a, st, st.d4[buf][wave], m4s, wa, wr, 128u * row_bytes, w_off + static_cast<uint32_t>(zero), nbi + szero,
+                                  first, ncols, R0, pslot, lane + zero, acc);
+        if constexpr (!Q41) {
+            // The other buffer was last read by slice sl - 1 of this wave.
+            if (lane < nbi * 4) st.d4[buf ^ 1][wave][lane >> 2][lane & 3] = dn;
+            __builtin_amdgcn_wave_barrier();
+        }
+        store_down_tile(a, acc, NS, first, ncols, R0);
+    }
+}
+
 template<bool Dbg, bool Q41>
-__global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
+__global__ __launch_bounds__(256, 2) void k_down_mfma(FfnArgs a) {
     __shared__ std::conditional_t<Q41, DownStageQ41, DownStage> st;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = a.shape.I / 32;
     const int slices = (H + 127) / 128;
-    const Unit un = mfma_unit(a.routes.item_counts[1], slices);
+    const bool staged = nbi <= kDnMaxBlocks;
+    const int span = down_span(nbi, Q41);
+    const Unit un = mfma_unit(a.routes.item_counts[1], down_groups(H, nbi, Q41));
     if (!un.ok) return;
     const Item *itp = a.routes.mfma_items + un.item;
     const int expert = itp->expert, first = itp->first, ncols = itp->ncols;
-    const int R0 = un.slice * 128 + wave * 32;
+    const int s0 = un.slice * span, s1 = std::min(slices, s0 + span);
+    const int R0 = s0 * 128 + wave * 32;
     const bool active = R0 < H;      // wave-uniform
     const int nsub = (ncols + kSub - 1) / kSub;
     const int m = lane & 31, h = lane >> 5;
@@ -911,14 +1079,13 @@ __global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
     const size_t rbase = static_cast<size_t>(expert) * H + (active ? R0 : 0);
     const uint32_t row_bytes = static_cast<uint32_t>(nbi) * 16u;
     const uint16_t *scales = a.bank.down_scales + rbase * nbi;        // [nbi][32] halfs of this 32-row group
-    float acc[kSubs][16];
-    if (nbi <= kDnMaxBlocks) {
-        // Weight blocks first (their HBM latency overlaps the staging).
+    if (staged) {
+        // The first weight blocks first (their HBM latency overlaps the staging).
         const auto wr = buffer_rsrc(a.bank.down_codes + rbase * row_bytes, 32u * row_bytes);
         const uint32_t w_off = static_cast<uint32_t>(prow) * row_bytes;
-        uint4 wa[kDnMaxBlocks];
+        uint4 wa[kDnWin];
 #pragma unroll
-        for (int b = 0; b < kDnMaxBlocks; ++b) wa[b] = buffer_load16(wr, w_off, static_cast<uint32_t>(b < nbi ? b : 0) * 16u);
+        for (int b = 0; b < kDnWin; ++b) wa[b] = buffer_load16(wr, w_off, static_cast<uint32_t>(b < nbi ? b : 0) * 16u);
         // Middle codes and heads of the item's pairs, every load issued
         // before the first LDS write.  Thread t keeps one (block, half) of the
         // code rows, block (t % 32) / 2 and half t % 2, for pairs t / 32 + 8 i,
@@ -951,77 +1118,55 @@ __global__ __launch_bounds__(256) void k_down_mfma(FfnArgs a) {
             if (16 * i < cols && hb < nbi) st.hd[hb][hj + 16 * i] = hv[i];
         if (active)
             for (int c = lane; c < nbi * 4; c += 64)
-                st.d4[wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(scales)[c];
-        const uint4 (*m4s)[4] = nullptr;
+                st.d4[0][wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(scales)[c];
         if constexpr (Q41) {
             const uint16_t *mins = a.bank.down_mins + rbase * nbi;   // same layout as the scales
             if (active)
                 for (int c = lane; c < nbi * 4; c += 64)
                     st.m4[wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(mins)[c];
-            m4s = st.m4[wave];
         }
         __syncthreads();
         if (!active) return;
         switch (nsub) {
-        case 1: down_staged<1, Dbg, Q41>(a, st, m4s, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
-        case 2: down_staged<2, Dbg, Q41>(a, st, m4s, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
-        case 3: down_staged<3, Dbg, Q41>(a, st, m4s, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
-        default: down_staged<4, Dbg, Q41>(a, st, m4s, wave, wa, nbi, first, ncols, R0, prow, pslot, acc); break;
+        case 1: down_slices<1, Dbg, Q41>(a, st, wave, wa, nbi, expert, first, ncols, s0, s1, w_off, pslot); break;
+        case 2: down_slices<2, Dbg, Q41>(a, st, wave, wa, nbi, expert, first, ncols, s0, s1, w_off, pslot); break;
+        case 3: down_slices<3, Dbg, Q41>(a, st, wave, wa, nbi, expert, first, ncols, s0, s1, w_off, pslot); break;
+        default: down_slices<4, Dbg, Q41>(a, st, wave, wa, nbi, expert, first, ncols, s0, s1, w_off, pslot); break;
         }
-    } else {
-        if (!active) return;   // no barrier on this path
-        const uint32_t pairs = static_cast<uint32_t>(a.pairs_bound);
-        TileArgs t;
-        t.wr = buffer_rsrc(a.bank.down_codes + rbase * row_bytes, 32u * row_bytes);
-        t.sr = buffer_rsrc(scales, static_cast<uint32_t>(nbi) * 64u);
-        t.mr = buffer_rsrc(Q41 ? a.bank.down_mins + rbase * nbi : scales, static_cast<uint32_t>(nbi) * 64u);
-        t.xr = buffer_rsrc(a.mq.codes, pairs * static_cast<uint32_t>(nbi) * 32u);
-        t.hr = buffer_rsrc(a.mq.heads, pairs * static_cast<uint32_t>(nbi) * 4u);
-        t.w_off = static_cast<uint32_t>(prow) * row_bytes;
-        t.s_off0 = 32u * h;
-        t.s_off1 = 32u * h + 16u;
-        t.s_step = 64u;
-#pragma unroll
-        for (int s = 0; s < kSubs; ++s) {
-            const uint32_t p = static_cast<uint32_t>(first + std::min(kSub * s + m, ncols - 1));
-            t.x_off[s] = p * static_cast<uint32_t>(nbi) * 32u + 16u * h;
-            t.h_off[s] = p * static_cast<uint32_t>(nbi) * 4u;
-        }
-        t.cscale = scales + pslot;
-        t.cstride = 32;
-        t.nb = nbi;
-        t.shift = 4 * h;
-        t.dots = Dbg ? a.down_dots : nullptr;
-        t.dot_rows = static_cast<size_t>(H);
-        t.dot_row0 = R0;
-        t.dot_pair0 = first;
-        t.ncols = ncols;
-        t.m = m;
-        t.h = h;
-        tile_dispatch<Dbg, true, Q41>(t, nsub, acc);
+        return;
     }
-
-    // Lane half h holds rows 4q + 2h (v = q) and 4q + 2h + 1 (v = 8 + q),
-    // q = 0..7.  After the trade lane half h holds rows 16h .. 16h + 15.
+    if (!active) return;   // no barrier on this path
+    float acc[kSubs][16];
+    const uint32_t pairs = static_cast<uint32_t>(a.pairs_bound);
+    TileArgs t;
+    t.wr = buffer_rsrc(a.bank.down_codes + rbase * row_bytes, 32u * row_bytes);
+    t.sr = buffer_rsrc(scales, static_cast<uint32_t>(nbi) * 64u);
+    t.mr = buffer_rsrc(Q41 ? a.bank.down_mins + rbase * nbi : scales, static_cast<uint32_t>(nbi) * 64u);
+    t.xr = buffer_rsrc(a.mq.codes, pairs * static_cast<uint32_t>(nbi) * 32u);
+    t.hr = buffer_rsrc(a.mq.heads, pairs * static_cast<uint32_t>(nbi) * 4u);
+    t.w_off = static_cast<uint32_t>(prow) * row_bytes;
+    t.s_off0 = 32u * h;
+    t.s_off1 = 32u * h + 16u;
+    t.s_step = 64u;
 #pragma unroll
     for (int s = 0; s < kSubs; ++s) {
-        if (s >= nsub) break;
-        const int j = kSub * s + m;
-        const bool valid = j < ncols;
-        const int p = first + std::min(j, ncols - 1);
-        const size_t orow = static_cast<size_t>(a.routes.pair_token[p]) * a.out_stride_k + a.routes.pair_rank[p];
-        float *dst = a.out + orow * H + R0 + 16 * h;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float send0 = h ? acc[s][q] : acc[s][4 + q];
-            const float send1 = h ? acc[s][8 + q] : acc[s][12 + q];
-            const float recv0 = __shfl_xor(send0, 32, 64);
-            const float recv1 = __shfl_xor(send1, 32, 64);
-            const float4 o = h ? make_float4(recv0, recv1, acc[s][4 + q], acc[s][12 + q])
-                               : make_float4(acc[s][q], acc[s][8 + q], recv0, recv1);
-            if (valid) *reinterpret_cast<float4 *>(dst + 4 * q) = o;
-        }
+        const uint32_t p = static_cast<uint32_t>(first + std::min(kSub * s + m, ncols - 1));
+        t.x_off[s] = p * static_cast<uint32_t>(nbi) * 32u + 16u * h;
+        t.h_off[s] = p * static_cast<uint32_t>(nbi) * 4u;
     }
+    t.cscale = scales + pslot;
+    t.cstride = 32;
+    t.nb = nbi;
+    t.shift = 4 * h;
+    t.dots = Dbg ? a.down_dots : nullptr;
+    t.dot_rows = static_cast<size_t>(H);
+    t.dot_row0 = R0;
+    t.dot_pair0 = first;
+    t.ncols = ncols;
+    t.m = m;
+    t.h = h;
+    tile_dispatch<Dbg, true, Q41>(t, nsub, acc);
+    store_down_tile(a, acc, nsub, first, ncols, R0);
 }
 
 // Upper bound on MFMA items: a group of n >= mfma_min pairs gives
@@ -1193,8 +1338,8 @@ hipError_t launch_gate_up_mfma(const FfnArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_down_mfma(const FfnArgs &a, hipStream_t s) {
-    const unsigned grid = mfma_grid(a, (a.shape.H + 127) / 128);
     const bool q41 = a.bank.down_mins != nullptr;
+    const unsigned grid = mfma_grid(a, down_groups(a.shape.H, a.shape.I / 32, q41));
     if (a.down_dots) {
         if (q41) k_down_mfma<true, true><<<grid, 256, 0, s>>>(a);
         else k_down_mfma<true, false><<<grid, 256, 0, s>>>(a);

@@ -67,7 +67,9 @@ PATHS = {
 }
 
 
-@pytest.mark.parametrize("H,I", [(2560, 640), (1024, 256)])
+# (1344, 512): 10.5 row slices of 128, so the down kernel's last
+# four-slice work unit is short and its last slice half empty.
+@pytest.mark.parametrize("H,I", [(2560, 640), (1024, 256), (1344, 512)])
 @pytest.mark.parametrize("path", list(PATHS))
 def test_layer_shape_paths(H, I, path):
     E, K, N = 16, 4, 40
