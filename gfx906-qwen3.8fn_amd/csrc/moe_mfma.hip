@@ -382,7 +382,7 @@ __device__ __forceinline__ void lane_sums(const GuTile &t, int j, float (&a0)[16
         const BlockLoads l = block_loads(t, b);
         const uint32_t d4[8] = {l.d0.x, l.d0.y, l.d0.z, l.d0.w, l.d1.x, l.d1.y, l.d1.z, l.d1.w};
         const v16i I0 = fragment_dots<0>(t, l), I1 = fragment_dots<1>(t, l);
-        const float d8 = half_lo(l.hd), c4 = -4.0f * half_hi(l.hd);
+        const float d8 = cvt_half_lo(l.hd), c4 = -4.0f * cvt_half_hi(l.hd);
         fragment_scale(a0, I0, d8, c4, d4);
         fragment_scale(a1, I1, d8, c4, d4);
         store_dots<Dbg>(t, b, I0, I1);
@@ -443,8 +443,8 @@ __device__ __forceinline__ void leaf_staged(const GuTile &t, const GuStage &g, i
     const uint4 a0 = da4[0], a1 = da4[1], b0 = db4[0], b1 = db4[1];
     const uint32_t da[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
     const uint32_t db[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-    const float d8a = half_lo(ha), c4a = -4.0f * half_hi(ha);
-    const float d8b = half_lo(hb), c4b = -4.0f * half_hi(hb);
+    const float d8a = cvt_half_lo(ha), c4a = -4.0f * cvt_half_hi(ha);
+    const float d8b = cvt_half_lo(hb), c4b = -4.0f * cvt_half_hi(hb);
     float u0[16];
     v16i keep_a0, keep_b0;
     {
@@ -587,8 +587,8 @@ __device__ __forceinline__ void leaf_grouped(const GuTile &t, const GuStage &g, 
     const uint4 a0 = da4[0], a1 = da4[1], b0 = db4[0], b1 = db4[1];
     const uint32_t da[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
     const uint32_t db[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-    const float d8a = half_lo(ha), c4a = -4.0f * half_hi(ha);
-    const float d8b = half_lo(hb), c4b = -4.0f * half_hi(hb);
+    const float d8a = cvt_half_lo(ha), c4a = -4.0f * cvt_half_hi(ha);
+    const float d8b = cvt_half_lo(hb), c4b = -4.0f * cvt_half_hi(hb);
     const uint4 xa = G.xa[i], xb = G.xb[i];
     float u0[16];
     v16i keep_a0, keep_b0;
