@@ -1215,12 +1215,17 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
     const int m = lane & 31, h = lane >> 5;
     float l1[16], l2[16];
     if constexpr (Fold == kFoldGrouped) {
+        // Node q + 1's weight half is in flight while node q computes.
+        uint4 wn[2];
+        half_load_w(t, w_off, 4 * wave, wn);
 #pragma unroll 1
         for (int q = 0; q < 4; ++q) {
             const int p = 4 * wave + q;
             HalfGroup G;
-            half_load_w(t, w_off, p, G.w);
+            G.w[0] = wn[0];
+            G.w[1] = wn[1];
             half_load_x(t, p, G);
+            half_load_w(t, w_off, q < 3 ? p + 1 : p, wn);
             float w[16], x[16];
             leaf_grouped<false>(t, g, G, 0, 2 * p, m, h, w);
             leaf_grouped<false>(t, g, G, 1, 2 * p + 1, m, h, x);
