@@ -68,8 +68,10 @@ PATHS = {
 
 
 # (1344, 512): 10.5 row slices of 128, so the down kernel's last
-# four-slice work unit is short and its last slice half empty.
-@pytest.mark.parametrize("H,I", [(2560, 640), (1024, 256), (1344, 512)])
+# four-slice work unit is short and its last slice half empty.  (1024, 384)
+# and (512, 128): 12 and 4 down blocks per row, where the down kernel takes
+# one slice per work unit and its 8-block weight window does not wrap.
+@pytest.mark.parametrize("H,I", [(2560, 640), (1024, 256), (1344, 512), (1024, 384), (512, 128)])
 @pytest.mark.parametrize("path", list(PATHS))
 def test_layer_shape_paths(H, I, path):
     E, K, N = 16, 4, 40
