@@ -436,25 +436,30 @@ __global__ __launch_bounds__(256) void k_mark_quantize(GroupParams p, int mark_b
         if (flags) atomicOr(p.error, flags);
         return;
     }
-    // kQuantPer elements per thread, 256 apart (a workgroup quantizes 2048
-    // consecutive floats); loads first.  q_elements is a multiple of 32, so
-    // the bound check keeps or drops whole 32-lane blocks.
-    const size_t i0 = static_cast<size_t>(blockIdx.x - mark_blocks) * (256 * kQuantPer) + threadIdx.x;
-    float v[kQuantPer];
-#pragma unroll
-    for (int u = 0; u < kQuantPer; ++u) {
-        const size_t i = i0 + 256 * u;
-        v[u] = i < q_elements ? x[i] : 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < kQuantPer; ++u) {
-        const size_t i = i0 + 256 * u;
-        if (i >= q_elements) break;   // uniform per 32-lane block
-        const Q8Lane q = quantize32(v[u]);
-        const size_t block = i >> 5;
-        const int lane = static_cast<int>(i & 31);
-        xq.codes[block * 32 + lane] = static_cast<uint8_t>(q.code);
-        if (lane == 0) {
+    // A workgroup quantizes 64 blocks (2048 consecutive floats): wave w takes
+    // blocks 16w .. 16w + 15, lane l elements 8 (l / 16) .. + 7 of block
+    // 16w + l % 16 (two 16-byte loads, one 8-byte code store), reduced by
+    // quantize_part<4> (aligned subtrees of the reference's butterfly, the same
+    // bytes as quantize32).  q_elements is a multiple of 32, so the bound check
+    // keeps or drops whole blocks; every lane takes part in the shuffles.
+    static_assert(kQuantPer == 8, "k_mark_quantize: 8 elements per lane");
+    const int lane = static_cast<int>(threadIdx.x & 63), wave = static_cast<int>(threadIdx.x >> 6);
+    const int part = lane >> 4;
+    const size_t blk0 = static_cast<size_t>(blockIdx.x - mark_blocks) * 64;
+    const size_t block = blk0 + 16 * wave + (lane & 15);
+    const bool in = block * 32 < q_elements;
+    // The workgroup's 8 KB through one buffer descriptor (x needs only
+    // 4-byte alignment; past q_elements the loads read zeros).
+    const size_t left = q_elements - blk0 * 32;
+    const auto xr = buffer_rsrc(x + blk0 * 32, static_cast<uint32_t>(std::min<size_t>(left, 2048) * 4));
+    const uint32_t off = static_cast<uint32_t>((16 * wave + (lane & 15)) * 128 + 32 * part);
+    const uint4 a = buffer_load16(xr, off, 0), b = buffer_load16(xr, off, 16);
+    float v[kQuantPer] = {__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z), __uint_as_float(a.w),
+                          __uint_as_float(b.x), __uint_as_float(b.y), __uint_as_float(b.z), __uint_as_float(b.w)};
+    const Q8Part<4> q = quantize_part<4>(v);
+    if (in) {
+        *reinterpret_cast<uint2 *>(xq.codes + block * 32 + 8 * part) = make_uint2(q.codes[0], q.codes[1]);
+        if (part == 0) {
             xq.heads[block] = q.head;
             if (q.flags) atomicOr(p.error, q.flags);
         }
