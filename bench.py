@@ -514,16 +514,9 @@ def main():
         lib = moe_ffn.library()
         call = lambda: lib.moe_router_select(moe_ffn._ptr(lg), NR, 512, 10, None, moe_ffn._ptr(ids_r),
                                              moe_ffn._ptr(w_r), moe_ffn._ptr(err_r), moe_ffn._stream(None))
-        for _ in range(5):
-            call()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(50):
-            call()
-        e1.record()
-        torch.cuda.synchronize()
-        router[f"tokens_{NR}_us"] = e0.elapsed_time(e1) / 50 * 1e3
+        # Launches replayed from a graph: a few-microsecond kernel launched one
+        # Python call at a time would time the host.
+        router[f"tokens_{NR}_us"] = time_calls(call, iters=50) * 1e6
     if router:
         result["router_us"] = router
         log(f"[bench] router (softmax + top-10 of 512): {router}")

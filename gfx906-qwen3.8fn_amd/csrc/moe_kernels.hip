@@ -1446,9 +1446,44 @@ __global__ __launch_bounds__(256) void k_fold(const float *__restrict__ c, size_
 // moe_expf (the host C library's bits).
 constexpr int kRouterMaxPer = 32;   // experts <= 1024
 
+// Branch-free (selects, no exec-mask branches on the router's serial path).
 __device__ __forceinline__ float router_check(float x, int &flags, int bit) {
-    if (!isfinite(x)) { flags |= bit; return 0.0f; }
-    return x;
+    const bool bad = !isfinite(x);
+    flags |= bad ? bit : 0;
+    return bad ? 0.0f : x;
+}
+
+// The value of lane l ^ D within each 32-lane half (D = 1, 2, 4, 8, 16),
+// without the LDS round trip of a shuffle for D < 16: DPP quad permutes for
+// 1 and 2, a half-row mirror then a quad reversal for 4 (7 - i, then
+// i ^ 3 within the quad, is i ^ 4), a rotation by 8 of the 16-lane row for 8,
+// and one bit-mask swizzle for 16.  The exact XOR partner keeps the
+// butterfly sums in the reference's order.
+template<int D>
+__device__ __forceinline__ int lane_xor(int v) {
+    if constexpr (D == 1) return __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false);        // quad_perm 1,0,3,2
+    else if constexpr (D == 2) return __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false);   // quad_perm 2,3,0,1
+    else if constexpr (D == 4) {
+        const int m = __builtin_amdgcn_update_dpp(v, v, 0x141, 0xf, 0xf, false);                  // row_half_mirror
+        return __builtin_amdgcn_update_dpp(m, m, 0x1b, 0xf, 0xf, false);                          // quad_perm 3,2,1,0
+    } else if constexpr (D == 8) return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false); // row_ror:8
+    else {
+        static_assert(D == 16, "lane_xor: D in 1, 2, 4, 8, 16");
+        return __builtin_amdgcn_ds_swizzle(v, 0x401f);   // bit-mask mode: and 31, xor 16
+    }
+}
+template<int D>
+__device__ __forceinline__ float lane_xor(float v) {
+    return __int_as_float(lane_xor<D>(__float_as_int(v)));
+}
+// A butterfly over the 32 lanes of each half: op(v, partner) for D = 1 .. 16.
+template<class T, class Op>
+__device__ __forceinline__ T half_butterfly(T v, Op op) {
+    v = op(v, lane_xor<1>(v));
+    v = op(v, lane_xor<2>(v));
+    v = op(v, lane_xor<4>(v));
+    v = op(v, lane_xor<8>(v));
+    return op(v, lane_xor<16>(v));
 }
 
 // PER = experts / 32 values per lane (compile time, so every array index is
@@ -1469,8 +1504,7 @@ __global__ __launch_bounds__(64) void k_router(const float *__restrict__ logits,
     for (int k = 0; k < PER; ++k) x[k] = router_check(row[l + 32 * k], flags, 1);
 #pragma unroll
     for (int k = 0; k < PER; ++k) m = fmaxf(m, x[k]);
-#pragma unroll
-    for (int d = 1; d < 32; d <<= 1) m = fmaxf(m, __shfl_xor(m, d, 32));
+    m = half_butterfly(m, [](float a, float b) { return fmaxf(a, b); });
     float total = 0.0f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
@@ -1478,15 +1512,13 @@ __global__ __launch_bounds__(64) void k_router(const float *__restrict__ logits,
         w[k] = router_check(moe_expf_with(shifted, table), flags, 2);
         total = router_check(total + w[k], flags, 2);
     }
-#pragma unroll
-    for (int d = 1; d < 32; d <<= 1) total = total + __shfl_xor(total, d, 32);
+    total = half_butterfly(total, [](float a, float b) { return a + b; });
     total = router_check(total, flags, 2);
     if (!(total > 0.0f)) flags |= 2;
     const float inverse = total > 0.0f ? router_check(1.0f / total, flags, 2) : 0.0f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) w[k] = router_check(w[k] * inverse, flags, 2);
-#pragma unroll
-    for (int d = 1; d < 32; d <<= 1) flags |= __shfl_xor(flags, d, 32);
+    flags = half_butterfly(flags, [](int a, int b) { return a | b; });
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         if (flags) w[k] = 0.0f;
@@ -1495,17 +1527,47 @@ __global__ __launch_bounds__(64) void k_router(const float *__restrict__ logits,
     uint32_t taken = 0;
     float bucket = 0.0f;
     for (int i = 0; i < top_k; ++i) {
-        float bv = -INFINITY;
-        int bid = 0x7fffffff;
+        // The lane's best untaken entry by a pairwise tree over k (the left,
+        // lower id, wins ties), then the wave's best by value, ties to the
+        // lower id: the same choice as a scan in id order.  The two lanes
+        // that hold reference lane l split its entries (lanes < 32 the first
+        // half of k, lanes >= 32 the rest), so both halves of the wave work.
+        constexpr int HALF = (PER + 1) / 2;
+        const bool lo = threadIdx.x < 32;
+        float cv[HALF];
+        int ci[HALF];
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {   // ascending ids: a tie keeps the lower one
-            if (!((taken >> k) & 1u) && w[k] > bv) { bv = w[k]; bid = l + 32 * k; }
+        for (int j = 0; j < HALF; ++j) {
+            const int k = lo ? j : HALF + j;   // entries j (lanes < 32) or HALF + j (lanes >= 32)
+            const float wv = lo ? w[j] : (HALF + j < PER ? w[HALF + j < PER ? HALF + j : 0] : -INFINITY);
+            const bool free = k < PER && !((taken >> k) & 1u);
+            cv[j] = free ? wv : -INFINITY;
+            ci[j] = free ? l + 32 * k : 0x7fffffff;
         }
 #pragma unroll
-        for (int d = 1; d < 32; d <<= 1) {
-            const float ov = __shfl_xor(bv, d, 32);
-            const int oid = __shfl_xor(bid, d, 32);
-            if (ov > bv || (ov == bv && oid < bid)) { bv = ov; bid = oid; }
+        for (int st = 1; st < HALF; st <<= 1)
+#pragma unroll
+            for (int j = 0; j + st < HALF; j += 2 * st)
+                if (cv[j + st] > cv[j]) { cv[j] = cv[j + st]; ci[j] = ci[j + st]; }
+        float bv = cv[0];
+        int bid = ci[0];
+        auto take = [&](float ov, int oid) {
+            const bool better = (ov > bv) | ((ov == bv) & (oid < bid));   // non-short-circuit: selects, no branches
+            bv = better ? ov : bv;
+            bid = better ? oid : bid;
+        };
+        take(lane_xor<1>(bv), lane_xor<1>(bid));
+        take(lane_xor<2>(bv), lane_xor<2>(bid));
+        take(lane_xor<4>(bv), lane_xor<4>(bid));
+        take(lane_xor<8>(bv), lane_xor<8>(bid));
+        take(lane_xor<16>(bv), lane_xor<16>(bid));
+        {
+            // Lane l <-> l + 32: after a swap, lanes < 32 find the other
+            // half's value in the second result, lanes >= 32 in the first.
+            const auto sv = __builtin_amdgcn_permlane32_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+            const auto si = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(bid), static_cast<uint32_t>(bid), false,
+                                                             false);
+            take(__uint_as_float(lo ? sv[1] : sv[0]), static_cast<int>(lo ? si[1] : si[0]));
         }
         if ((bid & 31) == l) {
             taken |= 1u << (bid >> 5);
@@ -1513,8 +1575,7 @@ __global__ __launch_bounds__(64) void k_router(const float *__restrict__ logits,
         }
         if (threadIdx.x == 0) { sel_id[i] = bid; sel_v[i] = bv; }
     }
-#pragma unroll
-    for (int d = 1; d < 32; d <<= 1) bucket = bucket + __shfl_xor(bucket, d, 32);
+    bucket = half_butterfly(bucket, [](float a, float b) { return a + b; });
     const float lowest = 1.0f / 16384.0f;
     const float denominator = bucket < lowest ? lowest : bucket;
     const int dflags = (!(denominator > 0.0f) || !isfinite(denominator)) ? 2 : 0;
