@@ -47,7 +47,52 @@ __device__ __forceinline__ int dot_block(uint4 w, uint4 x0, uint4 x1) {
     return s;
 }
 
-__device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
+// The value of lane l ^ D (D = 1, 2, 4, 8, 16, 32) without the LDS round trip
+// of a shuffle: DPP quad permutes for 1 and 2, a half-row mirror then a quad
+// reversal for 4 (7 - i, then i ^ 3 within the quad, is i ^ 4), a rotation by
+// 8 of the 16-lane row for 8, one bit-mask swizzle for 16 and
+// v_permlane32_swap for 32 (the swap of a register with itself leaves the
+// partner half's value in the second result for lanes < 32 and in the first
+// for lanes >= 32).  D <= 16 stays within each 32-lane half, so the same
+// partner serves a butterfly of width 32.  The exact XOR partner keeps the
+// butterfly sums in the reference's order.
+template<int D>
+__device__ __forceinline__ int lane_xor(int v) {
+    if constexpr (D == 1) return __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false);        // quad_perm 1,0,3,2
+    else if constexpr (D == 2) return __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false);   // quad_perm 2,3,0,1
+    else if constexpr (D == 4) {
+        const int m = __builtin_amdgcn_update_dpp(v, v, 0x141, 0xf, 0xf, false);                  // row_half_mirror
+        return __builtin_amdgcn_update_dpp(m, m, 0x1b, 0xf, 0xf, false);                          // quad_perm 3,2,1,0
+    } else if constexpr (D == 8) return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false); // row_ror:8
+    else if constexpr (D == 16) return __builtin_amdgcn_ds_swizzle(v, 0x401f);   // bit-mask mode: and 31, xor 16
+    else {
+        static_assert(D == 32, "lane_xor: D in 1, 2, 4, 8, 16, 32");
+        const auto r = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false,
+                                                        false);
+        return static_cast<int>((threadIdx.x & 32) ? r[0] : r[1]);
+    }
+}
+template<int D>
+__device__ __forceinline__ float lane_xor(float v) {
+    return __int_as_float(lane_xor<D>(__float_as_int(v)));
+}
+// A butterfly over the 32 lanes of each half: op(v, partner) for D = 1 .. 16.
+template<class T, class Op>
+__device__ __forceinline__ T half_butterfly(T v, Op op) {
+    v = op(v, lane_xor<1>(v));
+    v = op(v, lane_xor<2>(v));
+    v = op(v, lane_xor<4>(v));
+    v = op(v, lane_xor<8>(v));
+    return op(v, lane_xor<16>(v));
+}
+template<int D>
+__device__ __forceinline__ float xor_sum(float v) { return v + lane_xor<D>(v); }
+// v + partner for D = M, M / 2, .. 1 (a butterfly sum from the widest stage).
+template<int M>
+__device__ __forceinline__ float xor_sum_from(float v) {
+    if constexpr (M >= 1) return xor_sum_from<M / 2>(xor_sum<M>(v));
+    else return v;
+}
 
 // The two fragment dots of one block in the reference CPU/MMVQ order
 // (src/cpu_expert.cpp:156-213): fragment f covers code bytes 8f..8f+7, i.e.
@@ -123,7 +168,7 @@ __device__ __forceinline__ float rows8_down_exact(const uint4 (&w)[8], uint4 d4p
         }
         const float send = c0 ? z[0] : z[1];
         const float keep = c0 ? z[1] : z[0];
-        v4[i] = keep + __shfl_xor(send, 1, 64);
+        v4[i] = keep + lane_xor<1>(send);
         __builtin_amdgcn_sched_barrier(0);   // one row pair at a time (register pressure)
     }
     float v2[2];
@@ -131,10 +176,10 @@ __device__ __forceinline__ float rows8_down_exact(const uint4 (&w)[8], uint4 d4p
     for (int i = 0; i < 2; ++i) {
         const float send = c1 ? v4[i] : v4[i + 2];
         const float keep = c1 ? v4[i + 2] : v4[i];
-        v2[i] = keep + __shfl_xor(send, 2, 64);
+        v2[i] = keep + lane_xor<2>(send);
     }
-    float v = (c2 ? v2[1] : v2[0]) + __shfl_xor(c2 ? v2[0] : v2[1], 4, 64);
-    v = xor_sum(v, 8);
+    float v = (c2 ? v2[1] : v2[0]) + lane_xor<4>(c2 ? v2[0] : v2[1]);
+    v = xor_sum<8>(v);
     return v + 0.0f;
 }
 
@@ -188,12 +233,12 @@ __device__ __forceinline__ float rows8_exact(const uint4 (&w)[8], uint4 d4p, uin
     for (int i = 0; i < 2; ++i) {
         const float send = b0 ? v4[i] : v4[i + 2];
         const float keep = b0 ? v4[i + 2] : v4[i];
-        v2[i] = keep + __shfl_xor(send, 1, 64);
+        v2[i] = keep + lane_xor<1>(send);
     }
-    float v = (b1 ? v2[1] : v2[0]) + __shfl_xor(b1 ? v2[0] : v2[1], 2, 64);
-    v = xor_sum(v, 4);
-    v = xor_sum(v, 8);
-    return xor_sum(v, 16);
+    float v = (b1 ? v2[1] : v2[0]) + lane_xor<2>(b1 ? v2[0] : v2[1]);
+    v = xor_sum<4>(v);
+    v = xor_sum<8>(v);
+    return xor_sum<16>(v);
 }
 
 // The same reduction for lane partials already summed over several blocks
@@ -221,12 +266,12 @@ __device__ __forceinline__ float fold_rows8(const float (&z)[8][2], int lane) {
     for (int i = 0; i < 2; ++i) {
         const float send = b0 ? v4[i] : v4[i + 2];
         const float keep = b0 ? v4[i + 2] : v4[i];
-        v2[i] = keep + __shfl_xor(send, 1, 64);
+        v2[i] = keep + lane_xor<1>(send);
     }
-    float v = (b1 ? v2[1] : v2[0]) + __shfl_xor(b1 ? v2[0] : v2[1], 2, 64);
-    v = xor_sum(v, 4);
-    v = xor_sum(v, 8);
-    return xor_sum(v, 16);
+    float v = (b1 ? v2[1] : v2[0]) + lane_xor<2>(b1 ? v2[0] : v2[1]);
+    v = xor_sum<4>(v);
+    v = xor_sum<8>(v);
+    return xor_sum<16>(v);
 }
 
 // rows8_exact for rows of 65..128 blocks: lane j holds blocks j (w, d4p, x0,
@@ -273,22 +318,16 @@ __device__ __forceinline__ Q8Lane quantize32(float x) {
     int bad = !isfinite(x);
     if (bad) x = 0.0f;
     float amax = fabsf(x);
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-        bad |= __shfl_xor(bad, m, 32);
-    }
-    float sum = x;
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) sum = sum + __shfl_xor(sum, m, 32);
+    amax = half_butterfly(amax, [](float a, float b) { return fmaxf(a, b); });
+    bad = half_butterfly(bad, [](int a, int b) { return a | b; });
+    const float sum = half_butterfly(x, [](float a, float b) { return a + b; });
     const float d = amax / 127.0f;
     const uint32_t hd = f2h(d), hs = f2h(sum);
     const bool representable = isfinite(sum) && (hs & 0x7c00u) != 0x7c00u &&
                                (hd & 0x7c00u) != 0x7c00u && (amax == 0.0f || d > 0.0f);
     const float code = (!bad && representable && amax != 0.0f) ? roundf(x / d) : 0.0f;
     int bad_code = !isfinite(code) || code < -127.0f || code > 127.0f;
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) bad_code |= __shfl_xor(bad_code, m, 32);
+    bad_code = half_butterfly(bad_code, [](int a, int b) { return a | b; });
     const bool valid = !bad && representable && !bad_code;
     Q8Lane q;
     q.code = valid ? static_cast<int8_t>(code) : int8_t{0};
@@ -330,13 +369,13 @@ __device__ __forceinline__ Q8Part<P> quantize_part(float (&v)[32 / P]) {
         for (int i = 0; i < w; ++i) t[i] = t[2 * i] + t[2 * i + 1];
     float sum = t[0];
     if constexpr (P == 4) {
-        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-        bad |= __shfl_xor(bad, 16, 64);
-        sum = sum + __shfl_xor(sum, 16, 64);
+        amax = fmaxf(amax, lane_xor<16>(amax));
+        bad |= lane_xor<16>(bad);
+        sum = sum + lane_xor<16>(sum);
     }
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    bad |= __shfl_xor(bad, 32, 64);
-    sum = sum + __shfl_xor(sum, 32, 64);   // commutative: every lane of the block agrees
+    amax = fmaxf(amax, lane_xor<32>(amax));
+    bad |= lane_xor<32>(bad);
+    sum = sum + lane_xor<32>(sum);   // commutative: every lane of the block agrees
     const float d = amax / 127.0f;
     const uint32_t hd = f2h(d), hs = f2h(sum);
     const bool representable = isfinite(sum) && (hs & 0x7c00u) != 0x7c00u &&
@@ -355,8 +394,8 @@ __device__ __forceinline__ Q8Part<P> quantize_part(float (&v)[32 / P]) {
         }
         q.codes[w] = word;
     }
-    if constexpr (P == 4) bad_code |= __shfl_xor(bad_code, 16, 64);
-    bad_code |= __shfl_xor(bad_code, 32, 64);
+    if constexpr (P == 4) bad_code |= lane_xor<16>(bad_code);
+    bad_code |= lane_xor<32>(bad_code);
     const bool valid = !bad && representable && !bad_code;
 #pragma unroll
     for (int w = 0; w < n / 4; ++w) q.codes[w] = valid ? q.codes[w] : 0u;

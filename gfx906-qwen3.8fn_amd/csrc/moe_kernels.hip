@@ -900,9 +900,7 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
                                 a.routes.pair_rank[pair];
 #pragma unroll
             for (int l = 0; l < LOADS; ++l) {
-                float v = acc[l][j];
-#pragma unroll
-                for (int m = LPR / 2; m >= 1; m >>= 1) v = xor_sum(v, m);
+                const float v = xor_sum_from<LPR / 2>(acc[l][j]);
                 if (kb0 == 0) a.out[orow * H + row0 + l * RPL + sub] = v;
             }
         }
@@ -1451,39 +1449,6 @@ __device__ __forceinline__ float router_check(float x, int &flags, int bit) {
     const bool bad = !isfinite(x);
     flags |= bad ? bit : 0;
     return bad ? 0.0f : x;
-}
-
-// The value of lane l ^ D within each 32-lane half (D = 1, 2, 4, 8, 16),
-// without the LDS round trip of a shuffle for D < 16: DPP quad permutes for
-// 1 and 2, a half-row mirror then a quad reversal for 4 (7 - i, then
-// i ^ 3 within the quad, is i ^ 4), a rotation by 8 of the 16-lane row for 8,
-// and one bit-mask swizzle for 16.  The exact XOR partner keeps the
-// butterfly sums in the reference's order.
-template<int D>
-__device__ __forceinline__ int lane_xor(int v) {
-    if constexpr (D == 1) return __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false);        // quad_perm 1,0,3,2
-    else if constexpr (D == 2) return __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false);   // quad_perm 2,3,0,1
-    else if constexpr (D == 4) {
-        const int m = __builtin_amdgcn_update_dpp(v, v, 0x141, 0xf, 0xf, false);                  // row_half_mirror
-        return __builtin_amdgcn_update_dpp(m, m, 0x1b, 0xf, 0xf, false);                          // quad_perm 3,2,1,0
-    } else if constexpr (D == 8) return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false); // row_ror:8
-    else {
-        static_assert(D == 16, "lane_xor: D in 1, 2, 4, 8, 16");
-        return __builtin_amdgcn_ds_swizzle(v, 0x401f);   // bit-mask mode: and 31, xor 16
-    }
-}
-template<int D>
-__device__ __forceinline__ float lane_xor(float v) {
-    return __int_as_float(lane_xor<D>(__float_as_int(v)));
-}
-// A butterfly over the 32 lanes of each half: op(v, partner) for D = 1 .. 16.
-template<class T, class Op>
-__device__ __forceinline__ T half_butterfly(T v, Op op) {
-    v = op(v, lane_xor<1>(v));
-    v = op(v, lane_xor<2>(v));
-    v = op(v, lane_xor<4>(v));
-    v = op(v, lane_xor<8>(v));
-    return op(v, lane_xor<16>(v));
 }
 
 // PER = experts / 32 values per lane (compile time, so every array index is

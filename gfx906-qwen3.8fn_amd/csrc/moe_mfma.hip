@@ -998,12 +998,15 @@ __device__ __forceinline__ void store_down_tile(const FfnArgs &a, const float (&
         float *dst = a.out + orow * a.shape.H + R0 + 16 * h;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float send0 = h ? acc[s][q] : acc[s][4 + q];
-            const float send1 = h ? acc[s][8 + q] : acc[s][12 + q];
-            const float recv0 = __shfl_xor(send0, 32, 64);
-            const float recv1 = __shfl_xor(send1, 32, 64);
-            const float4 o = h ? make_float4(recv0, recv1, acc[s][4 + q], acc[s][12 + q])
-                               : make_float4(acc[s][q], acc[s][8 + q], recv0, recv1);
+            // v_permlane32_swap(a, b): lanes < 32 get (own a, a of lane + 32),
+            // lanes >= 32 (b of lane - 32, own b) -- for both halves the
+            // float4's x and z; the same for y and w.
+            const auto xz = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[s][q]),
+                                                             __float_as_uint(acc[s][4 + q]), false, false);
+            const auto yw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[s][8 + q]),
+                                                             __float_as_uint(acc[s][12 + q]), false, false);
+            const float4 o = make_float4(__uint_as_float(xz[0]), __uint_as_float(yw[0]), __uint_as_float(xz[1]),
+                                         __uint_as_float(yw[1]));
             if (valid) *reinterpret_cast<float4 *>(dst + 4 * q) = o;
         }
     }
