@@ -785,6 +785,11 @@ def test_router_select_bit_exact():
     spread[:, :] = -60.0
     spread[:, 0] = 60.0                             # one winner, the rest underflow to 0
     _router_check(spread, 10, "one winner")
+    order = np.full((2, 512), -300.0, np.float32)   # the oracle's hand-derived lane-order case
+    order[:, 31] = 0.0
+    order[:, 0:512:32] = -16.7
+    order[1] = np.roll(order[1], 7)
+    _router_check(order, 10, "lane-order rounding")
 
 
 def test_router_select_flags_bad_rows():

@@ -406,6 +406,38 @@ def test_router_softmax_closed_forms():
     assert f == 1 and np.all(p[1] == 0) and np.all(p[0] > 0) and np.all(p[2] > 0)
 
 
+def test_router_softmax_lane_order_rounding():
+    # Hand-derived order case.  Sixteen small weights t = expf(-16.7) < 2^-24
+    # sit in lane 0 (columns 0, 32, .., 480) and a 1.0 (logit 0, the max) in
+    # lane 31 (column 31); every other logit underflows to weight 0.  In the
+    # reference's order lane 0 first sums its sixteen t's to T, and the XOR
+    # butterfly then adds lane 31's 1 to T, so the total is fl(T + 1) > 1.
+    # A left-to-right column sum would reach the 1 after one t, absorb each
+    # later t (t is below half an ulp of 1) and total exactly 1.
+    a = np.float32(-16.7)
+    t = O.expf_libm(np.array([a], np.float32))[0]
+    assert 0 < t < np.float32(2.0 ** -24)
+    x = np.full((2, 512), -300.0, np.float32)
+    x[:, 31] = 0.0
+    x[:, 0:512:32] = a
+    x[1] = np.roll(x[1], 7)          # the same pattern moved to lanes 7 and 6
+    p, f = O.router_softmax(x)
+    assert f == 0
+    T = np.float32(0)
+    for _ in range(16):
+        T = np.float32(T + t)
+    s = np.float32(T + np.float32(1))
+    assert s > 1
+    inv = np.float32(1) / s
+    for row, big, small in ((0, 31, slice(0, 512, 32)), (1, 38, slice(7, 512, 32))):
+        assert p[row, big] == np.float32(np.float32(1) * inv) != 1.0
+        assert np.all(p[row, small] == np.float32(t * inv))
+        others = np.ones(512, bool)
+        others[big] = False
+        others[small] = False
+        assert np.all(p[row, others] == 0)
+
+
 def test_router_softmax_matches_independent_emulation():
     x = (np.random.default_rng(2).standard_normal((64, 512)) * 3).astype(np.float32)
     p, f = O.router_softmax(x)
