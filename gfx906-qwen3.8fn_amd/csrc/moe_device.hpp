@@ -29,14 +29,22 @@ __device__ __forceinline__ uint32_t f2h(float v) {
     return __half_as_ushort(__float2half_rn(v));
 }
 
+// a . b (signed bytes) from a zero accumulator in one instruction: the VOP3P
+// v_dot4_i32_i8 takes the 0 inline, where the builtin becomes a v_mov of 0
+// into the destination plus the accumulating v_dot4c.
+__device__ __forceinline__ int sdot4_first(int a, int b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // Integer block dot over one Q4_0 code chunk (16 bytes: byte j holds element j
 // in its low nibble and element j+16 in its high nibble) and 32 Q8 codes
 // (x0 = codes 0..15, x1 = codes 16..31).  Nibbles are 0..15, so v_dot4_i32_i8
 // on the masked bytes is the exact unsigned-nibble x signed-code sum.
 __device__ __forceinline__ int dot_block(uint4 w, uint4 x0, uint4 x1) {
     constexpr uint32_t m = 0x0f0f0f0fu;
-    int s = 0;
-    s = __builtin_amdgcn_sdot4(static_cast<int>(w.x & m), static_cast<int>(x0.x), s, false);
+    int s = sdot4_first(static_cast<int>(w.x & m), static_cast<int>(x0.x));
     s = __builtin_amdgcn_sdot4(static_cast<int>(w.y & m), static_cast<int>(x0.y), s, false);
     s = __builtin_amdgcn_sdot4(static_cast<int>(w.z & m), static_cast<int>(x0.z), s, false);
     s = __builtin_amdgcn_sdot4(static_cast<int>(w.w & m), static_cast<int>(x0.w), s, false);
@@ -100,11 +108,11 @@ __device__ __forceinline__ float xor_sum_from(float v) {
 // nibbles, codes x1).  dot_block(w, x0, x1) is their sum.
 __device__ __forceinline__ void fragment_dots(uint4 w, uint4 x0, uint4 x1, int &f0, int &f1) {
     constexpr uint32_t m = 0x0f0f0f0fu;
-    f0 = __builtin_amdgcn_sdot4(static_cast<int>(w.x & m), static_cast<int>(x0.x), 0, false);
+    f0 = sdot4_first(static_cast<int>(w.x & m), static_cast<int>(x0.x));
     f0 = __builtin_amdgcn_sdot4(static_cast<int>(w.y & m), static_cast<int>(x0.y), f0, false);
     f0 = __builtin_amdgcn_sdot4(static_cast<int>((w.x >> 4) & m), static_cast<int>(x1.x), f0, false);
     f0 = __builtin_amdgcn_sdot4(static_cast<int>((w.y >> 4) & m), static_cast<int>(x1.y), f0, false);
-    f1 = __builtin_amdgcn_sdot4(static_cast<int>(w.z & m), static_cast<int>(x0.z), 0, false);
+    f1 = sdot4_first(static_cast<int>(w.z & m), static_cast<int>(x0.z));
     f1 = __builtin_amdgcn_sdot4(static_cast<int>(w.w & m), static_cast<int>(x0.w), f1, false);
     f1 = __builtin_amdgcn_sdot4(static_cast<int>((w.z >> 4) & m), static_cast<int>(x1.z), f1, false);
     f1 = __builtin_amdgcn_sdot4(static_cast<int>((w.w >> 4) & m), static_cast<int>(x1.w), f1, false);
