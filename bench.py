@@ -351,7 +351,7 @@ def main():
     ap.add_argument("--no-linear", action="store_true", help="skip the quantized linear projections")
     ap.add_argument("--no-graph", action="store_true", help="skip the graph-captured stack passes")
     ap.add_argument("--no-refshapes", action="store_true", help="skip the reference's component shapes (2560/640)")
-    ap.add_argument("--only", choices=["b8", "4k", "16k", "stack", "refshapes"],
+    ap.add_argument("--only", choices=["b8", "4k", "16k", "ep", "stack", "refshapes"],
                     help="run one section alone (for profiler runs); the JSON line then holds that section only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy x5 (FETCH_SIZE/WRITE_SIZE scale for rocprofv3 --pmc)")
@@ -484,27 +484,6 @@ def main():
             "hbm_frac": pbytes / gpu_p / 1e9 / HBM_PEAK_GBS, "group_hist": hp, "items": layer.last_stats(),
         }
         log(f"[bench] 4k prefill {wall_p*1e3:.3f} ms/layer, {NP/wall_p:.0f} tok/s")
-        # One GPU's share of this batch under 8-way expert parallelism:
-        # experts 0..63 (popularity is over a seeded permutation, so the share
-        # mixes popular and rare experts) and the (token, rank) pairs routed
-        # to them, received as rows with one local route of weight 1.  The
-        # routed fold and the shared expert run on each token's home GPU.
-        sel = idp < 64
-        tok = np.nonzero(sel)[0]
-        M = int(tok.size)
-        share = moe_ffn.MoeLayer(2048, 512, 64, 1, False, M, synthetic_seed=1500)
-        xs = dev(np.ascontiguousarray(xph[tok]))
-        ids_s = dev(np.ascontiguousarray(idp[sel].reshape(M, 1).astype(np.int32)))
-        w_s = dev(np.ones((M, 1), np.float32))
-        wall_s, gpu_s, _ = time_forward(share, xs, [(ids_s, w_s)], args.prefill_steps, 3)
-        hs = W.group_histogram(idp[sel].reshape(M, 1), experts=64)
-        result["prefill_4k_ep8_share"] = {
-            "experts": 64, "rows": M, "ms": wall_s * 1e3, "gpu_event_ms": gpu_s * 1e3,
-            "rows_per_s": M / wall_s, "group_hist": hs,
-            "note": "routed rows of experts 0..63 of the 4K batch, k=1, no shared expert; no all-to-all",
-        }
-        log(f"[bench] 4k ep8 share: {M} rows on 64 experts {wall_s*1e3:.3f} ms ({hs})")
-        share.close()
     if layer is not None and not args.no_16k:
         NP = 16384
         xph = W.activations(NP, seed=3002)
@@ -524,6 +503,32 @@ def main():
         layer.close()
         layer = None
         torch.cuda.empty_cache()
+
+    # ---- one GPU's share of the 4K batch under 8-way expert parallelism ----
+    # Experts 0..63 (popularity is over a seeded permutation, so the share
+    # mixes popular and rare experts) and the (token, rank) pairs routed to
+    # them, received as rows with one local route of weight 1.  The routed
+    # fold and the shared expert run on each token's home GPU.
+    if (only is None and not args.no_prefill) or only == "ep":
+        NP = 4096
+        xph = W.activations(NP, seed=2002)
+        idp, _ = W.routes_zipf(NP, 1.1, seed=2003)
+        sel = idp < 64
+        tok = np.nonzero(sel)[0]
+        M = int(tok.size)
+        share = moe_ffn.MoeLayer(2048, 512, 64, 1, False, M, synthetic_seed=1500)
+        xs = dev(np.ascontiguousarray(xph[tok]))
+        ids_s = dev(np.ascontiguousarray(idp[sel].reshape(M, 1).astype(np.int32)))
+        w_s = dev(np.ones((M, 1), np.float32))
+        wall_s, gpu_s, _ = time_forward(share, xs, [(ids_s, w_s)], args.prefill_steps, 3)
+        hs = W.group_histogram(idp[sel].reshape(M, 1), experts=64)
+        result["prefill_4k_ep8_share"] = {
+            "experts": 64, "rows": M, "ms": wall_s * 1e3, "gpu_event_ms": gpu_s * 1e3,
+            "rows_per_s": M / wall_s, "group_hist": hs,
+            "note": "routed rows of experts 0..63 of the 4K batch, k=1, no shared expert; no all-to-all",
+        }
+        log(f"[bench] 4k ep8 share: {M} rows on 64 experts {wall_s*1e3:.3f} ms ({hs})")
+        share.close()
 
     # ---- device router (softmax + top-10 of 512), the step before the layer --
     router = {}
