@@ -338,6 +338,29 @@ def test_prefill_16k_uniform_sampled_tokens(moe512):
     L.close()
 
 
+def test_max_tokens_layer(moe512):
+    """The largest batch a layer takes (max_tokens = 65536, Zipf(1.1) top-10):
+    its contribution buffer (65536 x 11 x 2048 fp32, 5.9 GB) is past 2^32
+    bytes, so 32-bit offsets anywhere in the grouped path would show here.
+    The first, last and sampled tokens against the oracle (middle Q8 rows
+    byte-equal, outputs within 1e-5 rms), then determinism of the whole
+    output."""
+    N = 65536
+    L = moe_ffn.MoeLayer(2048, 512, 512, 10, True, N, experts_q4=moe512["bank"], shared_q4=moe512["shared"])
+    x = W.activations(N, seed=59)
+    ids, w = W.routes_zipf(N, 1.1, seed=60)
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    yh = host(y)
+    assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
+    st = L.last_stats()
+    assert st["mfma_items"] > 0 and st["active_experts"] == 513
+    sample = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(61).choice(N, 6, replace=False)]))
+    layer_parity(L, x, ids, w, moe512["bank"], moe512["shared"], yh, sample, "65536-token layer")
+    y2, _ = L.forward(dev(x), dev(ids), dev(w))
+    assert np.array_equal(host(y2), yh)
+    L.close()
+
+
 def _sparse_bank(L, experts):
     """Canonical bank of layer L with only `experts` exported (others zero)."""
     eb = moe_ffn.expert_bytes(L.H, L.I)
