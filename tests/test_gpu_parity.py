@@ -361,6 +361,35 @@ def test_max_tokens_layer(moe512):
     L.close()
 
 
+@pytest.mark.parametrize("path", ["mfma", "stream"])
+def test_top_k_32_layer(path):
+    """The largest top-k a layer takes (32, half of 64 experts per token, +
+    shared): 33 routes per token are more than the decode kernels fold (16),
+    so the grouped path runs, and the fold takes its ranks in four chunks of
+    eight.  Sampled tokens against the oracle (middle Q8 rows byte-equal,
+    outputs within 1e-5 rms; bit-identical on the streaming path)."""
+    H, I, E, K, N = 2048, 512, 64, 32, 96
+    env = {"MOE_FFN_MFMA_MIN": 1 if path == "mfma" else 0}
+    bank = W.q4_bank(E, seed=901)
+    shared = W.q4_bank(1, seed=902)
+    L = _layer_env(env, H, I, E, K, True, N, experts_q4=bank, shared_q4=shared)
+    x = W.activations(N, seed=903)
+    ids, w = W.routes_zipf(N, 1.1, experts=E, k=K, seed=904)
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    yh = host(y)
+    assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
+    st = L.last_stats()
+    assert (st["mfma_items"] > 0) == (path == "mfma")
+    sample = np.random.default_rng(905).choice(N, 12, replace=False)
+    layer_parity(L, x, ids, w, bank, shared, yh, sample, f"top-32 layer, {path} path")
+    if path == "stream":
+        mask = np.zeros(N, np.uint8)
+        mask[sample] = 1
+        ref = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, token_mask=mask)
+        assert np.array_equal(yh[sample].view(np.uint32), ref["y"][sample].view(np.uint32))
+    L.close()
+
+
 def _sparse_bank(L, experts):
     """Canonical bank of layer L with only `experts` exported (others zero)."""
     eb = moe_ffn.expert_bytes(L.H, L.I)
