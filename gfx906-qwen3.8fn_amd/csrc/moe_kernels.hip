@@ -1128,7 +1128,7 @@ __global__ __launch_bounds__(512, Two ? 4 : 8) void k_decode_gate_up(DecodeArgs 
     const uint32_t lane_off = static_cast<uint32_t>(kb) * 16u;
     uint4 w[8];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) w[q] = buffer_load16(wr, lane_off, q * row_bytes);
+    for (int q = 0; q < 8; ++q) w[q] = buffer_load16_nt(wr, lane_off, q * row_bytes);
     const uint4 d4p = buffer_load16(sr, lane_off, 0);
     // Two: the lane's second block, lane + 64 (block 0 when past the row end).
     const bool has2 = Two && lane + 64 < nbh;
@@ -1137,7 +1137,7 @@ __global__ __launch_bounds__(512, Two ? 4 : 8) void k_decode_gate_up(DecodeArgs 
     uint4 d4p2 = make_uint4(0u, 0u, 0u, 0u);
     if constexpr (Two) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) w2[q] = buffer_load16(wr, lane_off2, q * row_bytes);
+        for (int q = 0; q < 8; ++q) w2[q] = buffer_load16_nt(wr, lane_off2, q * row_bytes);
         d4p2 = buffer_load16(sr, lane_off2, 0);
         // Every load is issued before the quantisation waits on x (the
         // scheduler would otherwise sink half of them behind that wait).
@@ -1246,7 +1246,7 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
         const auto hr = buffer_rsrc(a.mq.heads + xrow, static_cast<uint32_t>(nbi) * 4u);
         uint4 w[8];
 #pragma unroll
-        for (int l = 0; l < 8; ++l) w[l] = buffer_load16(wr, lane_off, 4 * l * row_bytes);
+        for (int l = 0; l < 8; ++l) w[l] = buffer_load16_nt(wr, lane_off, 4 * l * row_bytes);
         const uint4 d4p = buffer_load16(sr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
         uint4 m4p = make_uint4(0u, 0u, 0u, 0u);
         if constexpr (Q41) {
@@ -1263,7 +1263,7 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
             const uint32_t lane_off2 = static_cast<uint32_t>(sub * nbi + kb2) * 16u;
             uint4 w2[8];
 #pragma unroll
-            for (int l = 0; l < 8; ++l) w2[l] = buffer_load16(wr, lane_off2, 4 * l * row_bytes);
+            for (int l = 0; l < 8; ++l) w2[l] = buffer_load16_nt(wr, lane_off2, 4 * l * row_bytes);
             const uint4 d4p2 = buffer_load16(sr, static_cast<uint32_t>(kb2 * 32 + sub * 8) * 2u, 0);
             uint4 m4p2 = make_uint4(0u, 0u, 0u, 0u);
             if constexpr (Q41) {
