@@ -6,7 +6,12 @@ inputs resident in HBM.  The headline workload is BASELINE configs[1], B8
 decode (8 tokens, top-10 of 512 experts + 1 shared, H 2048, I 512), measured
 cold: step i runs layer i % 48 of 48 resident layers with their own weights
 (43.5 GB, far past the 256 MB Infinity Cache) on route set i % 64, so no step
-finds its weights in any cache.  The same rotation over ONE layer's bank is
+finds its weights in any cache.  The K timed steps are captured into one HIP
+graph (every rotated layer run once eagerly first) and the graph is replayed
+--repeats times, each replay its own timed region bracketed by synchronize;
+the value is the median replay, the line gives min / median / max, and the
+same steps launched eagerly from Python are reported beside it
+("b8_decode_eager").  The same rotation over ONE layer's bank is
 reported as "b8_decode_warm" (consecutive route sets share experts, so part
 of a step can hit the Infinity Cache).  Reported alongside: the 4K Zipf(1.1) prefill layer (configs[2], "prefill_4k"), the 16K
 uniform prefill layer (configs[3], "prefill_16k"), the 48-layer stack of 8 + 1024
@@ -38,31 +43,87 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_forward(layer, x, sets, steps, warmup):
-    """Wall and GPU-event time per forward; step i uses route set i % len(sets)
+def time_forward(layer, x, sets, steps, warmup, repeats=1):
+    """Wall and GPU-event seconds per forward; step i uses route set i % len(sets)
     and, when `layer` is a list of layers, layer i % len(layer) (each with its
     own resident weights, so a rotation over many layers reads every step's
-    weights from HBM)."""
+    weights from HBM).  Every forward is validated once and then enqueued
+    through MoeLayer.bind_forward, so the loop times the library, not the
+    per-call tensor checks.  The warm-up runs at least one forward on every
+    layer of the rotation.  With repeats > 1 the timed loop of `steps` forwards
+    runs that many times; returns (walls, gpus, y): per-repeat lists."""
     import torch
     layers = layer if isinstance(layer, (list, tuple)) else [layer]
     y = torch.empty((x.shape[0], layers[0].H), dtype=torch.float32, device=x.device)
     err = torch.zeros(1, dtype=torch.int32, device=x.device)
-    for i in range(warmup):
-        layers[i % len(layers)].forward(x, *sets[i % len(sets)], y=y, error=err)
+    n_calls = max(steps, warmup, len(layers))
+    calls = [layers[i % len(layers)].bind_forward(x, *sets[i % len(sets)], y=y, error=err) for i in range(n_calls)]
+    for i in range(max(warmup, len(layers))):
+        calls[i % n_calls]()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for i in range(steps):
-        layers[i % len(layers)].forward(x, *sets[i % len(sets)], y=y, error=err)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
-    gpu = e0.elapsed_time(e1) / 1e3 / steps
+    walls, gpus = [], []
+    for _ in range(repeats):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(steps):
+            calls[i]()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        walls.append((time.perf_counter() - t0) / steps)
+        gpus.append(e0.elapsed_time(e1) / 1e3 / steps)
     if int(err.cpu()[0]) != 0:
         raise RuntimeError(f"error flags {int(err.cpu()[0])}")
-    return wall, gpu, y
+    if repeats == 1:
+        return walls[0], gpus[0], y
+    return walls, gpus, y
+
+
+def time_forward_graph(layers, x, sets, steps, repeats):
+    """B8 steps replayed from one captured HIP graph: step i = layers[i % L]
+    on route set i % len(sets), each with its own output rows; the graph
+    holds exactly `steps` steps, so one replay is one timed region of `steps`
+    steps, bracketed by synchronize.  Every layer of the rotation runs once
+    eagerly before the capture.  Returns (walls, gpus): seconds per step of
+    each of `repeats` timed replays (wall clock and GPU events)."""
+    import torch
+    import moe_ffn
+    order = [layers[i % len(layers)] for i in range(steps)]
+    st = moe_ffn.MoeStack(order)
+    st.bind([x] * steps, [sets[i % len(sets)][0] for i in range(steps)],
+            [sets[i % len(sets)][1] for i in range(steps)])
+    err = torch.zeros(1, dtype=torch.int32, device=x.device)
+    y = torch.empty((x.shape[0], layers[0].H), dtype=torch.float32, device=x.device)
+    for i, L in enumerate(layers):   # every rotated layer once, outside the graph
+        L.forward(x, *sets[i % len(sets)], y=y, error=err)
+    st.capture()
+    st.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    walls, gpus = [], []
+    for _ in range(repeats):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        st.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        walls.append((time.perf_counter() - t0) / steps)
+        gpus.append(e0.elapsed_time(e1) / 1e3 / steps)
+    if int(st.error.cpu()[0]) != 0 or int(err.cpu()[0]) != 0:
+        raise RuntimeError(f"error flags {int(st.error.cpu()[0])} / {int(err.cpu()[0])}")
+    outs = st.outputs()
+    st.graph = None
+    return walls, gpus, outs
+
+
+def spread(values, scale=1.0):
+    """min / median / max of a list of timings (scaled), for the JSON line."""
+    v = np.sort(np.asarray(values, dtype=np.float64)) * scale
+    return {"min": float(v[0]), "median": float(np.median(v)), "max": float(v[-1]), "n": int(v.size)}
 
 
 def time_stages(layer, x, sets, steps):
@@ -108,7 +169,9 @@ def pmc_traffic(kernel, units, record="pmc_b8_decode.json"):
 def read_ceiling(nbytes, buffers=12, iters=48):
     """Time the library's plain streaming-read kernel (moe_read_probe) over
     `nbytes`, rotating `buffers` distinct buffers (together larger than the
-    256 MB Infinity Cache) so every read is cold.  Returns seconds per read."""
+    256 MB Infinity Cache) so every read is cold.  Returns seconds per read
+    (back to back: `iters` launches between two events; alone: the median of
+    `iters` launches each timed by its own events after a synchronize)."""
     import torch
     import moe_ffn
     nbytes = nbytes // 16 * 16
@@ -124,8 +187,17 @@ def read_ceiling(nbytes, buffers=12, iters=48):
         moe_ffn.read_probe(bufs[i % buffers], sink)
     e1.record(stream)
     torch.cuda.synchronize()
+    back = e0.elapsed_time(e1) / 1e3 / iters
+    lone = []
+    for i in range(iters):
+        torch.cuda.synchronize()
+        e0.record(stream)
+        moe_ffn.read_probe(bufs[i % buffers], sink)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        lone.append(e0.elapsed_time(e1) / 1e3)
     del bufs
-    return e0.elapsed_time(e1) / 1e3 / iters
+    return back, float(np.median(lone))
 
 
 def time_graph(stack, steps):
@@ -341,6 +413,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--repeats", type=int, default=5, help="timed repeats of the B8 headline (min/median/max)")
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -402,19 +475,35 @@ def main():
         touched = np.array([W.group_histogram(i)["touched"] for i, _ in route_sets])
         log(f"[bench] b8 decode: {R} route sets over {NL} layers, touched experts mean {touched.mean():.1f} "
             f"(min {touched.min()}, max {touched.max()})")
-        wall, gpu, _ = time_forward(layers, x, sets, args.steps, args.warmup)
+        # Headline: the steps replayed from one captured HIP graph (the
+        # library's launches on the GPU's clock, no Python between them).
+        walls_g, gpus_g, outs = time_forward_graph(layers, x, sets, args.steps, args.repeats)
+        wall, gpu = float(np.median(walls_g)), float(np.median(gpus_g))
+        # The graph's first step against the same forward run eagerly.
+        y_chk, _ = layers[0].forward(x, *sets[0])
+        torch.cuda.synchronize()
+        if not torch.equal(outs[0].view(torch.int32), y_chk.view(torch.int32)):
+            raise RuntimeError("graph replay output differs from the eager forward")
+        # The same rotation launched eagerly, one Python call per step
+        # (pre-validated forwards; every rotated layer warmed first).
+        walls_e, gpus_e, _ = time_forward(layers, x, sets, args.steps, args.warmup, repeats=args.repeats)
         stats = layers[0].last_stats()
         # Stage durations over the same rotation; step i touched[i % R] + 1 units.
         n_stage = max(R, args.steps)
-        t_stage = time_stages(layers, x, sets, n_stage)
+        t_stages = [time_stages(layers, x, sets, n_stage) for _ in range(args.repeats)]
+        gate_rep = [float(t[1]) / n_stage for t in t_stages]
+        pick = int(np.argsort(gate_rep)[len(gate_rep) // 2])   # the repeat with the median gate/up time
+        t_stage = t_stages[pick]
         units = touched[np.arange(n_stage) % R] + 1
         gate_bytes = float(np.sum(units)) * GATE_UP_BYTES_PER_EXPERT
         down_bytes = float(np.sum(units)) * DOWN_BYTES_PER_EXPERT
         t_prep, t_gate, t_down, t_fold = (t_stage / n_stage).tolist()
         achieved = gate_bytes / float(t_stage[1]) / 1e9
         layer_bytes = float(np.mean([W.algorithmic_bytes(N, int(t)) for t in touched]))
-        log(f"[bench] b8 cold wall {wall*1e6:.1f} us gpu {gpu*1e6:.1f} us; stages prep {t_prep*1e6:.1f} gate/up "
-            f"{t_gate*1e6:.1f} down {t_down*1e6:.1f} fold {t_fold*1e6:.1f} us; items {stats}")
+        log(f"[bench] b8 cold graph wall {wall*1e6:.2f} us (repeats {[round(w*1e6, 2) for w in walls_g]}) gpu "
+            f"{gpu*1e6:.2f} us; eager wall {np.median(walls_e)*1e6:.2f} us gpu {np.median(gpus_e)*1e6:.2f} us; "
+            f"stages prep {t_prep*1e6:.1f} gate/up {t_gate*1e6:.2f} (repeats {[round(g*1e6, 2) for g in gate_rep]}) "
+            f"down {t_down*1e6:.2f} fold {t_fold*1e6:.1f} us; items {stats}")
 
         result.update({
             "metric": "MoE Q4_0 expert FFN tokens/s (B8 decode, 4K prefill); % HBM/MFMA-i8 roofline",
@@ -434,8 +523,18 @@ def main():
                        "top_k": 10, "shared_experts": 1, "route_sets": R, "layers_rotated": NL,
                        "rotated_weight_gb": moe_ffn.memory_bytes(2048, 512, 512, 10, True, NS)[0] * NL / 1e9,
                        "touched_experts_mean": float(touched.mean()),
+                       "timing": f"median of {args.repeats} timed replays of one HIP graph holding the "
+                                 f"{args.steps} steps (each replay bracketed by synchronize)",
                        "gpu_event_us_per_layer": gpu * 1e6,
                        "layer_hbm_frac": layer_bytes / gpu / 1e9 / HBM_PEAK_GBS},
+            "b8_spread_us": {"graph_wall": spread(walls_g, 1e6), "graph_gpu": spread(gpus_g, 1e6),
+                             "eager_wall": spread(walls_e, 1e6), "eager_gpu": spread(gpus_e, 1e6),
+                             "gate_up_stage": spread(gate_rep, 1e6)},
+            "b8_decode_eager": {"tokens_per_s": N / float(np.median(walls_e)),
+                                "us_per_layer": float(np.median(walls_e)) * 1e6,
+                                "gpu_event_us": float(np.median(gpus_e)) * 1e6,
+                                "note": "the same rotation launched one Python call per step (pre-validated "
+                                        "forwards through ctypes), every rotated layer warmed first"},
             "roofline": {"kernel": "k_decode_gate_up (x Q8 + gate/up + SiLU + middle Q8)", "bound": "hbm",
                          "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                          "traffic": pmc_traffic("k_decode_gate_up", float(touched.mean()) + 1),
@@ -451,19 +550,25 @@ def main():
             "tokens_per_s": N / wall_w, "us_per_layer": wall_w * 1e6, "gpu_event_us": gpu_w * 1e6,
             "gate_up_us": tw[1] * 1e6, "down_us": tw[2] * 1e6,
             "gate_up_hbm_frac": gate_bytes / n_stage / tw[1] / 1e9 / HBM_PEAK_GBS,
-            "note": "one layer's bank, 64 rotated route sets: consecutive steps share experts, so part of a step "
-                    "can be served from the 256 MB Infinity Cache",
+            "note": "one layer's bank, 64 rotated route sets, eager: consecutive steps share experts, so part of "
+                    "a step can be served from the 256 MB Infinity Cache",
         }
         log(f"[bench] b8 warm (one bank) wall {wall_w*1e6:.1f} us; gate/up {tw[1]*1e6:.1f} down {tw[2]*1e6:.1f} us")
-        # Practical ceiling: a plain streaming read of the same byte count.
-        t_read = read_ceiling(int(gate_bytes / n_stage))
+        # Practical ceiling: a plain streaming read of the same byte count,
+        # launched back to back (as the layer's kernels follow each other)
+        # and launched alone (each read after a synchronize).
+        nb_gate = int(gate_bytes / n_stage)
+        t_read, t_lone = read_ceiling(nb_gate)
+        gbs = lambda t: gate_bytes / n_stage / t / 1e9
         result["read_ceiling"] = {
-            "bytes": int(gate_bytes / n_stage) // 16 * 16, "us": t_read * 1e6,
-            "GB/s": gate_bytes / n_stage / t_read / 1e9, "frac_of_peak": gate_bytes / n_stage / t_read / 1e9 / HBM_PEAK_GBS,
-            "gate_up_frac_of_ceiling": t_read / t_gate,
+            "bytes": nb_gate // 16 * 16,
+            "back_to_back_us": t_read * 1e6, "back_to_back_GB/s": gbs(t_read),
+            "back_to_back_frac_of_peak": gbs(t_read) / HBM_PEAK_GBS,
+            "lone_us": t_lone * 1e6, "lone_GB/s": gbs(t_lone), "lone_frac_of_peak": gbs(t_lone) / HBM_PEAK_GBS,
+            "gate_up_frac_of_back_to_back": t_read / t_gate, "gate_up_frac_of_lone": t_lone / t_gate,
         }
-        log(f"[bench] read ceiling at {gate_bytes / n_stage / 1e6:.1f} MB: {t_read * 1e6:.1f} us "
-            f"({gate_bytes / n_stage / t_read / 1e9:.0f} GB/s)")
+        log(f"[bench] read ceiling at {gate_bytes / n_stage / 1e6:.1f} MB: back to back {t_read * 1e6:.2f} us "
+            f"({gbs(t_read):.0f} GB/s), alone {t_lone * 1e6:.2f} us ({gbs(t_lone):.0f} GB/s)")
 
     # ---- 4K Zipf prefill and 16K uniform prefill ----
     layer = None

@@ -18,6 +18,28 @@
 
 namespace moe {
 
+// Makes `device` current for one host call of the C ABI and restores the
+// caller's current device on every return path (the calls that allocate,
+// copy or synchronise need their handle's device current; the caller's
+// choice of device must survive them).
+class DeviceScope {
+public:
+    explicit DeviceScope(int device) {
+        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+        ok_ = hipSetDevice(device) == hipSuccess;
+    }
+    ~DeviceScope() {
+        if (prev_ >= 0) (void)hipSetDevice(prev_);
+    }
+    DeviceScope(const DeviceScope &) = delete;
+    DeviceScope &operator=(const DeviceScope &) = delete;
+    bool ok() const { return ok_; }
+
+private:
+    int prev_ = -1;
+    bool ok_ = false;
+};
+
 // Routing and tiling constants.
 inline constexpr int kStreamTokens = 4;     // tokens per streaming (decode) work item
 inline constexpr int kMfmaTile = 128;       // tokens per MFMA work item (4 waves x 32)

@@ -70,6 +70,7 @@ struct moe_ffn_layer {
     const int32_t *last_ids = nullptr;
     float *last_y = nullptr;
     int *last_error = nullptr;
+    hipStream_t last_stream = nullptr;   // stream of the last forward (its side-stream work joins it)
     // Stage profiler (moe_ffn_profile): a ring of events, one set per forward.
     static constexpr int kStageMarks = MOE_STAGE_FOLD + 2;
     // Grouped forwards run the streaming items (small groups, bound by memory
@@ -243,11 +244,9 @@ int repack_experts(moe_ffn_layer *L, const uint8_t *staging, int first, int coun
     return hipSuccess;
 }
 
-int create_common(const moe_ffn_config *config, int device, moe_ffn_layer **layer, moe_ffn_layer *&L) {
-    if (!config_ok(config) || !layer) return kInvalid;
-    int count = 0;
-    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return kInvalid;
-    if (hipSetDevice(device) != hipSuccess) return kInvalid;
+// The layer's device must be current (the create entry points hold a
+// DeviceScope around the whole creation).
+int create_common(const moe_ffn_config *config, int device, moe_ffn_layer *&L) {
     L = new (std::nothrow) moe_ffn_layer();
     if (!L) return hipErrorOutOfMemory;
     L->cfg = *config;
@@ -263,6 +262,7 @@ int create_common(const moe_ffn_config *config, int device, moe_ffn_layer **laye
     if (r != hipSuccess) { moe_ffn_destroy(L); L = nullptr; return r; }
     return hipSuccess;
 }
+
 
 int upload(moe_ffn_layer *L, const void *experts, const void *shared, bool from_device) {
     const Shape &s = L->shape;
@@ -344,6 +344,27 @@ void mark_uploaded(moe_ffn_layer *L) {
     L->upload_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - L->create_start).count();
 }
 
+// Validates a create call before any HIP call, makes `device` current for
+// the creation (restoring the caller's device afterwards), and runs
+// `fill(L)` to put the weights into a new layer's planes.
+template<class Fill>
+int create_layer(const moe_ffn_config *config, int device, moe_ffn_layer **layer, Fill &&fill) {
+    if (!config_ok(config) || !layer) return kInvalid;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return kInvalid;
+    moe::DeviceScope scope(device);
+    if (!scope.ok()) return kInvalid;
+    moe_ffn_layer *L = nullptr;
+    int r = create_common(config, device, L);
+    if (r != hipSuccess) return r;
+    r = fill(L);
+    mark_uploaded(L);
+    if (r == hipSuccess) r = finish_create(L);
+    if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
+    *layer = L;
+    return hipSuccess;
+}
+
 moe::FfnArgs base_args(moe_ffn_layer *L, int tokens, int *error) {
     moe::FfnArgs a{};
     a.shape = L->shape;
@@ -377,15 +398,8 @@ int moe_ffn_memory_bytes(const moe_ffn_config *config, size_t *weight_bytes, siz
 int moe_ffn_create(const moe_ffn_config *config, const void *experts_q4, const void *shared_q4, int device,
                    moe_ffn_layer **layer) {
     if (!experts_q4 || (config && config->has_shared && !shared_q4)) return kInvalid;
-    moe_ffn_layer *L = nullptr;
-    int r = create_common(config, device, layer, L);
-    if (r != hipSuccess) return r;
-    r = upload(L, experts_q4, shared_q4, false);
-    mark_uploaded(L);
-    if (r == hipSuccess) r = finish_create(L);
-    if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
-    *layer = L;
-    return hipSuccess;
+    return create_layer(config, device, layer,
+                        [&](moe_ffn_layer *L) { return upload(L, experts_q4, shared_q4, false); });
 }
 
 int moe_ffn_create_from_device(const moe_ffn_config *config, const void *experts_q4_device,
@@ -393,15 +407,8 @@ int moe_ffn_create_from_device(const moe_ffn_config *config, const void *experts
     if (!experts_q4_device || !aligned(experts_q4_device, 2) ||
         (config && config->has_shared && !aligned(shared_q4_device, 2)))
         return kInvalid;
-    moe_ffn_layer *L = nullptr;
-    int r = create_common(config, device, layer, L);
-    if (r != hipSuccess) return r;
-    r = upload(L, experts_q4_device, shared_q4_device, true);
-    mark_uploaded(L);
-    if (r == hipSuccess) r = finish_create(L);
-    if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
-    *layer = L;
-    return hipSuccess;
+    return create_layer(config, device, layer,
+                        [&](moe_ffn_layer *L) { return upload(L, experts_q4_device, shared_q4_device, true); });
 }
 
 int moe_ffn_create_tensors(const moe_ffn_config *config, const void *gate_exps, const void *up_exps,
@@ -409,40 +416,27 @@ int moe_ffn_create_tensors(const moe_ffn_config *config, const void *gate_exps, 
                            const void *shared_down, int device, moe_ffn_layer **layer) {
     if (!gate_exps || !up_exps || !down_exps) return kInvalid;
     if (config && config->has_shared && (!shared_gate || !shared_up || !shared_down)) return kInvalid;
-    moe_ffn_layer *L = nullptr;
-    int r = create_common(config, device, layer, L);
-    if (r != hipSuccess) return r;
     const void *const routed[3] = {gate_exps, up_exps, down_exps};
     const void *const shared[3] = {shared_gate, shared_up, shared_down};
-    r = upload_tensors(L, routed, shared);
-    mark_uploaded(L);
-    if (r == hipSuccess) r = finish_create(L);
-    if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
-    *layer = L;
-    return hipSuccess;
+    return create_layer(config, device, layer, [&](moe_ffn_layer *L) { return upload_tensors(L, routed, shared); });
 }
 
 int moe_ffn_create_synthetic(const moe_ffn_config *config, uint64_t seed, int device, moe_ffn_layer **layer) {
-    moe_ffn_layer *L = nullptr;
-    int r = create_common(config, device, layer, L);
-    if (r != hipSuccess) return r;
-    const size_t blocks = static_cast<size_t>(L->shape.Ep) * L->shape.I * (L->shape.H / 32);
-    for (int m = 0; m < 3 && r == hipSuccess; ++m) {
-        const Plane pl = plane(L, m);
-        r = moe::launch_synthetic_weights(pl.codes, pl.scales, pl.mins, blocks, static_cast<size_t>(m) * blocks,
-                                          pl.blocks_per_row, pl.group, seed, nullptr);
-    }
-    if (r == hipSuccess) r = hipDeviceSynchronize();
-    mark_uploaded(L);
-    if (r == hipSuccess) r = finish_create(L);
-    if (r != hipSuccess) { moe_ffn_destroy(L); return r; }
-    *layer = L;
-    return hipSuccess;
+    return create_layer(config, device, layer, [&](moe_ffn_layer *L) {
+        const size_t blocks = static_cast<size_t>(L->shape.Ep) * L->shape.I * (L->shape.H / 32);
+        int r = hipSuccess;
+        for (int m = 0; m < 3 && r == hipSuccess; ++m) {
+            const Plane pl = plane(L, m);
+            r = moe::launch_synthetic_weights(pl.codes, pl.scales, pl.mins, blocks, static_cast<size_t>(m) * blocks,
+                                              pl.blocks_per_row, pl.group, seed, nullptr);
+        }
+        return r == hipSuccess ? static_cast<int>(hipDeviceSynchronize()) : r;
+    });
 }
 
 int moe_ffn_destroy(moe_ffn_layer *L) {
     if (!L) return kInvalid;
-    (void)hipSetDevice(L->device);
+    moe::DeviceScope scope(L->device);
     (void)hipDeviceSynchronize();
     profile_free(L);
     if (L->join) (void)hipEventDestroy(L->join);
@@ -460,7 +454,8 @@ int moe_ffn_export_expert(moe_ffn_layer *L, int expert, void *host_q4) {
     const size_t mblocks = matrix_blocks(s);
     const size_t ebytes = expert_bytes(s, L->down_q41);
     uint8_t *staging = nullptr;
-    if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
+    moe::DeviceScope scope(L->device);
+    if (!scope.ok()) return kInvalid;
     if (hipMalloc(&staging, ebytes) != hipSuccess) return hipErrorOutOfMemory;
     const size_t e = static_cast<size_t>(expert);
     int r = hipSuccess;
@@ -578,6 +573,7 @@ int forward_impl(moe_ffn_layer *L, const float *x, const void *x_q8, const int32
     L->last_shared_gate = shared_gate;
     L->last_y = y;
     L->last_error = error;
+    L->last_stream = s;
     return hipSuccess;
 }
 }  // namespace
@@ -729,7 +725,8 @@ int moe_ffn_expert_run(moe_ffn_layer *L, int expert, const float *x, int columns
     float *xd = L->contrib, *yd = L->contrib + elems;
     int *err = L->diag_error;
     const auto s = static_cast<hipStream_t>(stream);
-    if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
+    moe::DeviceScope scope(L->device);
+    if (!scope.ok()) return kInvalid;
     // One forward: quantize x, gate/up + SiLU*up + Q8, down (the work list
     // of the single group is built once, before the warm-up).
     auto pass = [&]() -> hipError_t {
@@ -821,16 +818,20 @@ int moe_ffn_debug_last(moe_ffn_layer *L, void *x_q8, void *middle_q8, int32_t *r
 int moe_ffn_last_stats(moe_ffn_layer *L, int32_t *stream_items, int32_t *mfma_items, int32_t *active_experts) {
     if (!L) return kInvalid;
     int32_t c[4] = {0, 0, 0, 0};
-    if (hipSetDevice(L->device) != hipSuccess) return kInvalid;
-    // Synchronous diagnostic: wait for the device first, so the counts are
-    // those of the last forward whatever stream it ran on.
-    if (hipDeviceSynchronize() != hipSuccess) return kInvalid;
+    moe::DeviceScope scope(L->device);
+    if (!scope.ok()) return kInvalid;
+    // Synchronous diagnostic: wait for the last forward's stream (its
+    // streaming chain on the side stream joins that stream before the fold),
+    // so the counts are that forward's; other streams keep running.
+    const hipStream_t s = L->last_stream;
+    if (hipStreamSynchronize(s) != hipSuccess) return kInvalid;
     if (L->last_decode && L->last_tokens > 0) {   // group the last batch's routes (not done by the decode path)
         const hipError_t g = moe::launch_prepare(nullptr, L->last_ids, L->last_weights, L->last_tokens, L->shape,
-                                                 L->xq, L->routes, L->active_mfma_min, L->diag_error, nullptr);
+                                                 L->xq, L->routes, L->active_mfma_min, L->diag_error, s);
         if (g != hipSuccess) return g;
     }
-    const hipError_t r = hipMemcpy(c, L->routes.item_counts, sizeof(c), hipMemcpyDeviceToHost);
+    hipError_t r = hipMemcpyAsync(c, L->routes.item_counts, sizeof(c), hipMemcpyDeviceToHost, s);
+    if (r == hipSuccess) r = hipStreamSynchronize(s);
     if (r != hipSuccess) return r;
     if (stream_items) *stream_items = c[0];
     if (mfma_items) *mfma_items = c[1];

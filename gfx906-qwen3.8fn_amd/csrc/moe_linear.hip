@@ -40,6 +40,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <cstdlib>
 #include <mutex>
@@ -162,6 +163,11 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex scratch_mutex;
 uint8_t *scratch_ptr[kMaxDevices] = {};
+// Set while a host thread is inside moe_linear_apply_noalloc for that GPU: a
+// second thread that enters meanwhile is refused instead of enqueueing work
+// on the same array.  (Calls enqueued one after another on different streams
+// can still overlap on the GPU; that is the caller's to order.)
+std::atomic<int> scratch_busy[kMaxDevices] = {};
 
 // Looks up (once per device, with that device current) the device address of
 // `scratch`.  Called by moe_linear_create, the library's set-up call, so that
@@ -233,7 +239,8 @@ int moe_linear_create(int type, int input, int output, int max_columns, const vo
         return kInvalid;
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return kInvalid;
-    if (hipSetDevice(device) != hipSuccess) return kInvalid;
+    moe::DeviceScope scope(device);   // the caller's current device is restored on return
+    if (!scope.ok()) return kInvalid;
     auto *L = new (std::nothrow) moe_linear;
     if (!L) return hipErrorOutOfMemory;
     L->type = type;
@@ -282,7 +289,7 @@ int moe_linear_create(int type, int input, int output, int max_columns, const vo
 
 int moe_linear_destroy(moe_linear *L) {
     if (!L) return kInvalid;
-    (void)hipSetDevice(L->device);
+    moe::DeviceScope scope(L->device);
     release(L);
     return 0;
 }
@@ -395,6 +402,11 @@ int moe_linear_apply_noalloc(moe_linear *L, const float *x, int columns, float *
     if (hipGetDevice(&device) != hipSuccess || device != L->device) return kInvalid;
     uint8_t *ws = noalloc_scratch(device);
     if (!ws) return hipErrorNotInitialized;
+    if (scratch_busy[device].exchange(1, std::memory_order_acquire)) return hipErrorContextAlreadyInUse;
+    struct Release {
+        std::atomic<int> &flag;
+        ~Release() { flag.store(0, std::memory_order_release); }
+    } release_busy{scratch_busy[device]};
     const auto s = static_cast<hipStream_t>(stream);
     const int capacity = static_cast<int>(kNoallocScratchBytes / (static_cast<size_t>(L->nb) * 36));
     if (use_mfma_within(L, columns, capacity)) {

@@ -247,6 +247,25 @@ class MoeLayer:
                                          _ptr(y), _ptr(error), _stream(stream)), "moe_ffn_forward")
         return y, error
 
+    def bind_forward(self, x, ids, weights, y, error, shared_gate=None, stream=None):
+        """Validate the tensors of a forward() once and return a no-argument
+        callable that enqueues that forward with no per-call checks (the
+        pointers and the stream handle are resolved here).  For loops that
+        time the library rather than the Python checks; the tensors must stay
+        alive and keep their shapes while the callable is used."""
+        import torch
+        n = x.shape[0]
+        _need(x, "x", torch.float32, (n, self.H), x.device)
+        self._io_check(n, x.device, ids, weights, shared_gate, y, error)
+        fn, handle = library().moe_ffn_forward, self.handle
+        args = (_ptr(x), _ptr(ids), _ptr(weights), n, _ptr(shared_gate), _ptr(y), _ptr(error), _stream(stream))
+
+        def call():
+            st = fn(handle, *args)
+            if st != 0:
+                raise MoeError("moe_ffn_forward", st)
+        return call
+
     def forward_q8(self, x_q8, ids, weights, shared_gate=None, y=None, error=None, stream=None):
         """forward() from canonical Q8_1 rows x_q8 (uint8 [tokens][H/32*36])."""
         import torch
@@ -437,6 +456,7 @@ class MoeLinear:
     def __init__(self, type_, input, output, weights, max_columns=0, device=0):
         import torch
         self.type, self.K, self.M, self.max_columns = type_, input, output, max_columns
+        self.device = device
         handle = ctypes.c_void_p()
         if isinstance(weights, np.ndarray):
             w = np.ascontiguousarray(weights, dtype=np.uint8)
@@ -496,9 +516,10 @@ class MoeLinear:
         workspace; y and error must be given (nothing is allocated)."""
         import torch
         n = x.shape[0]
-        _need(x, "x", torch.float32, (n, self.K), x.device)
-        _need(y, "y", torch.float32, (n, self.M), x.device)
-        _need(error, "error", torch.int32, (1,), x.device)
+        dev = torch.device("cuda", self.device)   # the static array is set up for the handle's GPU
+        _need(x, "x", torch.float32, (n, self.K), dev)
+        _need(y, "y", torch.float32, (n, self.M), dev)
+        _need(error, "error", torch.int32, (1,), dev)
         _check(library().moe_linear_apply_noalloc(self.handle, _ptr(x), n, _ptr(y), _ptr(error), _stream(stream)),
                "moe_linear_apply_noalloc")
         return y, error

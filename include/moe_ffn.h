@@ -231,11 +231,14 @@ int moe_ffn_replay_stage(moe_ffn_layer *layer, int stage, void *stream);
 int moe_ffn_profile(moe_ffn_layer *layer, int forwards);
 int moe_ffn_profile_read(moe_ffn_layer *layer, double *stage_ms, int *forwards);
 
-/* Last-forward statistics (host, synchronous: waits for the device first):
- * work items per path and the number of experts (incl. shared) that received
- * tokens.  After a decode-path forward it groups that forward's routes again
+/* Last-forward statistics (host, synchronous: waits for the last forward's
+ * stream, which must still exist, and for nothing else): work items per path
+ * and the number of experts (incl. shared) that received tokens.  After a
+ * decode-path forward it groups that forward's routes again on that stream
  * (its ids and weights must still be valid), flagging into a word inside the
- * layer, never into the forward's `error`. */
+ * layer, never into the forward's `error`.  Like every call here that needs
+ * the layer's device current (create, destroy, export, expert_run), it
+ * leaves the caller's current device as it found it. */
 int moe_ffn_last_stats(moe_ffn_layer *layer, int32_t *stream_items, int32_t *mfma_items,
                        int32_t *active_experts);
 
@@ -320,7 +323,10 @@ int moe_linear_apply(moe_linear *linear, const float *x, int columns, float *y, 
  * any HIP call; the handle's device must be current (moe_linear_create set
  * the array up for it), else 1.  Same outputs and flags as moe_linear_apply.
  * Every call on one GPU shares that GPU's array: calls that overlap on one
- * GPU (on any handle or stream) race. */
+ * GPU (on any handle or stream) race.  Issue them on one stream, or order
+ * the streams.  A host thread that enters this call while another thread is
+ * inside it for the same GPU gets 216 (hipErrorContextAlreadyInUse) and
+ * nothing is enqueued. */
 int moe_linear_apply_noalloc(moe_linear *linear, const float *x, int columns, float *y, int *error,
                              void *stream);
 

@@ -8,9 +8,18 @@
 // Weights, x and logits come from an integer hash (below), so the expected
 // outputs can be written by the CPU oracle without shipping the weights:
 // tests/golden/make_abi_case.py writes tests/golden/abi_caller_case.bin with
-// the oracle's ids, weights and y for two batches (2 tokens: the decode path;
-// 24 tokens: grouped streaming).  Both paths follow the reference's fp32
-// order, so every value must match bit for bit.
+// the oracle's ids, weights and y for three batches (2 tokens: the decode
+// path, no shared gate; 24 tokens: grouped streaming, gated; 3 tokens: the
+// decode path, gated).  Every path follows the reference's fp32 order, so
+// every value must match bit for bit.
+//
+// Gated batches follow the reference's shared_project: the shared expert's
+// scalar gate logit per token is the dense H -> 1 projection of the FFN input
+// (launch_dense_linear into f(16), src/session.hip:1399-1402), which stays
+// with the caller; moe_ffn_forward then takes those logits as `shared_gate`
+// and applies sigmoid(g) to the shared expert's row (shared_add,
+// src/session.hip:1404-1410).  Here the projection is a plain fp32 dot product
+// on the host in element order, which the case generator repeats.
 //
 // Usage: abi_caller <case.bin>   (exit 0 = pass)
 #include "moe_ffn.h"
@@ -55,6 +64,22 @@ float hashed(uint64_t tag, size_t i, float scale) {
     return static_cast<float>(static_cast<int>(mix(tag + i) & 0xFFFFu) - 32768) * scale;
 }
 
+// The shared gate's dense H -> 1 projection of each token row: g[t] = sum of
+// x[t][i] * gate_w[i], products rounded to fp32 and added left to right.
+#pragma clang fp contract(off)
+std::vector<float> gate_logits(const std::vector<float> &x, const std::vector<float> &gate_w, int n) {
+    std::vector<float> g(static_cast<size_t>(n));
+    for (int t = 0; t < n; ++t) {
+        float acc = 0.0f;
+        for (int i = 0; i < kH; ++i) {
+            const float p = x[static_cast<size_t>(t) * kH + i] * gate_w[static_cast<size_t>(i)];
+            acc = acc + p;
+        }
+        g[static_cast<size_t>(t)] = acc;
+    }
+    return g;
+}
+
 #define CHECK(call)                                                                       \
     do {                                                                                  \
         const int st_ = static_cast<int>(call);                                           \
@@ -71,14 +96,20 @@ int main(int argc, char **argv) {
     FILE *f = std::fopen(argv[1], "rb");
     if (!f) { std::fprintf(stderr, "cannot open %s\n", argv[1]); return 2; }
     int32_t head[8];
-    if (std::fread(head, 4, 8, f) != 8 || head[0] != 0x4D4F4531 || head[1] != kH || head[2] != kI || head[3] != kE ||
+    if (std::fread(head, 4, 8, f) != 8 || head[0] != 0x4D4F4532 || head[1] != kH || head[2] != kI || head[3] != kE ||
         head[4] != kK) {
         std::fprintf(stderr, "bad case file header\n");
         return 2;
     }
     const int ncases = head[5];
-    std::vector<int> tokens(ncases);
-    if (ncases < 1 || ncases > 2 || std::fread(tokens.data(), 4, ncases, f) != static_cast<size_t>(ncases)) return 2;
+    if (ncases < 1 || ncases > 8) return 2;
+    std::vector<int> tokens(ncases), gated(ncases);
+    if (std::fread(tokens.data(), 4, ncases, f) != static_cast<size_t>(ncases) ||
+        std::fread(gated.data(), 4, ncases, f) != static_cast<size_t>(ncases))
+        return 2;
+    // The shared gate's projection weights (ffn_gate_inp_shexp, H floats).
+    std::vector<float> gate_w(kH);
+    for (int i = 0; i < kH; ++i) gate_w[static_cast<size_t>(i)] = hashed(0x6A7E000000ull, static_cast<size_t>(i), 1.0f / 1048576);
 
     // The routed-expert tensors as Experts::ram holds them: [E][rows][blocks].
     std::vector<uint8_t> gate, up, down;
@@ -120,9 +151,14 @@ int main(int argc, char **argv) {
             std::fprintf(stderr, "case file truncated\n");
             return 2;
         }
-        float *dx = nullptr, *dlogits = nullptr, *dw = nullptr, *dy = nullptr;
+        float *dx = nullptr, *dlogits = nullptr, *dw = nullptr, *dy = nullptr, *dgate = nullptr;
         int32_t *dids = nullptr;
         int *derr = nullptr;
+        if (gated[c]) {   // f(16): the scalar gate logits, before the FFN call
+            const std::vector<float> g = gate_logits(x, gate_w, n);
+            CHECK(hipMalloc(&dgate, g.size() * 4));
+            CHECK(hipMemcpy(dgate, g.data(), g.size() * 4, hipMemcpyHostToDevice));
+        }
         CHECK(hipMalloc(&dx, x.size() * 4));
         CHECK(hipMalloc(&dlogits, logits.size() * 4));
         CHECK(hipMalloc(&dids, want_ids.size() * 4));
@@ -136,7 +172,7 @@ int main(int argc, char **argv) {
         // round trip between them (the reference downloads probabilities and
         // uploads routes here, src/session.hip:1422-1433, 393-410).
         CHECK(moe_router_select(dlogits, n, kE, kK, nullptr, dids, dw, derr, stream));
-        CHECK(moe_ffn_forward(layer, dx, dids, dw, n, nullptr, dy, derr, stream));
+        CHECK(moe_ffn_forward(layer, dx, dids, dw, n, dgate, dy, derr, stream));
         std::vector<int32_t> ids(want_ids.size());
         std::vector<float> w(want_w.size()), y(want_y.size());
         int err = -1;
@@ -150,8 +186,9 @@ int main(int argc, char **argv) {
         size_t ydiff = 0;
         for (size_t i = 0; i < y.size(); ++i) ydiff += std::memcmp(&y[i], &want_y[i], 4) != 0;
         const bool ok = err == 0 && ids_ok && w_ok && ydiff == 0;
-        std::printf("case %d: %d tokens, error word %d, ids %s, weights %s, y %zu of %zu values differ: %s\n", c, n, err,
-                    ids_ok ? "equal" : "DIFFER", w_ok ? "bit-equal" : "DIFFER", ydiff, y.size(), ok ? "ok" : "FAIL");
+        std::printf("case %d: %d tokens, %s, error word %d, ids %s, weights %s, y %zu of %zu values differ: %s\n", c,
+                    n, gated[c] ? "shared gate" : "no shared gate", err, ids_ok ? "equal" : "DIFFER",
+                    w_ok ? "bit-equal" : "DIFFER", ydiff, y.size(), ok ? "ok" : "FAIL");
         failures += !ok;
         CHECK(hipFree(dx));
         CHECK(hipFree(dlogits));
@@ -159,6 +196,7 @@ int main(int argc, char **argv) {
         CHECK(hipFree(dw));
         CHECK(hipFree(dy));
         CHECK(hipFree(derr));
+        if (dgate) CHECK(hipFree(dgate));
     }
     std::fclose(f);
     CHECK(hipStreamDestroy(stream));

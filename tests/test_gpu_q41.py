@@ -246,6 +246,31 @@ def test_q41_grouped_layer(q41_layer):
     assert np.array_equal(host(y5).view(np.uint32), ref5["y"].view(np.uint32))
 
 
+def test_q41_grouped_layer_streaming_bit_exact(q41_layer):
+    """The same 300-token Zipf(1.3) batch with MOE_FFN_MFMA_MIN=0: every group
+    of the grouped path streams (k_gate_up_lean / k_down_lean), whose gate/up,
+    Q4_1 down and fold all follow the reference's fp32 order, so the sampled
+    tokens' outputs are bit-identical to the oracle's at layer scale (groups of
+    up to several dozen pairs, shared expert included)."""
+    E = q41_layer["E"]
+    L = _layer_env({"MOE_FFN_MFMA_MIN": 0}, H, I, E, 10, True, 300, experts_q4=q41_layer["bank"],
+                   shared_q4=q41_layer["shared"], down_type=Q41)
+    x = W.activations(300, seed=741)
+    ids, w = W.routes_zipf(300, 1.3, experts=E, seed=742)
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    yh = host(y)
+    st = L.last_stats()
+    assert int(host(err)[0]) == 0
+    assert st["mfma_items"] == 0 and st["stream_items"] > 0
+    sample = np.random.default_rng(744).choice(300, 24, replace=False)
+    mask = np.zeros(300, np.uint8)
+    mask[sample] = 1
+    ref = O.moe_layer(x, H, I, E, q41_layer["bank"], ids, w, shared_q4=q41_layer["shared"], token_mask=mask,
+                      down_q41=True)
+    assert np.array_equal(yh[sample].view(np.uint32), ref["y"][sample].view(np.uint32))
+    L.close()
+
+
 def test_q41_tensors_and_synthetic_banks():
     """Q4_1 downs through the reference-tensor upload (three routed tensors,
     down with 20-byte blocks) and the synthetic generator: exports give the
