@@ -87,21 +87,32 @@ struct MoeExpfTable {
     MOE_EXPF_MEMBER uint64_t operator()(int i) const { return moe_expf_table(i); }
 };
 
-/* The function with the table lookup as a parameter (the kernels' epilogues
- * pass a lookup that reads the table from registers). */
-template<typename Table>
-MOE_EXPF_FN float moe_expf_with(float x, const Table &table) {
-    /* The table is read before any special-case return, by every lane: a
-     * lookup through lane shuffles needs all lanes of the wave present. */
+/* The function in three steps, so that callers evaluating several values can
+ * issue all table reads together: the argument reduction (k, as the shifted
+ * double kd and its bits ki), the table index, and the rest given the entry. */
+struct MoeExpfReduced {
+    double xd, kd;
+    uint64_t ki;
+};
+
+MOE_EXPF_FN MoeExpfReduced moe_expf_reduce(float x) {
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    MoeExpfReduced r;
+    r.xd = (double)x;
+    r.kd = __builtin_fma(inv_ln2_n, r.xd, shift);
+    r.ki = moe_expf_asuint64(r.kd);
+    return r;
+}
+
+MOE_EXPF_FN int moe_expf_index(const MoeExpfReduced &r) { return (int)(r.ki & 31u); }
+
+MOE_EXPF_FN float moe_expf_finish(float x, const MoeExpfReduced &red, uint64_t entry) {
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
     const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
     const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-    const double xd = (double)x;
-    double kd = __builtin_fma(inv_ln2_n, xd, shift);
-    const uint64_t ki = moe_expf_asuint64(kd);
-    const uint64_t entry = table((int)(ki & 31u));
     const uint32_t abstop = (moe_expf_asuint(x) >> 20) & 0x7ffu;
     if (abstop >= 0x42bu) {                                   /* |x| >= 88 (top bits of 88.0f) */
         if (moe_expf_asuint(x) == 0xff800000u) return 0.0f;   /* -inf */
@@ -109,15 +120,26 @@ MOE_EXPF_FN float moe_expf_with(float x, const Table &table) {
         if (x > 0x1.62e42ep6f) return __builtin_inff();       /* overflow */
         if (x < -0x1.9fe368p6f) return 0.0f;                  /* underflow */
     }
-    kd -= shift;
-    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    const double s = moe_expf_asdouble(entry + (ki << 47));
+    const double kd = red.kd - shift;
+    const double r = __builtin_fma(inv_ln2_n, red.xd, -kd);
+    const double s = moe_expf_asdouble(entry + (red.ki << 47));
     const double z = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     y = y * s;
     return (float)y;
+}
+
+/* The function with the table lookup as a parameter (the kernels' epilogues
+ * pass a lookup that reads the table from registers).  The table is read
+ * before any special-case return, by every lane: a lookup through lane
+ * shuffles needs all lanes of the wave present. */
+template<typename Table>
+MOE_EXPF_FN float moe_expf_with(float x, const Table &table) {
+    const MoeExpfReduced r = moe_expf_reduce(x);
+    const uint64_t entry = table(moe_expf_index(r));
+    return moe_expf_finish(x, r, entry);
 }
 
 MOE_EXPF_FN float moe_expf(float x) { return moe_expf_with(x, MoeExpfTable{}); }

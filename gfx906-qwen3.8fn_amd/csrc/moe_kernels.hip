@@ -1435,17 +1435,40 @@ __global__ __launch_bounds__(256) void k_fold(const float *__restrict__ c, size_
 }
 
 // ---------------------------------------------------------------- router ---
-// One token per wave; lanes l and l + 32 both play reference lane l (the
-// width-32 shuffles keep the halves apart).  Softmax as router_softmax
-// (src/hip/session_ops.hip:401-434): lane l holds logits l + 32k; nonfinite
-// inputs count as 0 with bit 1; row max; per-lane left sums of expf(x - max)
-// from +0; XOR butterfly 1..16 for the total; reciprocal and multiply; any
-// flag zeroes the row.  Selection as select_routes (src/session.hip:666-687):
-// top_k rounds of a wave-wide arg-max (larger value, then lower id), bucket
-// id % 32 accumulated by its lane in rank order, XOR butterfly, denominator
-// max(bucket 0, 1/16384), weight = value * (1 / denominator).  expf is
-// moe_expf (the host C library's bits).
-constexpr int kRouterMaxPer = 32;   // experts <= 1024
+// One token row per wave (a 64-thread workgroup), no barriers: lane L holds
+// the logits of experts L + 64 j, j < J = ceil(E / 64).
+//
+// Softmax as router_softmax (src/hip/session_ops.hip:401-434), whose 32 lanes
+// hold logits l + 32k: nonfinite inputs count as 0 with bit 1; row max (any
+// order gives the same max); e = expf(x - max); reference lane l's total is
+// the left sum from +0 of e[l + 32k] over k, then an ascending XOR butterfly
+// 1..16 across the 32 totals; reciprocal and multiply; any flag zeroes the
+// row.  Entry l + 32k sits on lane l (k even, j = k / 2) or lane l + 32 (k
+// odd), so a permlane32 swap hands lane l < 32 every entry of its reference
+// lane and it adds them in the reference's order.  The reference checks every
+// partial sum; its addends are finite and >= 0 (sanitised exponentials), so
+// partial sums only grow and the last one is nonfinite exactly when one of
+// them is: checking the lane total raises the same bit.  e * (1 / total)
+// cannot become nonfinite when no flag is set (e <= 1 <= total), and any flag
+// zeroes the row, so that check adds nothing.
+//
+// Selection as select_routes (src/session.hip:666-687): the top_k largest
+// probabilities, ties to the lower id.  Entry i's key is the integer
+// bits(p) * 1024 + (1023 - i) held in a double (below 2^40, so exact): p >= +0
+// makes bits(p) order like p, so larger keys are larger p, then lower id, and
+// the keys of a row are distinct.  A key's rank is the number of larger keys,
+// counted from the sign of the exact difference key_i - key_j (no
+// compare-and-carry chain through VCC).  Bound: the lanes' largest keys are
+// ranked among themselves; the one of rank top_k - 1 has top_k keys (the
+// larger lane maxima and itself) at or above it, so the row's top_k all lie
+// at or above it, and only the keys at or above it (at most top_k * J) are
+// ranked among themselves.  Then, in rank order, bucket id % 32 accumulates p
+// from +0, an ascending XOR butterfly, denominator max(bucket 0, 1/16384),
+// weight = p * (1 / denominator).  expf is moe_expf (the host C library's
+// bits).
+constexpr int kRouterMaxTopK = 32;
+constexpr int kRouterMaxJ = 16;      // experts <= 1024
+constexpr int kRouterBatch = 16;     // keys read from LDS per round trip
 
 // Branch-free (selects, no exec-mask branches on the router's serial path).
 __device__ __forceinline__ float router_check(float x, int &flags, int bit) {
@@ -1454,113 +1477,265 @@ __device__ __forceinline__ float router_check(float x, int &flags, int bit) {
     return bad ? 0.0f : x;
 }
 
-// PER = experts / 32 values per lane (compile time, so every array index is
-// static and the lane's values stay in registers).
-template<int PER>
-__global__ __launch_bounds__(64) void k_router(const float *__restrict__ logits, int top_k, float *__restrict__ prob,
-                                               int32_t *__restrict__ ids, float *__restrict__ weights, int *error) {
-    constexpr int E = 32 * PER;
-    __shared__ int sel_id[32];
-    __shared__ float sel_v[32];
-    const int t = blockIdx.x, l = threadIdx.x & 31;
-    const LaneExpfTable table{expf_table_word(threadIdx.x)};
+__device__ __forceinline__ double router_key(float p, int id) {
+    return static_cast<double>(__float_as_uint(p)) * 1024.0 + static_cast<double>(1023 - id);
+}
+// 1 when key j > key i: the sign bit of the exact difference (x - x = +0).
+__device__ __forceinline__ uint32_t router_larger(double ki, double kj) {
+    return static_cast<uint32_t>(__double_as_longlong(ki - kj) >> 32) >> 31;
+}
+
+// How many of the n keys at `keys` (LDS, 16-byte aligned; the entries up to
+// the next multiple of B are readable and hold -1) are larger than k: B keys
+// per LDS round trip.
+template<int B>
+__device__ __forceinline__ int router_rank(double k, const double *keys, int n) {
+    uint32_t c = 0;
+#pragma unroll 1
+    for (int j = 0; j < n; j += B) {
+        double v[B];
+#pragma unroll
+        for (int i = 0; i < B; ++i) v[i] = keys[j + i];
+#pragma unroll
+        for (int i = 0; i < B; i += 2) c += router_larger(k, v[i]) + router_larger(k, v[i + 1]);
+    }
+    return static_cast<int>(c);
+}
+
+// Lanes below this one in a wave mask.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+}
+
+// LDS fence between a wave's own writes and its reads of other lanes' values.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// SPREAD: one workgroup of J waves per token row; wave w evaluates the
+// exponentials of experts 64 w + lane (one each), then wave 0 alone
+// continues with all of them (latency: small batches).  Otherwise one wave
+// per row evaluates all J per lane, every table read issued together
+// (throughput: large batches).  FULL: E == 64 J, every lane holds J entries
+// (no per-lane guards).  K > 0: top_k == K (the loops over ranks end at K).
+template<int J, bool FULL, bool SPREAD, int K>
+__global__ __launch_bounds__(SPREAD ? 64 * J : 64) void k_router(const float *__restrict__ logits, int E, int top_k,
+                                                                float *__restrict__ prob, int32_t *__restrict__ ids,
+                                                                float *__restrict__ weights, int *error) {
+    constexpr int KT = K > 0 ? K : kRouterMaxTopK;                       // ranks the bucket loop visits
+    constexpr int NS = kRouterMaxTopK * 2 * J + kRouterBatch;            // survivor slots (+ padding)
+    __shared__ uint64_t etab[32];                                        // moe_expf's table
+    __shared__ float e_lds[SPREAD ? 64 * J : 1];
+    __shared__ int wflags[SPREAD ? J : 1];
+    __shared__ __align__(16) double lmax[32];
+    __shared__ __align__(16) double surv[NS];
+    __shared__ __align__(16) float top_p[kRouterMaxTopK];
+    __shared__ __align__(16) int top_id[kRouterMaxTopK];
+    const int t = blockIdx.x, L = threadIdx.x & 63;
+    const int wave = SPREAD ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)) : 0;
     const float *row = logits + static_cast<size_t>(t) * E;
+    // Every wave reads the whole row (its max and input flags), lane L the
+    // entries L + 64 j.
+    float x[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) x[j] = (FULL || L + 64 * j < E) ? row[L + 64 * j] : 0.0f;
+    if (wave == 0 && L < 32) etab[L] = moe_expf_table(L);
+    if (wave == 0 && L >= top_k && L < kRouterMaxTopK) top_p[L] = 0.0f;   // unused ranks add +0 to the buckets
     int flags = 0;
-    float x[PER], w[PER];
     float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) x[k] = router_check(row[l + 32 * k], flags, 1);
-#pragma unroll
-    for (int k = 0; k < PER; ++k) m = fmaxf(m, x[k]);
-    m = half_butterfly(m, [](float a, float b) { return fmaxf(a, b); });
-    float total = 0.0f;
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const float shifted = router_check(x[k] - m, flags, 2);
-        w[k] = router_check(moe_expf_with(shifted, table), flags, 2);
-        total = router_check(total + w[k], flags, 2);
+    for (int j = 0; j < J; ++j) {
+        const bool has = (FULL || L + 64 * j < E);
+        int f = 0;
+        x[j] = router_check(x[j], f, 1);
+        flags |= has ? f : 0;
+        m = has ? fmaxf(m, x[j]) : m;
     }
-    total = half_butterfly(total, [](float a, float b) { return a + b; });
+    m = fmaxf(m, lane_xor<1>(m));
+    m = fmaxf(m, lane_xor<2>(m));
+    m = fmaxf(m, lane_xor<4>(m));
+    m = fmaxf(m, lane_xor<8>(m));
+    m = fmaxf(m, lane_xor<16>(m));
+    m = fmaxf(m, lane_xor<32>(m));
+    float e[J];
+    if constexpr (SPREAD) {
+        // This wave's entry: x[wave] without indexing the register array by
+        // a runtime value.
+        float xw = x[0];
+#pragma unroll
+        for (int j = 1; j < J; ++j) xw = wave == j ? x[j] : xw;
+        const bool has = FULL || L + 64 * wave < E;
+        int f = 0;
+        const float shifted = router_check(has ? xw - m : 0.0f, f, 2);
+        const MoeExpfReduced red = moe_expf_reduce(shifted);
+        __syncthreads();   // etab
+        const float ew = router_check(moe_expf_finish(shifted, red, etab[moe_expf_index(red)]), f, 2);
+        flags |= has ? f : 0;
+        e_lds[L + 64 * wave] = has ? ew : 0.0f;
+        const bool b1 = __ballot(flags & 1) != 0, b2 = __ballot(flags & 2) != 0;
+        if (L == 0) wflags[wave] = (b1 ? 1 : 0) | (b2 ? 2 : 0);
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int j = 0; j < J; ++j) e[j] = e_lds[L + 64 * j];
+        flags = 0;
+#pragma unroll
+        for (int j = 0; j < J; ++j) flags |= wflags[j];
+    } else {
+        float sh[J];
+        MoeExpfReduced red[J];
+        uint64_t ent[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const bool has = (FULL || L + 64 * j < E);
+            int f = 0;
+            sh[j] = router_check(has ? x[j] - m : 0.0f, f, 2);
+            flags |= has ? f : 0;
+            red[j] = moe_expf_reduce(sh[j]);
+        }
+        wave_lds_sync();   // etab
+#pragma unroll
+        for (int j = 0; j < J; ++j) ent[j] = etab[moe_expf_index(red[j])];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const bool has = (FULL || L + 64 * j < E);
+            int f = 0;
+            e[j] = router_check(moe_expf_finish(sh[j], red[j], ent[j]), f, 2);
+            flags |= has ? f : 0;
+            e[j] = has ? e[j] : 0.0f;
+        }
+    }
+    // Reference lane l = L & 31 (lanes >= 32 repeat it): left sum of
+    // e[l + 32k] over k < E / 32; odd k come from lane l + 32.
+    float total = 0.0f;
+    {
+        float o[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) o[j] = lane_xor<32>(e[j]);
+        const bool lo = L < 32;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            total = total + (lo ? e[j] : o[j]);                                          // k = 2j
+            if (FULL || 32 * (2 * j + 1) < E) total = total + (lo ? o[j] : e[j]);   // k = 2j + 1
+        }
+    }
+    total = router_check(total, flags, 2);
+    total = total + lane_xor<1>(total);
+    total = total + lane_xor<2>(total);
+    total = total + lane_xor<4>(total);
+    total = total + lane_xor<8>(total);
+    total = total + lane_xor<16>(total);
     total = router_check(total, flags, 2);
     if (!(total > 0.0f)) flags |= 2;
     const float inverse = total > 0.0f ? router_check(1.0f / total, flags, 2) : 0.0f;
+    const int rflags = (__ballot(flags & 1) != 0 ? 1 : 0) | (__ballot(flags & 2) != 0 ? 2 : 0);
+    double key[J];
+    double kmax = -1.0;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) w[k] = router_check(w[k] * inverse, flags, 2);
-    flags = half_butterfly(flags, [](int a, int b) { return a | b; });
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        if (flags) w[k] = 0.0f;
-        if (prob && threadIdx.x < 32) prob[static_cast<size_t>(t) * E + l + 32 * k] = w[k];
+    for (int j = 0; j < J; ++j) {
+        const int i = L + 64 * j;
+        const bool has = FULL || i < E;
+        const float p = rflags ? 0.0f : e[j] * inverse;
+        if (prob && has) prob[static_cast<size_t>(t) * E + i] = p;
+        key[j] = has ? router_key(p, i) : -1.0;
+        kmax = fmax(kmax, key[j]);
     }
-    uint32_t taken = 0;
+    // The bound: the largest key of lanes 2g, 2g + 1 is ranked among the 32
+    // pair maxima; the one of rank top_k - 1 has top_k keys (the larger pair
+    // maxima and itself) at or above it, so the row's top_k all lie at or
+    // above it.  With fewer than top_k nonempty pairs every key is kept.
+    kmax = fmax(kmax, __hiloint2double(lane_xor<1>(__double2hiint(kmax)), lane_xor<1>(__double2loint(kmax))));
+    if ((L & 1) == 0) lmax[L >> 1] = kmax;
+    wave_lds_sync();
+    double bound = -0.5;
+    if (FULL || (min(E, 64) + 1) / 2 >= top_k) {   // uniform
+        const int r = router_rank<32>(kmax, lmax, 32);
+        const uint64_t at = __ballot((L & 1) == 0 && kmax >= 0.0 && r == top_k - 1);
+        const int src = static_cast<int>(__builtin_ctzll(at));
+        const int blo = __builtin_amdgcn_readlane(__double2loint(kmax), src);
+        const int bhi = __builtin_amdgcn_readlane(__double2hiint(kmax), src);
+        bound = __hiloint2double(bhi, blo);
+    }
+    // Survivors (the keys at or above the bound: at most 2 J per selected
+    // pair) into surv[0..ns); other lanes write to the last padding slot.
+    int ns = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint64_t keep = __ballot(key[j] >= bound);
+        surv[((keep >> L) & 1) ? ns + lanes_below(keep) : NS - 1] = key[j];
+        ns += __popcll(keep);
+    }
+    wave_lds_sync();
+    if (L < kRouterBatch) surv[ns + L] = -1.0;   // padding of the last batch
+    wave_lds_sync();
+    for (int c0 = 0; c0 < ns; c0 += 64) {
+        const double k = surv[min(c0 + L, ns + kRouterBatch - 1)];   // lanes past ns read padding
+        const int r = router_rank<kRouterBatch>(k, surv, ns);
+        if (c0 + L < ns && r < top_k) {
+            const int64_t bits = static_cast<int64_t>(k);
+            top_p[r] = __uint_as_float(static_cast<uint32_t>(bits >> 10));
+            top_id[r] = 1023 - static_cast<int>(bits & 1023);
+        }
+    }
+    wave_lds_sync();
+    // Bucket l of select_routes: p of the ids with id % 32 == l, in rank
+    // order from +0 (another bucket's entry, or an unused rank, whose p is
+    // +0, adds +0, which changes nothing).
+    const int l = L & 31;
+    float tp[KT];
+    int ti[KT];
+#pragma unroll
+    for (int i = 0; i < KT; ++i) {
+        tp[i] = top_p[i];
+        ti[i] = top_id[i];
+    }
+    const float my_p = top_p[min(L, kRouterMaxTopK - 1)];
+    const int my_id = top_id[min(L, kRouterMaxTopK - 1)];
     float bucket = 0.0f;
-    for (int i = 0; i < top_k; ++i) {
-        // The lane's best untaken entry by a pairwise tree over k (the left,
-        // lower id, wins ties), then the wave's best by value, ties to the
-        // lower id: the same choice as a scan in id order.  The two lanes
-        // that hold reference lane l split its entries (lanes < 32 the first
-        // half of k, lanes >= 32 the rest), so both halves of the wave work.
-        constexpr int HALF = (PER + 1) / 2;
-        const bool lo = threadIdx.x < 32;
-        float cv[HALF];
-        int ci[HALF];
 #pragma unroll
-        for (int j = 0; j < HALF; ++j) {
-            const int k = lo ? j : HALF + j;   // entries j (lanes < 32) or HALF + j (lanes >= 32)
-            const float wv = lo ? w[j] : (HALF + j < PER ? w[HALF + j < PER ? HALF + j : 0] : -INFINITY);
-            const bool free = k < PER && !((taken >> k) & 1u);
-            cv[j] = free ? wv : -INFINITY;
-            ci[j] = free ? l + 32 * k : 0x7fffffff;
-        }
-#pragma unroll
-        for (int st = 1; st < HALF; st <<= 1)
-#pragma unroll
-            for (int j = 0; j + st < HALF; j += 2 * st)
-                if (cv[j + st] > cv[j]) { cv[j] = cv[j + st]; ci[j] = ci[j + st]; }
-        float bv = cv[0];
-        int bid = ci[0];
-        auto take = [&](float ov, int oid) {
-            const bool better = (ov > bv) | ((ov == bv) & (oid < bid));   // non-short-circuit: selects, no branches
-            bv = better ? ov : bv;
-            bid = better ? oid : bid;
-        };
-        take(lane_xor<1>(bv), lane_xor<1>(bid));
-        take(lane_xor<2>(bv), lane_xor<2>(bid));
-        take(lane_xor<4>(bv), lane_xor<4>(bid));
-        take(lane_xor<8>(bv), lane_xor<8>(bid));
-        take(lane_xor<16>(bv), lane_xor<16>(bid));
-        {
-            // Lane l <-> l + 32: after a swap, lanes < 32 find the other
-            // half's value in the second result, lanes >= 32 in the first.
-            const auto sv = __builtin_amdgcn_permlane32_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
-            const auto si = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(bid), static_cast<uint32_t>(bid), false,
-                                                             false);
-            take(__uint_as_float(lo ? sv[1] : sv[0]), static_cast<int>(lo ? si[1] : si[0]));
-        }
-        if ((bid & 31) == l) {
-            taken |= 1u << (bid >> 5);
-            bucket = bucket + bv;
-        }
-        if (threadIdx.x == 0) { sel_id[i] = bid; sel_v[i] = bv; }
-    }
-    bucket = half_butterfly(bucket, [](float a, float b) { return a + b; });
+    for (int i = 0; i < KT; ++i) bucket = bucket + ((ti[i] & 31) == l ? tp[i] : 0.0f);
+    bucket = bucket + lane_xor<1>(bucket);
+    bucket = bucket + lane_xor<2>(bucket);
+    bucket = bucket + lane_xor<4>(bucket);
+    bucket = bucket + lane_xor<8>(bucket);
+    bucket = bucket + lane_xor<16>(bucket);
+    bucket = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__float_as_int(bucket)));   // bucket 0
     const float lowest = 1.0f / 16384.0f;
     const float denominator = bucket < lowest ? lowest : bucket;
     const int dflags = (!(denominator > 0.0f) || !isfinite(denominator)) ? 2 : 0;
     const float dinv = dflags ? 0.0f : 1.0f / denominator;
-    __syncthreads();
-    if (static_cast<int>(threadIdx.x) < top_k) {
-        const size_t o = static_cast<size_t>(t) * top_k + threadIdx.x;
-        ids[o] = sel_id[threadIdx.x];
-        weights[o] = sel_v[threadIdx.x] * dinv;
+    if (L < top_k) {
+        const size_t o = static_cast<size_t>(t) * top_k + L;
+        ids[o] = my_id;
+        weights[o] = my_p * dinv;
     }
-    if (threadIdx.x == 0 && (flags | dflags)) atomicOr(error, flags | dflags);
+    if (L == 0 && (rflags | dflags)) atomicOr(error, rflags | dflags);
 }
 
-template<int PER>
-void router_launch(const float *logits, int tokens, int top_k, float *prob, int32_t *ids, float *weights,
-                   int *error, hipStream_t s) {
-    k_router<PER><<<tokens, 64, 0, s>>>(logits, top_k, prob, ids, weights, error);
+// Batches of at most kRouterSpreadTokens rows spread each row's
+// exponentials over J waves (lower latency); larger batches run one wave per
+// row (more rows resident).  Measured on MI355X (graph replays, E = 512,
+// top-10), spread against one wave per row: 256 rows 3.99 vs 4.49 us (257),
+// 512 rows 4.49 vs 4.67 us, 1024 rows 5.35 vs 4.95 us, 4096 rows 13.2 vs
+// 7.8 us.
+constexpr int kRouterSpreadTokens = 512;
+
+template<int J>
+void router_launch(const float *logits, int tokens, int experts, int top_k, float *prob, int32_t *ids,
+                   float *weights, int *error, hipStream_t s) {
+    const bool spread = tokens <= kRouterSpreadTokens;
+    if constexpr (J == 8) {
+        if (experts == 512 && top_k == 10) {   // the model's router: 512 experts, top-10
+            if (spread) k_router<8, true, true, 10><<<tokens, 512, 0, s>>>(logits, experts, top_k, prob, ids, weights, error);
+            else k_router<8, true, false, 10><<<tokens, 64, 0, s>>>(logits, experts, top_k, prob, ids, weights, error);
+            return;
+        }
+    }
+    if (spread) k_router<J, false, true, 0><<<tokens, 64 * J, 0, s>>>(logits, experts, top_k, prob, ids, weights, error);
+    else k_router<J, false, false, 0><<<tokens, 64, 0, s>>>(logits, experts, top_k, prob, ids, weights, error);
 }
 
 inline unsigned blocks_for(size_t n, unsigned per) { return static_cast<unsigned>((n + per - 1) / per); }
@@ -1822,16 +1997,13 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
 
 hipError_t launch_router(const float *logits, int tokens, int experts, int top_k, float *prob, int32_t *ids,
                          float *weights, int *error, hipStream_t s) {
-    using Launch = void (*)(const float *, int, int, float *, int32_t *, float *, int *, hipStream_t);
-    static constexpr Launch table[kRouterMaxPer] = {
-        router_launch<1>, router_launch<2>, router_launch<3>, router_launch<4>, router_launch<5>,
-        router_launch<6>, router_launch<7>, router_launch<8>, router_launch<9>, router_launch<10>,
-        router_launch<11>, router_launch<12>, router_launch<13>, router_launch<14>, router_launch<15>,
-        router_launch<16>, router_launch<17>, router_launch<18>, router_launch<19>, router_launch<20>,
-        router_launch<21>, router_launch<22>, router_launch<23>, router_launch<24>, router_launch<25>,
-        router_launch<26>, router_launch<27>, router_launch<28>, router_launch<29>, router_launch<30>,
-        router_launch<31>, router_launch<32>};
-    table[experts / 32 - 1](logits, tokens, top_k, prob, ids, weights, error, s);
+    using Launch = void (*)(const float *, int, int, int, float *, int32_t *, float *, int *, hipStream_t);
+    static constexpr Launch table[kRouterMaxJ] = {
+        router_launch<1>, router_launch<2>, router_launch<3>, router_launch<4>, router_launch<5>, router_launch<6>,
+        router_launch<7>, router_launch<8>, router_launch<9>, router_launch<10>, router_launch<11>,
+        router_launch<12>, router_launch<13>, router_launch<14>, router_launch<15>, router_launch<16>};
+    if (top_k > kRouterMaxTopK || experts > 64 * kRouterMaxJ) return hipErrorInvalidValue;
+    table[(experts + 63) / 64 - 1](logits, tokens, experts, top_k, prob, ids, weights, error, s);
     return hipGetLastError();
 }
 

@@ -842,18 +842,36 @@ def test_router_select_bit_exact():
     order[:, 0:512:32] = -16.7
     order[1] = np.roll(order[1], 7)
     _router_check(order, 10, "lane-order rounding")
+    _router_check((rng.standard_normal((16, 1024)) * 2).astype(np.float32), 32, "1024 experts, top-32")
+    wide = rng.standard_normal((8, 1024)).astype(np.float32)
+    wide[:, 500:560] = 4.0                          # sixty equal leaders across the two halves
+    _router_check(wide, 32, "1024 experts, equal leaders")
+    _router_check(rng.standard_normal((16, 32)).astype(np.float32), 32, "32 experts, all selected")
+    _router_check(rng.standard_normal((16, 96)).astype(np.float32), 7, "96 experts, top-7")
+    # More than 256 rows: one wave per row (the small batches above spread a
+    # row's exponentials over several waves); same bits either way.
+    _router_check((rng.standard_normal((300, 1024)) * 2).astype(np.float32), 32, "300 x 1024, top-32, one wave per row")
+    _router_check(rng.standard_normal((400, 96)).astype(np.float32), 7, "400 x 96, top-7, one wave per row")
+    big_tie = rng.standard_normal((300, 512)).astype(np.float32)
+    big_tie[:, 100:140] = 5.0
+    _router_check(big_tie, 10, "300 rows, equal leaders, one wave per row")
 
 
 def test_router_select_flags_bad_rows():
     x = np.random.default_rng(701).standard_normal((6, 512)).astype(np.float32)
     x[1, 3] = np.nan
     x[4, 9] = np.inf
+    x[2, 5], x[2, 6] = 3e38, -3e38   # x - max overflows to -inf: the arithmetic bit
     ids, w, p, err = moe_ffn.router_select(dev(x), top_k=10, probabilities=True)
-    assert int(host(err)[0]) & 1
+    assert int(host(err)[0]) == 3
     ph, ih, wh = host(p), host(ids), host(w)
-    for t in (1, 4):   # zero row: ids 0..9, zero weights
+    for t in (1, 2, 4):   # zero row: ids 0..9, zero weights
         assert np.all(ph[t] == 0) and list(ih[t]) == list(range(10)) and np.all(wh[t] == 0)
     _router_check(x, 10, "rows with nonfinite logits")
+    big = np.random.default_rng(704).standard_normal((300, 512)).astype(np.float32)
+    big[7, 11] = np.nan
+    big[250, 3], big[250, 4] = 3e38, -3e38
+    _router_check(big, 10, "300 rows with bad rows, one wave per row")
 
 
 def test_router_then_forward_matches_oracle(moe512):
