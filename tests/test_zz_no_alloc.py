@@ -3,7 +3,12 @@ whose Q8_1 staging is a static device array of the library) against
 moe_linear_apply on the same handle: outputs and error flags bit-identical,
 on two calls in a row with the second smaller, on the vector kernel and on
 the MFMA kernel; sizes past the 4 MiB array are rejected before any launch;
-the calls leave the device's free memory unchanged."""
+the calls leave the device's free memory unchanged.
+
+Every call here is issued on torch's current stream, one after another: the
+static array is shared by all calls on a GPU, so calls on two streams that
+are not ordered against each other would race on it (the entry point only
+refuses a second host thread entering while one is inside it)."""
 import numpy as np
 import pytest
 
@@ -24,6 +29,7 @@ def gpu_ready():
 
 
 def _run_pair(lin, n, seed):
+    assert torch.cuda.current_stream() == torch.cuda.default_stream(), "calls share one stream"
     x = torch.from_numpy(W.activations(n, hidden=lin.K, seed=seed)).to(DEV)
     y_ref, e_ref = lin.apply(x)
     y = torch.full((n, lin.M), float("nan"), dtype=torch.float32, device=DEV)
