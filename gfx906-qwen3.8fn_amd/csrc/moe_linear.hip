@@ -358,8 +358,11 @@ int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, 
         if (hold2) moe::k_linear<true, 2, 2><<<g, b, 0, s>>>(a);
         else moe::k_linear<true, 1, 4><<<g, b, 0, s>>>(a);
     } else {
-        if (hold2) moe::k_linear<false, 2, 2><<<g, b, 0, s>>>(a);
-        else moe::k_linear<false, 1, 4><<<g, b, 0, s>>>(a);
+        // Q4_0 takes one block slot per load round for every row length and
+        // keeps its weights for 4 columns: 8192 x 8192 at N = 1 / 8 / 16,
+        // 11.2 / 22.9 / 39.1 us with two slots and 2 columns per round
+        // against 9.8 / 19.8 / 33.6 us (MI355X, cold weights).
+        moe::k_linear<false, 1, 4><<<g, b, 0, s>>>(a);
     }
     return hipGetLastError();
 }
