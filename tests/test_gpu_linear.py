@@ -102,6 +102,11 @@ CASES = [
     (Q41, 6144, 40, 2),       # three slots (odd count with two held)
     (Q40, 2048, 512, 128),    # the reference's tiled maximum
     (Q40, 1024, 256, 300),    # past it, one launch
+    (Q40, 8192, 64, 8),       # 256 blocks: four slots per lane
+    (Q41, 8192, 24, 7),
+    (Q40, 4096, 40, 13),
+    (Q40, 1024, 8192, 5),     # 1024 row slices
+    (Q41, 2048, 6000, 16),
 ]
 
 
