@@ -424,7 +424,7 @@ def main():
     ap.add_argument("--no-linear", action="store_true", help="skip the quantized linear projections")
     ap.add_argument("--no-graph", action="store_true", help="skip the graph-captured stack passes")
     ap.add_argument("--no-refshapes", action="store_true", help="skip the reference's component shapes (2560/640)")
-    ap.add_argument("--only", choices=["b8", "4k", "16k", "ep", "stack", "refshapes"],
+    ap.add_argument("--only", choices=["b8", "4k", "16k", "ep", "stack", "refshapes", "router", "linear"],
                     help="run one section alone (for profiler runs); the JSON line then holds that section only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy x5 (FETCH_SIZE/WRITE_SIZE scale for rocprofv3 --pmc)")
@@ -450,7 +450,8 @@ def main():
     only = args.only
     want = lambda section: only is None or only == section
     if only is not None:
-        args.no_cpu = args.no_linear = True
+        args.no_cpu = True
+        args.no_linear = only != "linear"
         args.no_refshapes = only != "refshapes"
         args.no_prefill = only not in ("4k", "16k")
         args.no_16k = only != "16k"
@@ -637,7 +638,7 @@ def main():
 
     # ---- device router (softmax + top-10 of 512), the step before the layer --
     router = {}
-    for NR in ((8, 4096) if only is None else ()):
+    for NR in ((8, 4096) if only in (None, "router") else ()):
         lg = dev(np.random.default_rng(4000 + NR).standard_normal((NR, 512)).astype(np.float32))
         ids_r = torch.empty((NR, 10), dtype=torch.int32, device="cuda:0")
         w_r = torch.empty((NR, 10), dtype=torch.float32, device="cuda:0")
