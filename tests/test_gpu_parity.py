@@ -848,13 +848,18 @@ def test_router_select_bit_exact():
     _router_check(wide, 32, "1024 experts, equal leaders")
     _router_check(rng.standard_normal((16, 32)).astype(np.float32), 32, "32 experts, all selected")
     _router_check(rng.standard_normal((16, 96)).astype(np.float32), 7, "96 experts, top-7")
-    # More than 256 rows: one wave per row (the small batches above spread a
+    # More than 512 rows: one wave per row (batches up to 512 rows spread a
     # row's exponentials over several waves); same bits either way.
-    _router_check((rng.standard_normal((300, 1024)) * 2).astype(np.float32), 32, "300 x 1024, top-32, one wave per row")
-    _router_check(rng.standard_normal((400, 96)).astype(np.float32), 7, "400 x 96, top-7, one wave per row")
-    big_tie = rng.standard_normal((300, 512)).astype(np.float32)
+    _router_check((rng.standard_normal((600, 1024)) * 2).astype(np.float32), 32, "600 x 1024, top-32, one wave per row")
+    _router_check(rng.standard_normal((700, 96)).astype(np.float32), 7, "700 x 96, top-7, one wave per row")
+    _router_check(rng.standard_normal((513, 64)).astype(np.float32), 32, "513 x 64, top-32 (the pair bound at its limit)")
+    _router_check(rng.standard_normal((520, 32)).astype(np.float32), 32, "520 x 32, all selected, one wave per row")
+    big_tie = rng.standard_normal((600, 512)).astype(np.float32)
     big_tie[:, 100:140] = 5.0
-    _router_check(big_tie, 10, "300 rows, equal leaders, one wave per row")
+    _router_check(big_tie, 10, "600 rows, equal leaders, one wave per row")
+    # The same shapes at 300 rows take the spread form.
+    _router_check((rng.standard_normal((300, 1024)) * 2).astype(np.float32), 32, "300 x 1024, top-32, spread")
+    _router_check(rng.standard_normal((400, 96)).astype(np.float32), 7, "400 x 96, top-7, spread")
 
 
 def test_router_select_flags_bad_rows():
@@ -868,10 +873,11 @@ def test_router_select_flags_bad_rows():
     for t in (1, 2, 4):   # zero row: ids 0..9, zero weights
         assert np.all(ph[t] == 0) and list(ih[t]) == list(range(10)) and np.all(wh[t] == 0)
     _router_check(x, 10, "rows with nonfinite logits")
-    big = np.random.default_rng(704).standard_normal((300, 512)).astype(np.float32)
-    big[7, 11] = np.nan
-    big[250, 3], big[250, 4] = 3e38, -3e38
-    _router_check(big, 10, "300 rows with bad rows, one wave per row")
+    for rows in (300, 600):   # spread, then one wave per row
+        big = np.random.default_rng(704 + rows).standard_normal((rows, 512)).astype(np.float32)
+        big[7, 11] = np.nan
+        big[250, 3], big[250, 4] = 3e38, -3e38
+        _router_check(big, 10, f"{rows} rows with bad rows")
 
 
 def test_router_then_forward_matches_oracle(moe512):
