@@ -372,23 +372,6 @@ __device__ __forceinline__ void store_dots(const GuTile &t, int b, v16i I0, v16i
     }
 }
 
-// acc[2j+f] of the reference lane array for the wave's 16 outputs per lane:
-// sequential fmas over blocks j, j+64, ... (< nb).
-template<bool Dbg>
-__device__ __forceinline__ void lane_sums(const GuTile &t, int j, float (&a0)[16], float (&a1)[16]) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) { a0[v] = 0.0f; a1[v] = 0.0f; }
-    for (int b = j; b < t.nb; b += 64) {
-        const BlockLoads l = block_loads(t, b);
-        const uint32_t d4[8] = {l.d0.x, l.d0.y, l.d0.z, l.d0.w, l.d1.x, l.d1.y, l.d1.z, l.d1.w};
-        const v16i I0 = fragment_dots<0>(t, l), I1 = fragment_dots<1>(t, l);
-        const float d8 = cvt_half_lo(l.hd), c4 = -4.0f * cvt_half_hi(l.hd);
-        fragment_scale(a0, I0, d8, c4, d4);
-        fragment_scale(a1, I1, d8, c4, d4);
-        store_dots<Dbg>(t, b, I0, I1);
-    }
-}
-
 // ---- H <= 2048 (one block per reference lane): staged scales and heads,
 // weights and activations prefetched one leaf pair ahead.
 constexpr int kGuMaxBlocks = 64;
@@ -666,11 +649,45 @@ __device__ __forceinline__ void fold_tree_grouped(const GuTile &t, const GuStage
 }
 
 // ---- H > 2048 (reference lanes holding several blocks): per-block loads.
+// One block of a reference lane's chain: both fragment dots scaled into the
+// lane's accumulators, acc = fma(d4, fma(float(I_f), d8, c4), acc).
+template<bool Dbg>
+__device__ __forceinline__ void chain_block(const GuTile &t, const BlockLoads &l, int b, float (&c0)[16],
+                                            float (&c1)[16]) {
+    const uint32_t d4[8] = {l.d0.x, l.d0.y, l.d0.z, l.d0.w, l.d1.x, l.d1.y, l.d1.z, l.d1.w};
+    const v16i I0 = fragment_dots<0>(t, l), I1 = fragment_dots<1>(t, l);
+    const float d8 = cvt_half_lo(l.hd), c4 = -4.0f * cvt_half_hi(l.hd);
+    fragment_scale(c0, I0, d8, c4, d4);
+    fragment_scale(c1, I1, d8, c4, d4);
+    store_dots<Dbg>(t, b, I0, I1);
+}
+
+// Leaf kp for rows of more than 64 blocks: reference lanes kp and kp + 32,
+// each the chain over its blocks j, j + 64, ... in increasing order (the
+// reference lane array's acc[2j + f]), walked as one sequence -- kp's chain,
+// then kp + 32's -- with
+// each block's loads issued before the previous block is scaled.
 template<bool Dbg>
 __device__ __forceinline__ void fold_leaf_multi(const GuTile &t, int kp, float (&v)[16]) {
     float a0[16], a1[16], b0[16], b1[16];
-    lane_sums<Dbg>(t, kp, a0, a1);
-    lane_sums<Dbg>(t, kp + 32, b0, b1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { a0[i] = 0.0f; a1[i] = 0.0f; b0[i] = 0.0f; b1[i] = 0.0f; }
+    // nb > 64 here, so kp + 32 < nb and both chains hold a block.
+    const int na = (t.nb - kp + 63) / 64, nc = (t.nb - kp - 32 + 63) / 64;
+    BlockLoads cur = block_loads(t, kp);
+#pragma unroll 1
+    for (int s = 0; s < na; ++s) {   // uniform
+        const BlockLoads nxt = block_loads(t, s + 1 < na ? kp + 64 * (s + 1) : kp + 32);
+        chain_block<Dbg>(t, cur, kp + 64 * s, a0, a1);
+        cur = nxt;
+    }
+#pragma unroll 1
+    for (int s = 0; s < nc; ++s) {   // uniform
+        BlockLoads nxt = cur;
+        if (s + 1 < nc) nxt = block_loads(t, kp + 32 + 64 * (s + 1));
+        chain_block<Dbg>(t, cur, kp + 32 + 64 * s, b0, b1);
+        cur = nxt;
+    }
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = (a0[i] + b0[i]) + (a1[i] + b1[i]);
     __builtin_amdgcn_sched_barrier(0);
