@@ -552,9 +552,108 @@ __device__ __forceinline__ v16i frag_mfma2(uint32_t a0, uint32_t a1, uint32_t x0
     return __builtin_amdgcn_mfma_i32_32x32x16_i8(A, B, v16i{}, 0, 0, 0);
 }
 
+// Rows of 65..96 blocks in the grouped form (the reference model's 2560:
+// 80 blocks).  Reference lane j also holds block j + 64 when j + 64 < nb, and
+// its accumulator continues with fma(d4, t, acc) over that block; lane j + 32
+// holds no second block (j + 96 >= nb).  So leaf kp's chain A gets one more
+// block, kp + 64, for kp < nb - 64.  Its operands per node (leaves 2p, 2p+1):
+// the lane's row chunk of the block, the token's half block and its head.
+struct ExtraBlk {
+    uint4 w[2], x[2];
+    uint32_t hd[2];
+};
+
+__device__ __forceinline__ void extra_load(const GuTile &t, int p, ExtraBlk &E) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t e = static_cast<uint32_t>(std::min(64 + 2 * p + i, t.nb - 1));   // past nb: unused
+        E.w[i] = buffer_load16(t.wr, t.w_off, e * 16u);
+        E.x[i] = buffer_load16(t.xr, t.x_off, e * 32u);
+        E.hd[i] = buffer_load4(t.hr, t.h_off, e * 4u);
+    }
+}
+
+// acc[v] = fma(d4[v], fma(float(I[v]), d8, c4), acc[v]) for block kp + 64's
+// fragment F, after block kp's value (the chain of reference lane kp).
+template<int F>
+__device__ __forceinline__ v16i extra_dots(const ExtraBlk &E, int i, int shift) {
+    return frag_mfma<F>(Blk{E.w[i], E.x[i]}, shift);
+}
+__device__ __forceinline__ void extra_scale(const GuStage &g, const ExtraBlk &E, int i, int blk, int h, v16i I,
+                                            float (&acc)[16]) {
+    const uint4 *de4 = reinterpret_cast<const uint4 *>(g.d4 + blk * 16 + 8 * h);
+    const uint4 e0 = de4[0], e1 = de4[1];
+    const uint32_t de[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+    const float d8 = cvt_half_lo(E.hd[i]), c4 = -4.0f * cvt_half_hi(E.hd[i]);
+    fragment_scale(acc, I, d8, c4, de);
+}
+
+// Leaf kp with block kp + 64 in chain A: v = (A0 + B0) + (A1 + B1), with
+// A_f = fma(d4', t', fma(d4, t, +0)) over blocks kp, kp + 64 and B_f block
+// kp + 32's value, as leaf_grouped without the extra block.
 template<bool Dbg>
+__device__ __forceinline__ void leaf_grouped_extra(const GuTile &t, const GuStage &g, const HalfGroup &G,
+                                                   const ExtraBlk &E, int i, int kp, int h, float (&v)[16]) {
+    const uint4 wi = G.w[i];
+    const uint32_t wv[4] = {wi.x, wi.y, wi.z, wi.w};
+    uint32_t opa[4], opb[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const auto r = __builtin_amdgcn_permlane32_swap(wv[d] & kNibbles, (wv[d] >> 4) & kNibbles, false, false);
+        opa[d] = r[0];
+        opb[d] = r[1];
+    }
+    const uint32_t ha = i ? G.ha.y : G.ha.x, hb = i ? G.hb.y : G.hb.x;
+    const uint4 *da4 = reinterpret_cast<const uint4 *>(g.d4 + kp * 16 + 8 * h);
+    const uint4 *db4 = reinterpret_cast<const uint4 *>(g.d4 + (kp + 32) * 16 + 8 * h);
+    const uint4 a0 = da4[0], a1 = da4[1], b0 = db4[0], b1 = db4[1];
+    const uint32_t da[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const uint32_t db[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const float d8a = cvt_half_lo(ha), c4a = -4.0f * cvt_half_hi(ha);
+    const float d8b = cvt_half_lo(hb), c4b = -4.0f * cvt_half_hi(hb);
+    const uint4 xa = G.xa[i], xb = G.xb[i];
+    float u0[16];
+    v16i keep_a0, keep_b0, keep_e0;
+    {
+        float za[16];
+        const v16i Ia = frag_mfma2(opa[0], opa[1], xa.x, xa.y);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) za[j] = frag_value(Ia[j], d8a, c4a, da, j);
+        const v16i Ie = extra_dots<0>(E, i, t.shift);
+        extra_scale(g, E, i, kp + 64, h, Ie, za);
+        const v16i Ib = frag_mfma2(opb[0], opb[1], xb.x, xb.y);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) u0[j] = za[j] + frag_value(Ib[j], d8b, c4b, db, j);
+        if constexpr (Dbg) { keep_a0 = Ia; keep_b0 = Ib; keep_e0 = Ie; }
+    }
+    {
+        float za[16];
+        const v16i Ia = frag_mfma2(opa[2], opa[3], xa.z, xa.w);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) za[j] = frag_value(Ia[j], d8a, c4a, da, j);
+        const v16i Ie = extra_dots<1>(E, i, t.shift);
+        extra_scale(g, E, i, kp + 64, h, Ie, za);
+        const v16i Ib = frag_mfma2(opb[2], opb[3], xb.z, xb.w);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = u0[j] + (za[j] + frag_value(Ib[j], d8b, c4b, db, j));
+        if constexpr (Dbg) {
+            store_dots<Dbg>(t, kp, keep_a0, Ia);
+            store_dots<Dbg>(t, kp + 32, keep_b0, Ib);
+            store_dots<Dbg>(t, kp + 64, keep_e0, Ie);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template<bool Dbg, bool Extra = false>
 __device__ __forceinline__ void leaf_grouped(const GuTile &t, const GuStage &g, const HalfGroup &G, int i, int kp, int m,
-                                             int h, float (&v)[16]) {
+                                             int h, float (&v)[16], const ExtraBlk *E = nullptr) {
+    if constexpr (Extra) {
+        if (kp < t.nb - 64) {   // uniform
+            leaf_grouped_extra<Dbg>(t, g, G, *E, i, kp, h, v);
+            return;
+        }
+    }
     const uint4 wi = G.w[i];
     const uint32_t wv[4] = {wi.x, wi.y, wi.z, wi.w};
     uint32_t opa[4], opb[4];
@@ -625,7 +724,7 @@ __device__ __forceinline__ void tree_merge(float (*park)[16][64], int lane, int 
     }
 }
 
-template<bool Dbg>
+template<bool Dbg, bool Extra = false>
 __device__ __forceinline__ void fold_tree_grouped(const GuTile &t, const GuStage &g, uint32_t w_off, float (*park)[16][64],
                                                   int lane, float (&res)[16]) {
     const int m = lane & 31, h = lane >> 5;
@@ -638,10 +737,14 @@ __device__ __forceinline__ void fold_tree_grouped(const GuTile &t, const GuStage
         G.w[0] = wn[0];
         G.w[1] = wn[1];
         half_load_x(t, p, G);
+        ExtraBlk E;
+        if constexpr (Extra) {
+            if (2 * p < t.nb - 64) extra_load(t, p, E);   // uniform
+        }
         half_load_w(t, w_off, p < 15 ? p + 1 : p, wn);   // node p + 1's weights in flight during node p
         float w[16], x[16];
-        leaf_grouped<Dbg>(t, g, G, 0, 2 * p, m, h, w);
-        leaf_grouped<Dbg>(t, g, G, 1, 2 * p + 1, m, h, x);
+        leaf_grouped<Dbg, Extra>(t, g, G, 0, 2 * p, m, h, w, &E);
+        leaf_grouped<Dbg, Extra>(t, g, G, 1, 2 * p + 1, m, h, x, &E);
 #pragma unroll
         for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
         tree_merge(park, lane, p, w, l1, l2, res);
@@ -741,16 +844,20 @@ __device__ __forceinline__ void fold_tree_multi(const GuTile &t, float (*park)[1
 // are elements 16h..16h+15 of one Q8_1 block.  Units are ordered
 // (item, slice, sub) so the 4 tiles of an item that read the same weight rows
 // are adjacent on one XCD.
-// Fold: kFoldStaged (H < 2048), kFoldGrouped (H = 2048), kFoldMulti
-// (H > 2048); one instantiation per shape keeps only that path's registers.
-enum { kFoldStaged = 0, kFoldGrouped = 1, kFoldMulti = 2 };
+// Fold: kFoldStaged (H < 2048), kFoldGrouped (H = 2048), kFoldGrouped96
+// (2048 < H <= 3072: the grouped leaves plus block kp + 64 in chain A;
+// 2560/640 4K Zipf layer 3.40 -> 2.83 ms with Q4_0 downs, 3.54 -> 2.98 ms
+// with Q4_1, against kFoldMulti), kFoldMulti (H > 3072); one instantiation
+// per shape keeps only that path's registers.
+enum { kFoldStaged = 0, kFoldGrouped = 1, kFoldMulti = 2, kFoldGrouped96 = 3 };
+constexpr int kGu96MaxBlocks = 96;
 
 template<int Fold, bool Dbg>
 __global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
     // Pending tree levels 3-4 per wave; after the tree the up wave's area
     // carries its result to the gate wave.
     __shared__ float park[2][2][16][64];
-    __shared__ uint4 d4_lds[2][kGuMaxBlocks][4];          // [mat][block][32 halfs]
+    __shared__ uint4 d4_lds[2][Fold == kFoldGrouped96 ? kGu96MaxBlocks : kGuMaxBlocks][4];   // [mat][block][32 halfs]
     float (*xch)[64] = park[1][0];
     const int mat = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, I = a.shape.I, nb = H / 32, nbi = I / 32;
@@ -799,8 +906,9 @@ __global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
         }
         __syncthreads();
         const GuStage g{reinterpret_cast<const uint32_t *>(&d4_lds[mat][0][0]), nullptr};
-        if constexpr (Fold == kFoldGrouped)
-            fold_tree_grouped<Dbg>(t, g, static_cast<uint32_t>(prow) * row_bytes + 32u * 16u * h, park[mat], lane, res);
+        if constexpr (Fold == kFoldGrouped || Fold == kFoldGrouped96)
+            fold_tree_grouped<Dbg, Fold == kFoldGrouped96>(t, g, static_cast<uint32_t>(prow) * row_bytes + 32u * 16u * h,
+                                                           park[mat], lane, res);
         else fold_tree_staged<false, Dbg>(t, g, park[mat], lane, res);
     } else {
         fold_tree_multi<Dbg>(t, park[mat], lane, res);
@@ -1352,6 +1460,9 @@ hipError_t launch_gate_up_mfma(const FfnArgs &a, hipStream_t s) {
     if (nb == kGuMaxBlocks) {
         if (dbg) k_gate_up_mfma<kFoldGrouped, true><<<grid, 128, 0, s>>>(a);
         else k_gate_up_mfma<kFoldGrouped, false><<<grid, 128, 0, s>>>(a);
+    } else if (nb > kGuMaxBlocks && nb <= kGu96MaxBlocks) {
+        if (dbg) k_gate_up_mfma<kFoldGrouped96, true><<<grid, 128, 0, s>>>(a);
+        else k_gate_up_mfma<kFoldGrouped96, false><<<grid, 128, 0, s>>>(a);
     } else if (nb < kGuMaxBlocks) {
         if (dbg) k_gate_up_mfma<kFoldStaged, true><<<grid, 128, 0, s>>>(a);
         else k_gate_up_mfma<kFoldStaged, false><<<grid, 128, 0, s>>>(a);
