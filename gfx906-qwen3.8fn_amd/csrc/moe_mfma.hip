@@ -996,26 +996,33 @@ __host__ __device__ constexpr int down_groups(int H, int nbi, bool q41) {
 // (this slice's 32 rows, and the next slice's 32 rows at next_off when there
 // is a next slice: past its end the descriptor reads zeros), at lane offset
 // w_off.
-template<int NS, bool Dbg, bool Q41, class Stage>
+template<int NS, bool Dbg, bool Q41, class Stage, int B0 = 0>
 __device__ __forceinline__ void down_staged(const FfnArgs &a, const Stage &st, const uint4 (*d4s)[4], const uint4 (*m4s)[4],
                                             uint4 (&wa)[kDnWin], __amdgpu_buffer_rsrc_t wr, uint32_t next_off,
                                             uint32_t w_off, int nbi, int first, int ncols, int R0, int pslot, int lane,
                                             float (&acc)[kSubs][16]) {
     const int m = lane & 31, h = lane >> 5, shift = 4 * h;
+    // Blocks B0 .. B0 + nloc - 1 are staged at local indices 0 .. nloc - 1
+    // (the scales, mins, codes and heads); the weight window and the dots
+    // use the block's own index.
+    static_assert(B0 % kDnWin == 0, "block B0 + b sits in window register b % kDnWin");
+    const int nloc = min(nbi - B0, kDnMaxBlocks);
     const uint16_t *d4h = reinterpret_cast<const uint16_t *>(&d4s[0][0]);
     if constexpr (Q41) {
+        if constexpr (B0 == 0) {
 #pragma unroll
-        for (int s = 0; s < NS; ++s)
+            for (int s = 0; s < NS; ++s)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[s][v] = 0.0f;
+                for (int v = 0; v < 16; ++v) acc[s][v] = 0.0f;
+        }
     } else {
     // Seed: -8 * sum_b d4 s8, 16 blocks in one f16 MFMA.
     uint32_t dw[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int k0 = 8 * h + 2 * e, k1 = k0 + 1;
-        const uint32_t lo = k0 < nbi ? d4h[k0 * 32 + pslot] : 0u;
-        const uint32_t hi = k1 < nbi ? d4h[k1 * 32 + pslot] : 0u;
+        const uint32_t lo = k0 < nloc ? d4h[k0 * 32 + pslot] : 0u;
+        const uint32_t hi = k1 < nloc ? d4h[k1 * 32 + pslot] : 0u;
         dw[e] = lo | (hi << 16);
     }
     const v8h da = pack8(dw);
@@ -1025,13 +1032,13 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const Stage &st, c
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int k0 = 8 * h + 2 * e, k1 = k0 + 1;
-            const uint32_t lo = k0 < nbi ? st.hd[k0][kSub * s + m] >> 16 : 0u;
-            const uint32_t hi = k1 < nbi ? st.hd[k1][kSub * s + m] & 0xffff0000u : 0u;
+            const uint32_t lo = k0 < nloc ? st.hd[k0][kSub * s + m] >> 16 : 0u;
+            const uint32_t hi = k1 < nloc ? st.hd[k1][kSub * s + m] & 0xffff0000u : 0u;
             sw[e] = lo | hi;
         }
         const v16f corr = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, pack8(sw), v16f{}, 0, 0, 0);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[s][v] = -8.0f * corr[v];
+        for (int v = 0; v < 16; ++v) acc[s][v] = B0 == 0 ? -8.0f * corr[v] : acc[s][v] + -8.0f * corr[v];
     }
     }
     v16i magic;
@@ -1043,7 +1050,7 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const Stage &st, c
     uint32_t hx = st.hd[0][m];
 #pragma unroll
     for (int b = 0; b < kDnMaxBlocks; ++b) {
-        if (b < nbi) {   // uniform; a guard rather than a break keeps the loop unrolled
+        if (b < nloc) {   // uniform; a guard rather than a break keeps the loop unrolled
         const uint4 w = wa[b % kDnWin];
         const uint4 d0 = d4s[b][2 * h], d1 = d4s[b][2 * h + 1];
         const uint32_t d4[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
@@ -1064,7 +1071,7 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const Stage &st, c
                        static_cast<int>((w.z >> shift) & kNibbles), static_cast<int>((w.w >> shift) & kNibbles)};
         {
             // The offset goes into the per-lane operand, which the range check covers.
-            const int nb = b + kDnWin;
+            const int nb = B0 + b + kDnWin;
             const uint32_t o = nb < nbi ? static_cast<uint32_t>(nb) * 16u : next_off + static_cast<uint32_t>(nb - nbi) * 16u;
             wa[b % kDnWin] = buffer_load16(wr, w_off + o, 0);
         }
@@ -1080,7 +1087,7 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const Stage &st, c
                 if (a.down_dots && j < ncols)
 #pragma unroll
                     for (int v = 0; v < 16; ++v)
-                        a.down_dots[(static_cast<size_t>(first + j) * a.shape.H + R0 + 4 * (v & 7) + 2 * h + (v >> 3)) * nbi + b] =
+                        a.down_dots[(static_cast<size_t>(first + j) * a.shape.H + R0 + 4 * (v & 7) + 2 * h + (v >> 3)) * nbi + B0 + b] =
                             rp[v] - kMagic;
             }
         };
@@ -1182,6 +1189,95 @@ __device__ __forceinline__ void down_slices(const FfnArgs &a, Stage &st, int wav
     }
 }
 
+// Stages blocks B0 .. B0 + 15 (those below nbi) of an item's middle codes
+// and heads, and of each active wave's 32-row scale (and min) tile, at local
+// block indices 0..15.  Thread t keeps one (block, half) of the code rows,
+// local block (t % 32) / 2 and half t % 2, for pairs t / 32 + 8 i, and one
+// block of the heads, t % 16, for pairs t / 16 + 16 i.  The descriptors end
+// at the item's last pair: pairs past ncols read zero.  All loads are issued
+// before the first LDS write.
+struct DownStager {
+    __amdgpu_buffer_rsrc_t xr, hr;
+    const uint4 *scales, *mins;   // the wave's [nbi][4] chunks
+    uint32_t pair_bytes;
+    int cols, nbi, xb, xh, xj, hb, hj;
+
+    __device__ static DownStager make(const FfnArgs &a, int first, int ncols, int nsub, int nbi, size_t rbase) {
+        static_assert(kMfmaTile == 128 && kDnMaxBlocks == 16, "staging map: 256 threads, 128 pairs, 16 blocks");
+        DownStager g;
+        g.pair_bytes = static_cast<uint32_t>(nbi) * 32u;
+        g.xr = buffer_rsrc(a.mq.codes + static_cast<size_t>(first) * g.pair_bytes, static_cast<uint32_t>(ncols) * g.pair_bytes);
+        g.hr = buffer_rsrc(a.mq.heads + static_cast<size_t>(first) * nbi, static_cast<uint32_t>(ncols * nbi) * 4u);
+        g.scales = reinterpret_cast<const uint4 *>(a.bank.down_scales + rbase * nbi);
+        g.mins = a.bank.down_mins ? reinterpret_cast<const uint4 *>(a.bank.down_mins + rbase * nbi) : nullptr;
+        g.cols = nsub * kSub;
+        g.nbi = nbi;
+        const int tid = static_cast<int>(threadIdx.x);
+        g.xb = (tid & 31) >> 1;
+        g.xh = tid & 1;
+        g.xj = tid >> 5;
+        g.hb = tid & 15;
+        g.hj = tid >> 4;
+        return g;
+    }
+
+    template<class Stage>
+    __device__ void run(Stage &st, int B0, int wave, int lane, bool active) const {
+        const int bx = B0 + xb, bh = B0 + hb;
+        const uint32_t x_off = static_cast<uint32_t>(xj) * pair_bytes + static_cast<uint32_t>(32 * bx + 16 * xh);
+        const uint32_t h_off = static_cast<uint32_t>(hj * nbi + bh) * 4u;
+        uint4 xv[kMfmaTile / 8];
+        uint32_t hv[kMfmaTile / 16];
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 8; ++i)
+            if (8 * i < cols && bx < nbi) xv[i] = buffer_load16(xr, x_off, 8u * i * pair_bytes);
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 16; ++i)
+            if (16 * i < cols && bh < nbi) hv[i] = buffer_load4(hr, h_off, 64u * i * static_cast<uint32_t>(nbi));
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 8; ++i)
+            if (8 * i < cols && bx < nbi) st.x[xb][xj + 8 * i][xh] = xv[i];
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 16; ++i)
+            if (16 * i < cols && bh < nbi) st.hd[hb][hj + 16 * i] = hv[i];
+        const int nl = min(nbi - B0, kDnMaxBlocks);
+        if (active)
+            for (int c = lane; c < nl * 4; c += 64) st.d4[0][wave][c >> 2][c & 3] = scales[B0 * 4 + c];
+        if constexpr (std::is_same_v<Stage, DownStageQ41>) {
+            if (active)
+                for (int c = lane; c < nl * 4; c += 64) st.m4[wave][c >> 2][c & 3] = mins[B0 * 4 + c];
+        }
+    }
+};
+
+// Rows of 17..32 down blocks (I = 544..1024; the reference model's 640: 20):
+// one 128-row slice per workgroup, its blocks staged in two rounds into the
+// same LDS (0..15, then 16..nbi - 1) with the accumulators carried across.
+// The weight window already holds blocks 16..23 when the second round
+// starts.  Every wave reaches both barriers.
+template<int NS, bool Dbg, bool Q41, class Stage>
+__device__ __forceinline__ void down_two_rounds(const FfnArgs &a, Stage &st, const DownStager &sg, int wave, bool active,
+                                                uint4 (&wa)[kDnWin], int nbi, int first, int ncols, int R0, size_t rbase,
+                                                uint32_t w_off, int pslot) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t row_bytes = static_cast<uint32_t>(nbi) * 16u;
+    // This slice's 32 rows; past them (no next slice) the descriptor reads zeros.
+    const auto wr = buffer_rsrc(a.bank.down_codes + rbase * row_bytes, 32u * row_bytes);
+    const uint4 (*m4s)[4] = nullptr;
+    if constexpr (Q41) m4s = st.m4[wave];
+    float acc[kSubs][16];
+    if (active)
+        down_staged<NS, Dbg, Q41, Stage, 0>(a, st, st.d4[0][wave], m4s, wa, wr, 32u * row_bytes, w_off, nbi, first, ncols,
+                                            R0, pslot, lane, acc);
+    __syncthreads();   // every wave is done with blocks 0..15
+    sg.run(st, kDnMaxBlocks, wave, lane, active);
+    __syncthreads();
+    if (!active) return;
+    down_staged<NS, Dbg, Q41, Stage, kDnMaxBlocks>(a, st, st.d4[0][wave], m4s, wa, wr, 32u * row_bytes, w_off, nbi, first,
+                                                   ncols, R0, pslot, lane, acc);
+    store_down_tile(a, acc, NS, first, ncols, R0);
+}
+
 template<bool Dbg, bool Q41>
 __global__ __launch_bounds__(256, 2) void k_down_mfma(FfnArgs a) {
     __shared__ std::conditional_t<Q41, DownStageQ41, DownStage> st;
@@ -1189,7 +1285,9 @@ __global__ __launch_bounds__(256, 2) void k_down_mfma(FfnArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = a.shape.I / 32;
     const int slices = (H + 127) / 128;
-    const bool staged = nbi <= kDnMaxBlocks;
+    // Rows of 17..32 blocks take two staging rounds; the debug build (per-block
+    // dots) keeps them on the tile path, whose register use it can afford.
+    const bool staged = nbi <= (Dbg ? kDnMaxBlocks : 2 * kDnMaxBlocks);
     const int span = down_span(nbi, Q41);
     const Unit un = mfma_unit(a.routes.item_counts[1], down_groups(H, nbi, Q41));
     if (!un.ok) return;
@@ -1215,45 +1313,19 @@ __global__ __launch_bounds__(256, 2) void k_down_mfma(FfnArgs a) {
 #pragma unroll
         for (int b = 0; b < kDnWin; ++b) wa[b] = buffer_load16(wr, w_off, static_cast<uint32_t>(b < nbi ? b : 0) * 16u);
         // Middle codes and heads of the item's pairs, every load issued
-        // before the first LDS write.  Thread t keeps one (block, half) of the
-        // code rows, block (t % 32) / 2 and half t % 2, for pairs t / 32 + 8 i,
-        // and one block of the heads, t % 16, for pairs t / 16 + 16 i.  The
-        // descriptors end at the item's last pair: pairs past ncols read zero.
-        static_assert(kMfmaTile == 128 && kDnMaxBlocks == 16, "staging map: 256 threads, 128 pairs, 16 blocks");
-        const int cols = nsub * kSub;
-        const uint32_t pair_bytes = static_cast<uint32_t>(nbi) * 32u;
-        const auto xr = buffer_rsrc(a.mq.codes + static_cast<size_t>(first) * pair_bytes,
-                                    static_cast<uint32_t>(ncols) * pair_bytes);
-        const auto hr = buffer_rsrc(a.mq.heads + static_cast<size_t>(first) * nbi,
-                                    static_cast<uint32_t>(ncols * nbi) * 4u);
-        const int tid = static_cast<int>(threadIdx.x);
-        const int xb = (tid & 31) >> 1, xh = tid & 1, xj = tid >> 5, hb = tid & 15, hj = tid >> 4;
-        const uint32_t x_off = static_cast<uint32_t>(xj) * pair_bytes + static_cast<uint32_t>(32 * xb + 16 * xh);
-        const uint32_t h_off = static_cast<uint32_t>(hj * nbi + hb) * 4u;
-        uint4 xv[kMfmaTile / 8];
-        uint32_t hv[kMfmaTile / 16];
-#pragma unroll
-        for (int i = 0; i < kMfmaTile / 8; ++i)
-            if (8 * i < cols && xb < nbi) xv[i] = buffer_load16(xr, x_off, 8u * i * pair_bytes);
-#pragma unroll
-        for (int i = 0; i < kMfmaTile / 16; ++i)
-            if (16 * i < cols && hb < nbi) hv[i] = buffer_load4(hr, h_off, 64u * i * static_cast<uint32_t>(nbi));
-#pragma unroll
-        for (int i = 0; i < kMfmaTile / 8; ++i)
-            if (8 * i < cols && xb < nbi) st.x[xb][xj + 8 * i][xh] = xv[i];
-#pragma unroll
-        for (int i = 0; i < kMfmaTile / 16; ++i)
-            if (16 * i < cols && hb < nbi) st.hd[hb][hj + 16 * i] = hv[i];
-        if (active)
-            for (int c = lane; c < nbi * 4; c += 64)
-                st.d4[0][wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(scales)[c];
-        if constexpr (Q41) {
-            const uint16_t *mins = a.bank.down_mins + rbase * nbi;   // same layout as the scales
-            if (active)
-                for (int c = lane; c < nbi * 4; c += 64)
-                    st.m4[wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(mins)[c];
-        }
+        // before the first LDS write (DownStager).
+        const DownStager sg = DownStager::make(a, first, ncols, nsub, nbi, rbase);
+        sg.run(st, 0, wave, lane, active);
         __syncthreads();
+        if (!Dbg && nbi > kDnMaxBlocks) {   // two staging rounds; every wave takes part in their barriers
+            if constexpr (!Dbg) switch (nsub) {
+            case 1: down_two_rounds<1, Dbg, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
+            case 2: down_two_rounds<2, Dbg, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
+            case 3: down_two_rounds<3, Dbg, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
+            default: down_two_rounds<4, Dbg, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
+            }
+            return;
+        }
         if (!active) return;
         switch (nsub) {
         case 1: down_slices<1, Dbg, Q41>(a, st, wave, wa, nbi, expert, first, ncols, s0, s1, w_off, pslot); break;
