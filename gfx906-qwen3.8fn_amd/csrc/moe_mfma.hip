@@ -1414,7 +1414,8 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
                                          float (&res)[16]) {
     const int m = lane & 31, h = lane >> 5;
     float l1[16], l2[16];
-    if constexpr (Fold == kFoldGrouped) {
+    if constexpr (Fold == kFoldGrouped || Fold == kFoldGrouped96) {
+        constexpr bool X = Fold == kFoldGrouped96;
         // Node q + 1's weight half is in flight while node q computes.
         uint4 wn[2];
         half_load_w(t, w_off, 4 * wave, wn);
@@ -1425,10 +1426,14 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
             G.w[0] = wn[0];
             G.w[1] = wn[1];
             half_load_x(t, p, G);
+            ExtraBlk E;
+            if constexpr (X) {
+                if (2 * p < t.nb - 64) extra_load(t, p, E);   // uniform
+            }
             half_load_w(t, w_off, q < 3 ? p + 1 : p, wn);
             float w[16], x[16];
-            leaf_grouped<false>(t, g, G, 0, 2 * p, m, h, w);
-            leaf_grouped<false>(t, g, G, 1, 2 * p + 1, m, h, x);
+            leaf_grouped<false, X>(t, g, G, 0, 2 * p, m, h, w, &E);
+            leaf_grouped<false, X>(t, g, G, 1, 2 * p + 1, m, h, x, &E);
 #pragma unroll
             for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
             subtree4_merge(q, w, l1, l2, res);
@@ -1455,7 +1460,7 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
 template<int Fold>
 __global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
     __shared__ float roots[4][16][64];          // subtree roots [wave][value][lane]
-    __shared__ uint4 d4_lds[kGuMaxBlocks][4];   // [block][32 halfs]
+    __shared__ uint4 d4_lds[Fold == kFoldGrouped96 ? kGu96MaxBlocks : kGuMaxBlocks][4];   // [block][32 halfs]
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int id = static_cast<int>(blockIdx.x), local = id >> 3;
     const int rt = (id & 7) + 8 * (local / a.col_tiles), ct = local % a.col_tiles;
@@ -1520,6 +1525,7 @@ __global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
 hipError_t launch_linear_mfma(const LinearMfmaArgs &a, hipStream_t s) {
     const unsigned grid = static_cast<unsigned>((a.row_tiles + 7) / 8 * 8) * static_cast<unsigned>(a.col_tiles);
     if (a.nb == kGuMaxBlocks) k_linear_mfma<kFoldGrouped><<<grid, 256, 0, s>>>(a);
+    else if (a.nb > kGuMaxBlocks && a.nb <= kGu96MaxBlocks) k_linear_mfma<kFoldGrouped96><<<grid, 256, 0, s>>>(a);
     else if (a.nb < kGuMaxBlocks) k_linear_mfma<kFoldStaged><<<grid, 256, 0, s>>>(a);
     else k_linear_mfma<kFoldMulti><<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
