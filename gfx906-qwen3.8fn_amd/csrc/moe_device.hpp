@@ -310,6 +310,29 @@ __device__ __forceinline__ float rows8_exact2(const uint4 (&w)[8], uint4 d4p, ui
     return fold_rows8(acc, lane);
 }
 
+// rows8_exact2 with the second block's t values already formed: lane j (has2)
+// holds t2[q][f] = fma(float(I_f), d8', -4 s8') of row q and block j + 64 and
+// that block's scales d4p2; the arithmetic and fold are rows8_exact2's.
+__device__ __forceinline__ float rows8_exact2t(const uint4 (&w)[8], uint4 d4p, uint4 x0, uint4 x1, uint32_t head,
+                                               uint4 d4p2, const float (&t2)[8][2], bool has2, int lane) {
+    const float d8 = h2f(head), c4 = -4.0f * h2f(head >> 16);
+    float acc[8][2];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        int f0, f1;
+        fragment_dots(w[q], x0, x1, f0, f1);
+        const uint32_t da = (&d4p.x)[q >> 1] >> (16 * (q & 1)), db = (&d4p2.x)[q >> 1] >> (16 * (q & 1));
+        const float a4 = h2f(da), b4 = h2f(db);
+        const float a0 = fmaf(a4, fmaf(static_cast<float>(f0), d8, c4), 0.0f);
+        const float a1 = fmaf(a4, fmaf(static_cast<float>(f1), d8, c4), 0.0f);
+        const float s0 = fmaf(b4, t2[q][0], a0);
+        const float s1 = fmaf(b4, t2[q][1], a1);
+        acc[q][0] = has2 ? s0 : a0;
+        acc[q][1] = has2 ? s1 : a1;
+    }
+    return fold_rows8(acc, lane);
+}
+
 // One Q8_1 block from 32 lanes (lane32 = element index).  Semantics of the
 // reference GPU quantizer (src/hip/linear.hip:121-149): a nonfinite element
 // poisons its block (bit 1), an unrepresentable scale/sum/code sets bit 2,
