@@ -996,8 +996,120 @@ __host__ __device__ constexpr int down_groups(int H, int nbi, bool q41) {
 // (this slice's 32 rows, and the next slice's 32 rows at next_off when there
 // is a next slice: past its end the descriptor reads zeros), at lane offset
 // w_off.
-template<int NS, bool Dbg, bool Q41, class Stage, int B0 = 0>
+template<int NS, bool Dbg, bool Q41, class Stage>
 __device__ __forceinline__ void down_staged(const FfnArgs &a, const Stage &st, const uint4 (*d4s)[4], const uint4 (*m4s)[4],
+                                            uint4 (&wa)[kDnWin], __amdgpu_buffer_rsrc_t wr, uint32_t next_off,
+                                            uint32_t w_off, int nbi, int first, int ncols, int R0, int pslot, int lane,
+                                            float (&acc)[kSubs][16]) {
+    const int m = lane & 31, h = lane >> 5, shift = 4 * h;
+    const uint16_t *d4h = reinterpret_cast<const uint16_t *>(&d4s[0][0]);
+    if constexpr (Q41) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[s][v] = 0.0f;
+    } else {
+    // Seed: -8 * sum_b d4 s8, 16 blocks in one f16 MFMA.
+    uint32_t dw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int k0 = 8 * h + 2 * e, k1 = k0 + 1;
+        const uint32_t lo = k0 < nbi ? d4h[k0 * 32 + pslot] : 0u;
+        const uint32_t hi = k1 < nbi ? d4h[k1 * 32 + pslot] : 0u;
+        dw[e] = lo | (hi << 16);
+    }
+    const v8h da = pack8(dw);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        uint32_t sw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int k0 = 8 * h + 2 * e, k1 = k0 + 1;
+            const uint32_t lo = k0 < nbi ? st.hd[k0][kSub * s + m] >> 16 : 0u;
+            const uint32_t hi = k1 < nbi ? st.hd[k1][kSub * s + m] & 0xffff0000u : 0u;
+            sw[e] = lo | hi;
+        }
+        const v16f corr = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, pack8(sw), v16f{}, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[s][v] = -8.0f * corr[v];
+    }
+    }
+    v16i magic;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) magic[v] = kMagic;
+    // Each step's B operand and head are read from LDS one step ahead (block
+    // b + 1's first at block b's last step; past nbi they are never used).
+    uint4 xb = st.x[0][m][h];
+    uint32_t hx = st.hd[0][m];
+#pragma unroll
+    for (int b = 0; b < kDnMaxBlocks; ++b) {
+        if (b < nbi) {   // uniform; a guard rather than a break keeps the loop unrolled
+        const uint4 w = wa[b % kDnWin];
+        const uint4 d0 = d4s[b][2 * h], d1 = d4s[b][2 * h + 1];
+        const uint32_t d4[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+        uint32_t m4[8] = {};
+        float d4f[16];
+        if constexpr (Q41) {
+            const uint4 n0 = m4s[b][2 * h], n1 = m4s[b][2 * h + 1];
+            m4[0] = n0.x; m4[1] = n0.y; m4[2] = n0.z; m4[3] = n0.w;
+            m4[4] = n1.x; m4[5] = n1.y; m4[6] = n1.z; m4[7] = n1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                d4f[2 * e] = cvt_half_lo(d4[e]);
+                d4f[2 * e + 1] = cvt_half_hi(d4[e]);
+            }
+        }
+        const v4i A = {static_cast<int>((w.x >> shift) & kNibbles), static_cast<int>((w.y >> shift) & kNibbles),
+                       static_cast<int>((w.z >> shift) & kNibbles), static_cast<int>((w.w >> shift) & kNibbles)};
+        {
+            // The offset goes into the per-lane operand, which the range check covers.
+            const int nb = b + kDnWin;
+            const uint32_t o = nb < nbi ? static_cast<uint32_t>(nb) * 16u : next_off + static_cast<uint32_t>(nb - nbi) * 16u;
+            wa[b % kDnWin] = buffer_load16(wr, w_off + o, 0);
+        }
+        // Each tile's MFMA is issued before the previous tile is scaled, so
+        // the matrix unit works under the scaling and two results are live.
+        v16i rp;
+        uint32_t hp = 0;
+        auto scale_prev = [&](int sp) {
+            if constexpr (Q41) scale_block_q41(acc[sp], rp, hp, d4, m4);
+            else scale_block_f32(acc[sp], rp, hp, d4f);
+            if constexpr (Dbg) {
+                const int j = kSub * sp + m;
+                if (a.down_dots && j < ncols)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        a.down_dots[(static_cast<size_t>(first + j) * a.shape.H + R0 + 4 * (v & 7) + 2 * h + (v >> 3)) * nbi + b] =
+                            rp[v] - kMagic;
+            }
+        };
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const v4i B = {static_cast<int>(xb.x), static_cast<int>(xb.y), static_cast<int>(xb.z), static_cast<int>(xb.w)};
+            const v16i r = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, magic, 0, 0, 0);
+            const uint32_t hs = hx;
+            if (s + 1 < NS) {
+                xb = st.x[b][kSub * (s + 1) + m][h];
+                hx = st.hd[b][kSub * (s + 1) + m];
+            } else if (b + 1 < kDnMaxBlocks) {
+                xb = st.x[b + 1][m][h];
+                hx = st.hd[b + 1][m];
+            }
+            if (s > 0) scale_prev(s - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            rp = r;
+            hp = hs;
+        }
+        scale_prev(NS - 1);
+        }
+    }
+}
+
+// down_staged for one of two staging rounds (down_two_rounds): blocks B0 ..
+// B0 + 15 of the row sit at local indices 0..15.
+template<int NS, bool Dbg, bool Q41, class Stage, int B0>
+__device__ __forceinline__ void down_staged_round(const FfnArgs &a, const Stage &st, const uint4 (*d4s)[4], const uint4 (*m4s)[4],
                                             uint4 (&wa)[kDnWin], __amdgpu_buffer_rsrc_t wr, uint32_t next_off,
                                             uint32_t w_off, int nbi, int first, int ncols, int R0, int pslot, int lane,
                                             float (&acc)[kSubs][16]) {
@@ -1006,7 +1118,9 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const Stage &st, c
     // (the scales, mins, codes and heads); the weight window and the dots
     // use the block's own index.
     static_assert(B0 % kDnWin == 0, "block B0 + b sits in window register b % kDnWin");
-    const int nloc = min(nbi - B0, kDnMaxBlocks);
+    // (B0 == 0: every local index below kDnMaxBlocks is also below nbi, so
+    // nbi itself bounds the first round.)
+    const int nloc = B0 == 0 ? nbi : min(nbi - B0, kDnMaxBlocks);
     const uint16_t *d4h = reinterpret_cast<const uint16_t *>(&d4s[0][0]);
     if constexpr (Q41) {
         if constexpr (B0 == 0) {
@@ -1038,7 +1152,10 @@ __device__ __forceinline__ void down_staged(const FfnArgs &a, const Stage &st, c
         }
         const v16f corr = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, pack8(sw), v16f{}, 0, 0, 0);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[s][v] = B0 == 0 ? -8.0f * corr[v] : acc[s][v] + -8.0f * corr[v];
+        for (int v = 0; v < 16; ++v) {
+            if constexpr (B0 == 0) acc[s][v] = -8.0f * corr[v];
+            else acc[s][v] = acc[s][v] + -8.0f * corr[v];
+        }
     }
     }
     v16i magic;
@@ -1267,27 +1384,27 @@ __device__ __forceinline__ void down_two_rounds(const FfnArgs &a, Stage &st, con
     if constexpr (Q41) m4s = st.m4[wave];
     float acc[kSubs][16];
     if (active)
-        down_staged<NS, Dbg, Q41, Stage, 0>(a, st, st.d4[0][wave], m4s, wa, wr, 32u * row_bytes, w_off, nbi, first, ncols,
+        down_staged_round<NS, Dbg, Q41, Stage, 0>(a, st, st.d4[0][wave], m4s, wa, wr, 32u * row_bytes, w_off, nbi, first, ncols,
                                             R0, pslot, lane, acc);
     __syncthreads();   // every wave is done with blocks 0..15
     sg.run(st, kDnMaxBlocks, wave, lane, active);
     __syncthreads();
     if (!active) return;
-    down_staged<NS, Dbg, Q41, Stage, kDnMaxBlocks>(a, st, st.d4[0][wave], m4s, wa, wr, 32u * row_bytes, w_off, nbi, first,
+    down_staged_round<NS, Dbg, Q41, Stage, kDnMaxBlocks>(a, st, st.d4[0][wave], m4s, wa, wr, 32u * row_bytes, w_off, nbi, first,
                                                    ncols, R0, pslot, lane, acc);
     store_down_tile(a, acc, NS, first, ncols, R0);
 }
 
-template<bool Dbg, bool Q41>
+// R2: rows of 17..32 blocks, staged in two rounds (down_two_rounds); a
+// separate instantiation, so the other shapes' kernel keeps its registers.
+template<bool Dbg, bool Q41, bool R2 = false>
 __global__ __launch_bounds__(256, 2) void k_down_mfma(FfnArgs a) {
     __shared__ std::conditional_t<Q41, DownStageQ41, DownStage> st;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = a.shape.I / 32;
     const int slices = (H + 127) / 128;
-    // Rows of 17..32 blocks take two staging rounds; the debug build (per-block
-    // dots) keeps them on the tile path, whose register use it can afford.
-    const bool staged = nbi <= (Dbg ? kDnMaxBlocks : 2 * kDnMaxBlocks);
+    const bool staged = R2 || nbi <= kDnMaxBlocks;
     const int span = down_span(nbi, Q41);
     const Unit un = mfma_unit(a.routes.item_counts[1], down_groups(H, nbi, Q41));
     if (!un.ok) return;
@@ -1312,13 +1429,13 @@ __global__ __launch_bounds__(256, 2) void k_down_mfma(FfnArgs a) {
         uint4 wa[kDnWin];
 #pragma unroll
         for (int b = 0; b < kDnWin; ++b) wa[b] = buffer_load16(wr, w_off, static_cast<uint32_t>(b < nbi ? b : 0) * 16u);
-        // Middle codes and heads of the item's pairs, every load issued
-        // before the first LDS write (DownStager).
-        const DownStager sg = DownStager::make(a, first, ncols, nsub, nbi, rbase);
-        sg.run(st, 0, wave, lane, active);
-        __syncthreads();
-        if (!Dbg && nbi > kDnMaxBlocks) {   // two staging rounds; every wave takes part in their barriers
-            if constexpr (!Dbg) switch (nsub) {
+        if constexpr (R2) {
+            // Middle codes and heads of the item's pairs, every load issued
+            // before the first LDS write (DownStager).
+            const DownStager sg = DownStager::make(a, first, ncols, nsub, nbi, rbase);
+            sg.run(st, 0, wave, lane, active);
+            __syncthreads();
+            switch (nsub) {   // two staging rounds; every wave takes part in their barriers
             case 1: down_two_rounds<1, Dbg, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
             case 2: down_two_rounds<2, Dbg, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
             case 3: down_two_rounds<3, Dbg, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
@@ -1326,6 +1443,46 @@ __global__ __launch_bounds__(256, 2) void k_down_mfma(FfnArgs a) {
             }
             return;
         }
+        // Middle codes and heads of the item's pairs, every load issued
+        // before the first LDS write.  Thread t keeps one (block, half) of the
+        // code rows, block (t % 32) / 2 and half t % 2, for pairs t / 32 + 8 i,
+        // and one block of the heads, t % 16, for pairs t / 16 + 16 i.  The
+        // descriptors end at the item's last pair: pairs past ncols read zero.
+        static_assert(kMfmaTile == 128 && kDnMaxBlocks == 16, "staging map: 256 threads, 128 pairs, 16 blocks");
+        const int cols = nsub * kSub;
+        const uint32_t pair_bytes = static_cast<uint32_t>(nbi) * 32u;
+        const auto xr = buffer_rsrc(a.mq.codes + static_cast<size_t>(first) * pair_bytes,
+                                    static_cast<uint32_t>(ncols) * pair_bytes);
+        const auto hr = buffer_rsrc(a.mq.heads + static_cast<size_t>(first) * nbi,
+                                    static_cast<uint32_t>(ncols * nbi) * 4u);
+        const int tid = static_cast<int>(threadIdx.x);
+        const int xb = (tid & 31) >> 1, xh = tid & 1, xj = tid >> 5, hb = tid & 15, hj = tid >> 4;
+        const uint32_t x_off = static_cast<uint32_t>(xj) * pair_bytes + static_cast<uint32_t>(32 * xb + 16 * xh);
+        const uint32_t h_off = static_cast<uint32_t>(hj * nbi + hb) * 4u;
+        uint4 xv[kMfmaTile / 8];
+        uint32_t hv[kMfmaTile / 16];
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 8; ++i)
+            if (8 * i < cols && xb < nbi) xv[i] = buffer_load16(xr, x_off, 8u * i * pair_bytes);
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 16; ++i)
+            if (16 * i < cols && hb < nbi) hv[i] = buffer_load4(hr, h_off, 64u * i * static_cast<uint32_t>(nbi));
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 8; ++i)
+            if (8 * i < cols && xb < nbi) st.x[xb][xj + 8 * i][xh] = xv[i];
+#pragma unroll
+        for (int i = 0; i < kMfmaTile / 16; ++i)
+            if (16 * i < cols && hb < nbi) st.hd[hb][hj + 16 * i] = hv[i];
+        if (active)
+            for (int c = lane; c < nbi * 4; c += 64)
+                st.d4[0][wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(scales)[c];
+        if constexpr (Q41) {
+            const uint16_t *mins = a.bank.down_mins + rbase * nbi;   // same layout as the scales
+            if (active)
+                for (int c = lane; c < nbi * 4; c += 64)
+                    st.m4[wave][c >> 2][c & 3] = reinterpret_cast<const uint4 *>(mins)[c];
+        }
+        __syncthreads();
         if (!active) return;
         switch (nsub) {
         case 1: down_slices<1, Dbg, Q41>(a, st, wave, wa, nbi, expert, first, ncols, s0, s1, w_off, pslot); break;
@@ -1554,9 +1711,16 @@ hipError_t launch_gate_up_mfma(const FfnArgs &a, hipStream_t s) {
 hipError_t launch_down_mfma(const FfnArgs &a, hipStream_t s) {
     const bool q41 = a.bank.down_mins != nullptr;
     const unsigned grid = mfma_grid(a, down_groups(a.shape.H, a.shape.I / 32, q41));
+    // Rows of 17..32 blocks take two staging rounds; the debug build (per-block
+    // dots) keeps them on the tile path, whose register use it can afford.
+    const int nbi = a.shape.I / 32;
+    const bool r2 = nbi > kDnMaxBlocks && nbi <= 2 * kDnMaxBlocks;
     if (a.down_dots) {
         if (q41) k_down_mfma<true, true><<<grid, 256, 0, s>>>(a);
         else k_down_mfma<true, false><<<grid, 256, 0, s>>>(a);
+    } else if (r2) {
+        if (q41) k_down_mfma<false, true, true><<<grid, 256, 0, s>>>(a);
+        else k_down_mfma<false, false, true><<<grid, 256, 0, s>>>(a);
     } else if (q41) k_down_mfma<false, true><<<grid, 256, 0, s>>>(a);
     else k_down_mfma<false, false><<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
