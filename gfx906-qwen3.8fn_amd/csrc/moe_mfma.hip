@@ -67,6 +67,31 @@ __device__ __forceinline__ int dealt_unit(int id) {
     return (k * 8 + x) * kUnitChunk + (n + k) % kUnitChunk;
 }
 
+// Chunks of kGuChunkRows row slices per XCD (the gate/up kernel): the
+// item-major sequence of (item, row slice) pairs is cut into chunks of
+// kGuChunkRows, chunk c runs on XCD c % 8, and the activations of an item's
+// token tiles, read by every row slice, are fetched into fewer L2s.  Within a
+// chunk, row slice r's token tiles are rotated by r + c over the four
+// positions so each engine sees every tile index.  Chunk rows, layer ms
+// (2048/512, two runs each): 1 (one row slice): 4K 1.47-1.49, 16K 4.61,
+// stack 26.65; 4: 1.47-1.48, 4.53-4.55, 26.56; 8: 1.46-1.47, 4.51-4.56,
+// 26.90; 16 (whole items): 1.48-1.50, 4.52, 27.7 (items dealt whole leave
+// the XCDs unevenly loaded on the stack's 1,032-token layers).
+constexpr int kGuChunkRows = 4;
+constexpr int kGuChunk = kGuChunkRows * kSubs;
+
+__device__ __forceinline__ Unit row_chunk_unit(int count, int slices) {
+    const int id = static_cast<int>(blockIdx.x);
+    const int n = id >> 3, x = id & 7, k = n / kGuChunk, p = n - k * kGuChunk;
+    const int rl = p / kSubs;
+    const int u = (k * 8 + x) * kGuChunk + rl * kSubs + (p + rl + k) % kSubs;
+    Unit r;
+    r.ok = u < count * slices;
+    r.item = r.ok ? u / slices : 0;
+    r.slice = r.ok ? u % slices : 0;
+    return r;
+}
+
 __device__ __forceinline__ Unit mfma_unit(int count, int slices) {
     const int units = count * slices;
     const int u = dealt_unit(static_cast<int>(blockIdx.x));
@@ -862,7 +887,7 @@ __global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
     const int mat = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, I = a.shape.I, nb = H / 32, nbi = I / 32;
     const int slices = nbi * kSubs;
-    const Unit un = mfma_unit(a.routes.item_counts[1], slices);
+    const Unit un = row_chunk_unit(a.routes.item_counts[1], slices);
     if (!un.ok) return;   // uniform per workgroup
     const Item *itp = a.routes.mfma_items + un.item;
     const int expert = itp->expert, first = itp->first, ncols = itp->ncols;
@@ -1528,13 +1553,23 @@ __global__ __launch_bounds__(256, 2) void k_down_mfma(FfnArgs a) {
 
 // Upper bound on MFMA items: a group of n >= mfma_min pairs gives
 // ceil(n / 128) items, and at most min(Ep, pairs / mfma_min) groups qualify.
-unsigned mfma_grid(const FfnArgs &a, int slices) {
+size_t mfma_item_bound(const FfnArgs &a) {
     const size_t P = static_cast<size_t>(a.pairs_bound);
     const size_t G = std::min(P, static_cast<size_t>(a.shape.Ep));
     const size_t big = a.mfma_min >= 1 ? std::min(G, P / static_cast<size_t>(a.mfma_min)) : G;
-    const size_t bound = std::max<size_t>(P / kMfmaTile + big, 1);
-    const size_t units = bound * static_cast<size_t>(slices);
+    return std::max<size_t>(P / kMfmaTile + big, 1);
+}
+
+unsigned mfma_grid(const FfnArgs &a, int slices) {
+    const size_t units = mfma_item_bound(a) * static_cast<size_t>(slices);
     const size_t round = 8 * static_cast<size_t>(kUnitChunk);
+    return static_cast<unsigned>((units + round - 1) / round * round);
+}
+
+// row_chunk_unit's grid: the units rounded up to whole rounds of 8 chunks.
+unsigned chunk_grid(const FfnArgs &a, int slices) {
+    const size_t units = mfma_item_bound(a) * static_cast<size_t>(slices);
+    const size_t round = 8 * static_cast<size_t>(kGuChunk);
     return static_cast<unsigned>((units + round - 1) / round * round);
 }
 
@@ -1690,7 +1725,7 @@ hipError_t launch_linear_mfma(const LinearMfmaArgs &a, hipStream_t s) {
 
 hipError_t launch_gate_up_mfma(const FfnArgs &a, hipStream_t s) {
     const bool dbg = a.middle_f32 || a.gate_dots || a.up_dots;
-    const unsigned grid = mfma_grid(a, a.shape.I / 32 * kSubs);
+    const unsigned grid = chunk_grid(a, a.shape.I / 32 * kSubs);
     const int nb = a.shape.H / 32;
     if (nb == kGuMaxBlocks) {
         if (dbg) k_gate_up_mfma<kFoldGrouped, true><<<grid, 128, 0, s>>>(a);
