@@ -129,6 +129,8 @@ MFMA_CASES = [
     (32, 1, 40),          # one block, one row (31 padding rows)
     (2560, 640, 40),      # 80 blocks (lanes holding several blocks)
     (2080, 1000, 33),     # 65 blocks, rows not a multiple of 32
+    (3072, 256, 64),      # 96 blocks, the last row length of the chained-second-block leaves
+    (4096, 96, 32),       # 128 blocks, every block chained through per-block loads
 ]
 
 

@@ -71,7 +71,15 @@ PATHS = {
 # four-slice work unit is short and its last slice half empty.  (1024, 384)
 # and (512, 128): 12 and 4 down blocks per row, where the down kernel takes
 # one slice per work unit and its 8-block weight window does not wrap.
-@pytest.mark.parametrize("H,I", [(2560, 640), (1024, 256), (1344, 512), (1024, 384), (512, 128)])
+# (2112, 544) and (3072, 1024): 66 and 96 gate/up blocks per row (the
+# shortest layer row past 64 blocks, hidden being a multiple of 64, and the
+# longest row of the MFMA gate/up form whose reference lanes chain a second
+# block; the decode gate/up's spread and plain two-slot forms)
+# with 17 and 32 down blocks (the MFMA down kernel's second staging round
+# holding one block and a full 16).  (4096, 256): 128 gate/up blocks, the
+# MFMA gate/up form that chains every block through per-block loads.
+@pytest.mark.parametrize("H,I", [(2560, 640), (1024, 256), (1344, 512), (1024, 384), (512, 128), (2112, 544),
+                                 (3072, 1024), (4096, 256)])
 @pytest.mark.parametrize("path", list(PATHS))
 def test_layer_shape_paths(H, I, path):
     E, K, N = 16, 4, 40
