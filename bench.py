@@ -221,9 +221,11 @@ def time_graph(stack, steps):
     return wall, e0.elapsed_time(e1) / 1e3 / steps
 
 
-def time_stack(layers, inputs, steps, warmup):
+def time_stack(layers, inputs, steps, warmup, repeats=1):
     """Seconds per pass of the whole stack: layer l runs on its own resident
-    batch inputs[l] = (x, ids, weights), back to back on one stream."""
+    batch inputs[l] = (x, ids, weights), back to back on one stream.  With
+    repeats > 1 the timed loop runs that many times; returns (walls, gpus):
+    per-repeat lists."""
     import torch
     outs = [torch.empty((x.shape[0], L.H), dtype=torch.float32, device=x.device) for L, (x, _, _) in
             zip(layers, inputs)]
@@ -237,17 +239,23 @@ def time_stack(layers, inputs, steps, warmup):
         one_pass()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(steps):
-        one_pass()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
+    walls, gpus = [], []
+    for _ in range(repeats):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(steps):
+            one_pass()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        walls.append((time.perf_counter() - t0) / steps)
+        gpus.append(e0.elapsed_time(e1) / 1e3 / steps)
     if int(err.cpu()[0]) != 0:
         raise RuntimeError(f"error flags {int(err.cpu()[0])}")
-    return wall, e0.elapsed_time(e1) / 1e3 / steps
+    if repeats == 1:
+        return walls[0], gpus[0]
+    return walls, gpus
 
 
 def time_linear(K, M, N, iters=64, cold_bytes=320e6):
@@ -581,11 +589,13 @@ def main():
         idp, wp = W.routes_zipf(NP, 1.1, seed=2003)
         hp = W.group_histogram(idp)
         log(f"[bench] 4k prefill: {hp}")
-        wall_p, gpu_p, _ = time_forward(layer, dev(xph), [(dev(idp), dev(wp))], args.prefill_steps, 3)
+        walls, gpus, _ = time_forward(layer, dev(xph), [(dev(idp), dev(wp))], args.prefill_steps, 3, repeats=3)
+        wall_p, gpu_p = float(np.median(walls)), float(np.median(gpus))
         ops = W.int8_ops(NP)
         pbytes = W.algorithmic_bytes(NP, hp["touched"])
         result["prefill_4k"] = {
             "tokens_per_s": NP / wall_p, "ms_per_layer": wall_p * 1e3, "gpu_event_ms": gpu_p * 1e3,
+            "ms_spread": {"wall": spread(walls, 1e3), "gpu": spread(gpus, 1e3)},
             "int8_tops": ops / gpu_p / 1e12, "int8_mfma_frac": ops / gpu_p / 1e12 / INT8_PEAK_TOPS,
             "hbm_frac": pbytes / gpu_p / 1e9 / HBM_PEAK_GBS, "group_hist": hp, "items": layer.last_stats(),
         }
@@ -596,11 +606,14 @@ def main():
         idp, wp = W.routes_uniform(NP, seed=3003)
         hp = W.group_histogram(idp)
         log(f"[bench] 16k prefill: {hp}")
-        wall_p, gpu_p, _ = time_forward(layer, dev(xph), [(dev(idp), dev(wp))], max(3, args.prefill_steps // 2), 2)
+        walls, gpus, _ = time_forward(layer, dev(xph), [(dev(idp), dev(wp))], max(3, args.prefill_steps // 2), 2,
+                                      repeats=3)
+        wall_p, gpu_p = float(np.median(walls)), float(np.median(gpus))
         ops = W.int8_ops(NP)
         pbytes = W.algorithmic_bytes(NP, hp["touched"])
         result["prefill_16k"] = {
             "tokens_per_s": NP / wall_p, "ms_per_layer": wall_p * 1e3, "gpu_event_ms": gpu_p * 1e3,
+            "ms_spread": {"wall": spread(walls, 1e3), "gpu": spread(gpus, 1e3)},
             "int8_tops": ops / gpu_p / 1e12, "int8_mfma_frac": ops / gpu_p / 1e12 / INT8_PEAK_TOPS,
             "hbm_frac": pbytes / gpu_p / 1e9 / HBM_PEAK_GBS, "group_hist": hp, "items": layer.last_stats(),
         }
@@ -676,11 +689,13 @@ def main():
             ids_l, w_l = W.routes_zipf(NS, 1.3, seed=6000 + l)
             touched_s.append(W.group_histogram(ids_l)["touched"])
             inputs.append((dev(W.activations(NS, seed=7000 + l)), dev(ids_l), dev(w_l)))
-        wall_s, gpu_s = time_stack(layers, inputs, args.stack_steps, 1)
+        walls, gpus = time_stack(layers, inputs, args.stack_steps, 1, repeats=3)
+        wall_s, gpu_s = float(np.median(walls)), float(np.median(gpus))
         sbytes = float(sum(W.algorithmic_bytes(NS, t) for t in touched_s))
         resident = moe_ffn.memory_bytes(2048, 512, 512, 10, True, NS)[0] * NL
         result["stack_48"] = {
             "ms_per_stack": wall_s * 1e3, "gpu_event_ms": gpu_s * 1e3, "us_per_layer": wall_s / NL * 1e6,
+            "ms_spread": {"wall": spread(walls, 1e3), "gpu": spread(gpus, 1e3)},
             "tokens_per_s": NS / wall_s, "tokens_per_layer": NS,
             "hbm_frac": sbytes / gpu_s / 1e9 / HBM_PEAK_GBS, "int8_tops": W.int8_ops(NS) * NL / gpu_s / 1e12,
             "touched_experts_mean": float(np.mean(touched_s)), "resident_weight_gb": resident / 1e9,
