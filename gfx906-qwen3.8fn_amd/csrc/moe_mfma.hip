@@ -1601,16 +1601,15 @@ __device__ __forceinline__ void subtree4_merge(int q, float (&w)[16], float (&l1
     for (int i = 0; i < 16; ++i) res[i] = l2[i] + w[i];
 }
 
+// wn: the wave's first node's weight half, already in flight (grouped folds).
 template<int Fold>
 __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint32_t w_off, int wave, int lane,
-                                         float (&res)[16]) {
+                                         uint4 (&wn)[2], float (&res)[16]) {
     const int m = lane & 31, h = lane >> 5;
     float l1[16], l2[16];
     if constexpr (Fold == kFoldGrouped || Fold == kFoldGrouped96) {
         constexpr bool X = Fold == kFoldGrouped96;
         // Node q + 1's weight half is in flight while node q computes.
-        uint4 wn[2];
-        half_load_w(t, w_off, 4 * wave, wn);
 #pragma unroll 1
         for (int q = 0; q < 4; ++q) {
             const int p = 4 * wave + q;
@@ -1678,6 +1677,11 @@ __global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
     t.dots = nullptr;
     t.dot_base = 0;
     t.dot_ok = false;
+    // The first node's weight half is issued before the scale staging, so the
+    // two round trips overlap.
+    const uint32_t w_off = static_cast<uint32_t>(prow) * row_bytes + 32u * 16u * h;
+    uint4 wn[2] = {};
+    if constexpr (Fold == kFoldGrouped || Fold == kFoldGrouped96) half_load_w(t, w_off, 4 * wave, wn);
     if constexpr (Fold != kFoldMulti) {
         // Scale group g (rows 8g..8g+7) of block b lands at halfs 8g..8g+7 of d4_lds[b].
         for (int c = threadIdx.x; c < 4 * nb; c += blockDim.x) {
@@ -1688,7 +1692,7 @@ __global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
     }
     const GuStage g{reinterpret_cast<const uint32_t *>(&d4_lds[0][0]), nullptr};
     float res[16];
-    subtree4<Fold>(t, g, static_cast<uint32_t>(prow) * row_bytes + 32u * 16u * h, wave, lane, res);
+    subtree4<Fold>(t, g, w_off, wave, lane, wn, res);
 #pragma unroll
     for (int v = 0; v < 16; ++v) roots[wave][v][lane] = res[v];
     __syncthreads();
