@@ -751,11 +751,10 @@ __device__ __forceinline__ void tree_merge(float (*park)[16][64], int lane, int 
 
 template<bool Dbg, bool Extra = false>
 __device__ __forceinline__ void fold_tree_grouped(const GuTile &t, const GuStage &g, uint32_t w_off, float (*park)[16][64],
-                                                  int lane, float (&res)[16]) {
+                                                  int lane, uint4 (&wn)[2], float (&res)[16]) {
+    // wn: node 0's weight half, already in flight.
     const int m = lane & 31, h = lane >> 5;
     float l1[16], l2[16];
-    uint4 wn[2];
-    half_load_w(t, w_off, 0, wn);
 #pragma unroll 1
     for (int p = 0; p < 16; ++p) {
         HalfGroup G;
@@ -920,6 +919,11 @@ __global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
     t.dot_ok = Dbg && t.dots && j < ncols;
 
     float res[16];
+    // Node 0's weight half is issued before the scale staging, so the two
+    // round trips overlap.
+    const uint32_t w_off = static_cast<uint32_t>(prow) * row_bytes + 32u * 16u * h;
+    uint4 wn[2] = {};
+    if constexpr (Fold == kFoldGrouped || Fold == kFoldGrouped96) half_load_w(t, w_off, 0, wn);
     if constexpr (Fold != kFoldMulti) {
         // Stage the tile's scales (both matrices) and its tokens' Q8 heads.
         // Scale group g (rows 8g..8g+7) of block b is one 16-byte chunk of the
@@ -932,8 +936,7 @@ __global__ __launch_bounds__(128, 2) void k_gate_up_mfma(FfnArgs a) {
         __syncthreads();
         const GuStage g{reinterpret_cast<const uint32_t *>(&d4_lds[mat][0][0]), nullptr};
         if constexpr (Fold == kFoldGrouped || Fold == kFoldGrouped96)
-            fold_tree_grouped<Dbg, Fold == kFoldGrouped96>(t, g, static_cast<uint32_t>(prow) * row_bytes + 32u * 16u * h,
-                                                           park[mat], lane, res);
+            fold_tree_grouped<Dbg, Fold == kFoldGrouped96>(t, g, w_off, park[mat], lane, wn, res);
         else fold_tree_staged<false, Dbg>(t, g, park[mat], lane, res);
     } else {
         fold_tree_multi<Dbg>(t, park[mat], lane, res);
