@@ -191,6 +191,29 @@ __device__ __forceinline__ float rows8_down_exact(const uint4 (&w)[8], uint4 d4p
     return v + 0.0f;
 }
 
+// One down (row, block) chunk as rows8_down_exact forms it before its block
+// tree: both fragments scaled, then (z0 + z1) + 0, or +0 for a block past the
+// row end.  d4h / m4h hold the row's fp16 scale / min in their low halves.
+template<bool Q41>
+__device__ __forceinline__ float down_chunk(uint4 w, uint32_t d4h, uint32_t m4h, uint4 x0, uint4 x1, uint32_t head,
+                                            bool has) {
+    const float d8 = h2f(head), s8 = h2f(head >> 16), c4 = -4.0f * s8;
+    int f0, f1;
+    fragment_dots(w, x0, x1, f0, f1);
+    float z0, z1;
+    if constexpr (Q41) {
+        const float d4 = h2f(d4h), m4 = h2f(m4h);
+        const float dd = h2f(f2h(d4 * d8)), hm = h2f(f2h(m4 * s8)) * 0.5f;
+        z0 = fmaf(static_cast<float>(f0), dd, hm);
+        z1 = fmaf(static_cast<float>(f1), dd, hm);
+    } else {
+        const float t0 = fmaf(static_cast<float>(f0), d8, c4), t1 = fmaf(static_cast<float>(f1), d8, c4);
+        z0 = mul_half_lo(d4h, t0);
+        z1 = mul_half_lo(d4h, t1);
+    }
+    return has ? (z0 + z1) + 0.0f : 0.0f;
+}
+
 // Eight weight rows (w[q], scales d4p: row q at half q) against one token's
 // Q8 block per lane (lane = block, H/32 <= 64), summed in the reference's
 // exact fp32 order (src/cpu_expert.cpp:156-213, the gfx906 MMVQ reduction):

@@ -1251,7 +1251,14 @@ __global__ __launch_bounds__(512, Two ? (Spread ? 6 : 4) : 8) void k_decode_gate
 // takes block kl + 16.  The reference's fold pairs blocks k and k ^ 16 last,
 // so the row is (tree over blocks 0..15) + (tree over blocks 16..31), each
 // tree as rows8_down_exact sums it.
-template<bool Q41, bool Two>
+// Spread (I/32 in 17..20, the reference model's 640: 20): the second tree
+// holds at most blocks 16..19, i.e. ((n16 + n17) + (n18 + n19)) with n the
+// chunks of rows8_down_exact (its other lanes add +0).  The wave's 32 rows x
+// 4 second-slot chunks go two to a lane instead of 8 rows per lane: lane l
+// takes block 16 + (l & 3) of rows l / 4 and 16 + l / 4, the lane quad sums
+// a row's four chunks in that order (XOR 1, then 2), and ds_bpermute brings
+// each row's sum to the lane that holds the row's first tree.
+template<bool Q41, bool Two, bool Spread = false>
 __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
     __shared__ float part[kDecodeMaxPairs][32];
     __shared__ int valid[kDecodeMaxPairs];
@@ -1300,7 +1307,44 @@ __global__ __launch_bounds__(1024) void k_decode_down_fold(DecodeArgs d) {
         const uint4 x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
         const uint32_t hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
         float v = rows8_down_exact<Q41>(w, d4p, m4p, x0, x1, hx, has, lane);
-        if constexpr (Two) {
+        if constexpr (Spread) {
+            const int j = lane & 3, kb2 = 16 + j;
+            const bool has2 = kb2 < nbi;
+            const int kk = has2 ? kb2 : 0;
+            float sr2[2];
+            const uint4 y0 = buffer_load16(xr, static_cast<uint32_t>(kk) * 32u, 0);
+            const uint4 y1 = buffer_load16(xr, static_cast<uint32_t>(kk) * 32u, 16);
+            const uint32_t hy = buffer_load4(hr, static_cast<uint32_t>(kk) * 4u, 0);
+            uint4 wc[2];
+            uint32_t dh[2], mh[2] = {0u, 0u};
+            const auto mr = buffer_rsrc(Q41 ? a.bank.down_mins + mrow * nbi : a.bank.down_scales, 4 * row_bytes);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int rr = 16 * u + (lane >> 2);   // row within the slice
+                wc[u] = buffer_load16_nt(wr, static_cast<uint32_t>(rr) * row_bytes + static_cast<uint32_t>(kk) * 16u, 0);
+                // Scale plane: [32-row group][block][32 halves], row r at half (r & 3) * 8 + r / 4.
+                const uint32_t hi = static_cast<uint32_t>(kk * 32 + (rr & 3) * 8 + (rr >> 2));
+                const uint32_t dw = buffer_load4(sr, (hi >> 1) * 4u, 0);
+                dh[u] = (hi & 1) ? dw >> 16 : dw & 0xffffu;
+                if constexpr (Q41) {
+                    const uint32_t mw = buffer_load4(mr, (hi >> 1) * 4u, 0);
+                    mh[u] = (hi & 1) ? mw >> 16 : mw & 0xffffu;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                float n = down_chunk<Q41>(wc[u], dh[u], mh[u], y0, y1, hy, has2);
+                n = n + lane_xor<1>(n);
+                sr2[u] = n + lane_xor<2>(n);
+            }
+            // This lane's first-tree row (meaningful where lane & 8 == 0): 4 lr + sub.
+            const int lr = 4 * (lane & 1) + 2 * ((lane >> 1) & 1) + ((lane >> 2) & 1);
+            const int row = 4 * lr + (lane >> 4);
+            const int src = 4 * (row & 15);
+            const float a0 = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * src, __float_as_int(sr2[0])));
+            const float a1 = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * src, __float_as_int(sr2[1])));
+            v = v + ((row >> 4) ? a1 : a0);
+        } else if constexpr (Two) {
             const bool has2 = kl + 16 < nbi;
             const int kb2 = has2 ? kl + 16 : 0;
             const uint32_t lane_off2 = static_cast<uint32_t>(sub * nbi + kb2) * 16u;
@@ -1987,12 +2031,14 @@ hipError_t launch_decode_down_fold(const DecodeArgs &d, hipStream_t s) {
     const int P1 = sh.k + (sh.Ep > sh.E ? 1 : 0);
     const unsigned groups = static_cast<unsigned>((sh.H / 32 + 7) / 8);
     const dim3 grid(8u * groups * d.f.tokens), block(64 * P1);
-    const bool two = sh.I > 512;
+    const bool two = sh.I > 512, spread = two && sh.I <= 20 * 32;
     if (d.f.bank.down_mins) {
-        if (two) k_decode_down_fold<true, true><<<grid, block, 0, s>>>(d);
+        if (spread) k_decode_down_fold<true, true, true><<<grid, block, 0, s>>>(d);
+        else if (two) k_decode_down_fold<true, true><<<grid, block, 0, s>>>(d);
         else k_decode_down_fold<true, false><<<grid, block, 0, s>>>(d);
     } else {
-        if (two) k_decode_down_fold<false, true><<<grid, block, 0, s>>>(d);
+        if (spread) k_decode_down_fold<false, true, true><<<grid, block, 0, s>>>(d);
+        else if (two) k_decode_down_fold<false, true><<<grid, block, 0, s>>>(d);
         else k_decode_down_fold<false, false><<<grid, block, 0, s>>>(d);
     }
     return hipGetLastError();
