@@ -993,18 +993,25 @@ constexpr int kDnMaxBlocks = 16;
 constexpr int kDnWin = 8;
 constexpr int kDnSlicesPerGroup = 4;
 
-template<int NB>
+template<int NB, int W = 4>
 struct DownStageT {
+    static constexpr bool kMins = false;
     uint4 x[kDnMaxBlocks][kMfmaTile][2];     // middle codes [block][pair][32 bytes]
     uint32_t hd[kDnMaxBlocks][kMfmaTile];    // middle heads [block][pair]
-    uint4 d4[NB][4][kDnMaxBlocks][4];        // [buffer][wave]: scales [block][32 slots]
+    uint4 d4[NB][W][kDnMaxBlocks][4];        // [buffer][wave]: scales [block][32 slots]
 };
 using DownStage = DownStageT<2>;             // Q4_0 rows: 80 KiB, two workgroups per CU
 // Q4_1 rows also stage their mins (80 KiB: two workgroups per CU) and take
 // one slice per workgroup (a second scale buffer would not fit twice).
-struct DownStageQ41 : DownStageT<1> {
-    uint4 m4[4][kDnMaxBlocks][4];            // per wave: mins [block][32 slots]
+template<int W = 4>
+struct DownStageQ41T : DownStageT<1, W> {
+    static constexpr bool kMins = true;
+    uint4 m4[W][kDnMaxBlocks][4];            // per wave: mins [block][32 slots]
 };
+using DownStageQ41 = DownStageQ41T<4>;
+// Rows of 17..32 Q4_0 blocks: a workgroup of 8 waves takes two 128-row
+// slices against one staging of each round (80 KiB).
+using DownStage2 = DownStageT<1, 8>;
 
 // Slices of 128 rows per work unit of the down kernel.  Running on into the
 // next slice keeps block j of every slice in window register j % kDnWin only
@@ -1341,6 +1348,7 @@ __device__ __forceinline__ void down_slices(const FfnArgs &a, Stage &st, int wav
 // block of the heads, t % 16, for pairs t / 16 + 16 i.  The descriptors end
 // at the item's last pair: pairs past ncols read zero.  All loads are issued
 // before the first LDS write.
+template<int T>
 struct DownStager {
     __amdgpu_buffer_rsrc_t xr, hr;
     const uint4 *scales, *mins;   // the wave's [nbi][4] chunks
@@ -1348,7 +1356,8 @@ struct DownStager {
     int cols, nbi, xb, xh, xj, hb, hj;
 
     __device__ static DownStager make(const FfnArgs &a, int first, int ncols, int nsub, int nbi, size_t rbase) {
-        static_assert(kMfmaTile == 128 && kDnMaxBlocks == 16, "staging map: 256 threads, 128 pairs, 16 blocks");
+        static_assert(kMfmaTile == 128 && kDnMaxBlocks == 16 && (T == 256 || T == 512),
+                      "staging map: 256 or 512 threads, 128 pairs, 16 blocks");
         DownStager g;
         g.pair_bytes = static_cast<uint32_t>(nbi) * 32u;
         g.xr = buffer_rsrc(a.mq.codes + static_cast<size_t>(first) * g.pair_bytes, static_cast<uint32_t>(ncols) * g.pair_bytes);
@@ -1371,24 +1380,27 @@ struct DownStager {
         const int bx = B0 + xb, bh = B0 + hb;
         const uint32_t x_off = static_cast<uint32_t>(xj) * pair_bytes + static_cast<uint32_t>(32 * bx + 16 * xh);
         const uint32_t h_off = static_cast<uint32_t>(hj * nbi + bh) * 4u;
-        uint4 xv[kMfmaTile / 8];
-        uint32_t hv[kMfmaTile / 16];
+        // Thread t keeps (block, half) ((t % 32) / 2, t % 2) of pairs t / 32 + PX i
+        // and the head of block t % 16 of pairs t / 16 + PH i.
+        constexpr int PX = T / 32, PH = T / 16;
+        uint4 xv[kMfmaTile / PX];
+        uint32_t hv[kMfmaTile / PH];
 #pragma unroll
-        for (int i = 0; i < kMfmaTile / 8; ++i)
-            if (8 * i < cols && bx < nbi) xv[i] = buffer_load16(xr, x_off, 8u * i * pair_bytes);
+        for (int i = 0; i < kMfmaTile / PX; ++i)
+            if (PX * i < cols && bx < nbi) xv[i] = buffer_load16(xr, x_off, static_cast<uint32_t>(PX * i) * pair_bytes);
 #pragma unroll
-        for (int i = 0; i < kMfmaTile / 16; ++i)
-            if (16 * i < cols && bh < nbi) hv[i] = buffer_load4(hr, h_off, 64u * i * static_cast<uint32_t>(nbi));
+        for (int i = 0; i < kMfmaTile / PH; ++i)
+            if (PH * i < cols && bh < nbi) hv[i] = buffer_load4(hr, h_off, static_cast<uint32_t>(PH * i * nbi) * 4u);
 #pragma unroll
-        for (int i = 0; i < kMfmaTile / 8; ++i)
-            if (8 * i < cols && bx < nbi) st.x[xb][xj + 8 * i][xh] = xv[i];
+        for (int i = 0; i < kMfmaTile / PX; ++i)
+            if (PX * i < cols && bx < nbi) st.x[xb][xj + PX * i][xh] = xv[i];
 #pragma unroll
-        for (int i = 0; i < kMfmaTile / 16; ++i)
-            if (16 * i < cols && bh < nbi) st.hd[hb][hj + 16 * i] = hv[i];
+        for (int i = 0; i < kMfmaTile / PH; ++i)
+            if (PH * i < cols && bh < nbi) st.hd[hb][hj + PH * i] = hv[i];
         const int nl = min(nbi - B0, kDnMaxBlocks);
         if (active)
             for (int c = lane; c < nl * 4; c += 64) st.d4[0][wave][c >> 2][c & 3] = scales[B0 * 4 + c];
-        if constexpr (std::is_same_v<Stage, DownStageQ41>) {
+        if constexpr (Stage::kMins) {
             if (active)
                 for (int c = lane; c < nl * 4; c += 64) st.m4[wave][c >> 2][c & 3] = mins[B0 * 4 + c];
         }
@@ -1400,8 +1412,8 @@ struct DownStager {
 // same LDS (0..15, then 16..nbi - 1) with the accumulators carried across.
 // The weight window already holds blocks 16..23 when the second round
 // starts.  Every wave reaches both barriers.
-template<int NS, bool Dbg, bool Q41, class Stage>
-__device__ __forceinline__ void down_two_rounds(const FfnArgs &a, Stage &st, const DownStager &sg, int wave, bool active,
+template<int NS, bool Dbg, bool Q41, class Stage, class Stager>
+__device__ __forceinline__ void down_two_rounds(const FfnArgs &a, Stage &st, const Stager &sg, int wave, bool active,
                                                 uint4 (&wa)[kDnWin], int nbi, int first, int ncols, int R0, size_t rbase,
                                                 uint32_t w_off, int pslot) {
     const int lane = threadIdx.x & 63;
@@ -1460,7 +1472,7 @@ __global__ __launch_bounds__(256, 2) void k_down_mfma(FfnArgs a) {
         if constexpr (R2) {
             // Middle codes and heads of the item's pairs, every load issued
             // before the first LDS write (DownStager).
-            const DownStager sg = DownStager::make(a, first, ncols, nsub, nbi, rbase);
+            const DownStager<256> sg = DownStager<256>::make(a, first, ncols, nsub, nbi, rbase);
             sg.run(st, 0, wave, lane, active);
             __syncthreads();
             switch (nsub) {   // two staging rounds; every wave takes part in their barriers
@@ -1552,6 +1564,48 @@ __global__ __launch_bounds__(256, 2) void k_down_mfma(FfnArgs a) {
     t.h = h;
     tile_dispatch<Dbg, true, Q41>(t, nsub, acc);
     store_down_tile(a, acc, nsub, first, ncols, R0);
+}
+
+// Q4_0 rows of 17..32 down blocks without debug outputs: a workgroup of 8
+// waves takes slices 2u (waves 0-3) and 2u + 1 (waves 4-7) of an item, so
+// each staging round (down_two_rounds) serves 256 rows instead of 128.  The
+// CU holds one such workgroup (8 waves at 236 VGPRs: two per SIMD, as two
+// 4-wave workgroups would).
+__global__ __launch_bounds__(512, 1) void k_down_mfma_pair(FfnArgs a) {
+    constexpr bool Q41 = false;
+    __shared__ DownStage2 st;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int H = a.shape.H, nbi = a.shape.I / 32;
+    const int slices = (H + 127) / 128;
+    const Unit un = mfma_unit(a.routes.item_counts[1], (slices + 1) / 2);
+    if (!un.ok) return;   // uniform per workgroup
+    const Item *itp = a.routes.mfma_items + un.item;
+    const int expert = itp->expert, first = itp->first, ncols = itp->ncols;
+    const int R0 = (2 * un.slice + (wave >> 2)) * 128 + (wave & 3) * 32;
+    const bool active = R0 < H;      // wave-uniform
+    const int nsub = (ncols + kSub - 1) / kSub;
+    const int m = lane & 31;
+    const int mv = 4 * (m >> 3) + (m & 3);
+    const int prow = 4 * (mv & 7) + 2 * ((m >> 2) & 1) + (mv >> 3);
+    const int pslot = (prow & 3) * 8 + (prow >> 2);
+    const size_t rbase = static_cast<size_t>(expert) * H + (active ? R0 : 0);
+    const uint32_t row_bytes = static_cast<uint32_t>(nbi) * 16u;
+    // The first weight blocks first (their HBM latency overlaps the staging).
+    const auto wr = buffer_rsrc(a.bank.down_codes + rbase * row_bytes, 32u * row_bytes);
+    const uint32_t w_off = static_cast<uint32_t>(prow) * row_bytes;
+    uint4 wa[kDnWin];
+#pragma unroll
+    for (int b = 0; b < kDnWin; ++b) wa[b] = buffer_load16(wr, w_off, static_cast<uint32_t>(b) * 16u);
+    const DownStager<512> sg = DownStager<512>::make(a, first, ncols, nsub, nbi, rbase);
+    sg.run(st, 0, wave, lane, active);
+    __syncthreads();
+    switch (nsub) {   // two staging rounds; every wave takes part in their barriers
+    case 1: down_two_rounds<1, false, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
+    case 2: down_two_rounds<2, false, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
+    case 3: down_two_rounds<3, false, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
+    default: down_two_rounds<4, false, Q41>(a, st, sg, wave, active, wa, nbi, first, ncols, R0, rbase, w_off, pslot); break;
+    }
 }
 
 // Upper bound on MFMA items: a group of n >= mfma_min pairs gives
@@ -1760,9 +1814,14 @@ hipError_t launch_down_mfma(const FfnArgs &a, hipStream_t s) {
     if (a.down_dots) {
         if (q41) k_down_mfma<true, true><<<grid, 256, 0, s>>>(a);
         else k_down_mfma<true, false><<<grid, 256, 0, s>>>(a);
+    } else if (r2 && !q41) {
+        // Two slices per 8-wave workgroup (2560/640 4K Zipf(1.1) layer with
+        // Q4_0 downs 2.70-2.71 -> 2.46 ms); with Q4_1 rows (254 VGPRs, 88 KB
+        // of LDS) it ran 2.71 -> 2.75 ms, so those keep one slice per workgroup.
+        const unsigned pgrid = mfma_grid(a, ((a.shape.H + 127) / 128 + 1) / 2);   // k_down_mfma_pair's units per item
+        k_down_mfma_pair<<<pgrid, 512, 0, s>>>(a);
     } else if (r2) {
-        if (q41) k_down_mfma<false, true, true><<<grid, 256, 0, s>>>(a);
-        else k_down_mfma<false, false, true><<<grid, 256, 0, s>>>(a);
+        k_down_mfma<false, true, true><<<grid, 256, 0, s>>>(a);
     } else if (q41) k_down_mfma<false, true><<<grid, 256, 0, s>>>(a);
     else k_down_mfma<false, false><<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
