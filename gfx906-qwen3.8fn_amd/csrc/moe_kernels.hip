@@ -698,7 +698,11 @@ __global__ __launch_bounds__(512) void k_gate_up_stream(FfnArgs a) {
 // j also holds block j + 64 (rows8_exact2, the reference lane's FMA chain).
 // One unit (item, slice) of k_gate_up_lean; false once the item is past the
 // stream item count (which it stores in `count`).
-template<bool Full, bool Two, bool Dbg>
+// Spread (H/32 in 65..80, the reference model's 2560: 80): the second
+// slot's 8 x (H/32 - 64) chunks go over the lanes as in k_decode_gate_up's
+// spread form (lane 16k + j: rows k and k + 4 of block 64 + j) and each
+// token's t values reach their rows' lanes by ds_bpermute (rows8_exact2t).
+template<bool Full, bool Two, bool Dbg, bool Spread = false>
 __device__ __forceinline__ bool gate_up_lean_unit(const FfnArgs &a, int uid, int &count,
                                                   float (&gu)[2][32][kStreamTokens]) {
     constexpr int T = kStreamTokens;
@@ -745,9 +749,17 @@ __device__ __forceinline__ bool gate_up_lean_unit(const FfnArgs &a, int uid, int
     const uint4 d4p = buffer_load16(sr, lane_off, 0);
     const bool has2 = Two && lane + 64 < nbh;
     const uint32_t lane_off2 = has2 ? static_cast<uint32_t>(lane + 64) * 16u : 0u;
-    uint4 w2[8];
+    // Spread: this lane's chunks, rows xk and xk + 4 of block 64 + xj.
+    const int xk = lane >> 4, xj = lane & 15;
+    const bool xhas = Spread && xj < nbh - 64;
+    const uint32_t x_off2 = xhas ? static_cast<uint32_t>(64 + xj) * 16u : 0u;
+    uint4 w2[Spread ? 2 : 8];
     uint4 d4p2 = make_uint4(0u, 0u, 0u, 0u);
-    if constexpr (Two) {
+    if constexpr (Spread) {
+        w2[0] = buffer_load16(wr, x_off2 + static_cast<uint32_t>(xk) * row_bytes, 0);
+        w2[1] = buffer_load16(wr, x_off2 + static_cast<uint32_t>(xk + 4) * row_bytes, 0);
+        d4p2 = buffer_load16(sr, lane_off2, 0);
+    } else if constexpr (Two) {
 #pragma unroll
         for (int r = 0; r < 8; ++r) w2[r] = buffer_load16(wr, lane_off2, r * row_bytes);
         d4p2 = buffer_load16(sr, lane_off2, 0);
@@ -767,9 +779,11 @@ __device__ __forceinline__ bool gate_up_lean_unit(const FfnArgs &a, int uid, int
         b.x1 = buffer_load16(xr, 2 * lane_off, 16);
         b.hx = buffer_load4(hr, lane_off / 4, 0);
         if constexpr (Two) {
-            b.y0 = buffer_load16(xr, 2 * lane_off2, 0);
-            b.y1 = buffer_load16(xr, 2 * lane_off2, 16);
-            b.hy = buffer_load4(hr, lane_off2 / 4, 0);
+            // Spread: the block of this lane's chunks (64 + xj); else block lane + 64.
+            const uint32_t o2 = Spread ? x_off2 : lane_off2;
+            b.y0 = buffer_load16(xr, 2 * o2, 0);
+            b.y1 = buffer_load16(xr, 2 * o2, 16);
+            b.hy = buffer_load4(hr, o2 / 4, 0);
         }
     };
     Xb cur;
@@ -792,10 +806,31 @@ __device__ __forceinline__ bool gate_up_lean_unit(const FfnArgs &a, int uid, int
                             dot_block(w2[r], cur.y0, cur.y1);
             }
             float v;
-            if constexpr (Two)
+            if constexpr (Spread) {
+                const float e8 = h2f(cur.hy), e4 = -4.0f * h2f(cur.hy >> 16);
+                float tx[2][2];
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    int g0, g1;
+                    fragment_dots(w2[c], cur.y0, cur.y1, g0, g1);
+                    tx[c][0] = fmaf(static_cast<float>(g0), e8, e4);
+                    tx[c][1] = fmaf(static_cast<float>(g1), e8, e4);
+                }
+                // Row q of block 64 + j sits in lane j + 16 (q % 4), chunk q / 4.
+                float t2[8][2];
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+#pragma unroll
+                    for (int f = 0; f < 2; ++f)
+                        t2[q][f] = (q & 3) == 0 ? tx[q >> 2][f]
+                                                : __int_as_float(__builtin_amdgcn_ds_bpermute(
+                                                      4 * ((lane & 15) + 16 * (q & 3)), __float_as_int(tx[q >> 2][f])));
+                v = rows8_exact2t(w, d4p, cur.x0, cur.x1, cur.hx, d4p2, t2, has2, lane);
+            } else if constexpr (Two) {
                 v = rows8_exact2(w, d4p, cur.x0, cur.x1, cur.hx, w2, d4p2, cur.y0, cur.y1, cur.hy, has2, lane);
-            else
+            } else {
                 v = rows8_exact<Full>(w, d4p, cur.x0, cur.x1, cur.hx, has, lane);
+            }
             if ((lane & 28) == 0) gu[mat][(wave & 3) * 8 + rho][j] = v;
             cur = nxt;
         }
@@ -823,13 +858,13 @@ __device__ __forceinline__ bool gate_up_lean_unit(const FfnArgs &a, int uid, int
 // Units id, id + grid, ...: the grid is capped (kLeanGridCap), a multiple of
 // 8 and of I/32, so a workgroup keeps its XCD and slice and a batch with no
 // streaming items starts few workgroups.
-template<bool Full, bool Two, bool Dbg>
-__global__ __launch_bounds__(512, Two ? 2 : 3) void k_gate_up_lean(FfnArgs a) {
+template<bool Full, bool Two, bool Dbg, bool Spread = false>
+__global__ __launch_bounds__(512, Two && !Spread ? 2 : 3) void k_gate_up_lean(FfnArgs a) {
     __shared__ float gu[2][32][kStreamTokens];
     const int S = a.shape.I / 32;
     int count = INT_MAX;
     for (int u = static_cast<int>(blockIdx.x); u / S < count; u += static_cast<int>(gridDim.x))
-        if (!gate_up_lean_unit<Full, Two, Dbg>(a, u, count, gu)) break;
+        if (!gate_up_lean_unit<Full, Two, Dbg, Spread>(a, u, count, gu)) break;
 }
 
 // Down projection, streaming path.  Work unit = (item, slice of 64 output
@@ -1996,6 +2031,7 @@ hipError_t launch_gate_up(const FfnArgs &a, bool mfma, hipStream_t s) {
         const unsigned lgrid = lean_grid(stream_item_bound(a), static_cast<unsigned>(a.shape.I / 32));
         if (nbl == 2) {
             if (dbg) k_gate_up_lean<false, true, true><<<lgrid, 512, 0, s>>>(a);
+            else if (a.shape.H <= 80 * 32) k_gate_up_lean<false, true, false, true><<<lgrid, 512, 0, s>>>(a);
             else k_gate_up_lean<false, true, false><<<lgrid, 512, 0, s>>>(a);
         } else if (dbg) k_gate_up_lean<false, false, true><<<lgrid, 512, 0, s>>>(a);
         else if (a.shape.H == 2048) k_gate_up_lean<true, false, false><<<lgrid, 512, 0, s>>>(a);
