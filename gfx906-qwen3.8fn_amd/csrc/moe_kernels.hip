@@ -956,7 +956,9 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
 // fold.
 // One unit (item, slice of 64 rows) of k_down_lean; false once the item is
 // past the stream item count (stored in `count`).
-template<int NBI, bool Q41, bool Two, bool Dbg>
+// Spread (I/32 in 17..20): the second tree's chunks go two to a lane as in
+// k_decode_down_fold's spread form, the weights held across the item's pairs.
+template<int NBI, bool Q41, bool Two, bool Dbg, bool Spread = false>
 __device__ __forceinline__ bool down_lean_unit(const FfnArgs &a, int uid, int &count) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = a.shape.H, nbi = NBI ? NBI : a.shape.I / 32;
@@ -998,9 +1000,29 @@ __device__ __forceinline__ bool down_lean_unit(const FfnArgs &a, int uid, int &c
     if constexpr (Q41) m4p = buffer_load16(mr, static_cast<uint32_t>(kb * 32 + sub * 8) * 2u, 0);
     const bool has2 = Two && kl + 16 < nbi;
     const int kb2 = has2 ? kl + 16 : 0;
-    uint4 w2[8];
+    // Spread: this lane's chunks, block 16 + (lane & 3) of rows lane / 4 and
+    // 16 + lane / 4 of the wave's 32.
+    const int sj = lane & 3;
+    const bool shas = Spread && 16 + sj < nbi;
+    const int skb = shas ? 16 + sj : 0;
+    uint4 w2[Spread ? 2 : 8];
+    uint32_t sdh[2] = {0u, 0u}, smh[2] = {0u, 0u};
     uint4 d4p2 = make_uint4(0u, 0u, 0u, 0u), m4p2 = make_uint4(0u, 0u, 0u, 0u);
-    if constexpr (Two) {
+    if constexpr (Spread) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int rr = 16 * u + (lane >> 2);
+            w2[u] = buffer_load16(wr, static_cast<uint32_t>(rr) * row_bytes + static_cast<uint32_t>(skb) * 16u, 0);
+            // Scale plane: [32-row group][block][32 halves], row r at half (r & 3) * 8 + r / 4.
+            const uint32_t hi = static_cast<uint32_t>(skb * 32 + (rr & 3) * 8 + (rr >> 2));
+            const uint32_t dw = buffer_load4(sr, (hi >> 1) * 4u, 0);
+            sdh[u] = (hi & 1) ? dw >> 16 : dw & 0xffffu;
+            if constexpr (Q41) {
+                const uint32_t mw = buffer_load4(mr, (hi >> 1) * 4u, 0);
+                smh[u] = (hi & 1) ? mw >> 16 : mw & 0xffffu;
+            }
+        }
+    } else if constexpr (Two) {
         const uint32_t lane_off2 = static_cast<uint32_t>(sub * nbi + kb2) * 16u;
 #pragma unroll
         for (int l = 0; l < 8; ++l) w2[l] = buffer_load16(wr, lane_off2, 4 * l * row_bytes);
@@ -1021,9 +1043,11 @@ __device__ __forceinline__ bool down_lean_unit(const FfnArgs &a, int uid, int &c
         b.x1 = buffer_load16(xr, static_cast<uint32_t>(kb) * 32u, 16);
         b.hx = buffer_load4(hr, static_cast<uint32_t>(kb) * 4u, 0);
         if constexpr (Two) {
-            b.y0 = buffer_load16(xr, static_cast<uint32_t>(kb2) * 32u, 0);
-            b.y1 = buffer_load16(xr, static_cast<uint32_t>(kb2) * 32u, 16);
-            b.hy = buffer_load4(hr, static_cast<uint32_t>(kb2) * 4u, 0);
+            // Spread: the block of this lane's chunks (16 + lane % 4); else block kl + 16.
+            const uint32_t b2 = static_cast<uint32_t>(Spread ? skb : kb2);
+            b.y0 = buffer_load16(xr, b2 * 32u, 0);
+            b.y1 = buffer_load16(xr, b2 * 32u, 16);
+            b.hy = buffer_load4(hr, b2 * 4u, 0);
         }
     };
     const int toks[kStreamTokens] = {tok.x, tok.y, tok.z, tok.w};
@@ -1048,7 +1072,23 @@ __device__ __forceinline__ bool down_lean_unit(const FfnArgs &a, int uid, int &c
                             dot_block(w2[l], cur.y0, cur.y1);
             }
             float v = rows8_down_exact<Q41>(w, d4p, m4p, cur.x0, cur.x1, cur.hx, has, lane);
-            if constexpr (Two) v = v + rows8_down_exact<Q41>(w2, d4p2, m4p2, cur.y0, cur.y1, cur.hy, has2, lane);
+            if constexpr (Spread) {
+                // ((n16 + n17) + (n18 + n19)) per row in its lane quad, then to
+                // the lane holding the row's first tree (row 4 lr + sub).
+                float sq[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    float n = down_chunk<Q41>(w2[u], sdh[u], smh[u], cur.y0, cur.y1, cur.hy, shas);
+                    n = n + lane_xor<1>(n);
+                    sq[u] = n + lane_xor<2>(n);
+                }
+                const int row = 4 * lr + sub, src = 4 * (row & 15);
+                const float a0 = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * src, __float_as_int(sq[0])));
+                const float a1 = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * src, __float_as_int(sq[1])));
+                v = v + ((row >> 4) ? a1 : a0);
+            } else if constexpr (Two) {
+                v = v + rows8_down_exact<Q41>(w2, d4p2, m4p2, cur.y0, cur.y1, cur.hy, has2, lane);
+            }
             if ((lane & 8) == 0) {
                 const size_t orow = static_cast<size_t>(toks[j]) * a.out_stride_k + rnks[j];
                 a.out[orow * H + row0 + 4 * lr + sub] = v;
@@ -1061,12 +1101,12 @@ __device__ __forceinline__ bool down_lean_unit(const FfnArgs &a, int uid, int &c
 
 // Units id, id + grid, ... over a capped grid (a multiple of 8 and of H/64,
 // as in k_gate_up_lean).
-template<int NBI, bool Q41, bool Two, bool Dbg>
-__global__ __launch_bounds__(128, Two ? 2 : 4) void k_down_lean(FfnArgs a) {
+template<int NBI, bool Q41, bool Two, bool Dbg, bool Spread = false>
+__global__ __launch_bounds__(128, Two ? (Spread ? 3 : 2) : 4) void k_down_lean(FfnArgs a) {
     const int S = a.shape.H / 64;
     int count = INT_MAX;
     for (int u = static_cast<int>(blockIdx.x); u / S < count; u += static_cast<int>(gridDim.x))
-        if (!down_lean_unit<NBI, Q41, Two, Dbg>(a, u, count)) break;
+        if (!down_lean_unit<NBI, Q41, Two, Dbg, Spread>(a, u, count)) break;
 }
 
 // ----------------------------------------------------- ungrouped decode ---
@@ -2105,11 +2145,14 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
         }
     } else if (nbi <= 32) {
         const unsigned g = lean_grid(stream_item_bound(a), static_cast<unsigned>(a.shape.H / 64));
+        const bool spread = nbi <= 20;
         if (q41) {
             if (dbg) k_down_lean<0, true, true, true><<<g, 128, 0, s>>>(a);
+            else if (spread) k_down_lean<0, true, true, false, true><<<g, 128, 0, s>>>(a);
             else k_down_lean<0, true, true, false><<<g, 128, 0, s>>>(a);
         } else {
             if (dbg) k_down_lean<0, false, true, true><<<g, 128, 0, s>>>(a);
+            else if (spread) k_down_lean<0, false, true, false, true><<<g, 128, 0, s>>>(a);
             else k_down_lean<0, false, true, false><<<g, 128, 0, s>>>(a);
         }
     } else if (q41) {
