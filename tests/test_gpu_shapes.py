@@ -120,3 +120,45 @@ def test_layer_shape_paths(H, I, path):
         scale = float(np.sqrt(np.mean(np.square(ref["y"].astype(np.float64)))))
         assert err_ <= 1e-5 * scale, (path, err_, scale)
     L.close()
+
+
+def test_reference_shape_grouped_layer_multi_tile_items():
+    """The reference model's shape (2560/640, Q4_0 downs) on a batch whose
+    groups span several 32-pair token tiles and several 128-pair items (600
+    tokens, 64 experts + shared, top-8, Zipf(1.1)), every group on the MFMA
+    path: the gate/up form whose reference lanes chain a second block and the
+    20-block down kernel that takes two slices per workgroup.  Sampled tokens
+    against the oracle (outputs within 1e-5 rms); every token's middle Q8 rows
+    equal to the streaming path's, whose order is the reference's, and every
+    output within 1e-5 rms of it; deterministic."""
+    H, I, E, K, N = 2560, 640, 64, 8, 600
+    bank = W.q4_bank(E, hidden=H, intermediate=I, seed=91)
+    shared = W.q4_bank(1, hidden=H, intermediate=I, seed=92)
+    x = W.activations(N, hidden=H, seed=93)
+    ids, w = W.routes_zipf(N, 1.1, experts=E, k=K, seed=94)
+    sizes = np.bincount(ids.reshape(-1), minlength=E)
+    assert sizes.max() > 128   # at least one group of several items
+    L = _layer_env(PATHS["mfma"], H, I, E, K, True, N, experts_q4=bank, shared_q4=shared)
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    yh = host(y)
+    assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
+    st = L.last_stats()
+    assert st["stream_items"] == 0 and st["mfma_items"] > E
+    sample = np.random.default_rng(95).choice(N, 12, replace=False)
+    mask = np.zeros(N, np.uint8)
+    mask[sample] = 1
+    ref = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, token_mask=mask)
+    ref_y = ref["y"][sample].astype(np.float64)
+    scale = float(np.sqrt(np.mean(np.square(ref_y))))
+    assert float(np.max(np.abs(yh[sample].astype(np.float64) - ref_y))) <= 1e-5 * scale
+    S = _layer_env(PATHS["stream"], H, I, E, K, True, N, experts_q4=bank, shared_q4=shared)
+    ys, es = S.forward(dev(x), dev(ids), dev(w))
+    ysh = host(ys)
+    assert int(host(es)[0]) == 0 and S.last_stats()["mfma_items"] == 0
+    assert np.array_equal(host(S.debug_last(N)["middle_q8"]), host(L.debug_last(N)["middle_q8"]))
+    s_all = float(np.sqrt(np.mean(np.square(ysh.astype(np.float64)))))
+    assert float(np.max(np.abs(yh.astype(np.float64) - ysh))) <= 1e-5 * s_all
+    S.close()
+    y2, _ = L.forward(dev(x), dev(ids), dev(w))
+    assert np.array_equal(host(y2), yh)
+    L.close()
