@@ -186,7 +186,8 @@ hipError_t launch_down_mfma(const FfnArgs &a, hipStream_t s);
 struct LinearMfmaArgs {
     const uint8_t *codes;     // [Mp][nb][16 B]
     const uint16_t *scales;   // [Mp/8][nb][8]
-    Act xq;                   // [N][nb]
+    Act xq;                   // [N][nb] planes, read when q8 is null
+    const uint8_t *q8;        // canonical Q8_1 columns [N][nb][36 B] {d, s, qs[32]}, or null
     float *y;                 // [N][M]
     int nb, M, N;
     int row_tiles;            // Mp / 32

@@ -23,10 +23,11 @@
 // [rows/8][blocks][8], rows padded to a multiple of 32 with zero blocks, so a
 // lane's 8 row codes are eight 16-byte loads and its 8 scales one more.
 //
-// Wide batches (Q4_0, within the handle's workspace, at least 32 columns and
-// kMfmaMinOutputs outputs) go to int8 MFMA instead (k_linear_mfma in
-// moe_mfma.hip): the same fp32 order, with the per-fragment integer dots from
-// v_mfma_i32_32x32x16_i8.
+// Wide batches (Q4_0, at least 32 columns and kMfmaMinOutputs outputs) go to
+// int8 MFMA instead (k_linear_mfma in moe_mfma.hip): the same fp32 order, with
+// the per-fragment integer dots from v_mfma_i32_32x32x16_i8.  forward_q8's
+// MFMA launch reads the caller's canonical blocks in place (any column
+// count); apply quantizes into split planes in the handle's workspace.
 //
 // Work: one wave per (8 rows, column tile).  The wave loads its 8 rows'
 // blocks once per 4 columns (2 when a row has more than 64 blocks) and keeps
@@ -199,8 +200,8 @@ struct moe_linear {
     uint8_t *planes = nullptr;   // codes | scales | mins (one allocation)
     uint8_t *codes = nullptr;
     uint16_t *scales = nullptr, *mins = nullptr;
-    // Activation workspace, max_columns x nb x 36 B: canonical Q8_1 blocks
-    // (apply, narrow batches) or split planes (wide batches on MFMA).
+    // apply's activation workspace, max_columns x nb x 36 B: canonical Q8_1
+    // blocks (narrow batches) or split planes (wide batches on MFMA).
     void *q8 = nullptr;
 };
 
@@ -317,11 +318,13 @@ moe::Act staging_planes(const moe_linear *L, void *base_ptr, int columns) {
 }
 moe::Act workspace_planes(const moe_linear *L, int columns) { return staging_planes(L, L->q8, columns); }
 
-int launch_mfma(const moe_linear *L, moe::Act xq, int columns, float *y, hipStream_t s) {
+// x_q8: canonical Q8_1 columns read in place, else the split planes xq.
+int launch_mfma(const moe_linear *L, moe::Act xq, const void *x_q8, int columns, float *y, hipStream_t s) {
     moe::LinearMfmaArgs a{};
     a.codes = L->codes;
     a.scales = L->scales;
     a.xq = xq;
+    a.q8 = static_cast<const uint8_t *>(x_q8);
     a.y = y;
     a.nb = L->nb;
     a.M = L->output;
@@ -372,12 +375,9 @@ int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, 
 int moe_linear_forward_q8(moe_linear *L, const void *x_q8, int columns, float *y, void *stream) {
     if (!L || !aligned(x_q8, 4) || !aligned(y, 4) || columns < 1 || columns > 65536) return kInvalid;
     const auto s = static_cast<hipStream_t>(stream);
-    if (use_mfma(L, columns)) {
-        const moe::Act xq = workspace_planes(L, columns);
-        const hipError_t r = moe::launch_canonical_to_planes(x_q8, xq, columns * L->nb, s);
-        if (r != hipSuccess) return r;
-        return launch_mfma(L, xq, columns, y, s);
-    }
+    // The MFMA kernel reads the canonical blocks in place: no staging, so
+    // any column count qualifies.
+    if (use_mfma_within(L, columns, 65536)) return launch_mfma(L, moe::Act{}, x_q8, columns, y, s);
     return launch_vector(L, x_q8, columns, y, s);
 }
 
@@ -389,7 +389,7 @@ int moe_linear_apply(moe_linear *L, const float *x, int columns, float *y, int *
         const moe::Act xq = workspace_planes(L, columns);
         const hipError_t r = moe::launch_quantize_planes(x, xq, L->input, columns, error, s);
         if (r != hipSuccess) return r;
-        return launch_mfma(L, xq, columns, y, s);
+        return launch_mfma(L, xq, nullptr, columns, y, s);
     }
     const hipError_t r = moe::launch_quantize_canonical(x, L->q8, L->input, columns, error, s);
     if (r != hipSuccess) return r;
@@ -416,7 +416,7 @@ int moe_linear_apply_noalloc(moe_linear *L, const float *x, int columns, float *
         const moe::Act xq = staging_planes(L, ws, columns);
         const hipError_t r = moe::launch_quantize_planes(x, xq, L->input, columns, error, s);
         if (r != hipSuccess) return r;
-        return launch_mfma(L, xq, columns, y, s);
+        return launch_mfma(L, xq, nullptr, columns, y, s);
     }
     const hipError_t r = moe::launch_quantize_canonical(x, ws, L->input, columns, error, s);
     if (r != hipSuccess) return r;

@@ -355,26 +355,32 @@ __device__ __forceinline__ void fragment_scale(float (&acc)[16], v16i I, float d
 
 struct GuTile {
     __amdgpu_buffer_rsrc_t wr, sr, xr, hr;
-    uint32_t w_off, s_off0, s_off1, x_off, h_off;
+    uint32_t w_off, s_off0, s_off1, x_off, h_off;   // token block b at x_off + b XStride / h_off + b HStride
     int nb, shift;
     int32_t *dots;     // debug: [pair][I][nb] or null
     size_t dot_base;   // dots index of (pair of this lane, row R0 + 16h, block 0)
     bool dot_ok;
 };
 
+// Per-block steps of a token's codes and head: split planes (32 / 4 bytes),
+// or canonical 36-byte Q8_1 blocks read in place (Canon).
+template<bool Canon> constexpr uint32_t XStride = Canon ? 36u : 32u;
+template<bool Canon> constexpr uint32_t HStride = Canon ? 36u : 4u;
+
 struct BlockLoads {
     uint4 w, d0, d1, x;
     uint32_t hd;
 };
 
+template<bool Canon = false>
 __device__ __forceinline__ BlockLoads block_loads(const GuTile &t, int b) {
     const uint32_t ub = static_cast<uint32_t>(b);
     BlockLoads l;
     l.w = buffer_load16(t.wr, t.w_off, ub * 16u);
     l.d0 = buffer_load16(t.sr, t.s_off0, ub * 16u);
     l.d1 = buffer_load16(t.sr, t.s_off1, ub * 16u);
-    l.x = buffer_load16(t.xr, t.x_off, ub * 32u);
-    l.hd = buffer_load4(t.hr, t.h_off, ub * 4u);
+    l.x = buffer_load16(t.xr, t.x_off, ub * XStride<Canon>);
+    l.hd = buffer_load4(t.hr, t.h_off, ub * HStride<Canon>);
     return l;
 }
 
@@ -410,9 +416,10 @@ struct Blk {
     uint4 w, x;           // code chunk of the lane's A row, Q8 codes of its token (16 bytes each)
 };
 
+template<bool Canon = false>
 __device__ __forceinline__ Blk blk_load(const GuTile &t, int b) {
     const uint32_t ub = static_cast<uint32_t>(b);
-    return Blk{buffer_load16(t.wr, t.w_off, ub * 16u), buffer_load16(t.xr, t.x_off, ub * 32u)};
+    return Blk{buffer_load16(t.wr, t.w_off, ub * 16u), buffer_load16(t.xr, t.x_off, ub * XStride<Canon>)};
 }
 
 // Fragment F's dots of one block with v_mfma_i32_32x32x16_i8 (K = 16 = one
@@ -438,14 +445,14 @@ __device__ __forceinline__ float frag_value(int I, float d8, float c4, const uin
 // acc[2j+f] the fragment-f value of block j (+0 past nb).  Full: nb == 64.
 // Blocks k' and k'+32 are loaded here; the fragment-0 pair is finished before
 // the fragment-1 MFMAs so only two MFMA results are live.
-template<bool Full, bool Dbg>
+template<bool Full, bool Dbg, bool Canon = false>
 __device__ __forceinline__ void leaf_staged(const GuTile &t, const GuStage &g, int kp, int m, int h, float (&v)[16]) {
     const int jb = kp + 32;
     const bool has_a = Full || kp < t.nb, has_b = Full || jb < t.nb;   // uniform
     const int ja = has_a ? kp : 0, jc = has_b ? jb : 0;
-    const Blk ka = blk_load(t, ja), kb = blk_load(t, jc);
-    const uint32_t ha = buffer_load4(t.hr, t.h_off, static_cast<uint32_t>(ja) * 4u);
-    const uint32_t hb = buffer_load4(t.hr, t.h_off, static_cast<uint32_t>(jc) * 4u);
+    const Blk ka = blk_load<Canon>(t, ja), kb = blk_load<Canon>(t, jc);
+    const uint32_t ha = buffer_load4(t.hr, t.h_off, static_cast<uint32_t>(ja) * HStride<Canon>);
+    const uint32_t hb = buffer_load4(t.hr, t.h_off, static_cast<uint32_t>(jc) * HStride<Canon>);
     const uint4 *da4 = reinterpret_cast<const uint4 *>(g.d4 + ja * 16 + 8 * h);
     const uint4 *db4 = reinterpret_cast<const uint4 *>(g.d4 + jc * 16 + 8 * h);
     const uint4 a0 = da4[0], a1 = da4[1], b0 = db4[0], b1 = db4[1];
@@ -559,16 +566,23 @@ __device__ __forceinline__ void half_load_w(const GuTile &t, uint32_t w_off, int
 #pragma unroll
     for (int i = 0; i < 2; ++i) w[i] = buffer_load16(t.wr, w_off, (b0 + i) * 16u);
 }
+template<bool Canon = false>
 __device__ __forceinline__ void half_load_x(const GuTile &t, int p, HalfGroup &G) {
+    constexpr uint32_t xs = XStride<Canon>, hs = HStride<Canon>;
     const uint32_t b0 = static_cast<uint32_t>(4 * (p >> 1) + 2 * (p & 1));
 #pragma unroll
-    for (int i = 0; i < 2; ++i) G.xa[i] = buffer_load16(t.xr, t.x_off, (b0 + i) * 32u);
+    for (int i = 0; i < 2; ++i) G.xa[i] = buffer_load16(t.xr, t.x_off, (b0 + i) * xs);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) G.xb[i] = buffer_load16(t.xr, t.x_off, (b0 + 32 + i) * 32u);
-    const auto a = __builtin_amdgcn_raw_buffer_load_b64(t.hr, t.h_off, b0 * 4u, 0);
-    const auto b = __builtin_amdgcn_raw_buffer_load_b64(t.hr, t.h_off, (b0 + 32) * 4u, 0);
-    G.ha = make_uint2(a[0], a[1]);
-    G.hb = make_uint2(b[0], b[1]);
+    for (int i = 0; i < 2; ++i) G.xb[i] = buffer_load16(t.xr, t.x_off, (b0 + 32 + i) * xs);
+    if constexpr (Canon) {
+        G.ha = make_uint2(buffer_load4(t.hr, t.h_off, b0 * hs), buffer_load4(t.hr, t.h_off, (b0 + 1) * hs));
+        G.hb = make_uint2(buffer_load4(t.hr, t.h_off, (b0 + 32) * hs), buffer_load4(t.hr, t.h_off, (b0 + 33) * hs));
+    } else {   // head plane: the two heads are adjacent
+        const auto a = __builtin_amdgcn_raw_buffer_load_b64(t.hr, t.h_off, b0 * hs, 0);
+        const auto b = __builtin_amdgcn_raw_buffer_load_b64(t.hr, t.h_off, (b0 + 32) * hs, 0);
+        G.ha = make_uint2(a[0], a[1]);
+        G.hb = make_uint2(b[0], b[1]);
+    }
 }
 
 __device__ __forceinline__ v16i frag_mfma2(uint32_t a0, uint32_t a1, uint32_t x0, uint32_t x1) {
@@ -588,13 +602,14 @@ struct ExtraBlk {
     uint32_t hd[2];
 };
 
+template<bool Canon = false>
 __device__ __forceinline__ void extra_load(const GuTile &t, int p, ExtraBlk &E) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const uint32_t e = static_cast<uint32_t>(std::min(64 + 2 * p + i, t.nb - 1));   // past nb: unused
         E.w[i] = buffer_load16(t.wr, t.w_off, e * 16u);
-        E.x[i] = buffer_load16(t.xr, t.x_off, e * 32u);
-        E.hd[i] = buffer_load4(t.hr, t.h_off, e * 4u);
+        E.x[i] = buffer_load16(t.xr, t.x_off, e * XStride<Canon>);
+        E.hd[i] = buffer_load4(t.hr, t.h_off, e * HStride<Canon>);
     }
 }
 
@@ -794,24 +809,24 @@ __device__ __forceinline__ void chain_block(const GuTile &t, const BlockLoads &l
 // reference lane array's acc[2j + f]), walked as one sequence -- kp's chain,
 // then kp + 32's -- with
 // each block's loads issued before the previous block is scaled.
-template<bool Dbg>
+template<bool Dbg, bool Canon = false>
 __device__ __forceinline__ void fold_leaf_multi(const GuTile &t, int kp, float (&v)[16]) {
     float a0[16], a1[16], b0[16], b1[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) { a0[i] = 0.0f; a1[i] = 0.0f; b0[i] = 0.0f; b1[i] = 0.0f; }
     // nb > 64 here, so kp + 32 < nb and both chains hold a block.
     const int na = (t.nb - kp + 63) / 64, nc = (t.nb - kp - 32 + 63) / 64;
-    BlockLoads cur = block_loads(t, kp);
+    BlockLoads cur = block_loads<Canon>(t, kp);
 #pragma unroll 1
     for (int s = 0; s < na; ++s) {   // uniform
-        const BlockLoads nxt = block_loads(t, s + 1 < na ? kp + 64 * (s + 1) : kp + 32);
+        const BlockLoads nxt = block_loads<Canon>(t, s + 1 < na ? kp + 64 * (s + 1) : kp + 32);
         chain_block<Dbg>(t, cur, kp + 64 * s, a0, a1);
         cur = nxt;
     }
 #pragma unroll 1
     for (int s = 0; s < nc; ++s) {   // uniform
         BlockLoads nxt = cur;
-        if (s + 1 < nc) nxt = block_loads(t, kp + 32 + 64 * (s + 1));
+        if (s + 1 < nc) nxt = block_loads<Canon>(t, kp + 32 + 64 * (s + 1));
         chain_block<Dbg>(t, cur, kp + 32 + 64 * s, b0, b1);
         cur = nxt;
     }
@@ -1659,7 +1674,7 @@ __device__ __forceinline__ void subtree4_merge(int q, float (&w)[16], float (&l1
 }
 
 // wn: the wave's first node's weight half, already in flight (grouped folds).
-template<int Fold>
+template<int Fold, bool Canon>
 __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint32_t w_off, int wave, int lane,
                                          uint4 (&wn)[2], float (&res)[16]) {
     const int m = lane & 31, h = lane >> 5;
@@ -1673,10 +1688,10 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
             HalfGroup G;
             G.w[0] = wn[0];
             G.w[1] = wn[1];
-            half_load_x(t, p, G);
+            half_load_x<Canon>(t, p, G);
             ExtraBlk E;
             if constexpr (X) {
-                if (2 * p < t.nb - 64) extra_load(t, p, E);   // uniform
+                if (2 * p < t.nb - 64) extra_load<Canon>(t, p, E);   // uniform
             }
             half_load_w(t, w_off, q < 3 ? p + 1 : p, wn);
             float w[16], x[16];
@@ -1692,11 +1707,11 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
             const int p = 4 * wave + q;
             float w[16], x[16];
             if constexpr (Fold == kFoldStaged) {
-                leaf_staged<false, false>(t, g, 2 * p, m, h, w);
-                leaf_staged<false, false>(t, g, 2 * p + 1, m, h, x);
+                leaf_staged<false, false, Canon>(t, g, 2 * p, m, h, w);
+                leaf_staged<false, false, Canon>(t, g, 2 * p + 1, m, h, x);
             } else {
-                fold_leaf_multi<false>(t, 2 * p, w);
-                fold_leaf_multi<false>(t, 2 * p + 1, x);
+                fold_leaf_multi<false, Canon>(t, 2 * p, w);
+                fold_leaf_multi<false, Canon>(t, 2 * p + 1, x);
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
@@ -1705,7 +1720,9 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
     }
 }
 
-template<int Fold>
+// Canon: the columns are canonical Q8_1 blocks, read in place (codes at
+// byte 4 of each 36-byte block, the head at byte 0); else the split planes.
+template<int Fold, bool Canon>
 __global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
     __shared__ float roots[4][16][64];          // subtree roots [wave][value][lane]
     __shared__ uint4 d4_lds[Fold == kFoldGrouped96 ? kGu96MaxBlocks : kGuMaxBlocks][4];   // [block][32 halfs]
@@ -1722,13 +1739,20 @@ __global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
     GuTile t;
     t.wr = buffer_rsrc(a.codes + static_cast<size_t>(R0) * row_bytes, 32u * row_bytes);
     t.sr = buffer_rsrc(a.scales + static_cast<size_t>(R0) * nb, 32u * static_cast<uint32_t>(nb) * 2u);
-    t.xr = buffer_rsrc(a.xq.codes, static_cast<uint32_t>(a.N) * static_cast<uint32_t>(nb) * 32u);
-    t.hr = buffer_rsrc(a.xq.heads, static_cast<uint32_t>(a.N) * static_cast<uint32_t>(nb) * 4u);
+    if constexpr (Canon) {
+        t.xr = buffer_rsrc(a.q8, static_cast<uint32_t>(a.N) * static_cast<uint32_t>(nb) * 36u);
+        t.hr = t.xr;
+        t.x_off = col * static_cast<uint32_t>(nb) * 36u + 4u + 16u * h;
+        t.h_off = col * static_cast<uint32_t>(nb) * 36u;
+    } else {
+        t.xr = buffer_rsrc(a.xq.codes, static_cast<uint32_t>(a.N) * static_cast<uint32_t>(nb) * 32u);
+        t.hr = buffer_rsrc(a.xq.heads, static_cast<uint32_t>(a.N) * static_cast<uint32_t>(nb) * 4u);
+        t.x_off = col * static_cast<uint32_t>(nb) * 32u + 16u * h;
+        t.h_off = col * static_cast<uint32_t>(nb) * 4u;
+    }
     t.w_off = static_cast<uint32_t>(prow) * row_bytes;
     t.s_off0 = static_cast<uint32_t>(2 * h * nb) * 16u;
     t.s_off1 = t.s_off0 + static_cast<uint32_t>(nb) * 16u;
-    t.x_off = col * static_cast<uint32_t>(nb) * 32u + 16u * h;
-    t.h_off = col * static_cast<uint32_t>(nb) * 4u;
     t.nb = nb;
     t.shift = 4 * h;
     t.dots = nullptr;
@@ -1749,7 +1773,7 @@ __global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
     }
     const GuStage g{reinterpret_cast<const uint32_t *>(&d4_lds[0][0]), nullptr};
     float res[16];
-    subtree4<Fold>(t, g, w_off, wave, lane, wn, res);
+    subtree4<Fold, Canon>(t, g, w_off, wave, lane, wn, res);
 #pragma unroll
     for (int v = 0; v < 16; ++v) roots[wave][v][lane] = res[v];
     __syncthreads();
@@ -1775,12 +1799,20 @@ __global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
 
 }  // namespace
 
+namespace {
+template<bool Canon>
+void launch_linear_mfma_t(const LinearMfmaArgs &a, unsigned grid, hipStream_t s) {
+    if (a.nb == kGuMaxBlocks) k_linear_mfma<kFoldGrouped, Canon><<<grid, 256, 0, s>>>(a);
+    else if (a.nb > kGuMaxBlocks && a.nb <= kGu96MaxBlocks) k_linear_mfma<kFoldGrouped96, Canon><<<grid, 256, 0, s>>>(a);
+    else if (a.nb < kGuMaxBlocks) k_linear_mfma<kFoldStaged, Canon><<<grid, 256, 0, s>>>(a);
+    else k_linear_mfma<kFoldMulti, Canon><<<grid, 256, 0, s>>>(a);
+}
+}  // namespace
+
 hipError_t launch_linear_mfma(const LinearMfmaArgs &a, hipStream_t s) {
     const unsigned grid = static_cast<unsigned>((a.row_tiles + 7) / 8 * 8) * static_cast<unsigned>(a.col_tiles);
-    if (a.nb == kGuMaxBlocks) k_linear_mfma<kFoldGrouped><<<grid, 256, 0, s>>>(a);
-    else if (a.nb > kGuMaxBlocks && a.nb <= kGu96MaxBlocks) k_linear_mfma<kFoldGrouped96><<<grid, 256, 0, s>>>(a);
-    else if (a.nb < kGuMaxBlocks) k_linear_mfma<kFoldStaged><<<grid, 256, 0, s>>>(a);
-    else k_linear_mfma<kFoldMulti><<<grid, 256, 0, s>>>(a);
+    if (a.q8) launch_linear_mfma_t<true>(a, grid, s);
+    else launch_linear_mfma_t<false>(a, grid, s);
     return hipGetLastError();
 }
 

@@ -165,6 +165,19 @@ def test_linear_mfma_bit_exact_vs_oracle(K, M, N):
     L.close()
 
 
+@pytest.mark.parametrize("K,M,N", [(2048, 264, 200), (1024, 256, 77), (2560, 640, 64), (4096, 96, 40)])
+def test_linear_mfma_forward_q8_past_the_workspace(K, M, N):
+    """forward_q8's MFMA kernel reads the canonical Q8_1 blocks in place, so a
+    handle with a small workspace (max_columns 8) still takes wide batches
+    onto MFMA: the same bits as the oracle, for each fold form."""
+    w = q4_matrix(K + 3 * M + N, K, M)
+    _, xq = _columns(K, N, seed=K * 3 + N)
+    L = _linear_env(1, Q40, K, M, w, max_columns=8)
+    y = host(L.forward_q8(dev(q8_bytes(xq).reshape(N, -1)), N))
+    assert np.array_equal(bits(y), bits(O.matrix_gpu_order(w, K, M, xq))), (K, M, N)
+    L.close()
+
+
 def test_linear_apply_device_weights_and_flags():
     """apply(x) quantizes with the reference quantizer's bytes and then gives
     forward_q8's bits; a handle built from device-resident weights gives the
