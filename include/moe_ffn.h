@@ -303,7 +303,8 @@ int moe_linear_bytes(const moe_linear *linear, size_t *weight_bytes);
  * [columns][input/32] (36-byte blocks, 4-byte aligned).  Replaces
  * launch_quantized_linear / _short / _tiled (src/hip/linear.cuh:70-87,
  * src/hip/linear.hip:444-490) for Q4_0 / Q4_1, with the same fp32 order
- * (bit-identical outputs), columns 1..65536 in one launch.  Enqueue only. */
+ * (bit-identical outputs), columns 1..65536 in one launch.  x_q8 is read in
+ * place (no workspace), so calls on one handle may overlap.  Enqueue only. */
 int moe_linear_forward_q8(moe_linear *linear, const void *x_q8, int columns, float *y, void *stream);
 
 /* Matrix::apply for Q4 types (src/session.hip:561-591): fp32 x
