@@ -50,7 +50,7 @@
 namespace moe {
 namespace {
 
-constexpr int kLinearCols = 4;          // column-tile granularity (a multiple of every G below)
+constexpr int kLinearCols = 4;          // column-tile granularity of the Q4_1 two-slot form (G = 2)
 constexpr int kLinearWaveTarget = 2048; // waves a launch aims for (8 XCDs x 32 CUs x 8)
 
 struct LinearArgs {
@@ -196,6 +196,7 @@ uint8_t *noalloc_scratch(int device) {
 struct moe_linear {
     int type = 0, input = 0, output = 0, max_columns = 0, device = 0;
     int mfma_mode = -1;          // MOE_LINEAR_MFMA at creation: 0 never, 1 whenever eligible, -1 by size
+    int vector_g = 0;            // MOE_LINEAR_G at creation: columns per pass of k_linear (1, 2, 4), 0 by size
     int nb = 0, Mp = 0;
     uint8_t *planes = nullptr;   // codes | scales | mins (one allocation)
     uint8_t *codes = nullptr;
@@ -251,6 +252,10 @@ int moe_linear_create(int type, int input, int output, int max_columns, const vo
     L->device = device;
     L->nb = input / 32;
     if (const char *env = std::getenv("MOE_LINEAR_MFMA")) L->mfma_mode = std::atoi(env) ? 1 : 0;
+    if (const char *env = std::getenv("MOE_LINEAR_G")) {
+        const int g = std::atoi(env);
+        L->vector_g = g == 1 || g == 2 || g == 4 ? g : 0;
+    }
     L->Mp = static_cast<int>(round_up(static_cast<size_t>(output), 32));
     const size_t pblocks = static_cast<size_t>(L->Mp) * L->nb;
     const size_t code_bytes = round_up(pblocks * 16, 256), scale_bytes = round_up(pblocks * 2, 256);
@@ -346,26 +351,50 @@ int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, 
     a.M = L->output;
     a.N = columns;
     a.slices = (L->output + 7) / 8;
-    // Column tiles: enough waves to cover the chip (kLinearWaveTarget), each
-    // tile a whole number of accumulation groups.
-    const int groups = (columns + moe::kLinearCols - 1) / moe::kLinearCols;
-    int tiles = std::max(1, std::min(groups, (moe::kLinearWaveTarget + a.slices - 1) / a.slices));
+    const bool q41 = L->type == MOE_TYPE_Q4_1, hold2 = L->nb > 64;
+    // Columns per pass over the held weights (G) and the wave target.  G = 4
+    // shares each weight load among the most columns but needs 219 VGPRs
+    // (2 waves per SIMD); G = 2 (141 VGPRs, 3 waves) and G = 1 (68, 7 waves)
+    // read the weights again from L2 per pass and give matrices with few
+    // 8-row slices enough waves.  The largest G whose launch still has about
+    // 2048 waves wins (MI355X, cold weights, us at G = 4 / 2 / 1: 8192 x 8192
+    // at N = 8 20.1 / 21.8 / 25.1, N = 4 15.8 / 13.6 / 15.5, N = 2 11.9 /
+    // 11.9 / 10.3; 2560 x 640 at N = 8 5.96 / 4.43 / 3.96; 2048 x 512 at
+    // N = 16 4.21 / 3.33 / 3.08).  One column: G = 4 (9.6 against 11.1 us
+    // at G = 1).  Q4_1 rows of more than 64 blocks keep the two-slot form.
+    int G = hold2 && q41 ? 2 : L->vector_g;
+    if (G == 0) {
+        const long s8 = a.slices;
+        G = columns == 1 || s8 * ((columns + 3) / 4) >= moe::kLinearWaveTarget       ? 4
+            : s8 * ((columns + 1) / 2) >= moe::kLinearWaveTarget                       ? 2
+                                                                                        : 1;
+    }
+    const int gran = hold2 && q41 ? moe::kLinearCols : G;
+    const int target = G == 4 || (hold2 && q41) ? moe::kLinearWaveTarget : G == 2 ? 2 * moe::kLinearWaveTarget
+                                                                                  : 4 * moe::kLinearWaveTarget;
+    // Column tiles: enough waves to cover the chip, each tile a whole number
+    // of passes.
+    const int groups = (columns + gran - 1) / gran;
+    int tiles = std::max(1, std::min(groups, (target + a.slices - 1) / a.slices));
     const int per = (groups + tiles - 1) / tiles;
-    a.tile_cols = per * moe::kLinearCols;
+    a.tile_cols = per * gran;
     a.tiles = (columns + a.tile_cols - 1) / a.tile_cols;
     const size_t grid = round_up(static_cast<size_t>(a.slices), 8) * a.tiles;
     if (grid > 0x7fffffffu) return kInvalid;
-    const bool q41 = L->type == MOE_TYPE_Q4_1, hold2 = L->nb > 64;
     const dim3 g(static_cast<unsigned>(grid)), b(64);
     if (q41) {
         if (hold2) moe::k_linear<true, 2, 2><<<g, b, 0, s>>>(a);
-        else moe::k_linear<true, 1, 4><<<g, b, 0, s>>>(a);
+        else if (G == 4) moe::k_linear<true, 1, 4><<<g, b, 0, s>>>(a);
+        else if (G == 2) moe::k_linear<true, 1, 2><<<g, b, 0, s>>>(a);
+        else moe::k_linear<true, 1, 1><<<g, b, 0, s>>>(a);
     } else {
-        // Q4_0 takes one block slot per load round for every row length and
-        // keeps its weights for 4 columns: 8192 x 8192 at N = 1 / 8 / 16,
-        // 11.2 / 22.9 / 39.1 us with two slots and 2 columns per round
-        // against 9.8 / 19.8 / 33.6 us (MI355X, cold weights).
-        moe::k_linear<false, 1, 4><<<g, b, 0, s>>>(a);
+        // Q4_0 takes one block slot per load round for every row length:
+        // 8192 x 8192 at N = 1 / 8 / 16, 11.2 / 22.9 / 39.1 us with two slots
+        // and 2 columns per round against 9.8 / 19.8 / 33.6 us at one slot and
+        // 4 columns (MI355X, cold weights).
+        if (G == 4) moe::k_linear<false, 1, 4><<<g, b, 0, s>>>(a);
+        else if (G == 2) moe::k_linear<false, 1, 2><<<g, b, 0, s>>>(a);
+        else moe::k_linear<false, 1, 1><<<g, b, 0, s>>>(a);
     }
     return hipGetLastError();
 }

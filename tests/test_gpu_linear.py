@@ -112,7 +112,7 @@ CASES = [
 
 @pytest.mark.parametrize("type_,K,M,N", CASES)
 def test_linear_bit_exact_vs_oracle(type_, K, M, N):
-    """Vector kernel (no workspace: every batch stays on k_linear)."""
+    """Vector kernel (every batch here is below the MFMA size threshold)."""
     w = _weights(type_, K, M, seed=K + M + N)
     x, xq = _columns(K, N, seed=K * 3 + N)
     L = moe_ffn.MoeLinear(type_, K, M, w)
@@ -134,17 +134,43 @@ MFMA_CASES = [
 ]
 
 
-def _linear_env(mode, *args, **kw):
-    """A linear handle created with MOE_LINEAR_MFMA = mode (read at creation)."""
-    old = os.environ.get("MOE_LINEAR_MFMA")
-    os.environ["MOE_LINEAR_MFMA"] = str(mode)
+def _linear_env(mode, *args, var="MOE_LINEAR_MFMA", **kw):
+    """A linear handle created with the environment variable `var` (read at
+    creation; MOE_LINEAR_MFMA by default) set to mode."""
+    old = os.environ.get(var)
+    os.environ[var] = str(mode)
     try:
         return moe_ffn.MoeLinear(*args, **kw)
     finally:
         if old is None:
-            del os.environ["MOE_LINEAR_MFMA"]
+            del os.environ[var]
         else:
-            os.environ["MOE_LINEAR_MFMA"] = old
+            os.environ[var] = old
+
+
+G_CASES = [
+    # type, K, M, N: the vector kernel with 1, 2 and 4 columns per pass
+    (Q40, 2560, 640, 8),      # 80 blocks, 80 row slices
+    (Q40, 8192, 64, 5),       # four slots per lane, a partial last pass
+    (Q40, 2080, 1000, 3),     # 65 blocks, rows not a multiple of 8
+    (Q41, 640, 2560, 6),      # the reference model's Q4_1 down
+    (Q41, 2560, 200, 9),
+    (Q41, 8192, 24, 7),       # two-slot form (G fixed at 2)
+]
+
+
+@pytest.mark.parametrize("G", [1, 2, 4])
+@pytest.mark.parametrize("type_,K,M,N", G_CASES)
+def test_linear_columns_per_pass_bit_exact(G, type_, K, M, N):
+    """Every column count per pass over the held weights (MOE_LINEAR_G, read
+    at creation; by default chosen from the launch's wave count) gives the
+    oracle's bits: each column's chain is the same whatever its pass."""
+    w = _weights(type_, K, M, seed=K + 5 * M + N)
+    _, xq = _columns(K, N, seed=K * 7 + N)
+    L = _linear_env(G, type_, K, M, w, var="MOE_LINEAR_G")
+    y = host(L.forward_q8(dev(q8_bytes(xq).reshape(N, -1)), N))
+    assert np.array_equal(bits(y), bits(_oracle(type_, w, K, M, xq))), (G, type_, K, M, N)
+    L.close()
 
 
 @pytest.mark.parametrize("K,M,N", MFMA_CASES)
