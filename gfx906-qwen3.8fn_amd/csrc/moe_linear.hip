@@ -351,7 +351,13 @@ int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, 
     a.M = L->output;
     a.N = columns;
     a.slices = (L->output + 7) / 8;
-    const bool q41 = L->type == MOE_TYPE_Q4_1, hold2 = L->nb > 64;
+    const bool q41 = L->type == MOE_TYPE_Q4_1;
+    // Q4_1 rows of more than 64 blocks take both slots per load round for a
+    // single column on fewer than 1024 slices (latency-bound: 2560 x 640 at
+    // N = 1 3.17 against 3.46 us with one slot); everything else one slot
+    // (2560 x 640 at N = 8 6.25 -> 3.89 us, 8192 x 8192 at N = 1 / 4 / 8
+    // 10.6 / 20.2 / 22.8 -> 9.9 / 14.7 / 20.8 us against two slots).
+    const bool hold2 = q41 && L->nb > 64 && columns == 1 && a.slices < 1024;
     // Columns per pass over the held weights (G) and the wave target.  G = 4
     // shares each weight load among the most columns but needs 219 VGPRs
     // (2 waves per SIMD); G = 2 (141 VGPRs, 3 waves) and G = 1 (68, 7 waves)
@@ -361,17 +367,17 @@ int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, 
     // at N = 8 20.1 / 21.8 / 25.1, N = 4 15.8 / 13.6 / 15.5, N = 2 11.9 /
     // 11.9 / 10.3; 2560 x 640 at N = 8 5.96 / 4.43 / 3.96; 2048 x 512 at
     // N = 16 4.21 / 3.33 / 3.08).  One column: G = 4 (9.6 against 11.1 us
-    // at G = 1).  Q4_1 rows of more than 64 blocks keep the two-slot form.
-    int G = hold2 && q41 ? 2 : L->vector_g;
+    // at G = 1).
+    int G = hold2 ? 2 : L->vector_g;
     if (G == 0) {
         const long s8 = a.slices;
         G = columns == 1 || s8 * ((columns + 3) / 4) >= moe::kLinearWaveTarget       ? 4
             : s8 * ((columns + 1) / 2) >= moe::kLinearWaveTarget                       ? 2
                                                                                         : 1;
     }
-    const int gran = hold2 && q41 ? moe::kLinearCols : G;
-    const int target = G == 4 || (hold2 && q41) ? moe::kLinearWaveTarget : G == 2 ? 2 * moe::kLinearWaveTarget
-                                                                                  : 4 * moe::kLinearWaveTarget;
+    const int gran = hold2 ? moe::kLinearCols : G;
+    const int target = G == 4 || hold2 ? moe::kLinearWaveTarget : G == 2 ? 2 * moe::kLinearWaveTarget
+                                                                         : 4 * moe::kLinearWaveTarget;
     // Column tiles: enough waves to cover the chip, each tile a whole number
     // of passes.
     const int groups = (columns + gran - 1) / gran;

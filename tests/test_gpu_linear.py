@@ -99,7 +99,9 @@ CASES = [
     (Q40, 4096, 264, 33),     # two full slots, several column groups
     (Q40, 16384, 64, 3),      # 512 blocks: eight slots per lane
     (Q41, 2560, 200, 9),
-    (Q41, 6144, 40, 2),       # three slots (odd count with two held)
+    (Q41, 6144, 40, 2),       # three slots, one per load round
+    (Q41, 6144, 40, 1),       # three slots, two held per round (odd count)
+    (Q41, 2560, 200, 1),      # 80 blocks, both slots held
     (Q40, 2048, 512, 128),    # the reference's tiled maximum
     (Q40, 1024, 256, 300),    # past it, one launch
     (Q40, 8192, 64, 8),       # 256 blocks: four slots per lane
@@ -155,7 +157,7 @@ G_CASES = [
     (Q40, 2080, 1000, 3),     # 65 blocks, rows not a multiple of 8
     (Q41, 640, 2560, 6),      # the reference model's Q4_1 down
     (Q41, 2560, 200, 9),
-    (Q41, 8192, 24, 7),       # two-slot form (G fixed at 2)
+    (Q41, 8192, 24, 7),       # four slots per lane
 ]
 
 
