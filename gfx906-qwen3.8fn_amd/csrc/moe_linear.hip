@@ -352,12 +352,15 @@ int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, 
     a.N = columns;
     a.slices = (L->output + 7) / 8;
     const bool q41 = L->type == MOE_TYPE_Q4_1;
-    // Q4_1 rows of more than 64 blocks take both slots per load round for a
-    // single column on fewer than 1024 slices (latency-bound: 2560 x 640 at
-    // N = 1 3.17 against 3.46 us with one slot); everything else one slot
-    // (2560 x 640 at N = 8 6.25 -> 3.89 us, 8192 x 8192 at N = 1 / 4 / 8
-    // 10.6 / 20.2 / 22.8 -> 9.9 / 14.7 / 20.8 us against two slots).
-    const bool hold2 = q41 && L->nb > 64 && columns == 1 && a.slices < 1024;
+    // A single column on rows of more than 64 blocks takes two slots per load
+    // round when that covers the row (65..128 blocks) or the matrix has
+    // fewer than 1024 slices (us, one slot -> two: Q4_0 2560 x 640 3.43 ->
+    // 3.16, 4096 x 1024 3.67 -> 3.34, 2560 x 8192 5.43 -> 5.11, 8192 x 2048
+    // 6.44 -> 5.97, but 8192 x 8192 9.77 -> 10.96; Q4_1 2560 x 640 3.46 ->
+    // 3.17).  Every other batch takes one slot (Q4_1 2560 x 640 at N = 8
+    // 6.25 -> 3.89 us, 8192 x 8192 at N = 4 / 8 20.2 / 22.8 -> 14.7 / 20.8 us
+    // against two slots).
+    const bool hold2 = L->nb > 64 && columns == 1 && (L->nb <= 128 || a.slices < 1024);
     // Columns per pass over the held weights (G) and the wave target.  G = 4
     // shares each weight load among the most columns but needs 219 VGPRs
     // (2 waves per SIMD); G = 2 (141 VGPRs, 3 waves) and G = 1 (68, 7 waves)
@@ -394,11 +397,12 @@ int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, 
         else if (G == 2) moe::k_linear<true, 1, 2><<<g, b, 0, s>>>(a);
         else moe::k_linear<true, 1, 1><<<g, b, 0, s>>>(a);
     } else {
-        // Q4_0 takes one block slot per load round for every row length:
-        // 8192 x 8192 at N = 1 / 8 / 16, 11.2 / 22.9 / 39.1 us with two slots
-        // and 2 columns per round against 9.8 / 19.8 / 33.6 us at one slot and
-        // 4 columns (MI355X, cold weights).
-        if (G == 4) moe::k_linear<false, 1, 4><<<g, b, 0, s>>>(a);
+        // Past one column Q4_0 takes one block slot per load round: 8192 x
+        // 8192 at N = 8 / 16, 22.9 / 39.1 us with two slots and 2 columns per
+        // round against 19.8 / 33.6 us at one slot and 4 columns (MI355X,
+        // cold weights).
+        if (hold2) moe::k_linear<false, 2, 2><<<g, b, 0, s>>>(a);
+        else if (G == 4) moe::k_linear<false, 1, 4><<<g, b, 0, s>>>(a);
         else if (G == 2) moe::k_linear<false, 1, 2><<<g, b, 0, s>>>(a);
         else moe::k_linear<false, 1, 1><<<g, b, 0, s>>>(a);
     }

@@ -94,6 +94,8 @@ CASES = [
     # type, K, M, N
     (Q40, 32, 1, 1),          # one block, one row (7 padding rows)
     (Q40, 2048, 2048, 1),     # decode projection, one block per lane
+    (Q40, 2080, 1000, 1),     # 65 blocks, one column: both slots per load round
+    (Q40, 6144, 40, 1),       # three slots, two held per round (odd count)
     (Q40, 2048, 13, 5),       # rows not a multiple of 8
     (Q40, 2080, 1000, 8),     # 65 blocks: lane 0 holds two
     (Q40, 4096, 264, 33),     # two full slots, several column groups
