@@ -305,6 +305,31 @@ __device__ __forceinline__ float fold_rows8(const float (&z)[8][2], int lane) {
     return xor_sum<16>(v);
 }
 
+// fold_rows8 for 4 rows: z[row][f] -> lane j + lane j ^ 32 per fragment (row
+// pairs i, i + 2), the two fragments, then XOR 1, 2, 4, 8, 16 -- per row the
+// same additions in the same order.  Lane l ends with row 2*(l>>5 & 1) +
+// (l & 1).
+__device__ __forceinline__ float fold_rows4(const float (&z)[4][2], int lane) {
+    const bool b0 = lane & 1;
+    float v2[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        float u[2];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(z[i][f]), __float_as_uint(z[i + 2][f]),
+                                                            false, false);
+            u[f] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+        v2[i] = u[0] + u[1];
+    }
+    float v = (b0 ? v2[1] : v2[0]) + lane_xor<1>(b0 ? v2[0] : v2[1]);
+    v = xor_sum<2>(v);
+    v = xor_sum<4>(v);
+    v = xor_sum<8>(v);
+    return xor_sum<16>(v);
+}
+
 // rows8_exact for rows of 65..128 blocks: lane j holds blocks j (w, d4p, x0,
 // x1, head) and j + 64 (w2, ..., present when has2).  The reference's lane
 // 2j + f accumulates its blocks in ascending order,

@@ -60,36 +60,42 @@ struct LinearArgs {
     const uint8_t *x;        // canonical Q8_1 [N][nb][36 B]
     float *y;                // [N][M]
     int nb, M, N;
-    int slices;              // Mp / 8
+    int slices;              // Mp / ROWS
     int tiles, tile_cols;    // column tiles per slice; columns per tile (multiple of kLinearCols)
 };
 
 // HOLD = block slots (64 blocks each) whose weights are loaded together;
-// G = columns accumulated per pass over the weights.
-template<bool Q41, int HOLD, int G>
-__global__ __launch_bounds__(64, 2) void k_linear(LinearArgs a) {
+// G = columns accumulated per pass over the weights; ROWS = rows per wave
+// (8, or 4: half an 8-row scale group, a.slices = Mp / 4).
+template<bool Q41, int HOLD, int G, int ROWS = 8>
+__global__ __launch_bounds__(64, ROWS == 4 ? (G == 4 ? 3 : 4) : 2) void k_linear(LinearArgs a) {
     const int lane = threadIdx.x;
     const int id = static_cast<int>(blockIdx.x), local = id >> 3;
     const int slice = (id & 7) + 8 * (local / a.tiles), tile = local % a.tiles;
     if (slice >= a.slices) return;   // uniform per workgroup (grid padded to 8 slices)
     const int c0 = tile * a.tile_cols, c1 = min(c0 + a.tile_cols, a.N);
     if (c0 >= c1) return;
-    const int nb = a.nb, row0 = slice * 8, slots = (nb + 63) / 64;
+    const int nb = a.nb, row0 = slice * ROWS, slots = (nb + 63) / 64;
     const uint32_t row_bytes = static_cast<uint32_t>(nb) * 16u;
-    const auto wr = buffer_rsrc(a.codes + static_cast<size_t>(row0) * row_bytes, 8 * row_bytes);
-    const auto sr = buffer_rsrc(a.scales + static_cast<size_t>(row0) * nb, row_bytes);
-    const auto mr = buffer_rsrc(Q41 ? a.mins + static_cast<size_t>(row0) * nb : a.scales, row_bytes);
+    const auto wr = buffer_rsrc(a.codes + static_cast<size_t>(row0) * row_bytes, ROWS * row_bytes);
+    // The slice's scale group (8 rows) and, for 4 rows, its half of each
+    // block's 8 scales.
+    const size_t g0 = static_cast<size_t>(row0 & ~7);
+    const uint32_t shalf = static_cast<uint32_t>(row0 & 4) * 2u;
+    const auto sr = buffer_rsrc(a.scales + g0 * nb, row_bytes);
+    const auto mr = buffer_rsrc(Q41 ? a.mins + g0 * nb : a.scales, row_bytes);
     const auto xr = buffer_rsrc(a.x, static_cast<uint32_t>(static_cast<size_t>(a.N) * nb * 36));
-    const int rho = 4 * ((lane >> 5) & 1) + 2 * (lane & 1) + ((lane >> 1) & 1);
+    const int rho = ROWS == 8 ? 4 * ((lane >> 5) & 1) + 2 * (lane & 1) + ((lane >> 1) & 1)
+                              : 2 * ((lane >> 5) & 1) + (lane & 1);
     for (int c = c0; c < c1; c += G) {   // uniform
-        float acc[G][8][2];
+        float acc[G][ROWS][2];
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int r = 0; r < 8; ++r) acc[g][r][0] = acc[g][r][1] = 0.0f;
+            for (int r = 0; r < ROWS; ++r) acc[g][r][0] = acc[g][r][1] = 0.0f;
         for (int i0 = 0; i0 < slots; i0 += HOLD) {   // uniform
-            uint4 w[HOLD][8];
-            float d4[HOLD][8], m4[HOLD][8];
+            uint4 w[HOLD][ROWS];
+            float d4[HOLD][ROWS], m4[HOLD][ROWS];
             bool has[HOLD];
             uint32_t kk[HOLD];
 #pragma unroll
@@ -100,14 +106,27 @@ __global__ __launch_bounds__(64, 2) void k_linear(LinearArgs a) {
                 has[h] = i0 + h < slots && k < nb;
                 kk[h] = has[h] ? static_cast<uint32_t>(k) : 0u;
 #pragma unroll
-                for (int r = 0; r < 8; ++r) w[h][r] = buffer_load16(wr, kk[h] * 16u, r * row_bytes);
-                const uint4 dp = buffer_load16(sr, kk[h] * 16u, 0);
+                for (int r = 0; r < ROWS; ++r) w[h][r] = buffer_load16(wr, kk[h] * 16u, r * row_bytes);
+                uint32_t dw[4], mw[4];
+                if constexpr (ROWS == 8) {
+                    const uint4 dp = buffer_load16(sr, kk[h] * 16u, 0);
+                    dw[0] = dp.x; dw[1] = dp.y; dw[2] = dp.z; dw[3] = dp.w;
+                } else {
+                    const auto dp = __builtin_amdgcn_raw_buffer_load_b64(sr, kk[h] * 16u + shalf, 0, 0);
+                    dw[0] = dp[0]; dw[1] = dp[1]; dw[2] = dw[3] = 0u;
+                }
 #pragma unroll
-                for (int r = 0; r < 8; ++r) d4[h][r] = h2f((&dp.x)[r >> 1] >> (16 * (r & 1)));
+                for (int r = 0; r < ROWS; ++r) d4[h][r] = h2f(dw[r >> 1] >> (16 * (r & 1)));
                 if constexpr (Q41) {
-                    const uint4 mp = buffer_load16(mr, kk[h] * 16u, 0);
+                    if constexpr (ROWS == 8) {
+                        const uint4 mp = buffer_load16(mr, kk[h] * 16u, 0);
+                        mw[0] = mp.x; mw[1] = mp.y; mw[2] = mp.z; mw[3] = mp.w;
+                    } else {
+                        const auto mp = __builtin_amdgcn_raw_buffer_load_b64(mr, kk[h] * 16u + shalf, 0, 0);
+                        mw[0] = mp[0]; mw[1] = mp[1]; mw[2] = mw[3] = 0u;
+                    }
 #pragma unroll
-                    for (int r = 0; r < 8; ++r) m4[h][r] = h2f((&mp.x)[r >> 1] >> (16 * (r & 1)));
+                    for (int r = 0; r < ROWS; ++r) m4[h][r] = h2f(mw[r >> 1] >> (16 * (r & 1)));
                 }
             }
 #pragma unroll
@@ -122,7 +141,7 @@ __global__ __launch_bounds__(64, 2) void k_linear(LinearArgs a) {
                     const uint4 x1 = buffer_load16(xr, xo + 20u, xs);
                     const float d8 = h2f(head), s8 = h2f(head >> 16), c4 = -4.0f * s8;
 #pragma unroll
-                    for (int r = 0; r < 8; ++r) {
+                    for (int r = 0; r < ROWS; ++r) {
                         int f[2];
                         fragment_dots(w[h][r], x0, x1, f[0], f[1]);
 #pragma unroll
@@ -143,9 +162,11 @@ __global__ __launch_bounds__(64, 2) void k_linear(LinearArgs a) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             if (c + g >= c1) break;   // uniform
-            const float v = fold_rows8(acc[g], lane);
+            float v;
+            if constexpr (ROWS == 8) v = fold_rows8(acc[g], lane);
+            else v = fold_rows4(acc[g], lane);
             const int row = row0 + rho;
-            if ((lane & 28) == 0 && row < a.M) a.y[static_cast<size_t>(c + g) * a.M + row] = v;
+            if ((lane & (ROWS == 8 ? 28 : 30)) == 0 && row < a.M) a.y[static_cast<size_t>(c + g) * a.M + row] = v;
         }
     }
 }
@@ -197,6 +218,7 @@ struct moe_linear {
     int type = 0, input = 0, output = 0, max_columns = 0, device = 0;
     int mfma_mode = -1;          // MOE_LINEAR_MFMA at creation: 0 never, 1 whenever eligible, -1 by size
     int vector_g = 0;            // MOE_LINEAR_G at creation: columns per pass of k_linear (1, 2, 4), 0 by size
+    int vector_rows = 0;         // MOE_LINEAR_ROWS at creation: rows per wave of k_linear (4, 8), 0 by size
     int nb = 0, Mp = 0;
     uint8_t *planes = nullptr;   // codes | scales | mins (one allocation)
     uint8_t *codes = nullptr;
@@ -255,6 +277,10 @@ int moe_linear_create(int type, int input, int output, int max_columns, const vo
     if (const char *env = std::getenv("MOE_LINEAR_G")) {
         const int g = std::atoi(env);
         L->vector_g = g == 1 || g == 2 || g == 4 ? g : 0;
+    }
+    if (const char *env = std::getenv("MOE_LINEAR_ROWS")) {
+        const int r = std::atoi(env);
+        L->vector_rows = r == 4 || r == 8 ? r : 0;
     }
     L->Mp = static_cast<int>(round_up(static_cast<size_t>(output), 32));
     const size_t pblocks = static_cast<size_t>(L->Mp) * L->nb;
@@ -339,6 +365,42 @@ int launch_mfma(const moe_linear *L, moe::Act xq, const void *x_q8, int columns,
     return moe::launch_linear_mfma(a, s);
 }
 
+// Column tiling of one vector launch over `slices` row slices: G columns per
+// pass over the held weights and `tile_cols` columns per wave.
+struct VectorPlan {
+    int G, tile_cols, tiles;
+};
+
+// G = 4 shares each weight load among the most columns but needs 219 VGPRs
+// (2 waves per SIMD at 8 rows); G = 2 (141 VGPRs, 3 waves) and G = 1 (68, 7
+// waves) read the weights again from L2 per pass and give matrices with few
+// slices enough waves.  The largest G whose launch still has about 2048 waves
+// wins (MI355X, cold weights, 8 rows, us at G = 4 / 2 / 1: 8192 x 8192 at N = 8
+// 20.1 / 21.8 / 25.1, N = 4 15.8 / 13.6 / 15.5, N = 2 11.9 / 11.9 / 10.3;
+// 2560 x 640 at N = 8 5.96 / 4.43 / 3.96; 2048 x 512 at N = 16 4.21 / 3.33 /
+// 3.08).  One column: G = 4 (9.6 against 11.1 us at G = 1).  hold2: the
+// two-slot form, G = 2 at a granularity of 4 columns.
+VectorPlan vector_plan(int slices, int columns, int forced_g, bool hold2) {
+    int G = hold2 ? 2 : forced_g;
+    if (G == 0) {
+        const long s = slices;
+        G = columns == 1 || s * ((columns + 3) / 4) >= moe::kLinearWaveTarget ? 4
+            : s * ((columns + 1) / 2) >= moe::kLinearWaveTarget               ? 2
+                                                                              : 1;
+    }
+    const int gran = hold2 ? moe::kLinearCols : G;
+    const int target = G == 4 || hold2 ? moe::kLinearWaveTarget
+                       : G == 2        ? 2 * moe::kLinearWaveTarget
+                                       : 4 * moe::kLinearWaveTarget;
+    // Column tiles: enough waves to cover the chip, each tile a whole number
+    // of passes.
+    const int groups = (columns + gran - 1) / gran;
+    const int tiles = std::max(1, std::min(groups, (target + slices - 1) / slices));
+    const int per = (groups + tiles - 1) / tiles;
+    const int tile_cols = per * gran;
+    return VectorPlan{G, tile_cols, (columns + tile_cols - 1) / tile_cols};
+}
+
 // The vector kernel on canonical Q8_1 columns x_q8.
 int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, hipStream_t s) {
     moe::LinearArgs a{};
@@ -350,8 +412,8 @@ int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, 
     a.nb = L->nb;
     a.M = L->output;
     a.N = columns;
-    a.slices = (L->output + 7) / 8;
     const bool q41 = L->type == MOE_TYPE_Q4_1;
+    const int slices8 = (L->output + 7) / 8;
     // A single column on rows of more than 64 blocks takes two slots per load
     // round when that covers the row (65..128 blocks) or the matrix has
     // fewer than 1024 slices (us, one slot -> two: Q4_0 2560 x 640 3.43 ->
@@ -360,39 +422,36 @@ int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, 
     // 3.17).  Every other batch takes one slot (Q4_1 2560 x 640 at N = 8
     // 6.25 -> 3.89 us, 8192 x 8192 at N = 4 / 8 20.2 / 22.8 -> 14.7 / 20.8 us
     // against two slots).
-    const bool hold2 = L->nb > 64 && columns == 1 && (L->nb <= 128 || a.slices < 1024);
-    // Columns per pass over the held weights (G) and the wave target.  G = 4
-    // shares each weight load among the most columns but needs 219 VGPRs
-    // (2 waves per SIMD); G = 2 (141 VGPRs, 3 waves) and G = 1 (68, 7 waves)
-    // read the weights again from L2 per pass and give matrices with few
-    // 8-row slices enough waves.  The largest G whose launch still has about
-    // 2048 waves wins (MI355X, cold weights, us at G = 4 / 2 / 1: 8192 x 8192
-    // at N = 8 20.1 / 21.8 / 25.1, N = 4 15.8 / 13.6 / 15.5, N = 2 11.9 /
-    // 11.9 / 10.3; 2560 x 640 at N = 8 5.96 / 4.43 / 3.96; 2048 x 512 at
-    // N = 16 4.21 / 3.33 / 3.08).  One column: G = 4 (9.6 against 11.1 us
-    // at G = 1).
-    int G = hold2 ? 2 : L->vector_g;
-    if (G == 0) {
-        const long s8 = a.slices;
-        G = columns == 1 || s8 * ((columns + 3) / 4) >= moe::kLinearWaveTarget       ? 4
-            : s8 * ((columns + 1) / 2) >= moe::kLinearWaveTarget                       ? 2
-                                                                                        : 1;
-    }
-    const int gran = hold2 ? moe::kLinearCols : G;
-    const int target = G == 4 || hold2 ? moe::kLinearWaveTarget : G == 2 ? 2 * moe::kLinearWaveTarget
-                                                                         : 4 * moe::kLinearWaveTarget;
-    // Column tiles: enough waves to cover the chip, each tile a whole number
-    // of passes.
-    const int groups = (columns + gran - 1) / gran;
-    int tiles = std::max(1, std::min(groups, (target + a.slices - 1) / a.slices));
-    const int per = (groups + tiles - 1) / tiles;
-    a.tile_cols = per * gran;
-    a.tiles = (columns + a.tile_cols - 1) / a.tile_cols;
+    const bool hold2 = L->nb > 64 && columns == 1 && (L->nb <= 128 || slices8 < 1024);
+    VectorPlan p = vector_plan(slices8, columns, L->vector_g, hold2);
+    // Rows per wave: 4 (130 / 81 / 56 VGPRs at G = 4 / 2 / 1: 3, 6 and 8
+    // waves per SIMD) where the 8-row launch leaves the chip short of waves
+    // or runs one column per pass on rows of at most 128 blocks; it reads
+    // each column's blocks twice as often.  us, 8 rows -> 4: 8192 x 8192 at
+    // N = 1 9.8 -> 8.8, 2048 x 2048 at N = 2 / 8 3.12 / 3.84 -> 2.83 / 3.66,
+    // 2560 x 640 at N = 8 / 31 3.96 / 5.71 -> 3.34 / 5.28, 2048 x 512 at
+    // N = 16 3.09 -> 2.85, Q4_1 640 x 2560 at N = 1 2.93 -> 2.69; but 8192 x
+    // 8192 at N = 2 / 8 10.3 / 19.2 -> 11.0 / 24.3 and 1024 x 8192 at N = 8
+    // 6.6 -> 7.5.
+    int rows = L->vector_rows;
+    if (rows == 0)
+        rows = !hold2 && (static_cast<long>(slices8) * p.tiles < moe::kLinearWaveTarget || (p.G == 1 && L->nb <= 128))
+                   ? 4
+                   : 8;
+    if (hold2) rows = 8;
+    a.slices = rows == 4 ? (L->output + 3) / 4 : slices8;
+    if (rows == 4) p = vector_plan(a.slices, columns, L->vector_g, false);
+    a.tile_cols = p.tile_cols;
+    a.tiles = p.tiles;
     const size_t grid = round_up(static_cast<size_t>(a.slices), 8) * a.tiles;
     if (grid > 0x7fffffffu) return kInvalid;
     const dim3 g(static_cast<unsigned>(grid)), b(64);
+    const int G = p.G;
     if (q41) {
         if (hold2) moe::k_linear<true, 2, 2><<<g, b, 0, s>>>(a);
+        else if (rows == 4 && G == 4) moe::k_linear<true, 1, 4, 4><<<g, b, 0, s>>>(a);
+        else if (rows == 4 && G == 2) moe::k_linear<true, 1, 2, 4><<<g, b, 0, s>>>(a);
+        else if (rows == 4) moe::k_linear<true, 1, 1, 4><<<g, b, 0, s>>>(a);
         else if (G == 4) moe::k_linear<true, 1, 4><<<g, b, 0, s>>>(a);
         else if (G == 2) moe::k_linear<true, 1, 2><<<g, b, 0, s>>>(a);
         else moe::k_linear<true, 1, 1><<<g, b, 0, s>>>(a);
@@ -402,6 +461,9 @@ int launch_vector(const moe_linear *L, const void *x_q8, int columns, float *y, 
         // round against 19.8 / 33.6 us at one slot and 4 columns (MI355X,
         // cold weights).
         if (hold2) moe::k_linear<false, 2, 2><<<g, b, 0, s>>>(a);
+        else if (rows == 4 && G == 4) moe::k_linear<false, 1, 4, 4><<<g, b, 0, s>>>(a);
+        else if (rows == 4 && G == 2) moe::k_linear<false, 1, 2, 4><<<g, b, 0, s>>>(a);
+        else if (rows == 4) moe::k_linear<false, 1, 1, 4><<<g, b, 0, s>>>(a);
         else if (G == 4) moe::k_linear<false, 1, 4><<<g, b, 0, s>>>(a);
         else if (G == 2) moe::k_linear<false, 1, 2><<<g, b, 0, s>>>(a);
         else moe::k_linear<false, 1, 1><<<g, b, 0, s>>>(a);

@@ -138,22 +138,29 @@ MFMA_CASES = [
 ]
 
 
-def _linear_env(mode, *args, var="MOE_LINEAR_MFMA", **kw):
-    """A linear handle created with the environment variable `var` (read at
-    creation; MOE_LINEAR_MFMA by default) set to mode."""
-    old = os.environ.get(var)
-    os.environ[var] = str(mode)
+def _linear_envs(env, *args, **kw):
+    """A linear handle created with the environment variables in `env` set
+    (the handle reads them at creation)."""
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
     try:
         return moe_ffn.MoeLinear(*args, **kw)
     finally:
-        if old is None:
-            del os.environ[var]
-        else:
-            os.environ[var] = old
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+def _linear_env(mode, *args, **kw):
+    """A linear handle created with MOE_LINEAR_MFMA = mode."""
+    return _linear_envs({"MOE_LINEAR_MFMA": mode}, *args, **kw)
 
 
 G_CASES = [
-    # type, K, M, N: the vector kernel with 1, 2 and 4 columns per pass
+    # type, K, M, N: the vector kernel with 1, 2 and 4 columns per pass and
+    # 4 or 8 rows per wave
     (Q40, 2560, 640, 8),      # 80 blocks, 80 row slices
     (Q40, 8192, 64, 5),       # four slots per lane, a partial last pass
     (Q40, 2080, 1000, 3),     # 65 blocks, rows not a multiple of 8
@@ -163,17 +170,20 @@ G_CASES = [
 ]
 
 
+@pytest.mark.parametrize("rows", [4, 8])
 @pytest.mark.parametrize("G", [1, 2, 4])
 @pytest.mark.parametrize("type_,K,M,N", G_CASES)
-def test_linear_columns_per_pass_bit_exact(G, type_, K, M, N):
-    """Every column count per pass over the held weights (MOE_LINEAR_G, read
-    at creation; by default chosen from the launch's wave count) gives the
-    oracle's bits: each column's chain is the same whatever its pass."""
+def test_linear_columns_per_pass_bit_exact(rows, G, type_, K, M, N):
+    """Every column count per pass over the held weights (MOE_LINEAR_G) and
+    row count per wave (MOE_LINEAR_ROWS; both read at creation, by default
+    chosen from the launch's wave count) gives the oracle's bits: each
+    column's chain is the same whatever its pass, and each row's fold the
+    same whatever rows share its wave."""
     w = _weights(type_, K, M, seed=K + 5 * M + N)
     _, xq = _columns(K, N, seed=K * 7 + N)
-    L = _linear_env(G, type_, K, M, w, var="MOE_LINEAR_G")
+    L = _linear_envs({"MOE_LINEAR_G": G, "MOE_LINEAR_ROWS": rows}, type_, K, M, w)
     y = host(L.forward_q8(dev(q8_bytes(xq).reshape(N, -1)), N))
-    assert np.array_equal(bits(y), bits(_oracle(type_, w, K, M, xq))), (G, type_, K, M, N)
+    assert np.array_equal(bits(y), bits(_oracle(type_, w, K, M, xq))), (rows, G, type_, K, M, N)
     L.close()
 
 
