@@ -253,3 +253,25 @@ def test_linear_rejects_bad_shapes():
     for args in ((Q40, 48, 8), (Q40, 64, 0), (7, 64, 8), (Q40, 64, 16385)):
         with pytest.raises(moe_ffn.MoeError):
             moe_ffn.MoeLinear(args[0], args[1], args[2], w)
+
+
+@pytest.mark.parametrize("type_,K,M", [(Q40, 2048, 256), (Q41, 640, 64)])
+def test_linear_maximum_columns(type_, K, M):
+    """65536 columns in one call, the entry point's limit: Q4_0 on the MFMA
+    kernel (canonical blocks read in place, 151 MB of them), Q4_1 on the
+    vector kernel.  256 distinct columns repeat across the batch; sampled
+    columns at both ends and inside are bit-identical to the oracle, and
+    65537 columns are rejected before any launch."""
+    N, base = 65536, 256
+    w = _weights(type_, K, M, seed=K + M)
+    _, xq = _columns(K, base, seed=K + 11)
+    xb = q8_bytes(xq).reshape(base, -1)
+    ref = _oracle(type_, w, K, M, xq).reshape(base, M)
+    L = moe_ffn.MoeLinear(type_, K, M, w)
+    x = dev(np.tile(xb, (N // base, 1)))
+    y = host(L.forward_q8(x, N))
+    for c in (0, 1, 255, 256, 31 * 1024 + 7, 40000, N - 2, N - 1):
+        assert np.array_equal(bits(y[c]), bits(ref[c % base])), (type_, c)
+    with pytest.raises((moe_ffn.MoeError, ValueError)):
+        L.forward_q8(dev(np.tile(xb, (N // base + 1, 1))[: N + 1]), N + 1)
+    L.close()
