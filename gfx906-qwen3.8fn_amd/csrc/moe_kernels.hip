@@ -867,41 +867,44 @@ __global__ __launch_bounds__(512, Two && !Spread ? 2 : 3) void k_gate_up_lean(Ff
         if (!gate_up_lean_unit<Full, Two, Dbg, Spread>(a, u, count, gu)) break;
 }
 
-// Down projection, streaming path.  Work unit = (item, slice of 64 output
-// rows); 8 waves x 8 rows.  With I/32 = 16 blocks a row is 256 code bytes, so
-// a wave load covers 4 rows (16 lanes per row).  Unweighted results go to the
-// contribution row (token * out_stride_k + rank) like the reference's scatter
-// (src/hip/session_ops.hip:357-373).  Q41: Q4_1 blocks, per block
-// dot * half(d4 d8) + half(m4 s8) (src/cpu_expert.cpp:167-194 summed over
-// the block's two fragments).
-template<int LPR, bool Q41, bool Dbg>
+// Down projection, streaming path, for rows of more than 32 blocks (I >
+// 1024).  Work unit = (item, slice of 32 output rows); 8 waves x 4 rows (8
+// rows a wave spilled: two accumulators per row and token).  A row spans the
+// wave: lane j holds blocks j, j + 64, ... and keeps one
+// accumulator per fragment over them in ascending order, as the reference's
+// lane 2 (k % 64) + f does (src/cpu_expert.cpp:156-213):
+//   Q4_0: acc = fma(d4, fma(float(I_f), d8, -4 s8), acc)
+//   Q4_1: acc = acc + fma(float(I_f), half(d4 d8), half(m4 s8) / 2)
+// then the reference's fold: lane j + lane j ^ 32 per fragment, the two
+// fragments, XOR 1 .. 16.  Unweighted results go to the contribution row
+// (token * out_stride_k + rank) like the reference's scatter
+// (src/hip/session_ops.hip:357-373).
+template<bool Q41, bool Dbg>
 __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
-    constexpr int T = kStreamTokens, RPL = 64 / LPR, LOADS = 8 / RPL;
+    constexpr int T = kStreamTokens, R = 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int H = a.shape.H, I = a.shape.I, nbi = I / 32, S = H / 64;
+    const int H = a.shape.H, I = a.shape.I, nbi = I / 32, S = H / 32;
     const int units = a.routes.item_counts[0] * S;
-    const int sub = lane / LPR, kb0 = lane % LPR;
     for (int u = blockIdx.x; u < units; u += gridDim.x) {
         const Item it = a.routes.stream_items[u / S];
-        const int row0 = (u % S) * 64 + wave * 8;
+        const int row0 = (u % S) * 32 + wave * R;
         const size_t mrow = static_cast<size_t>(it.expert) * H + row0;
         const uint8_t *codes = a.bank.down_codes + mrow * nbi * 16;
         const uint16_t *scales = a.bank.down_scales, *mins = a.bank.down_mins;
-        float acc[LOADS][T];
+        float acc[R][T][2];
 #pragma unroll
-        for (int l = 0; l < LOADS; ++l)
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int j = 0; j < T; ++j) acc[l][j] = 0.0f;
-        for (int kb = kb0; kb < nbi; kb += LPR) {
-            uint4 w[LOADS];
-            float d4[LOADS], m4[LOADS];
+            for (int j = 0; j < T; ++j) acc[r][j][0] = acc[r][j][1] = 0.0f;
+        for (int kb = lane; kb < nbi; kb += 64) {
+            uint4 w[R];
+            float d4[R], m4[R];
 #pragma unroll
-            for (int l = 0; l < LOADS; ++l) {
-                const int r = l * RPL + sub;
-                w[l] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbi + kb) * 16);
+            for (int r = 0; r < R; ++r) {
+                w[r] = *reinterpret_cast<const uint4 *>(codes + (static_cast<size_t>(r) * nbi + kb) * 16);
                 const size_t si = scale_index(mrow + r, kb, nbi, kScaleGroupDown);
-                d4[l] = h2f(scales[si]);
-                m4[l] = Q41 ? h2f(mins[si]) : 0.0f;
+                d4[r] = h2f(scales[si]);
+                m4[r] = Q41 ? h2f(mins[si]) : 0.0f;
             }
 #pragma unroll
             for (int j = 0; j < T; ++j) {
@@ -910,19 +913,23 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
                 const uint4 x0 = *reinterpret_cast<const uint4 *>(a.mq.codes + xb * 32);
                 const uint4 x1 = *reinterpret_cast<const uint4 *>(a.mq.codes + xb * 32 + 16);
                 const uint32_t hd = a.mq.heads[xb];
-                const float d8 = h2f(hd), s8 = h2f(hd >> 16), c8 = -8.0f * s8;
+                const float d8 = h2f(hd), s8 = h2f(hd >> 16), c4 = -4.0f * s8;
 #pragma unroll
-                for (int l = 0; l < LOADS; ++l) {
-                    const int dot = dot_block(w[l], x0, x1);
+                for (int r = 0; r < R; ++r) {
+                    int f[2];
+                    fragment_dots(w[r], x0, x1, f[0], f[1]);
                     if constexpr (Dbg) {
                         if (a.down_dots)
-                            a.down_dots[(static_cast<size_t>(it.first + j) * H + row0 + l * RPL + sub) * nbi + kb] = dot;
+                            a.down_dots[(static_cast<size_t>(it.first + j) * H + row0 + r) * nbi + kb] = f[0] + f[1];
                     }
-                    if constexpr (Q41) {
-                        const float dd = h2f(f2h(d4[l] * d8)), ms = h2f(f2h(m4[l] * s8));
-                        acc[l][j] = acc[l][j] + fmaf(static_cast<float>(dot), dd, ms);
-                    } else {
-                        acc[l][j] = fmaf(d4[l], fmaf(static_cast<float>(dot), d8, c8), acc[l][j]);
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        if constexpr (Q41) {
+                            const float dd = h2f(f2h(d4[r] * d8)), hm = h2f(f2h(m4[r] * s8)) * 0.5f;
+                            acc[r][j][q] = acc[r][j][q] + fmaf(static_cast<float>(f[q]), dd, hm);
+                        } else {
+                            acc[r][j][q] = fmaf(d4[r], fmaf(static_cast<float>(f[q]), d8, c4), acc[r][j][q]);
+                        }
                     }
                 }
             }
@@ -934,9 +941,15 @@ __global__ __launch_bounds__(512) void k_down_stream(FfnArgs a) {
             const size_t orow = static_cast<size_t>(a.routes.pair_token[pair]) * a.out_stride_k +
                                 a.routes.pair_rank[pair];
 #pragma unroll
-            for (int l = 0; l < LOADS; ++l) {
-                const float v = xor_sum_from<LPR / 2>(acc[l][j]);
-                if (kb0 == 0) a.out[orow * H + row0 + l * RPL + sub] = v;
+            for (int r = 0; r < R; ++r) {
+                const float v0 = xor_sum<32>(acc[r][j][0]), v1 = xor_sum<32>(acc[r][j][1]);
+                float v = v0 + v1;
+                v = xor_sum<1>(v);
+                v = xor_sum<2>(v);
+                v = xor_sum<4>(v);
+                v = xor_sum<8>(v);
+                v = xor_sum<16>(v);
+                if (lane == 0) a.out[orow * H + row0 + r] = v;
             }
         }
     }
@@ -2130,7 +2143,7 @@ hipError_t launch_decode_middle_grouped(Act mq, RouteOut routes, Shape shape, in
 hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
     if (mfma) return launch_down_mfma(a, s);   // Q4_0 and Q4_1 down rows
     const int nbi = a.shape.I / 32;
-    const unsigned grid = stream_grid(a, a.shape.H / 64);
+    const unsigned grid = stream_grid(a, a.shape.H / 32);   // k_down_stream's units: 32-row slices
     const bool dbg = a.down_dots != nullptr, q41 = a.bank.down_mins != nullptr;
     if (nbi <= 16) {
         const unsigned g = lean_grid(stream_item_bound(a), static_cast<unsigned>(a.shape.H / 64));
@@ -2156,11 +2169,11 @@ hipError_t launch_down(const FfnArgs &a, bool mfma, hipStream_t s) {
             else k_down_lean<0, false, true, false><<<g, 128, 0, s>>>(a);
         }
     } else if (q41) {
-        if (dbg) k_down_stream<64, true, true><<<grid, 512, 0, s>>>(a);
-        else k_down_stream<64, true, false><<<grid, 512, 0, s>>>(a);
+        if (dbg) k_down_stream<true, true><<<grid, 512, 0, s>>>(a);
+        else k_down_stream<true, false><<<grid, 512, 0, s>>>(a);
     } else {
-        if (dbg) k_down_stream<64, false, true><<<grid, 512, 0, s>>>(a);
-        else k_down_stream<64, false, false><<<grid, 512, 0, s>>>(a);
+        if (dbg) k_down_stream<false, true><<<grid, 512, 0, s>>>(a);
+        else k_down_stream<false, false><<<grid, 512, 0, s>>>(a);
     }
     return hipGetLastError();
 }

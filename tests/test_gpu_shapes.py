@@ -162,3 +162,59 @@ def test_reference_shape_grouped_layer_multi_tile_items():
     y2, _ = L.forward(dev(x), dev(ids), dev(w))
     assert np.array_equal(host(y2), yh)
     L.close()
+
+
+EXTREME_SHAPES = [
+    # H, I, down type: rows past every specialised form, and the smallest layer
+    (4160, 2080, moe_ffn.DOWN_Q4_0),   # 130 gate/up blocks (H > 4096: the streaming gate/up re-reads its rows per
+                                       # token, the MFMA gate/up chains blocks through per-block loads); 65 down
+                                       # blocks (the streaming down's 64-lane rows, the MFMA down's tile form)
+    (4160, 2080, moe_ffn.DOWN_Q4_1),
+    (1024, 1088, moe_ffn.DOWN_Q4_1),   # 34 down blocks with Q4_1 mins; the decode path stops at 32
+    (64, 32, moe_ffn.DOWN_Q4_0),       # 2 gate/up blocks and 1 down block a row
+]
+
+
+@pytest.mark.parametrize("H,I,down", EXTREME_SHAPES)
+@pytest.mark.parametrize("path", list(PATHS))
+def test_layer_extreme_shapes(H, I, down, path):
+    """Layers at shapes the benchmark never uses, on every path: each middle
+    Q8 row equals the oracle's cpu_expert middle byte for byte; outputs are
+    bit-identical on the decode and streaming paths (the reference's fp32
+    order for any row length) and within 1e-5 rms on the MFMA down."""
+    E, K, N = 8, 2, 24
+    q41 = down == moe_ffn.DOWN_Q4_1
+    if path == "decode" and (H > 4096 or I > 1024):
+        pytest.skip("the decode kernels cover H <= 4096 and I <= 1024")
+    bank = W.q4_bank(E, hidden=H, intermediate=I, seed=H + 3 * I, down_type=1 if q41 else 0)
+    shared = W.q4_bank(1, hidden=H, intermediate=I, seed=H + 3 * I + 1, down_type=1 if q41 else 0)
+    x = W.activations(N, hidden=H, seed=H + 5)
+    ids, w = W.routes_zipf(N, 1.0, experts=E, k=K, seed=I + 7)
+    L = _layer_env(PATHS[path], H, I, E, K, True, N, experts_q4=bank, shared_q4=shared, down_type=down)
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    yh = host(y)
+    assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
+    ref = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared, down_q41=q41)
+    dbg = L.debug_last(N)
+    assert np.array_equal(host(dbg["x_q8"]).reshape(-1), q8_bytes(ref["x_q8"]))
+    nbi = I // 32
+    mid = host(dbg["middle_q8"]).reshape(-1, nbi * 36)
+    groups = O.route_groups(ids, w, E)
+    P = int(groups["offsets"][-1])
+    eb = len(bank) // E
+    mb = (H // 32) * I * 18
+    xq = O.quantize_q8(x)
+    for p in range(P + N):
+        if p < P:
+            t, e_bytes = int(groups["token"][p]), bank[int(groups["expert"][p]) * eb:(int(groups["expert"][p]) + 1) * eb]
+        else:
+            t, e_bytes = p - P, shared
+        ro = O.expert_forward(e_bytes[:mb], e_bytes[mb:2 * mb], e_bytes[2 * mb:], H, I, xq[t:t + 1], down_q41=q41)
+        assert np.array_equal(mid[p], q8_bytes(ro["middle_q8"])), (path, p)
+    if path in ("decode", "stream"):
+        assert np.array_equal(yh.view(np.uint32), ref["y"].view(np.uint32)), path
+    else:
+        err_ = float(np.max(np.abs(yh.astype(np.float64) - ref["y"])))
+        scale = float(np.sqrt(np.mean(np.square(ref["y"].astype(np.float64)))))
+        assert err_ <= 1e-5 * scale, (path, err_, scale)
+    L.close()
