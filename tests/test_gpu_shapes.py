@@ -218,3 +218,41 @@ def test_layer_extreme_shapes(H, I, down, path):
         scale = float(np.sqrt(np.mean(np.square(ref["y"].astype(np.float64)))))
         assert err_ <= 1e-5 * scale, (path, err_, scale)
     L.close()
+
+
+@pytest.mark.parametrize("E", [1024, 4096])
+@pytest.mark.parametrize("N", [16, 300])
+def test_layer_many_experts(E, N):
+    """Up to the 4096 experts a layer accepts, on both grouping forms (one
+    workgroup at 16 tokens, the multi-kernel form at 300): every middle Q8
+    row byte-equal to the oracle's, outputs within 1e-5 rms (bit-identical
+    where every group streams)."""
+    H, I, K = 64, 32, 8
+    bank = W.q4_bank(E, hidden=H, intermediate=I, seed=E + N)
+    shared = W.q4_bank(1, hidden=H, intermediate=I, seed=E + N + 1)
+    x = W.activations(N, hidden=H, seed=E + 2)
+    ids, w = W.routes_zipf(N, 1.1, experts=E, k=K, seed=N + 3)
+    L = moe_ffn.MoeLayer(H, I, E, K, True, N, experts_q4=bank, shared_q4=shared)
+    y, err = L.forward(dev(x), dev(ids), dev(w))
+    yh = host(y)
+    assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh))
+    ref = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=shared)
+    dbg = L.debug_last(N)
+    nbi = I // 32
+    mid = host(dbg["middle_q8"]).reshape(-1, nbi * 36)
+    groups = O.route_groups(ids, w, E)
+    P = int(groups["offsets"][-1])
+    eb = len(bank) // E
+    mb = eb // 3
+    xq = O.quantize_q8(x)
+    for p in range(P + N):
+        if p < P:
+            t, e_bytes = int(groups["token"][p]), bank[int(groups["expert"][p]) * eb:(int(groups["expert"][p]) + 1) * eb]
+        else:
+            t, e_bytes = p - P, shared
+        ro = O.expert_forward(e_bytes[:mb], e_bytes[mb:2 * mb], e_bytes[2 * mb:], H, I, xq[t:t + 1])
+        assert np.array_equal(mid[p], q8_bytes(ro["middle_q8"])), (E, N, p)
+    err_ = float(np.max(np.abs(yh.astype(np.float64) - ref["y"])))
+    scale = float(np.sqrt(np.mean(np.square(ref["y"].astype(np.float64)))))
+    assert err_ <= 1e-5 * scale, (E, N, err_, scale)
+    L.close()
