@@ -172,6 +172,8 @@ EXTREME_SHAPES = [
     (4160, 2080, moe_ffn.DOWN_Q4_1),
     (1024, 1088, moe_ffn.DOWN_Q4_1),   # 34 down blocks with Q4_1 mins; the decode path stops at 32
     (64, 32, moe_ffn.DOWN_Q4_0),       # 2 gate/up blocks and 1 down block a row
+    (16384, 64, moe_ffn.DOWN_Q4_0),    # the longest gate/up rows: 512 blocks, 8 per lane
+    (64, 16384, moe_ffn.DOWN_Q4_1),    # the longest down rows: 512 blocks, 8 per lane
 ]
 
 
