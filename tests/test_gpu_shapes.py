@@ -219,6 +219,10 @@ def test_layer_extreme_shapes(H, I, down, path):
         err_ = float(np.max(np.abs(yh.astype(np.float64) - ref["y"])))
         scale = float(np.sqrt(np.mean(np.square(ref["y"].astype(np.float64)))))
         assert err_ <= 1e-5 * scale, (path, err_, scale)
+    # The same rows as canonical Q8_1 input (moe_ffn_forward_q8): the same bits.
+    yq, errq = L.forward_q8(dev(q8_bytes(ref["x_q8"]).reshape(N, -1)), dev(ids), dev(w))
+    assert int(host(errq)[0]) == 0
+    assert np.array_equal(host(yq).view(np.uint32), yh.view(np.uint32)), (path, "forward_q8")
     L.close()
 
 
