@@ -192,6 +192,7 @@ struct LinearMfmaArgs {
     int nb, M, N;
     int row_tiles;            // Mp / 32
     int col_tiles;            // ceil(N / 32)
+    int waves;                // waves per workgroup: 4, or 8 (two tree nodes a wave)
 };
 hipError_t launch_linear_mfma(const LinearMfmaArgs &a, hipStream_t s);
 

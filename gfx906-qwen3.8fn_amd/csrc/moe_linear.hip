@@ -362,6 +362,13 @@ int launch_mfma(const moe_linear *L, moe::Act xq, const void *x_q8, int columns,
     a.N = columns;
     a.row_tiles = L->Mp / 32;
     a.col_tiles = (columns + 31) / 32;
+    // 8-wave workgroups (two tree nodes a wave) for 64-block rows where the
+    // 4-wave grid gives at most one workgroup per CU (us, 4 -> 8 waves,
+    // forward_q8 cold: 2048 x 2048 at N = 80 / 128 10.5 / 11.1 -> 9.45 /
+    // 10.5, 2048 x 512 at N = 320 / 512 10.2 / 10.9 -> 9.25 / 10.45, 2048 x
+    // 1024 at N = 160 / 256 10.3 / 10.9 -> 9.35 / 10.5; larger grids lose:
+    // 2048 x 2048 at N = 192 / 1032 16.0 / 54.5 -> 17.2 / 67.5).
+    a.waves = L->nb == 64 && static_cast<long>(a.row_tiles) * a.col_tiles <= 256 ? 8 : 4;
     return moe::launch_linear_mfma(a, s);
 }
 

@@ -1674,17 +1674,30 @@ __device__ __forceinline__ void subtree4_merge(int q, float (&w)[16], float (&l1
 }
 
 // wn: the wave's first node's weight half, already in flight (grouped folds).
-template<int Fold, bool Canon>
-__device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint32_t w_off, int wave, int lane,
-                                         uint4 (&wn)[2], float (&res)[16]) {
+// The two-node form for 8-wave workgroups: res = node 0 + node 1.
+__device__ __forceinline__ void subtree2_merge(int q, float (&w)[16], float (&l1)[16], float (&res)[16]) {
+    if ((q & 1) == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) l1[i] = w[i];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) res[i] = l1[i] + w[i];
+}
+
+// NPW level-1 nodes per wave (4: a 4-wave workgroup, 2: an 8-wave one).
+template<int Fold, bool Canon, int NPW>
+__device__ __forceinline__ void subtree(const GuTile &t, const GuStage &g, uint32_t w_off, int wave, int lane,
+                                        uint4 (&wn)[2], float (&res)[16]) {
+    static_assert(NPW == 4 || NPW == 2, "subtree: 2 or 4 nodes per wave");
     const int m = lane & 31, h = lane >> 5;
     float l1[16], l2[16];
     if constexpr (Fold == kFoldGrouped || Fold == kFoldGrouped96) {
         constexpr bool X = Fold == kFoldGrouped96;
         // Node q + 1's weight half is in flight while node q computes.
 #pragma unroll 1
-        for (int q = 0; q < 4; ++q) {
-            const int p = 4 * wave + q;
+        for (int q = 0; q < NPW; ++q) {
+            const int p = NPW * wave + q;
             HalfGroup G;
             G.w[0] = wn[0];
             G.w[1] = wn[1];
@@ -1693,18 +1706,19 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
             if constexpr (X) {
                 if (2 * p < t.nb - 64) extra_load<Canon>(t, p, E);   // uniform
             }
-            half_load_w(t, w_off, q < 3 ? p + 1 : p, wn);
+            half_load_w(t, w_off, q < NPW - 1 ? p + 1 : p, wn);
             float w[16], x[16];
             leaf_grouped<false, X>(t, g, G, 0, 2 * p, m, h, w, &E);
             leaf_grouped<false, X>(t, g, G, 1, 2 * p + 1, m, h, x, &E);
 #pragma unroll
             for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
-            subtree4_merge(q, w, l1, l2, res);
+            if constexpr (NPW == 4) subtree4_merge(q, w, l1, l2, res);
+            else subtree2_merge(q, w, l1, res);
         }
     } else {
 #pragma unroll 1
-        for (int q = 0; q < 4; ++q) {
-            const int p = 4 * wave + q;
+        for (int q = 0; q < NPW; ++q) {
+            const int p = NPW * wave + q;
             float w[16], x[16];
             if constexpr (Fold == kFoldStaged) {
                 leaf_staged<false, false, Canon>(t, g, 2 * p, m, h, w);
@@ -1715,16 +1729,22 @@ __device__ __forceinline__ void subtree4(const GuTile &t, const GuStage &g, uint
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) w[i] = w[i] + x[i];
-            subtree4_merge(q, w, l1, l2, res);
+            if constexpr (NPW == 4) subtree4_merge(q, w, l1, l2, res);
+            else subtree2_merge(q, w, l1, res);
         }
     }
 }
 
 // Canon: the columns are canonical Q8_1 blocks, read in place (codes at
 // byte 4 of each 36-byte block, the head at byte 0); else the split planes.
-template<int Fold, bool Canon>
-__global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
-    __shared__ float roots[4][16][64];          // subtree roots [wave][value][lane]
+// W = 8: eight waves of two level-1 nodes each, the roots combined
+// ((R0 + R1) + (R2 + R3)) + ((R4 + R5) + (R6 + R7)) -- the same tree levels
+// as the 4-wave form's (R0 + R1) + (R2 + R3) over 4-node subtrees -- for
+// launches whose 4-wave grid leaves SIMDs with one wave.
+template<int Fold, bool Canon, int W = 4>
+__global__ __launch_bounds__(64 * W, W == 8 ? 1 : 2) void k_linear_mfma(LinearMfmaArgs a) {
+    constexpr int NPW = 16 / W, VPW = 16 / W;   // level-1 nodes and finished values per wave
+    __shared__ float roots[W][16][64];          // subtree roots [wave][value][lane]
     __shared__ uint4 d4_lds[Fold == kFoldGrouped96 ? kGu96MaxBlocks : kGuMaxBlocks][4];   // [block][32 halfs]
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int id = static_cast<int>(blockIdx.x), local = id >> 3;
@@ -1762,7 +1782,7 @@ __global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
     // two round trips overlap.
     const uint32_t w_off = static_cast<uint32_t>(prow) * row_bytes + 32u * 16u * h;
     uint4 wn[2] = {};
-    if constexpr (Fold == kFoldGrouped || Fold == kFoldGrouped96) half_load_w(t, w_off, 4 * wave, wn);
+    if constexpr (Fold == kFoldGrouped || Fold == kFoldGrouped96) half_load_w(t, w_off, NPW * wave, wn);
     if constexpr (Fold != kFoldMulti) {
         // Scale group g (rows 8g..8g+7) of block b lands at halfs 8g..8g+7 of d4_lds[b].
         for (int c = threadIdx.x; c < 4 * nb; c += blockDim.x) {
@@ -1773,36 +1793,45 @@ __global__ __launch_bounds__(256, 2) void k_linear_mfma(LinearMfmaArgs a) {
     }
     const GuStage g{reinterpret_cast<const uint32_t *>(&d4_lds[0][0]), nullptr};
     float res[16];
-    subtree4<Fold, Canon>(t, g, w_off, wave, lane, wn, res);
+    subtree<Fold, Canon, NPW>(t, g, w_off, wave, lane, wn, res);
 #pragma unroll
     for (int v = 0; v < 16; ++v) roots[wave][v][lane] = res[v];
     __syncthreads();
-    // Wave w finishes values 4w..4w+3: rows R0 + 16h + 4w + i of column c0 + m.
+    // Wave w finishes values VPW w .. VPW w + VPW - 1: rows R0 + 16h + VPW w + i
+    // of column c0 + m.
     const int c = c0 + m;
-    const int row = R0 + 16 * h + 4 * wave;
+    const int row = R0 + 16 * h + VPW * wave;
     if (c >= a.N || row >= a.M) return;
-    float out[4];
+    float out[VPW];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int v = 4 * wave + i;
-        out[i] = (roots[0][v][lane] + roots[1][v][lane]) + (roots[2][v][lane] + roots[3][v][lane]);
+    for (int i = 0; i < VPW; ++i) {
+        const int v = VPW * wave + i;
+        const float q0 = (roots[0][v][lane] + roots[1][v][lane]) + (roots[2][v][lane] + roots[3][v][lane]);
+        if constexpr (W == 4) out[i] = q0;
+        else out[i] = q0 + ((roots[4][v][lane] + roots[5][v][lane]) + (roots[6][v][lane] + roots[7][v][lane]));
     }
     float *yr = a.y + static_cast<size_t>(c) * a.M + row;
-    if (row + 4 <= a.M && (a.M & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
-        *reinterpret_cast<float4 *>(yr) = make_float4(out[0], out[1], out[2], out[3]);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (row + i < a.M) yr[i] = out[i];
+    if constexpr (W == 4) {
+        if (row + 4 <= a.M && (a.M & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
+            *reinterpret_cast<float4 *>(yr) = make_float4(out[0], out[1], out[2], out[3]);
+            return;
+        }
     }
+#pragma unroll
+    for (int i = 0; i < VPW; ++i)
+        if (row + i < a.M) yr[i] = out[i];
 }
 
 }  // namespace
 
 namespace {
-template<bool Canon>
+template<bool Canon, int W>
 void launch_linear_mfma_t(const LinearMfmaArgs &a, unsigned grid, hipStream_t s) {
-    if (a.nb == kGuMaxBlocks) k_linear_mfma<kFoldGrouped, Canon><<<grid, 256, 0, s>>>(a);
+    constexpr unsigned T = 64 * W;
+    // Only 64-block rows take the 8-wave form: for the other folds the
+    // compiler's register allocator (with the iterative-ILP scheduler this
+    // file is built with) fails on it.
+    if (a.nb == kGuMaxBlocks) k_linear_mfma<kFoldGrouped, Canon, W><<<grid, T, 0, s>>>(a);
     else if (a.nb > kGuMaxBlocks && a.nb <= kGu96MaxBlocks) k_linear_mfma<kFoldGrouped96, Canon><<<grid, 256, 0, s>>>(a);
     else if (a.nb < kGuMaxBlocks) k_linear_mfma<kFoldStaged, Canon><<<grid, 256, 0, s>>>(a);
     else k_linear_mfma<kFoldMulti, Canon><<<grid, 256, 0, s>>>(a);
@@ -1811,8 +1840,14 @@ void launch_linear_mfma_t(const LinearMfmaArgs &a, unsigned grid, hipStream_t s)
 
 hipError_t launch_linear_mfma(const LinearMfmaArgs &a, hipStream_t s) {
     const unsigned grid = static_cast<unsigned>((a.row_tiles + 7) / 8 * 8) * static_cast<unsigned>(a.col_tiles);
-    if (a.q8) launch_linear_mfma_t<true>(a, grid, s);
-    else launch_linear_mfma_t<false>(a, grid, s);
+    const bool w8 = a.waves == 8;
+    if (a.q8) {
+        if (w8) launch_linear_mfma_t<true, 8>(a, grid, s);
+        else launch_linear_mfma_t<true, 4>(a, grid, s);
+    } else {
+        if (w8) launch_linear_mfma_t<false, 8>(a, grid, s);
+        else launch_linear_mfma_t<false, 4>(a, grid, s);
+    }
     return hipGetLastError();
 }
 
