@@ -233,10 +233,12 @@ namespace {
 constexpr int kInvalid = hipErrorInvalidValue;
 constexpr int kMfmaMinColumns = 32;        // one MFMA column tile
 // Outputs (rows x columns) from which the MFMA kernel beats the vector one
-// (measured on MI355X: 2048 x 2048 at 64 columns 12.4 vs 12.6 us, at 128
-// columns 22.6 vs 13.5 us; 512 rows at 256 columns 12.2 vs 12.9 us, at 384
-// columns 17.2 vs 13.3 us; 8192 rows at 32 columns 78 vs 56 us).
-constexpr long kMfmaMinOutputs = 160 * 1024;
+// (MI355X, cold weights, vector / MFMA us with the per-launch vector plans
+// and the 8-wave MFMA form: 2048 x 2048 at 32 / 48 / 64 columns 6.6 / 9.9 /
+// 10.6 against 8.65 / 8.87 / 9.0; 512 rows at 128 / 192 / 256 columns 6.35 /
+// 9.8 / 10.6 against 8.3 / 8.6 / 8.9; 2560 x 2560 at 48 columns 19.0 against
+// 13.3; 8192 rows at 32 columns 56.8 against 48.2).
+constexpr long kMfmaMinOutputs = 96 * 1024;
 
 bool aligned(const void *p, size_t a) { return p && reinterpret_cast<uintptr_t>(p) % a == 0; }
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
