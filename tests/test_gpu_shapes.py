@@ -262,3 +262,68 @@ def test_layer_many_experts(E, N):
     scale = float(np.sqrt(np.mean(np.square(ref["y"].astype(np.float64)))))
     assert err_ <= 1e-5 * scale, (E, N, err_, scale)
     L.close()
+
+
+def _random_configs(n, seed):
+    """Seeded layer configurations inside the ranges the shape tests cover
+    (H multiple of 64 up to 4096, I multiple of 32 up to 1024)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        H = 64 * int(rng.integers(1, 65))
+        I = 32 * int(rng.integers(1, 33))
+        E = int(rng.choice([1, 2, 3, 7, 16, 33, 64]))
+        k = int(rng.integers(1, min(E, 20) + 1))
+        shared = bool(rng.integers(0, 2))
+        q41 = bool(rng.integers(0, 2))
+        N = int(rng.choice([1, 2, 5, 17, 40, 96]))
+        out.append((H, I, E, k, shared, q41, N))
+    return out
+
+
+@pytest.mark.parametrize("cfg", _random_configs(16, 2026))
+def test_layer_random_configs(cfg):
+    """Seeded random layers (hidden, intermediate, experts, top-k, shared
+    expert or not, Q4_0 or Q4_1 downs, batch size) on every path they allow:
+    every middle Q8 row byte-equal to the oracle's; outputs bit-identical on
+    the streaming path and, where it applies, the decode path, within 1e-5
+    rms on the MFMA path and the automatic choice."""
+    H, I, E, k, shared, q41, N = cfg
+    down = moe_ffn.DOWN_Q4_1 if q41 else moe_ffn.DOWN_Q4_0
+    seed = H * 7 + I * 3 + E + k + N
+    bank = W.q4_bank(E, hidden=H, intermediate=I, seed=seed, down_type=1 if q41 else 0)
+    sh = W.q4_bank(1, hidden=H, intermediate=I, seed=seed + 1, down_type=1 if q41 else 0) if shared else None
+    x = W.activations(N, hidden=H, seed=seed + 2)
+    ids, w = W.routes_zipf(N, 1.0, experts=E, k=k, seed=seed + 3)
+    ref = O.moe_layer(x, H, I, E, bank, ids, w, shared_q4=sh, down_q41=q41)
+    groups = O.route_groups(ids, w, E)
+    P = int(groups["offsets"][-1])
+    eb = len(bank) // E
+    mb = (H // 32) * I * 18
+    xq = O.quantize_q8(x)
+    middles = []
+    for p in range(P + (N if shared else 0)):
+        if p < P:
+            t, e_bytes = int(groups["token"][p]), bank[int(groups["expert"][p]) * eb:(int(groups["expert"][p]) + 1) * eb]
+        else:
+            t, e_bytes = p - P, sh
+        ro = O.expert_forward(e_bytes[:mb], e_bytes[mb:2 * mb], e_bytes[2 * mb:], H, I, xq[t:t + 1], down_q41=q41)
+        middles.append(q8_bytes(ro["middle_q8"]))
+    decode_fits = H <= 4096 and I <= 1024 and k + (1 if shared else 0) <= 16
+    for path in PATHS:
+        if path == "decode" and not decode_fits:
+            continue
+        L = _layer_env(PATHS[path], H, I, E, k, shared, N, experts_q4=bank, shared_q4=sh, down_type=down)
+        y, err = L.forward(dev(x), dev(ids), dev(w))
+        yh = host(y)
+        assert int(host(err)[0]) == 0 and np.all(np.isfinite(yh)), (cfg, path)
+        mid = host(L.debug_last(N)["middle_q8"]).reshape(-1, (I // 32) * 36)
+        for p, m in enumerate(middles):
+            assert np.array_equal(mid[p], m), (cfg, path, p)
+        if path in ("decode", "stream"):
+            assert np.array_equal(yh.view(np.uint32), ref["y"].view(np.uint32)), (cfg, path)
+        else:
+            err_ = float(np.max(np.abs(yh.astype(np.float64) - ref["y"])))
+            scale = float(np.sqrt(np.mean(np.square(ref["y"].astype(np.float64)))))
+            assert err_ <= 1e-5 * scale, (cfg, path, err_, scale)
+        L.close()
