@@ -327,3 +327,40 @@ def test_layer_random_configs(cfg):
             scale = float(np.sqrt(np.mean(np.square(ref["y"].astype(np.float64)))))
             assert err_ <= 1e-5 * scale, (cfg, path, err_, scale)
         L.close()
+
+
+@pytest.mark.parametrize("N", [8, 300])
+def test_two_layers_on_two_streams(N):
+    """Two layer handles forwarding at once on two streams (decode path at 8
+    tokens, grouped at 300) give the bits each gives alone: no state is
+    shared between handles."""
+    H, I, E, K = 1024, 256, 64, 8
+    layers, inputs, alone = [], [], []
+    for j in range(2):
+        bank = W.q4_bank(E, hidden=H, intermediate=I, seed=300 + j)
+        shared = W.q4_bank(1, hidden=H, intermediate=I, seed=310 + j)
+        L = moe_ffn.MoeLayer(H, I, E, K, True, N, experts_q4=bank, shared_q4=shared)
+        x = dev(W.activations(N, hidden=H, seed=320 + j))
+        ids, w = W.routes_zipf(N, 1.1, experts=E, k=K, seed=330 + j)
+        inp = (x, dev(ids), dev(w))
+        y, err = L.forward(*inp)
+        alone.append(host(y).copy())
+        assert int(host(err)[0]) == 0
+        layers.append(L)
+        inputs.append(inp)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = []
+    for _ in range(3):
+        for j in range(2):
+            y = torch.empty((N, H), dtype=torch.float32, device=DEV)
+            err = torch.zeros(1, dtype=torch.int32, device=DEV)
+            streams[j].wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(streams[j]):
+                layers[j].forward(*inputs[j], y=y, error=err, stream=streams[j])
+            outs.append((j, y, err))
+    torch.cuda.synchronize()
+    for j, y, err in outs:
+        assert int(host(err)[0]) == 0
+        assert np.array_equal(host(y).view(np.uint32), alone[j].view(np.uint32)), (N, j)
+    for L in layers:
+        L.close()
